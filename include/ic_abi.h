@@ -1,0 +1,127 @@
+/*
+ * ic_abi.h - C ABI of the MI355X (gfx950) per-layer quantization library
+ * (libicq.so).
+ *
+ * Conventions
+ *  - All pointers are DEVICE pointers owned by the caller; matrices are
+ *    row-major with an explicit leading dimension in elements.
+ *  - Every call is asynchronous on `stream` (a hipStream_t passed as void*,
+ *    NULL = default stream) and returns IC_OK (0) or a negative IC_ERR_*;
+ *    ic_last_error() returns the message of the last failure in this thread.
+ *  - Scratch memory is passed in by the caller; its size comes from the
+ *    matching *_workspace_bytes() query.  No entry point allocates device
+ *    memory unless its comment says so.
+ *  - fp16 values travel as uint16_t bit patterns.
+ *
+ * Each entry point names the reference function whose arithmetic it
+ * replaces (paths relative to the reference repository root).
+ */
+#ifndef IC_ABI_H
+#define IC_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IC_OK 0
+#define IC_ERR_ARG (-1)
+#define IC_ERR_HIP (-2)
+#define IC_ERR_RANGE (-3)
+
+#define IC_DTYPE_F32 0
+#define IC_DTYPE_BF16 1
+#define IC_DTYPE_F16 2
+
+#define IC_ABI_VERSION 1
+
+int ic_abi_version(void);
+const char* ic_last_error(void);
+
+/* ---------------------------------------------------------------- rotation */
+
+/* Group-wise Hadamard rotation of rows: dst[r, :] = pad(src[r, :]) @ Hr^T for
+ * every group of `rot` columns, where Hr is the regular Hadamard (H4/2)^kron
+ * for powers of 4 and the normalised Sylvester matrix for other powers of 2.
+ * src is f32/bf16/f16 [rows, cols] (ld_src), dst is f32 [rows, cols_pad]
+ * (ld_dst) with cols_pad = cols rounded up to a multiple of rot; the padding
+ * is zero before rotation.  src may alias dst when dtype is f32 and
+ * ld_src == ld_dst.  rot: power of 2 in [1, 4096].
+ * Replaces converter/rotation.py:95-125 (rotate_weights) and :128-153
+ * (rotate_activations, same operation on a [-1, in] view). */
+int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                   float* dst, int64_t cols_pad, int64_t ld_dst, int rot, void* stream);
+
+/* Two-sided rotation R^T H R of `batch` square fp32 matrices [n, n] stored
+ * back to back with leading dimension ld (n multiple of rot), in place.
+ * Replaces converter/rotation.py:156-248 (rotate_hessian, after padding). */
+int ic_rotate_hessian(float* H, int64_t batch, int64_t n, int64_t ld, int rot, void* stream);
+
+/* Per-row min / max / max-abs of an fp32 matrix; NaN propagates like
+ * torch.amin/amax.  Any output pointer may be NULL.
+ * Replaces the amin/amax/abs().amax reductions of converter/scales.py:85,
+ * 144, 258-259, 338-339 and converter/gptq.py:257-258, 316. */
+int ic_row_stats(const float* x, int64_t rows, int64_t cols, int64_t ld,
+                 float* row_min, float* row_max, float* row_absmax, void* stream);
+
+/* ---------------------------------------------------------------- RTN */
+
+/* Per-row (= per group, with groups laid out as rows) RTN scales and
+ * zero-points, with the optional clipping-ratio MSE search.
+ *   bits 4 or 8; asym 0/1; ratios: HOST array of n_ratios (<= 16) floats.
+ *   out scale16[rows] fp16 bits; zp[rows] int8 (asym only, else may be NULL).
+ * Replaces converter/scales.py:25-99 (calculate_scales), 126-160
+ * (calculate_scales_int8), 184-229 (_fix_asymmetric_scale), 232-282
+ * (calculate_scales_asymmetric), 316-361 (calculate_scales_int8_asymmetric). */
+int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t ld, int bits, int asym,
+                  const float* ratios, int n_ratios, uint16_t* scale16, int8_t* zp, void* stream);
+
+/* RTN codes q = clamp(rhaz(W / scale [+ zp])) per row, scale[rows] read as
+ * fp16 bits (scale_kind 0) or fp32 (1), zp[rows] fp32 (integral) or NULL.
+ * Writes int8 codes [rows, cols] (ld_q) when `codes` is not NULL and packed
+ * INT4 bytes [rows, ceil(cols/2)] (ld_p) when `packed` is not NULL (bits 4).
+ * Replaces converter/scales.py:102-123, 163-178, 285-313, 364-384
+ * (quantize_weights*), fused with converter/packing.py:30-46. */
+int ic_rtn_quantize(const float* W, int64_t rows, int64_t cols, int64_t ld, int bits,
+                    const void* scale, int scale_kind, const float* zp,
+                    int8_t* codes, int64_t ld_q, uint8_t* packed, int64_t ld_p, void* stream);
+
+/* ---------------------------------------------------------------- packing */
+
+/* Validate and pack INT4 values.  src: int8 (src_kind 0) or f32 (1)
+ * [rows, cols] (ld_src); dst uint8 [rows, ceil(cols/2)] (ld_dst), low nibble =
+ * even column, odd tail padded with 0; dst NULL validates only.  flags
+ * (device int32[3]) receives {any non-finite, any value < -8, any value > 7}
+ * so the caller can raise INT4PackingError exactly like
+ * converter/packing.py:17-27; the bytes are only meaningful when all three
+ * flags are 0.  f32 values are truncated toward zero like .to(torch.int8).
+ * Replaces converter/packing.py:17-46 (validate_int4_range, pack_int4). */
+int ic_pack_int4(const void* src, int src_kind, int64_t rows, int64_t cols, int64_t ld_src,
+                 uint8_t* dst, int64_t ld_dst, int32_t* flags, void* stream);
+
+/* Unpack INT4 bytes to int8 [rows, k].  Replaces converter/packing.py:49-66. */
+int ic_unpack_int4(const uint8_t* src, int64_t rows, int64_t k, int64_t ld_src,
+                   int8_t* dst, int64_t ld_dst, void* stream);
+
+/* ---------------------------------------------------------------- verification */
+
+/* Quantisation error of codes against W: dequant = (q - zp) * scale with
+ * scale read as fp16 bits (scale_kind 0) or fp32 (1) and zp NULL or int8.
+ * Writes the fp64 sum of squared errors and the max |error| into
+ * out_sumsq[0] / out_maxabs[0] (device).  mse = sumsq / (rows*cols).  The
+ * reduction order is fixed, so repeated calls give identical bits.
+ * workspace: ic_quant_error_workspace_bytes() bytes of device memory.
+ * Replaces converter/pipeline.py:919-937 and the metric lines of
+ * converter/gptq.py:398-405, ldlq.py:262-269. */
+int64_t ic_quant_error_workspace_bytes(void);
+int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld,
+                   const int8_t* codes, int64_t ld_q, const void* scale, int scale_kind,
+                   const int8_t* zp, double* out_sumsq, float* out_maxabs, void* workspace,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IC_ABI_H */

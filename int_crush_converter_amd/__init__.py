@@ -1,0 +1,32 @@
+"""MI355X-native per-layer quantization path of int_crush_converter.
+
+Public names mirror the reference package ``converter`` (its ``__init__.py``)
+for the hot path: rotation, RTN scales, packing, GPTQ / LDLQ layers, the
+pipeline and the value types.  All arithmetic runs in the gfx950 HIP library
+``libicq.so`` (see ``include/ic_abi.h``); there is no CPU fallback.
+"""
+
+from .rotation import rotate_weights, rotate_activations, rotate_hessian, make_hadamard_regular, get_hadamard
+from .packing import pack_int4, unpack_int4, validate_int4_range
+from .scales import (
+    calculate_scales,
+    quantize_weights,
+    calculate_scales_int8,
+    quantize_weights_int8,
+    calculate_scales_asymmetric,
+    quantize_weights_asymmetric,
+    calculate_scales_int8_asymmetric,
+    quantize_weights_int8_asymmetric,
+)
+from .config import INT4_SCALE_DIVISOR, INT8_SCALE_DIVISOR
+from .types import QuantizationResult, QuantizeConfig, ProgressInfo, ProgressSummary, ProgressCallback
+
+__all__ = [
+    "rotate_weights", "rotate_activations", "rotate_hessian", "make_hadamard_regular", "get_hadamard",
+    "pack_int4", "unpack_int4", "validate_int4_range",
+    "calculate_scales", "quantize_weights", "calculate_scales_int8", "quantize_weights_int8",
+    "calculate_scales_asymmetric", "quantize_weights_asymmetric",
+    "calculate_scales_int8_asymmetric", "quantize_weights_int8_asymmetric",
+    "INT4_SCALE_DIVISOR", "INT8_SCALE_DIVISOR",
+    "QuantizationResult", "QuantizeConfig", "ProgressInfo", "ProgressSummary", "ProgressCallback",
+]

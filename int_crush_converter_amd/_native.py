@@ -1,0 +1,126 @@
+"""Loader and thin typed wrappers for the HIP library ``libicq.so``.
+
+There is no fallback: if the library is missing or no GPU is visible, every
+compute entry point raises ``RuntimeError``.  Tensors live on the GPU; CPU
+tensors handed to the public API are copied to ``cuda:0`` and results are
+copied back by the calling module.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import threading
+
+import torch
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libicq.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG), "include", "ic_abi.h")
+
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+
+_lib = None
+_lock = threading.Lock()
+
+_c = ctypes
+_vp = _c.c_void_p
+_i64 = _c.c_int64
+_i32 = _c.c_int
+_f32 = _c.c_float
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "ic_abi_version": (_i32, []),
+    "ic_last_error": (_c.c_char_p, []),
+    "ic_rotate_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
+    "ic_rotate_hessian": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp]),
+    "ic_row_stats": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "ic_rtn_scales": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _c.POINTER(_f32), _i32, _vp, _vp, _vp]),
+    "ic_rtn_quantize": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "ic_pack_int4": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "ic_unpack_int4": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "ic_quant_error_workspace_bytes": (_i64, []),
+    "ic_quant_error": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+}
+
+
+def header_functions() -> list[str]:
+    """Names of the functions declared in include/ic_abi.h."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ic_[a-z0-9_]+)\s*\(", text)))
+
+
+def load(require_gpu: bool = True):
+    """Load the library once; raise RuntimeError if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "(hipcc --offload-arch=gfx950).  There is no CPU fallback.")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def lib():
+    if not torch.cuda.is_available():
+        raise RuntimeError("int_crush_converter_amd needs a ROCm GPU (gfx950); none is visible")
+    return load()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.ic_last_error().decode(errors="replace") if _lib is not None else ""
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def device() -> torch.device:
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_gpu(t: torch.Tensor) -> torch.Tensor:
+    """Move a tensor to the current GPU (no copy if already there)."""
+    lib()
+    if t.device.type == "cuda":
+        return t
+    return t.to(device(), non_blocking=False)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DT_F32
+    if t.dtype == torch.bfloat16:
+        return DT_BF16
+    if t.dtype == torch.float16:
+        return DT_F16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def row_ld(t: torch.Tensor) -> int:
+    """Leading dimension of a 2-D tensor whose rows are contiguous."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("expected a 2-D tensor with contiguous rows")
+    return max(t.stride(0), t.shape[1]) if t.shape[0] > 1 else t.shape[1]

@@ -1,0 +1,105 @@
+// Shared device/host helpers for the gfx950 kernels of the quantization path.
+//
+// Numerics contract: every file is compiled with -ffp-contract=off and
+// IEEE-correct fp32 division, so a*b+c is two roundings unless a kernel asks
+// for __builtin_fmaf explicitly, and x/y is the correctly rounded quotient.
+// The bit-exact parts of the path (RTN codes, the in-block GPTQ/LDLQ sweep,
+// packing) rely on this to reproduce the reference's fp32 roundings.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/ic_abi.h"
+
+namespace icq {
+
+// ------------------------------------------------------------ error state
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define IC_CHECK_HIP(expr)                                                        \
+    do {                                                                          \
+        hipError_t e_ = (expr);                                                   \
+        if (e_ != hipSuccess)                                                     \
+            return ::icq::fail(IC_ERR_HIP, std::string(#expr " failed: ") +       \
+                                               hipGetErrorString(e_));            \
+    } while (0)
+
+#define IC_CHECK_LAUNCH() IC_CHECK_HIP(hipGetLastError())
+
+#define IC_REQUIRE(cond, msg)                                                     \
+    do {                                                                          \
+        if (!(cond)) return ::icq::fail(IC_ERR_ARG, msg);                         \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------ element access
+
+__device__ __forceinline__ float load_as_f32(const void* p, int dtype, int64_t i) {
+    if (dtype == IC_DTYPE_F32) return reinterpret_cast<const float*>(p)[i];
+    uint16_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    if (dtype == IC_DTYPE_BF16) return __uint_as_float(uint32_t(h) << 16);
+    return __half2float(__ushort_as_half(h));
+}
+
+// Round half away from zero exactly as floor(x + 0.5) / ceil(x - 0.5) in fp32.
+// The +-0.5 is an fp32 addition (rounded), e.g. 0.49999997f -> 1.
+__device__ __forceinline__ float rhaz(float x) {
+    return x >= 0.0f ? floorf(x + 0.5f) : ceilf(x - 0.5f);
+}
+
+// Round half to even (torch.round).
+__device__ __forceinline__ float rhte(float x) { return rintf(x); }
+
+__device__ __forceinline__ float clampf(float x, float lo, float hi) {
+    // torch.clamp(x, lo, hi) = min(max(x, lo), hi); NaN propagates.
+    return x != x ? x : fminf(fmaxf(x, lo), hi);
+}
+
+// fp32 -> fp16 with round-to-nearest-even (matches tensor.to(torch.float16)).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    return __half_as_ushort(__float2half_rn(x));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+// Total-order key of an fp32 value so that unsigned comparisons order floats.
+__device__ __forceinline__ uint32_t float_key(float x) {
+    uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+// ------------------------------------------------------------ wave reductions
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+}  // namespace icq

@@ -1,0 +1,377 @@
+// Row statistics, RTN scales / zero-points (with clipping-ratio search), RTN
+// quantisation fused with INT4 packing, pack/unpack, and the quantisation
+// error used for verification.  All bandwidth-bound; one wave owns one row
+// for the row-wise reductions, elementwise kernels stream 16 columns per lane.
+//
+// Bit-exactness: codes and fp16 scales reproduce the fp32 formulas of
+// converter/scales.py exactly (IEEE division, no contraction, rhaz with the
+// literal +-0.5, round-half-even in the clip search).  The clip-search MSE is
+// accumulated in fp64, so only candidates whose fp32 MSEs tie to within the
+// reference's own fp32 summation noise could be chosen differently.
+#include "common.hpp"
+
+namespace icq {
+
+// NaN-propagating min/max (torch.amin / amax / maximum semantics).
+__device__ __forceinline__ float nmax(float a, float b) { return (a != a || a > b) ? a : b; }
+__device__ __forceinline__ float nmin(float a, float b) { return (a != a || a < b) ? a : b; }
+
+__device__ __forceinline__ float wave_nmax(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = nmax(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_nmin(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = nmin(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+struct RowStats { float mn, mx, amax; };
+
+__device__ RowStats row_stats_wave(const float* __restrict__ x, int64_t cols) {
+    const int lane = threadIdx.x & 63;
+    float mn = INFINITY, mx = -INFINITY, am = 0.0f;
+    for (int64_t c = lane; c < cols; c += 64) {
+        float v = x[c];
+        mn = nmin(mn, v); mx = nmax(mx, v); am = nmax(am, fabsf(v));
+    }
+    return {wave_nmin(mn), wave_nmax(mx), wave_nmax(am)};
+}
+
+__global__ __launch_bounds__(256) void row_stats_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                        int64_t ld, float* rmin, float* rmax, float* ramax) {
+    const int64_t wpb = blockDim.x >> 6;
+    for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
+        RowStats s = row_stats_wave(x + r * ld, cols);
+        if ((threadIdx.x & 63) == 0) {
+            if (rmin) rmin[r] = s.mn;
+            if (rmax) rmax[r] = s.mx;
+            if (ramax) ramax[r] = s.amax;
+        }
+    }
+}
+
+__device__ __forceinline__ float clamp_scale(float s) { return clampf(s, 1e-5f, 65500.0f); }
+
+// Zero-point clamp fix of converter/scales.py:184-229 (both masks are taken
+// from the incoming scale, then the two corrections apply in order).
+__device__ __forceinline__ float fix_asym(float s, float wmin, float wmax, float qmin, float qmax) {
+    const float spread = qmax - qmin;
+    float zraw = qmin - rhaz(wmin / s);
+    bool lo = zraw < qmin, hi = zraw > qmax;
+    if (lo) s = nmax(s, clamp_scale(wmax / spread));
+    if (hi) s = nmax(s, clamp_scale(-wmin / spread));
+    return s;
+}
+
+// Candidate scale of one clip ratio (or of the plain formula when !has_ratio).
+struct Cand { float s, z; };
+
+// Clipping ratios travel by value in the kernel arguments.
+constexpr int MAX_RATIOS = 16;
+struct Ratios { float v[MAX_RATIOS]; };
+
+__device__ __forceinline__ Cand rtn_candidate(const RowStats& st, int bits, int asym, bool has_ratio, float ratio) {
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    Cand c;
+    if (!asym) {
+        const float div = bits == 4 ? 7.0f : 127.0f;
+        float a = has_ratio ? st.amax * ratio : st.amax;
+        c.s = clamp_scale(a / div);
+        c.z = 0.0f;
+    } else {
+        const float spread = bits == 4 ? 15.0f : 255.0f;
+        float range = st.mx - st.mn;
+        if (has_ratio) range = range * ratio;
+        float s = clamp_scale(range / spread);
+        s = fix_asym(s, st.mn, st.mx, qmin, qmax);
+        c.s = s;
+        c.z = clampf(qmin - rhaz(st.mn / s), qmin, qmax);
+    }
+    return c;
+}
+
+// One wave per row: stats, then either the closed form or the clip search.
+__global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
+                                                         int64_t ld, int bits, int asym, int n_ratios,
+                                                         Ratios rt, uint16_t* __restrict__ scale16, int8_t* __restrict__ zp) {
+    const int64_t wpb = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
+        const float* x = W + r * ld;
+        RowStats st = row_stats_wave(x, cols);
+        Cand best;
+        if (n_ratios == 0) {
+            best = rtn_candidate(st, bits, asym, false, 1.0f);
+            // zero groups map zero to zero in the INT4 closed form only (scales.py:265-267)
+            if (asym && bits == 4 && st.mn == 0.0f && st.mx == 0.0f) best.z = 0.0f;
+        } else {
+            double best_m = 0.0;
+            for (int k = 0; k < n_ratios; ++k) {
+                float ratio = rt.v[k];
+                Cand c = rtn_candidate(st, bits, asym, true, ratio);
+                double acc = 0.0;
+                for (int64_t j = lane; j < cols; j += 64) {
+                    float w = x[j];
+                    float d;
+                    if (asym) {
+                        float q = clampf(rhte(w / c.s + c.z), qmin, qmax);
+                        d = (q - c.z) * c.s;
+                    } else {
+                        float q = clampf(rhte(w / c.s), qmin, qmax);
+                        d = q * c.s;
+                    }
+                    float e = w - d;
+                    acc += (double)e * (double)e;
+                }
+                acc = wave_sum(acc);
+                // strict '<' keeps the first ratio on ties; NaN never wins
+                if (k == 0 || acc < best_m) { best = c; best_m = acc; }
+            }
+        }
+        if (lane == 0) {
+            scale16[r] = f32_to_f16_bits(best.s);
+            if (asym && zp) zp[r] = (int8_t)(int)best.z;
+        }
+    }
+}
+
+__device__ __forceinline__ uint8_t nib(float q) { return (uint8_t)(((int)q) & 0xF); }
+
+// 16 columns per lane.  codes: int8 [rows, ld_q]; packed: uint8 [rows, ld_p].
+__global__ __launch_bounds__(256) void rtn_quant_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
+                                                        int64_t ld, int bits, const void* __restrict__ scale,
+                                                        int scale_kind, const float* __restrict__ zp,
+                                                        int8_t* __restrict__ codes, int64_t ld_q,
+                                                        uint8_t* __restrict__ packed, int64_t ld_p) {
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    const int64_t cpr = cdiv(cols, 16);
+    const int64_t total = rows * cpr;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = g / cpr;
+        const int64_t c0 = (g - r * cpr) * 16;
+        const float s = scale_kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[r])
+                                        : reinterpret_cast<const float*>(scale)[r];
+        const float z = zp ? zp[r] : 0.0f;
+        const float* x = W + r * ld + c0;
+        float q[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (c0 + i < cols) {
+                float y = x[i] / s;
+                if (zp) y = y + z;
+                q[i] = clampf(rhaz(y), qmin, qmax);
+            } else {
+                q[i] = 0.0f;
+            }
+        }
+        if (codes) {
+            int8_t* o = codes + r * ld_q + c0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (c0 + i < cols) o[i] = (int8_t)(int)q[i];
+        }
+        if (packed) {
+            uint8_t* o = packed + r * ld_p + c0 / 2;
+#pragma unroll
+            for (int i = 0; i < 16; i += 2)
+                if (c0 + i < cols) o[i / 2] = (uint8_t)(nib(q[i]) | (nib(q[i + 1]) << 4));
+        }
+    }
+}
+
+// flags: [0] any non-finite, [1] any value < -8, [2] any value > 7
+__global__ __launch_bounds__(256) void pack_int4_kernel(const void* __restrict__ src, int kind, int64_t rows,
+                                                        int64_t cols, int64_t ld_src, uint8_t* __restrict__ dst,
+                                                        int64_t ld_dst, int32_t* flags) {
+    const int64_t bpr = cdiv(cols, 2);
+    const int64_t total = rows * bpr;
+    int nf = 0, lo = 0, hi = 0;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = g / bpr;
+        const int64_t c = (g - r * bpr) * 2;
+        int v[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (c + i < cols) {
+                if (kind == 0) {
+                    v[i] = reinterpret_cast<const int8_t*>(src)[r * ld_src + c + i];
+                } else {
+                    float f = reinterpret_cast<const float*>(src)[r * ld_src + c + i];
+                    nf |= !isfinite(f);
+                    lo |= f < -8.0f;
+                    hi |= f > 7.0f;
+                    v[i] = isfinite(f) ? (int)f : 0;   // .to(int8) truncates toward zero
+                }
+                lo |= v[i] < -8;
+                hi |= v[i] > 7;
+            } else {
+                v[i] = 0;
+            }
+        }
+        if (dst) dst[r * ld_dst + c / 2] = (uint8_t)((v[0] & 0xF) | ((v[1] & 0xF) << 4));
+    }
+    if (__any(nf)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 0, 1); }
+    if (__any(lo)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 1, 1); }
+    if (__any(hi)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 2, 1); }
+}
+
+__global__ void unpack_int4_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t k, int64_t ld_src,
+                                   int8_t* __restrict__ dst, int64_t ld_dst) {
+    const int64_t total = rows * k;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = g / k, c = g - r * k;
+        uint8_t b = src[r * ld_src + c / 2];
+        int v = (c & 1) ? (b >> 4) : (b & 0xF);
+        dst[r * ld_dst + c] = (int8_t)(v >= 8 ? v - 16 : v);
+    }
+}
+
+constexpr int QERR_BLOCKS = 1024;
+
+__global__ __launch_bounds__(256) void quant_error_partial(const float* __restrict__ W, int64_t rows, int64_t cols,
+                                                           int64_t ld, const int8_t* __restrict__ codes, int64_t ld_q,
+                                                           const void* __restrict__ scale, int scale_kind,
+                                                           const int8_t* __restrict__ zp, double* part_sum,
+                                                           float* part_max) {
+    const int64_t total = rows * cols;
+    double acc = 0.0;
+    float mx = 0.0f;
+    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = g / cols, c = g - r * cols;
+        float s = scale_kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[r])
+                                  : reinterpret_cast<const float*>(scale)[r];
+        float q = (float)codes[r * ld_q + c];
+        float d = zp ? (q - (float)zp[r]) * s : q * s;
+        float e = W[r * ld + c] - d;
+        acc += (double)e * (double)e;
+        mx = nmax(mx, fabsf(e));
+    }
+    __shared__ double ss[4];
+    __shared__ float sm[4];
+    acc = wave_sum(acc);
+    mx = wave_nmax(mx);
+    if ((threadIdx.x & 63) == 0) { ss[threadIdx.x >> 6] = acc; sm[threadIdx.x >> 6] = mx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double a = 0.0;
+        float m = 0.0f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) { a += ss[w]; m = nmax(m, sm[w]); }
+        part_sum[blockIdx.x] = a;
+        part_max[blockIdx.x] = m;
+    }
+}
+
+__global__ void quant_error_final(const double* part_sum, const float* part_max, int n, double* out_sum,
+                                  float* out_max) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        double a = 0.0;
+        float m = 0.0f;
+        for (int i = 0; i < n; ++i) { a += part_sum[i]; m = nmax(m, part_max[i]); }
+        *out_sum = a;
+        *out_max = m;
+    }
+}
+
+static int rows_grid(int64_t rows, int waves_per_block) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(rows, waves_per_block), 65535));
+}
+static int elem_grid(int64_t work) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 256 * 64));
+}
+
+}  // namespace icq
+
+using namespace icq;
+
+extern "C" int ic_row_stats(const float* x, int64_t rows, int64_t cols, int64_t ld, float* row_min, float* row_max,
+                            float* row_absmax, void* stream) {
+    IC_REQUIRE(x && ld >= cols, "ic_row_stats: bad arguments");
+    if (rows == 0) return IC_OK;
+    hipLaunchKernelGGL(row_stats_kernel, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), x, rows, cols,
+                       ld, row_min, row_max, row_absmax);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t ld, int bits, int asym,
+                             const float* ratios, int n_ratios, uint16_t* scale16, int8_t* zp, void* stream) {
+    IC_REQUIRE(W && scale16 && ld >= cols && cols > 0, "ic_rtn_scales: bad arguments");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_rtn_scales: bits must be 4 or 8");
+    IC_REQUIRE(!asym || zp, "ic_rtn_scales: asymmetric needs zp output");
+    IC_REQUIRE(n_ratios >= 0 && n_ratios <= MAX_RATIOS, "ic_rtn_scales: at most 16 clipping ratios are supported");
+    IC_REQUIRE(n_ratios == 0 || ratios, "ic_rtn_scales: null ratios");
+    if (rows == 0) return IC_OK;
+    Ratios rt;
+    for (int i = 0; i < MAX_RATIOS; ++i) rt.v[i] = i < n_ratios ? ratios[i] : 1.0f;
+    hipLaunchKernelGGL(rtn_scales_kernel, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows, cols,
+                       ld, bits, asym, n_ratios, rt, scale16, zp);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int ic_rtn_quantize(const float* W, int64_t rows, int64_t cols, int64_t ld, int bits,
+                               const void* scale, int scale_kind, const float* zp, int8_t* codes, int64_t ld_q,
+                               uint8_t* packed, int64_t ld_p, void* stream) {
+    IC_REQUIRE(W && scale && ld >= cols, "ic_rtn_quantize: bad arguments");
+    IC_REQUIRE(scale_kind == 0 || scale_kind == 1, "ic_rtn_quantize: scale_kind must be 0 (f16) or 1 (f32)");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_rtn_quantize: bits must be 4 or 8");
+    IC_REQUIRE(!packed || bits == 4, "ic_rtn_quantize: packing needs bits == 4");
+    IC_REQUIRE(!codes || ld_q >= cols, "ic_rtn_quantize: bad ld_q");
+    IC_REQUIRE(!packed || ld_p >= cdiv(cols, 2), "ic_rtn_quantize: bad ld_p");
+    if (rows == 0 || cols == 0) return IC_OK;
+    hipLaunchKernelGGL(rtn_quant_kernel, dim3(elem_grid(rows * cdiv(cols, 16))), dim3(256), 0, as_stream(stream), W,
+                       rows, cols, ld, bits, scale, scale_kind, zp, codes, ld_q, packed, ld_p);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int ic_pack_int4(const void* src, int src_kind, int64_t rows, int64_t cols, int64_t ld_src,
+                            uint8_t* dst, int64_t ld_dst, int32_t* flags, void* stream) {
+    IC_REQUIRE(src && flags && ld_src >= cols && (!dst || ld_dst >= cdiv(cols, 2)), "ic_pack_int4: bad arguments");
+    IC_REQUIRE(src_kind == 0 || src_kind == 1, "ic_pack_int4: src_kind must be 0 (int8) or 1 (f32)");
+    hipStream_t st = as_stream(stream);
+    IC_CHECK_HIP(hipMemsetAsync(flags, 0, 3 * sizeof(int32_t), st));
+    if (rows == 0 || cols == 0) return IC_OK;
+    hipLaunchKernelGGL(pack_int4_kernel, dim3(elem_grid(rows * cdiv(cols, 2))), dim3(256), 0, st, src, src_kind, rows,
+                       cols, ld_src, dst, ld_dst, flags);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int ic_unpack_int4(const uint8_t* src, int64_t rows, int64_t k, int64_t ld_src, int8_t* dst,
+                              int64_t ld_dst, void* stream) {
+    IC_REQUIRE(src && dst && ld_src >= cdiv(k, 2) && ld_dst >= k, "ic_unpack_int4: bad arguments");
+    if (rows == 0 || k == 0) return IC_OK;
+    hipLaunchKernelGGL(unpack_int4_kernel, dim3(elem_grid(rows * k)), dim3(256), 0, as_stream(stream), src, rows, k,
+                       ld_src, dst, ld_dst);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int64_t ic_quant_error_workspace_bytes(void) {
+    return QERR_BLOCKS * (int64_t)(sizeof(double) + sizeof(float));
+}
+
+extern "C" int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld, const int8_t* codes,
+                              int64_t ld_q, const void* scale, int scale_kind, const int8_t* zp, double* out_sumsq,
+                              float* out_maxabs, void* workspace, void* stream) {
+    IC_REQUIRE(W && codes && scale && out_sumsq && out_maxabs && workspace, "ic_quant_error: null pointer");
+    IC_REQUIRE(ld >= cols && ld_q >= cols, "ic_quant_error: bad leading dimension");
+    IC_REQUIRE(scale_kind == 0 || scale_kind == 1, "ic_quant_error: scale_kind must be 0 (f16) or 1 (f32)");
+    hipStream_t st = as_stream(stream);
+    double* ps = reinterpret_cast<double*>(workspace);
+    float* pm = reinterpret_cast<float*>(ps + QERR_BLOCKS);
+    hipLaunchKernelGGL(quant_error_partial, dim3(QERR_BLOCKS), dim3(256), 0, st, W, rows, cols, ld, codes, ld_q,
+                       scale, scale_kind, zp, ps, pm);
+    IC_CHECK_LAUNCH();
+    hipLaunchKernelGGL(quant_error_final, dim3(1), dim3(64), 0, st, ps, pm, QERR_BLOCKS, out_sumsq, out_maxabs);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}

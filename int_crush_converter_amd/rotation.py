@@ -1,0 +1,151 @@
+"""ConvRot group-wise Hadamard rotation (API of ``converter/rotation.py``).
+
+``make_hadamard_*`` / ``get_hadamard`` build the dense matrices (used for
+reference and inverse transforms by callers); the rotations themselves run as
+a fast Walsh-Hadamard transform in the HIP library (``ic_rotate_rows``,
+``ic_rotate_hessian``): 2·log4(R) flops per element instead of the dense
+R-wide dot product.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import _native as nat
+
+_hadamard_cache: dict[tuple[int, str, str], torch.Tensor] = {}
+
+
+def _is_power_of_four(n: int) -> bool:
+    return n >= 4 and (n & (n - 1)) == 0 and (n & 0x55555555) == n
+
+
+def _is_power_of_two(n: int) -> bool:
+    return n > 0 and (n & (n - 1)) == 0
+
+
+def make_hadamard_sylvester(n: int, dtype: torch.dtype = torch.float16, device: str = "cpu") -> torch.Tensor:
+    """Normalised Sylvester Hadamard matrix (reference rotation.py:26-36)."""
+    if not _is_power_of_two(n):
+        raise ValueError(f"n must be a power of 2, got {n}")
+    h = torch.ones(1, 1, dtype=dtype, device=device)
+    base = torch.tensor([[1.0, 1.0], [1.0, -1.0]], dtype=dtype, device=device)
+    while h.shape[0] < n:
+        h = torch.kron(base, h)
+    return h * (1.0 / math.sqrt(n))
+
+
+def make_hadamard_regular(n: int, dtype: torch.dtype = torch.float16, device: str = "cpu") -> torch.Tensor:
+    """Regular Hadamard (H4/2)^{kron k} for n = 4^k (reference rotation.py:39-62)."""
+    if not _is_power_of_four(n):
+        raise ValueError(f"Regular Hadamard requires power of 4, got {n}. Use rot_size=16/64/256.")
+    h4 = torch.tensor([[1.0, 1.0, 1.0, -1.0],
+                       [1.0, 1.0, -1.0, 1.0],
+                       [1.0, -1.0, 1.0, 1.0],
+                       [-1.0, 1.0, 1.0, 1.0]], dtype=dtype, device=device) / 2.0
+    h = h4
+    while h.shape[0] < n:
+        h = torch.kron(h, h4)
+    return h
+
+
+def get_hadamard(size: int, dtype: torch.dtype = torch.float16, device: str = "cpu") -> torch.Tensor:
+    key = (size, str(dtype), str(device))
+    if key not in _hadamard_cache:
+        _hadamard_cache[key] = make_hadamard_regular(size, dtype=dtype, device=device)
+    return _hadamard_cache[key]
+
+
+def clear_hadamard_cache() -> None:
+    _hadamard_cache.clear()
+
+
+def _check_rot(rot_size: int) -> None:
+    if not _is_power_of_two(rot_size):
+        raise ValueError(f"rot_size must be a power of 2, got {rot_size}")
+    if rot_size > 4096:
+        raise ValueError(f"rot_size {rot_size} exceeds the supported maximum 4096")
+
+
+def rotate_rows_gpu(W: torch.Tensor, rot_size: int) -> torch.Tensor:
+    """Rotate the rows of a 2-D GPU tensor (f32/bf16/f16) into a fresh fp32
+    [rows, cols_pad] GPU tensor.  Internal fast path used by the pipeline."""
+    W = W.contiguous()
+    rows, cols = W.shape
+    cols_pad = -(-cols // rot_size) * rot_size
+    out = torch.empty(rows, cols_pad, dtype=torch.float32, device=W.device)
+    L = nat.lib()
+    nat.check(L.ic_rotate_rows(W.data_ptr(), nat.dtype_code(W), rows, cols, cols, out.data_ptr(),
+                               cols_pad, cols_pad, rot_size, nat.stream()), "ic_rotate_rows")
+    return out
+
+
+def rotate_weights(W: torch.Tensor, rot_size: int) -> torch.Tensor:
+    """[out, in] -> [out, in_padded]: zero-pad to a multiple of ``rot_size`` and
+    rotate every group of ``rot_size`` columns (reference rotation.py:95-125).
+    The result has W's dtype and device; arithmetic is fp32."""
+    if W.dim() != 2:
+        raise ValueError(f"Expected 2D tensor, got {W.dim()}D")
+    _check_rot(rot_size)
+    if W.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        W = W.float()
+    out = rotate_rows_gpu(nat.to_gpu(W), rot_size)
+    if W.dtype != torch.float32:
+        out = out.to(W.dtype)
+    return out.to(W.device)
+
+
+def rotate_activations(x: torch.Tensor, rot_size: int) -> torch.Tensor:
+    """Same rotation on the last dimension of any-rank activations
+    (reference rotation.py:128-153)."""
+    _check_rot(rot_size)
+    lead = x.shape[:-1]
+    flat = x.reshape(-1, x.shape[-1])
+    out = rotate_weights(flat, rot_size) if flat.shape[0] > 0 else F.pad(flat, (0, (-flat.shape[1]) % rot_size))
+    return out.reshape(*lead, out.shape[-1])
+
+
+def rotate_hessian_gpu(H: torch.Tensor, rot_size: int) -> torch.Tensor:
+    """R^T H R of a 2-D or 3-D fp32 GPU Hessian (padded first for 2-D); a new
+    tensor.  Internal fast path used by the GPTQ/LDLQ drivers."""
+    H = H.float().contiguous()
+    if H.dim() == 2:
+        n = H.shape[0]
+        if n % rot_size:
+            p = rot_size - n % rot_size
+            H = F.pad(H, (0, p, 0, p))
+        else:
+            H = H.clone()
+        batch, n = 1, H.shape[0]
+    else:
+        batch, n = H.shape[0], H.shape[1]
+        H = H.clone()
+    if H.numel():
+        nat.check(nat.lib().ic_rotate_hessian(H.data_ptr(), batch, n, n, rot_size, nat.stream()),
+                  "ic_rotate_hessian")
+    return H
+
+
+def rotate_hessian(H, rot_size: int):
+    """Hessian in the rotated weight space: H_rot = R^T H R (reference
+    rotation.py:156-248).  2-D input is zero-padded to a multiple of
+    ``rot_size``; 3-D [blocks, bs, bs] input needs bs % rot_size == 0."""
+    if not _is_power_of_two(rot_size):
+        raise ValueError(f"rot_size must be a power of 2, got {rot_size}")
+    if isinstance(H, dict):
+        raise NotImplementedError("DLR Hessians are not supported by this build")
+    if H.dim() == 2:
+        if H.shape[0] != H.shape[1]:
+            raise ValueError(f"Expected square Hessian, got {H.shape}")
+    elif H.dim() == 3:
+        if H.shape[1] != H.shape[2]:
+            raise ValueError(f"Expected square blocks, got block shape ({H.shape[1]}, {H.shape[2]})")
+        if H.shape[1] % rot_size != 0:
+            raise ValueError(f"Block size {H.shape[1]} is not divisible by rot_size {rot_size}")
+    else:
+        raise ValueError(f"Expected 2D or 3D Hessian, got {H.dim()}D")
+    _check_rot(rot_size)
+    return rotate_hessian_gpu(nat.to_gpu(H), rot_size).to(H.device)

@@ -1,0 +1,185 @@
+"""Write golden input/output vectors from the reference implementation.
+
+Run in the development container only (the reference is not present on the
+GPU box):
+
+    PYTHONPATH=/root/reference python tests/golden/make_golden.py
+
+It covers the functions whose results no closed form pins bit for bit
+because they depend on fp32 LAPACK/BLAS rounding or fp32 reduction order:
+GPTQ / LDLQ / greedy codes, LDLQ iteration decisions, clipping-ratio choices
+and a small end-to-end pipeline file.  Every case is a small seeded input;
+the outputs are stored as ``.safetensors`` next to this script.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+import tempfile
+
+import torch
+from safetensors.torch import save_file, load_file
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF = os.environ.get("IC_REFERENCE", "/root/reference")
+sys.path.insert(0, REF)
+
+from converter.gptq import gptq_quantize_layer, gptq_quantize_layer_rtn  # noqa: E402
+from converter.ldlq import ldlq_quantize_layer  # noqa: E402
+from converter.scales import (  # noqa: E402
+    calculate_scales, calculate_scales_asymmetric,
+    calculate_scales_int8, calculate_scales_int8_asymmetric,
+)
+from converter.rotation import rotate_weights, rotate_hessian  # noqa: E402
+from converter.pipeline import quantize_model  # noqa: E402
+from converter.types import QuantizeConfig  # noqa: E402
+
+
+def lognormal_hessian(n: int, samples: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    s = torch.exp(torch.randn(n, generator=g))
+    X = torch.randn(samples, n, generator=g) * s
+    return X.T @ X / samples
+
+
+def weights(m: int, n: int, seed: int, std: float = 0.02) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(m, n, generator=g) * std
+
+
+def gptq_cases(out: dict, meta: dict) -> None:
+    cases = [
+        # name, M, N, samples, bits, asym, method, block, rot
+        ("gptq_a", 32, 256, 512, 4, False, "hinv", 128, 0),
+        ("gptq_b", 48, 256, 128, 4, False, "hinv", 64, 256),
+        ("gptq_c", 64, 512, 256, 4, False, "hinv", 128, 256),
+        ("gptq_d", 32, 192, 400, 8, False, "hinv", 128, 64),
+        ("gptq_e", 32, 256, 400, 8, True, "hinv", 128, 16),
+        ("gptq_f", 32, 256, 300, 4, False, "cholesky", 128, 0),
+    ]
+    for i, (name, M, N, S, bits, asym, hm, B, rot) in enumerate(cases):
+        W = weights(M, N, 100 + i)
+        H = lognormal_hessian(N, S, 200 + i)
+        if rot:
+            W = rotate_weights(W, rot)
+            H = rotate_hessian(H, rot)
+        r = gptq_quantize_layer(W, H, block_size=B, damping=0.01, int_bits=bits,
+                                asymmetric=asym, hessian_method=hm)
+        out[f"{name}.W"] = W.contiguous()
+        out[f"{name}.H"] = H.contiguous()
+        out[f"{name}.q"] = r.quantized_W
+        out[f"{name}.scales"] = r.scales
+        if r.zero_points is not None:
+            out[f"{name}.zp"] = r.zero_points
+        meta[name] = dict(kind="gptq", bits=bits, asym=asym, method=hm, block=B,
+                          mse=r.mse, max_err=r.max_err)
+    # 3-D block-diagonal Hessian
+    M, N, bs = 32, 512, 256
+    W = weights(M, N, 150)
+    g = torch.Generator().manual_seed(250)
+    blocks = []
+    for _ in range(N // bs):
+        s = torch.exp(torch.randn(bs, generator=g))
+        X = torch.randn(300, bs, generator=g) * s
+        blocks.append(X.T @ X / 300)
+    H3 = torch.stack(blocks)
+    r = gptq_quantize_layer(W, H3, block_size=128, damping=0.01, int_bits=4)
+    out["gptq3d.W"] = W
+    out["gptq3d.H"] = H3
+    out["gptq3d.q"] = r.quantized_W
+    out["gptq3d.scales"] = r.scales
+    out["gptq3d.zp"] = r.zero_points
+    meta["gptq3d"] = dict(kind="gptq", bits=4, asym=False, method="hinv", block=128,
+                          mse=r.mse, max_err=r.max_err)
+
+
+def ldlq_cases(out: dict, meta: dict) -> None:
+    cases = [
+        # name, M, N, bits, iters, greedy, block, with_H
+        ("ldlq_a", 32, 128, 4, 1, 0, 64, False),
+        ("ldlq_b", 32, 128, 4, 2, 0, 128, False),
+        ("ldlq_c", 24, 96, 4, 2, 3, 32, False),
+        ("ldlq_d", 32, 128, 8, 1, 2, 64, False),
+        ("ldlq_e", 32, 128, 4, 1, 2, 64, True),
+    ]
+    for i, (name, M, N, bits, iters, gp, B, with_h) in enumerate(cases):
+        g = torch.Generator().manual_seed(300 + i)
+        W = torch.randn(M, N, generator=g) * 0.02
+        H = lognormal_hessian(N, 256, 400 + i) if with_h else None
+        import warnings
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            r = ldlq_quantize_layer(W, hessian=H, block_size=B, damping=0.01, int_bits=bits,
+                                    iterations=iters, greedy_passes=gp)
+        out[f"{name}.W"] = W
+        if H is not None:
+            out[f"{name}.H"] = H
+        out[f"{name}.q"] = r.quantized_W
+        out[f"{name}.scales"] = r.scales
+        meta[name] = dict(kind="ldlq", bits=bits, iters=iters, greedy=gp, block=B,
+                          mse=r.mse, max_err=r.max_err, method_used=r.method_used)
+
+
+def clip_cases(out: dict, meta: dict) -> None:
+    g = torch.Generator().manual_seed(500)
+    W = torch.randn(64, 512, generator=g) * 0.02
+    cols = torch.randperm(512, generator=g)[:5]
+    W[:, cols] *= 20
+    ratios = [0.8, 0.85, 0.9, 0.95, 1.0]
+    out["clip.W"] = W
+    out["clip.s4"] = calculate_scales(W, W.shape[1], clipping_ratios=ratios)
+    s, z = calculate_scales_asymmetric(W, W.shape[1], clipping_ratios=ratios)
+    out["clip.s4a"], out["clip.z4a"] = s, z
+    out["clip.s8"] = calculate_scales_int8(W, clipping_ratios=ratios)
+    s, z = calculate_scales_int8_asymmetric(W, clipping_ratios=ratios)
+    out["clip.s8a"], out["clip.z8a"] = s, z
+    meta["clip"] = dict(kind="clip", ratios=ratios)
+
+
+def pipeline_cases(out: dict, meta: dict) -> None:
+    # C1-shaped RTN run (8 layers [64,256] fp32, rot 256, INT4)
+    g = torch.Generator().manual_seed(42)
+    state = {f"layers.{i}.q_proj.weight": torch.randn(64, 256, generator=g) * 0.02
+             for i in range(8)}
+    state["layers.0.q_proj.bias"] = torch.randn(64, generator=g)
+    state["model.norm.weight"] = torch.randn(256, generator=g)
+    # a layer whose in_features is not a multiple of 256 (padding path)
+    state["layers.9.up.weight"] = torch.randn(16, 200, generator=g) * 0.02
+    with tempfile.TemporaryDirectory() as td:
+        src = os.path.join(td, "in.safetensors")
+        save_file(state, src)
+        for tag, kw in [("pipe_rtn4", dict(rot_size=256, int_bits=4)),
+                        ("pipe_rtn8a", dict(rot_size=64, int_bits=8, asymmetric=True,
+                                            clipping_ratios=[0.8, 0.85, 0.9, 0.95, 1.0]))]:
+            od = os.path.join(td, tag)
+            quantize_model(QuantizeConfig(input_path=src, output_dir=od, **kw))
+            res = load_file(os.path.join(od, "model.safetensors"))
+            from safetensors import safe_open
+            with safe_open(os.path.join(od, "model.safetensors"), framework="pt") as f:
+                md = f.metadata()
+            for k, v in res.items():
+                out[f"{tag}/{k}"] = v
+            meta[tag] = dict(kind="pipeline", config=kw, metadata=md)
+        for k, v in state.items():
+            out[f"pipe_in/{k}"] = v
+
+
+def main() -> None:
+    torch.set_num_threads(1)
+    out: dict[str, torch.Tensor] = {}
+    meta: dict = {}
+    gptq_cases(out, meta)
+    ldlq_cases(out, meta)
+    clip_cases(out, meta)
+    pipeline_cases(out, meta)
+    out = {k: v.contiguous() for k, v in out.items()}
+    save_file(out, os.path.join(HERE, "golden.safetensors"))
+    with open(os.path.join(HERE, "golden.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+    print(f"wrote {len(out)} tensors, {len(meta)} cases")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,188 @@
+"""GPU parity: rotation, RTN scales/codes, clipping search, INT4 packing and
+the verification error, HIP library vs the CPU oracle.
+
+Bars: codes, packed bytes and fp16 scales bit-exact given the same fp32
+input (RTN is integer-valued arithmetic on identical fp32 operands);
+rotation within 2e-6 relative to the row norm (the FWHT and the reference's
+dense GEMM round differently); fp64 MSE within 1e-9 relative.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import torch_ref as ref
+from tests.conftest import lognormal_hessian
+
+pytestmark = pytest.mark.gpu
+
+RATIOS = [0.8, 0.85, 0.9, 0.95, 1.0]
+
+
+def _w(m, n, seed, std=0.02, outliers=0):
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(m, n, generator=g) * std
+    if outliers:
+        cols = torch.randperm(n, generator=g)[:outliers]
+        W[:, cols] *= 20
+    return W
+
+
+@pytest.mark.parametrize("rot", [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024])
+@pytest.mark.parametrize("n", [256, 300])
+def test_rotate_weights_matches_oracle(gpu_dev, rot, n):
+    from int_crush_converter_amd.rotation import rotate_weights
+    W = _w(33, n, rot + n, std=1.0)
+    want = ref.rotate_weights(W, rot)
+    got = rotate_weights(W.to(gpu_dev), rot).cpu()
+    assert got.shape == want.shape and got.dtype == torch.float32
+    tol = 2e-6 * W.norm(dim=1, keepdim=True).clamp(min=1)
+    assert torch.all((got - want).abs() <= tol), (got - want).abs().max()
+
+
+def test_rotate_weights_bf16_source(gpu_dev):
+    from int_crush_converter_amd.rotation import rotate_rows_gpu
+    W = _w(64, 4096, 3).to(torch.bfloat16)
+    want = ref.rotate_weights(W.float(), 256)
+    got = rotate_rows_gpu(W.to(gpu_dev), 256).cpu()
+    assert torch.allclose(got, want, atol=1e-7, rtol=0)
+
+
+def test_rotate_weights_deterministic(gpu_dev):
+    from int_crush_converter_amd.rotation import rotate_rows_gpu
+    W = _w(128, 1024, 4).to(gpu_dev)
+    a = rotate_rows_gpu(W, 256)
+    b = rotate_rows_gpu(W, 256)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("rot,n", [(16, 64), (64, 192), (256, 512), (256, 300), (128, 256)])
+def test_rotate_hessian_2d(gpu_dev, rot, n):
+    from int_crush_converter_amd.rotation import rotate_hessian
+    H = lognormal_hessian(n, 2 * n, 5)
+    want = ref.rotate_hessian(H, rot)
+    got = rotate_hessian(H.to(gpu_dev), rot).cpu()
+    assert got.shape == want.shape
+    assert torch.allclose(got, want, atol=2e-6 * want.abs().max().item(), rtol=0)
+
+
+def test_rotate_hessian_3d(gpu_dev):
+    from int_crush_converter_amd.rotation import rotate_hessian
+    H = torch.stack([lognormal_hessian(256, 300, s) for s in range(3)])
+    want = ref.rotate_hessian(H, 64)
+    got = rotate_hessian(H.to(gpu_dev), 64).cpu()
+    assert torch.allclose(got, want, atol=2e-6 * want.abs().max().item(), rtol=0)
+
+
+@pytest.mark.parametrize("bits,asym", [(4, False), (4, True), (8, False), (8, True)])
+@pytest.mark.parametrize("ratios", [None, RATIOS])
+def test_rtn_bit_exact(gpu_dev, bits, asym, ratios):
+    from int_crush_converter_amd import scales as S
+    W = ref.rotate_weights(_w(97, 320, bits * 10 + asym, outliers=3), 64)
+    W[5] = 0.0                # zero row
+    W[6] = W[6] + 3.0         # far from zero: zero-point clamp fix
+    W[7] = W[7] - 4.0
+    Wg = W.to(gpu_dev)
+    s_want, z_want, q_want = None, None, None
+    if bits == 4 and not asym:
+        s_want = ref.scales_int4_sym(W, W.shape[1], ratios)
+        q_want = ref.quant_int4_sym(W, s_want, W.shape[1])
+        s_got = S.calculate_scales(Wg, W.shape[1], clipping_ratios=ratios)
+        q_got = S.quantize_weights(Wg, s_got, W.shape[1])
+    elif bits == 4:
+        s_want, z_want = ref.scales_int4_asym(W, W.shape[1], ratios)
+        q_want = ref.quant_int4_asym(W, s_want, z_want, W.shape[1])
+        s_got, z_got = S.calculate_scales_asymmetric(Wg, W.shape[1], clipping_ratios=ratios)
+        q_got = S.quantize_weights_asymmetric(Wg, s_got, z_got, W.shape[1])
+    elif not asym:
+        s_want = ref.scales_int8_sym(W, ratios)
+        q_want = ref.quant_int8_sym(W, s_want)
+        s_got = S.calculate_scales_int8(Wg, clipping_ratios=ratios)
+        q_got = S.quantize_weights_int8(Wg, s_got)
+    else:
+        s_want, z_want = ref.scales_int8_asym(W, ratios)
+        q_want = ref.quant_int8_asym(W, s_want, z_want)
+        s_got, z_got = S.calculate_scales_int8_asymmetric(Wg, clipping_ratios=ratios)
+        q_got = S.quantize_weights_int8_asymmetric(Wg, s_got, z_got)
+    assert torch.equal(s_got.cpu(), s_want)
+    if z_want is not None:
+        assert torch.equal(z_got.cpu(), z_want)
+    assert torch.equal(q_got.cpu(), q_want)
+
+
+def test_rtn_group_wise(gpu_dev):
+    from int_crush_converter_amd import scales as S
+    W = _w(16, 200, 9, std=1.0)
+    for gs in (32, 64, 128):
+        s_want = ref.scales_int4_sym(W, gs, RATIOS)
+        got = S.calculate_scales(W.to(gpu_dev), group_size=gs, clipping_ratios=RATIOS).cpu()
+        assert torch.equal(got, s_want)
+        assert torch.equal(S.quantize_weights(W.to(gpu_dev), got.to(gpu_dev), gs).cpu(),
+                           ref.quant_int4_sym(W, s_want, gs))
+
+
+def test_clip_golden_gpu(gpu_dev, golden):
+    from int_crush_converter_amd import scales as S
+    t, _ = golden
+    W = t["clip.W"].to(gpu_dev)
+    assert torch.equal(S.calculate_scales(W, W.shape[1], clipping_ratios=RATIOS).cpu(), t["clip.s4"])
+    s, z = S.calculate_scales_asymmetric(W, W.shape[1], clipping_ratios=RATIOS)
+    assert torch.equal(s.cpu(), t["clip.s4a"]) and torch.equal(z.cpu(), t["clip.z4a"])
+    assert torch.equal(S.calculate_scales_int8(W, clipping_ratios=RATIOS).cpu(), t["clip.s8"])
+    s, z = S.calculate_scales_int8_asymmetric(W, clipping_ratios=RATIOS)
+    assert torch.equal(s.cpu(), t["clip.s8a"]) and torch.equal(z.cpu(), t["clip.z8a"])
+
+
+def test_rtn_extreme_values(gpu_dev):
+    """fp16 scale clamp limits (reference tests/test_scales.py:369-496)."""
+    from int_crush_converter_amd import scales as S
+    W = torch.cat([torch.full((2, 64), 1e8), torch.full((2, 64), 1e-9), torch.zeros(2, 64)])
+    for fn in (S.calculate_scales, S.calculate_scales_int8):
+        s = fn(W.to(gpu_dev)).cpu()
+        assert s.dtype == torch.float16 and torch.isfinite(s).all() and (s > 0).all()
+    assert torch.equal(S.calculate_scales(W.to(gpu_dev)).cpu(), ref.scales_int4_sym(W, 128))
+
+
+@pytest.mark.parametrize("shape", [(7,), (4, 33), (3, 5, 16), (1, 1)])
+def test_pack_unpack_bit_exact(gpu_dev, shape):
+    from int_crush_converter_amd.packing import pack_int4, unpack_int4
+    g = torch.Generator().manual_seed(1)
+    v = torch.randint(-8, 8, shape, generator=g, dtype=torch.int8)
+    p = pack_int4(v.to(gpu_dev)).cpu()
+    assert torch.equal(p, ref.pack_int4(v))
+    assert torch.equal(unpack_int4(p.to(gpu_dev), shape[-1]).cpu(), v)
+
+
+def test_pack_validation(gpu_dev):
+    from int_crush_converter_amd.packing import pack_int4, validate_int4_range, INT4PackingError
+    with pytest.raises(INT4PackingError):
+        validate_int4_range(torch.tensor([8], dtype=torch.int8, device=gpu_dev))
+    with pytest.raises(INT4PackingError):
+        validate_int4_range(torch.tensor([-9], dtype=torch.int8, device=gpu_dev))
+    with pytest.raises(INT4PackingError):
+        pack_int4(torch.tensor([1.0, float("nan")], device=gpu_dev))
+    validate_int4_range(torch.tensor([-8, -1, 0, 7], device=gpu_dev))
+    # float input is truncated like .to(torch.int8)
+    f = torch.tensor([-7.5, 3.7, 0.2, -0.9], device=gpu_dev)
+    assert torch.equal(pack_int4(f).cpu(), ref.pack_int4(f.cpu().to(torch.int8)))
+
+
+def test_quant_error_matches_oracle(gpu_dev):
+    import ctypes
+    from int_crush_converter_amd import _native as nat
+    W = ref.rotate_weights(_w(64, 512, 2), 256)
+    s, z = ref.scales_int4_asym(W, W.shape[1])
+    q = ref.quant_int4_asym(W, s, z, W.shape[1])
+    d = (q.float() - z.float()) * s.float()
+    want_mse = (W - d).double().pow(2).mean().item()
+    want_max = (W - d).abs().max().item()
+    Wg, qg, sg, zg = (x.to(gpu_dev).contiguous() for x in (W, q, s, z))
+    out_s = torch.zeros(1, dtype=torch.float64, device=gpu_dev)
+    out_m = torch.zeros(1, dtype=torch.float32, device=gpu_dev)
+    ws = torch.empty(nat.lib().ic_quant_error_workspace_bytes(), dtype=torch.uint8, device=gpu_dev)
+    nat.check(nat.lib().ic_quant_error(Wg.data_ptr(), 64, 512, 512, qg.data_ptr(), 512, sg.data_ptr(), 0,
+                                       zg.data_ptr(), out_s.data_ptr(), out_m.data_ptr(), ws.data_ptr(),
+                                       nat.stream()), "ic_quant_error")
+    assert out_s.item() / W.numel() == pytest.approx(want_mse, rel=1e-9)
+    assert out_m.item() == want_max

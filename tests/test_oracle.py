@@ -1,0 +1,351 @@
+"""Pins the CPU oracle (oracle/torch_ref.py) against things other than itself:
+closed forms, the reference's own known-answer tests, independent numpy
+float32 restatements on tiny inputs, brute force, and golden vectors written
+by the reference (tests/golden/).  CPU only."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_ref as ref
+from tests.conftest import lognormal_hessian
+
+f32 = np.float32
+
+
+# ---------------------------------------------------------------- Hadamard
+
+@pytest.mark.parametrize("n", [4, 16, 64, 256])
+def test_hadamard_regular_closed_form(n):
+    H = ref.hadamard_regular(n, torch.float64)
+    k = int(round(math.log(n, 4)))
+    assert torch.all(H.abs() == 2.0 ** -k)
+    assert torch.equal(H, H.T)                        # symmetric
+    assert torch.allclose(H @ H, torch.eye(n, dtype=torch.float64), atol=0, rtol=0)
+    assert torch.all(H.sum(dim=1) == 2.0 ** k / 2.0 ** k * 1.0) or torch.allclose(
+        H.sum(dim=1), torch.full((n,), 2.0 ** k / 2.0 ** k))  # regular: equal row sums
+    # Kronecker structure: H_n = kron(H_{n/4}, H_4)
+    if n > 4:
+        assert torch.equal(H, torch.kron(ref.hadamard_regular(n // 4, torch.float64),
+                                         ref.hadamard_regular(4, torch.float64)))
+
+
+@pytest.mark.parametrize("n", [2, 8, 32, 128])
+def test_hadamard_sylvester_orthonormal(n):
+    H = ref.hadamard_sylvester(n, torch.float64)
+    assert torch.allclose(H @ H.T, torch.eye(n, dtype=torch.float64), atol=1e-12)
+    assert torch.allclose(H.abs(), torch.full_like(H, 1 / math.sqrt(n)), atol=1e-12)
+
+
+def _dense_blockdiag(n_pad, rot):
+    R = torch.zeros(n_pad, n_pad, dtype=torch.float64)
+    h = ref._hadamard_for(rot, torch.float64)
+    for g in range(n_pad // rot):
+        R[g * rot:(g + 1) * rot, g * rot:(g + 1) * rot] = h
+    return R
+
+
+@pytest.mark.parametrize("rot,n", [(16, 64), (64, 192), (256, 256), (256, 300), (128, 256), (32, 40)])
+def test_rotate_weights_vs_dense(rot, n):
+    g = torch.Generator().manual_seed(rot + n)
+    W = torch.randn(9, n, generator=g)
+    out = ref.rotate_weights(W, rot)
+    n_pad = -(-n // rot) * rot
+    Wp = torch.zeros(9, n_pad, dtype=torch.float64)
+    Wp[:, :n] = W.double()
+    want = Wp @ _dense_blockdiag(n_pad, rot).T
+    assert out.shape == (9, n_pad)
+    assert torch.allclose(out.double(), want, atol=1e-5)
+    assert torch.allclose(out.double().norm(), W.double().norm(), rtol=1e-5)
+
+
+@pytest.mark.parametrize("rot,n", [(16, 64), (64, 128), (256, 256), (256, 300)])
+def test_rotate_hessian_two_sided(rot, n):
+    g = torch.Generator().manual_seed(7)
+    X = torch.randn(40, n, generator=g, dtype=torch.float64)
+    H = (X.T @ X).float()
+    out = ref.rotate_hessian(H, rot)
+    n_pad = -(-n // rot) * rot
+    Xp = torch.zeros(40, n_pad, dtype=torch.float64)
+    Xp[:, :n] = X
+    XR = Xp @ _dense_blockdiag(n_pad, rot)          # R symmetric
+    want = XR.T @ XR
+    assert torch.allclose(out.double(), want, atol=1e-3 * want.abs().max().item())
+    assert abs(out.double().trace().item() - H.double().trace().item()) < 1e-4 * H.double().trace().item()
+
+
+def test_rotate_hessian_3d_subblocks():
+    g = torch.Generator().manual_seed(3)
+    H3 = torch.randn(2, 128, 128, generator=g)
+    H3 = H3 @ H3.transpose(1, 2)
+    out = ref.rotate_hessian(H3, 64)
+    for b in range(2):
+        want = ref.rotate_hessian(H3[b], 64)
+        assert torch.allclose(out[b], want, atol=1e-3)
+
+
+# ---------------------------------------------------------------- rounding
+
+def test_rhaz_reference_kats():
+    # tests/unit/test_ldlq_hessian.py:34-49 of the reference
+    assert torch.equal(ref.rhaz(torch.tensor([0.5, 1.5, 2.5, 3.5])), torch.tensor([1.0, 2.0, 3.0, 4.0]))
+    assert torch.equal(ref.rhaz(torch.tensor([-0.5, -1.5, -2.5, -3.5])), torch.tensor([-1.0, -2.0, -3.0, -4.0]))
+    x = torch.tensor([-2.0, -1.0, 0.0, 1.0, 2.0])
+    assert torch.equal(ref.rhaz(x), x)
+
+
+def test_rhaz_literal_add_half():
+    # 0.49999997 + 0.5 rounds to 1.0 in fp32, so rhaz gives 1 (not 0)
+    x = torch.tensor([0.49999997, -0.49999997], dtype=torch.float32)
+    assert torch.equal(ref.rhaz(x), torch.tensor([1.0, -1.0]))
+
+
+def np_rhaz(x):
+    x = f32(x)
+    return f32(np.floor(f32(x + f32(0.5)))) if x >= 0 else f32(np.ceil(f32(x - f32(0.5))))
+
+
+# ---------------------------------------------------------------- scales / RTN
+
+def test_scale_kat():
+    # tests/test_scales.py:48-55 of the reference
+    W = torch.tensor([[1.0, -2.0, 3.0], [-7.0, 1.0, 0.5]])
+    s = ref.scales_int4_sym(W)
+    assert s.dtype == torch.float16 and s.shape == (2, 1)
+    assert abs(s[0].item() - 3 / 7) < 1e-3 and abs(s[1].item() - 1.0) < 1e-3
+
+
+def _np_row_rtn_sym(row, qmax_div, qmin, qmax):
+    amax = f32(np.max(np.abs(row)))
+    s = f32(np.clip(f32(amax / f32(qmax_div)), f32(1e-5), f32(65500)))
+    s16 = f32(np.float16(s))
+    q = [max(qmin, min(qmax, np_rhaz(f32(w / s16)))) for w in row]
+    return np.float16(s), np.array(q, dtype=np.int8)
+
+
+def _np_fix(s, wmin, wmax, qmin, qmax):
+    spread = f32(qmax - qmin)
+    zr = f32(qmin) - np_rhaz(f32(wmin / s))
+    if zr < qmin:
+        s = max(s, f32(np.clip(f32(wmax / spread), f32(1e-5), f32(65500))))
+    if zr > qmax:
+        s = max(s, f32(np.clip(f32(-wmin / spread), f32(1e-5), f32(65500))))
+    return f32(s)
+
+
+def _np_row_rtn_asym(row, qmin, qmax, zero_fix):
+    spread = f32(qmax - qmin)
+    wmin, wmax = f32(np.min(row)), f32(np.max(row))
+    s = f32(np.clip(f32(f32(wmax - wmin) / spread), f32(1e-5), f32(65500)))
+    s = _np_fix(s, wmin, wmax, qmin, qmax)
+    z = max(qmin, min(qmax, f32(qmin) - np_rhaz(f32(wmin / s))))
+    if zero_fix and wmin == 0 and wmax == 0:
+        z = f32(0)
+    s16 = f32(np.float16(s))
+    q = [max(qmin, min(qmax, np_rhaz(f32(f32(w / s16) + f32(z))))) for w in row]
+    return np.float16(s), np.int8(z), np.array(q, dtype=np.int8)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_rtn_formulas_vs_numpy(seed):
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(6, 37, generator=g) * 0.05
+    W[1] = 0.0
+    W[2] += 3.0        # far from zero: exercises the zero-point fix
+    W[3] -= 5.0
+    Wn = W.numpy()
+    s4 = ref.scales_int4_sym(W)
+    q4 = ref.quant_int4_sym(W, s4)
+    s8 = ref.scales_int8_sym(W)
+    q8 = ref.quant_int8_sym(W, s8)
+    s4a, z4a = ref.scales_int4_asym(W)
+    q4a = ref.quant_int4_asym(W, s4a, z4a)
+    s8a, z8a = ref.scales_int8_asym(W)
+    q8a = ref.quant_int8_asym(W, s8a, z8a)
+    for r in range(6):
+        s, q = _np_row_rtn_sym(Wn[r], 7.0, -8, 7)
+        assert s == s4[r, 0].numpy() and np.array_equal(q, q4[r].numpy())
+        s, q = _np_row_rtn_sym(Wn[r], 127.0, -128, 127)
+        assert s == s8[r, 0].numpy() and np.array_equal(q, q8[r].numpy())
+        s, z, q = _np_row_rtn_asym(Wn[r], -8, 7, True)
+        assert s == s4a[r, 0].numpy() and z == z4a[r, 0].numpy() and np.array_equal(q, q4a[r].numpy())
+        s, z, q = _np_row_rtn_asym(Wn[r], -128, 127, False)
+        assert s == s8a[r, 0].numpy() and z == z8a[r, 0].numpy() and np.array_equal(q, q8a[r].numpy())
+
+
+def test_clip_search_brute_force():
+    """Chosen ratio minimises the per-row fp32 MSE; ties keep the first."""
+    g = torch.Generator().manual_seed(11)
+    W = torch.randn(8, 64, generator=g)
+    ratios = [0.8, 0.85, 0.9, 0.95, 1.0]
+    s = ref.scales_int4_sym(W, ratios=ratios)
+    amax = W.abs().amax(dim=1)
+    for r in range(8):
+        best, best_m = None, None
+        for ratio in ratios:
+            cs = torch.clamp(amax[r:r + 1] * ratio / 7.0, 1e-5, 65500)
+            q = (W[r] / cs).round().clamp(-8, 7)
+            m = (W[r] - q * cs).pow(2).mean()
+            if best_m is None or m < best_m:
+                best, best_m = cs, m
+        assert best.half().item() == s[r, 0].item()
+
+
+def test_clip_golden(golden):
+    t, _ = golden
+    W = t["clip.W"]
+    ratios = [0.8, 0.85, 0.9, 0.95, 1.0]
+    assert torch.equal(ref.scales_int4_sym(W, ratios=ratios), t["clip.s4"])
+    s, z = ref.scales_int4_asym(W, ratios=ratios)
+    assert torch.equal(s, t["clip.s4a"]) and torch.equal(z, t["clip.z4a"])
+    assert torch.equal(ref.scales_int8_sym(W, ratios=ratios), t["clip.s8"])
+    s, z = ref.scales_int8_asym(W, ratios=ratios)
+    assert torch.equal(s, t["clip.s8a"]) and torch.equal(z, t["clip.z8a"])
+
+
+# ---------------------------------------------------------------- packing
+
+def test_pack_kat():
+    v = torch.tensor([-8, 7, 0, -1, 1, 2, 3], dtype=torch.int8)
+    p = ref.pack_int4(v)
+    # low nibble = even index; -8 -> 0x8, 7 -> 0x7; -1 -> 0xF; odd tail padded with 0
+    assert p.tolist() == [0x78, 0xF0, 0x21, 0x03]
+    assert torch.equal(ref.unpack_int4(p, 7), v)
+
+
+def test_pack_roundtrip_all_pairs():
+    a = torch.arange(-8, 8, dtype=torch.int8)
+    v = torch.stack(torch.meshgrid(a, a, indexing="ij"), -1).reshape(-1, 2)
+    p = ref.pack_int4(v)
+    assert p.shape == (256, 1) and len(set(p.flatten().tolist())) == 256
+    assert torch.equal(ref.unpack_int4(p, 2), v)
+
+
+# ---------------------------------------------------------------- Hessian inverse
+
+def test_prepare_hinv_is_inverse():
+    H = lognormal_hessian(64, 128, 1)
+    Hi = ref.prepare_hinv(H, 0.01)
+    Hd = ref.damp(H, 0.01).double()
+    assert torch.allclose(Hd @ Hi.double(), torch.eye(64, dtype=torch.float64), atol=1e-3)
+
+
+def test_invert_singular_uses_pinv():
+    H = torch.zeros(8, 8)
+    H[0, 0] = 1.0
+    with pytest.warns(UserWarning):
+        Hi = ref.invert_hessian(H)
+    assert torch.allclose(H @ Hi @ H, H, atol=1e-5)
+
+
+# ---------------------------------------------------------------- GPTQ sweep
+
+def _np_gptq_sweep(W, Hinv, s, z, B, qmin, qmax):
+    """Element-by-element float32 restatement of the sweep (independent)."""
+    W = W.astype(f32).copy()
+    M, N = W.shape
+    Q = np.zeros((M, N), dtype=np.int8)
+    for b0 in range(0, N, B):
+        b1 = min(b0 + B, N)
+        E = np.zeros((M, b1 - b0), dtype=f32)
+        for j in range(b0, b1):
+            for r in range(M):
+                w = W[r, j]
+                raw = f32(w / s[r])
+                if z is not None:
+                    raw = f32(raw + f32(z[r]))
+                q = f32(max(qmin, min(qmax, np_rhaz(raw))))
+                deq = f32(f32(q - f32(z[r])) * s[r]) if z is not None else f32(q * s[r])
+                e = f32(f32(w - deq) / Hinv[j, j])
+                e = f32(0.0) if np.isnan(e) else f32(min(100.0, max(-100.0, e)))
+                Q[r, j] = int(q)
+                E[r, j - b0] = e
+                for k in range(j + 1, b1):
+                    W[r, k] = f32(W[r, k] - f32(e * Hinv[j, k]))
+        if b1 < N:
+            W[:, b1:] = (W[:, b1:].astype(np.float64) - E.astype(np.float64) @ Hinv[b0:b1, b1:].astype(np.float64)).astype(f32)
+    return Q
+
+
+@pytest.mark.parametrize("asym", [False, True])
+def test_gptq_sweep_single_block_bit_exact(asym):
+    g = torch.Generator().manual_seed(5)
+    M, N = 6, 24
+    W = torch.randn(M, N, generator=g)
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 64, 2), 0.01)
+    s, z = ref.gptq_row_params(W, 4, False)
+    if not asym:
+        z = None
+    Q = torch.zeros(M, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, N, -8, 7, z)
+    Qn = _np_gptq_sweep(W.numpy(), Hinv.numpy(), s.squeeze(1).numpy(),
+                        None if z is None else z.squeeze(1).numpy().astype(f32), N, -8, 7)
+    assert np.array_equal(Q.numpy(), Qn)
+
+
+def test_gptq_sweep_multi_block_close():
+    g = torch.Generator().manual_seed(6)
+    M, N = 8, 48
+    W = torch.randn(M, N, generator=g)
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 96, 3), 0.01)
+    s, z = ref.gptq_row_params(W, 4, False)
+    Q = torch.zeros(M, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, 16, -8, 7, z)
+    Qn = _np_gptq_sweep(W.numpy(), Hinv.numpy(), s.squeeze(1).numpy(), z.squeeze(1).numpy().astype(f32), 16, -8, 7)
+    assert (Q.numpy() != Qn).mean() < 0.02
+
+
+@pytest.mark.parametrize("case", ["gptq_a", "gptq_b", "gptq_c", "gptq_d", "gptq_e", "gptq_f", "gptq3d"])
+def test_gptq_golden(golden, one_thread, case):
+    t, meta = golden
+    m = meta[case]
+    r = ref.gptq_quantize_layer(t[f"{case}.W"], t[f"{case}.H"], block_size=m["block"], damping=0.01,
+                                int_bits=m["bits"], asymmetric=m["asym"], hessian_method=m["method"])
+    assert torch.equal(r.quantized_W, t[f"{case}.q"])
+    assert torch.equal(r.scales, t[f"{case}.scales"])
+    if f"{case}.zp" in t:
+        assert torch.equal(r.zero_points, t[f"{case}.zp"])
+    assert r.mse == pytest.approx(m["mse"], rel=1e-12)
+
+
+# ---------------------------------------------------------------- LDLQ / greedy
+
+@pytest.mark.parametrize("case", ["ldlq_a", "ldlq_b", "ldlq_c", "ldlq_d", "ldlq_e"])
+def test_ldlq_golden(golden, one_thread, case):
+    t, meta = golden
+    m = meta[case]
+    r = ref.ldlq_quantize_layer(t[f"{case}.W"], hessian=t.get(f"{case}.H"), block_size=m["block"],
+                                damping=0.01, int_bits=m["bits"], iterations=m["iters"],
+                                greedy_passes=m["greedy"])
+    assert torch.equal(r.quantized_W, t[f"{case}.q"])
+    assert torch.equal(r.scales, t[f"{case}.scales"])
+    assert r.mse == pytest.approx(m["mse"], rel=1e-12)
+
+
+def test_greedy_coordinatewise_optimal():
+    """After a pass, no single-coordinate change lowers tr(dW H dW^T) for the
+    last column visited (brute force over the 16 INT4 values)."""
+    g = torch.Generator().manual_seed(9)
+    M, N = 5, 12
+    W = torch.randn(M, N, generator=g, dtype=torch.float32)
+    H = lognormal_hessian(N, 40, 4)
+    S = torch.full((M, N), 0.3)
+    Q0 = ref.rhaz(W / S).clamp(-8, 7)
+    Q = ref.greedy_pytorch(W, Q0.clone(), S, H, 1, -8, 7).float()
+
+    def proxy(Qm):
+        d = (Qm * S - W).double()
+        return (d @ H.double() * d).sum().item()
+
+    base = proxy(Q)
+    assert base <= proxy(Q0) + 1e-9
+    j = N - 1
+    for r in range(M):
+        for v in range(-8, 8):
+            Qt = Q.clone()
+            Qt[r, j] = v
+            assert proxy(Qt) >= base - 1e-6 * abs(base)
