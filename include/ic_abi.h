@@ -120,6 +120,75 @@ int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld,
                    const int8_t* zp, double* out_sumsq, float* out_maxabs, void* workspace,
                    void* stream);
 
+/* ---------------------------------------------------------------- fp32 GEMM */
+
+/* C = alpha * op(A) op(B) + beta * C on the fp32 matrix cores, row-major.
+ * cmask 0 full / 1 lower (i >= j) / 2 upper (i <= j) output; krange 0 full /
+ * 1 k >= max(tile i0, j0) / 2 k >= tile j0 / 3 k < tile i0 + 128 (skips the
+ * zero half of a triangular operand).  beta == 0 never reads C.
+ * Replaces the torch matmuls of converter/rounding.py:103 and
+ * converter/gptq_triton.py:178-180 (lazy trailing update) and the LAPACK
+ * level-3 kernels behind torch.linalg.cholesky / cholesky_inverse. */
+int ic_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
+             const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+             float* C, int64_t ldc, int cmask, int krange, void* stream);
+
+/* ---------------------------------------------------------------- Hessian inverse */
+
+/* In place on `batch` dense fp32 matrices [n, n] (back to back):
+ *   H <- H + fp32(damping) * max(mean(diag H), 1e-6) * I;  L = chol(H);
+ *   method 0 ("hinv"):     H <- H^-1 = L^-T L^-1 (full symmetric);
+ *   method 1 ("cholesky"): H <- chol(H^-1)^T (upper; lower part zero).
+ * info: device int32[2*batch]; info[b] > 0 is the 1-based column of the
+ * first non-positive pivot of chol(H_b) (then H_b is not a valid result and
+ * the caller falls back like converter/rounding.py:19-34); info[batch+b]
+ * likewise for chol(H_b^-1) in method 1.
+ * workspace: ic_hessian_inverse_workspace_bytes(batch, n) bytes.
+ * Replaces converter/gptq.py:91-121 (_prepare_hessian, _prepare_hinv),
+ * converter/rounding.py:19-34 (_invert_hessian, Cholesky branch),
+ * converter/ldlq.py:64-92, 169-171, 207-209. */
+int64_t ic_hessian_inverse_workspace_bytes(int64_t batch, int64_t n);
+int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damping, int method,
+                       int* info, void* workspace, void* stream);
+
+/* Lower Cholesky factor in place (upper part of the diagonal 128-blocks set
+ * to 0, the rest of the upper triangle untouched); info as above; workspace
+ * as for ic_hessian_inverse.  Replaces torch.linalg.cholesky. */
+int ic_cholesky(float* H, int64_t batch, int64_t n, int* info, void* workspace, void* stream);
+
+/* ---------------------------------------------------------------- GPTQ / LDLQ */
+
+/* Per-row GPTQ parameters from row statistics (converter/gptq.py:254-317):
+ * INT4, or INT8 asymmetric: s = clamp((max-min)/spread, 1e-5, 65500) with the
+ * zero-point clamp fix, zp = clamp(qmin - rhaz(min/s)), zero rows zp = 0;
+ * INT8 symmetric: s = clamp(absmax/127, 1e-5, 65500).  Outputs (any but s32
+ * may be NULL): s32 fp32, z32 fp32, s16 fp16 bits, z8 int8. */
+int ic_gptq_row_params(const float* row_min, const float* row_max, const float* row_absmax,
+                       int64_t rows, int bits, int asym, float* s32, float* z32, uint16_t* s16,
+                       int8_t* z8, void* stream);
+
+/* GPTQ sweep of a whole layer: W [rows, groups*gw] fp32 working weights
+ * (modified), Hinv [groups, gw, gw] (groups == 1: the full inverse; > 1: the
+ * block-diagonal inverses of a 3-D Hessian, each group of gw columns
+ * independent), per-row s32 / z32 (z32 NULL = symmetric), block <= 128
+ * columns of eager updates then one fp32-MFMA lazy update per block.
+ * Q: int8 codes [rows, groups*gw].  workspace:
+ * ic_gptq_workspace_bytes(rows, groups, block).
+ * Replaces converter/rounding.py:37-103 (_gptq_block), converter/gptq.py:27-88
+ * and 323-393 (_gptq_block_triton and the 2-D / 3-D dispatch),
+ * converter/gptq_triton.py:18-184 (gptq_loop_triton). */
+int64_t ic_gptq_workspace_bytes(int64_t rows, int64_t groups, int block);
+int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
+                     const float* s32, const float* z32, int bits, int block, int8_t* Q,
+                     void* workspace, void* stream);
+
+/* LDLQ sweep (converter/ldlq.py:369-417, converter/ldlq_triton.py:23-162,
+ * converter/rounding.py:115-155): per-element scales [rows, N] (floored at
+ * 1e-8), error times 1/max(Hinv_jj, 1e-8), no clamp, sign-flip rule.
+ * Hinv [N, N]; W modified; Q int8 [rows, N]; workspace as for GPTQ. */
+int ic_ldlq_quantize(float* W, int64_t rows, int64_t N, const float* Hinv, const float* scales,
+                     int bits, int block, int8_t* Q, void* workspace, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,14 @@ _SIGS = {
     "ic_unpack_int4": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ic_quant_error_workspace_bytes": (_i64, []),
     "ic_quant_error": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ic_sgemm": (_i32, [_i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64, _f32, _vp, _i64, _i32, _i32, _vp]),
+    "ic_hessian_inverse_workspace_bytes": (_i64, [_i64, _i64]),
+    "ic_hessian_inverse": (_i32, [_vp, _i64, _i64, _f32, _i32, _vp, _vp, _vp]),
+    "ic_cholesky": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "ic_gptq_row_params": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ic_gptq_workspace_bytes": (_i64, [_i64, _i64, _i32]),
+    "ic_gptq_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "ic_ldlq_quantize": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
 }
 
 
@@ -117,6 +125,11 @@ def dtype_code(t: torch.Tensor) -> int:
     if t.dtype == torch.float16:
         return DT_F16
     raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    """Caller-owned scratch for an ABI call (uint8, through torch's allocator)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
 
 
 def row_ld(t: torch.Tensor) -> int:

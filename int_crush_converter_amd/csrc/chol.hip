@@ -1,0 +1,264 @@
+// Damped-Hessian inverse H^-1 = L^-T L^-1 (the reference's
+// torch.linalg.cholesky + torch.cholesky_inverse, converter/rounding.py:19-34,
+// after the damping of converter/gptq.py:91-121), for one matrix or a batch
+// of equal-size diagonal blocks.
+//
+//  1. damp:   H += fp32(damping) * max(mean(diag H), 1e-6) * I   (per matrix)
+//  2. potrf:  blocked right-looking Cholesky, nb = 128.  The nb x nb diagonal
+//             block is factored in LDS by one workgroup, which also writes
+//             its triangular inverse Dinv_k; the panel is A21 <- A21 Dinv_k^T
+//             and the trailing update A22 -= A21 A21^T, both fp32-MFMA GEMMs.
+//  3. trtri:  X = L^-1 by right-looking block substitution on L X = I:
+//             X[k, :k] <- Dinv_k X[k, :k];  X[k, k] = Dinv_k;
+//             X[k+1:, :k+1] -= L[k+1:, k] X[k, :k+1]           (GEMMs)
+//  4. lauum:  H^-1 (upper triangle) = X^T X, one GEMM whose tile (I, J)
+//             only runs k >= max(I, J) because X is lower triangular.
+// Flops: n^3/3 each for 2-4; all but the nb x nb factorisations are MFMA.
+#include "gemm.hpp"
+
+namespace icq {
+
+constexpr int NB = 128;
+constexpr int TP = NB + 1;   // LDS pitch of the diagonal tile
+
+__global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
+    float* A = H + (int64_t)blockIdx.x * stride;
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) acc += (double)A[i * ld + i];
+    __shared__ double part[4];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += part[w];
+    float mean = (float)(tot / (double)n);
+    mean = mean > 1e-6f ? mean : (mean != mean ? mean : 1e-6f);
+    const float delta = damping * mean;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) A[i * ld + i] = A[i * ld + i] + delta;
+}
+
+// Factor the diagonal block [k0, k0+nb) of matrix blockIdx.x in place (lower,
+// upper part of the block set to 0) and write Dinv = L_kk^-1 (lower, upper 0)
+// to dinv (pitch NB).  info[b] gets the 1-based column of the first
+// non-positive pivot (LAPACK convention) if it is still 0.
+__global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
+                                                         float* dinv, int64_t dstride, int* info) {
+    __shared__ float T[NB * TP];
+    __shared__ float X[NB * TP];
+    __shared__ int bad;
+    const int b = blockIdx.x;
+    float* A = H + (int64_t)b * stride + k0 * ld + k0;
+    const int t = threadIdx.x;
+    if (t == 0) bad = 0;
+    for (int idx = t; idx < nb * nb; idx += blockDim.x) {
+        int i = idx / nb, j = idx - i * nb;
+        T[i * TP + j] = j <= i ? A[(int64_t)i * ld + j] : 0.0f;
+    }
+    __syncthreads();
+    // right-looking unblocked Cholesky
+    for (int j = 0; j < nb; ++j) {
+        float d = T[j * TP + j];
+        if (!(d > 0.0f)) {           // non-positive or NaN pivot
+            if (t == 0 && bad == 0) bad = j + 1;
+            d = 1.0f;
+        }
+        const float ljj = sqrtf(d);
+        __syncthreads();
+        if (t == 0) T[j * TP + j] = ljj;
+        for (int i = j + 1 + t; i < nb; i += blockDim.x) T[i * TP + j] = T[i * TP + j] / ljj;
+        __syncthreads();
+        const int m = nb - j - 1;                 // trailing size
+        // columns l = j+1.., rows i >= l; thread -> (column, row parity)
+        for (int c = t; c < m * 2; c += blockDim.x) {
+            const int l = j + 1 + (c >> 1);
+            const float llj = T[l * TP + j];
+            for (int i = l + (c & 1); i < nb; i += 2) T[i * TP + l] = T[i * TP + l] - T[i * TP + j] * llj;
+        }
+        __syncthreads();
+    }
+    // X = L^-1: for k, X[k,:] = R[k,:] / L[k][k], R[i,:] -= L[i][k] X[k,:] (i > k)
+    for (int idx = t; idx < nb * nb; idx += blockDim.x) {
+        int i = idx / nb, j = idx - i * nb;
+        X[i * TP + j] = i == j ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    for (int k = 0; k < nb; ++k) {
+        const float lkk = T[k * TP + k];
+        for (int j = t; j <= k; j += blockDim.x) X[k * TP + j] = X[k * TP + j] / lkk;
+        __syncthreads();
+        const int m = nb - k - 1;
+        for (int c = t; c < m * (k + 1); c += blockDim.x) {
+            const int i = k + 1 + c / (k + 1), j = c % (k + 1);
+            X[i * TP + j] = X[i * TP + j] - T[i * TP + k] * X[k * TP + j];
+        }
+        __syncthreads();
+    }
+    float* D = dinv + (int64_t)b * dstride;
+    for (int idx = t; idx < NB * NB; idx += blockDim.x) {
+        int i = idx / NB, j = idx - i * NB;
+        bool in = i < nb && j < nb;
+        if (in) A[(int64_t)i * ld + j] = j <= i ? T[i * TP + j] : 0.0f;
+        D[idx] = (in && j <= i) ? X[i * TP + j] : 0.0f;
+    }
+    if (t == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
+}
+
+// Copy Dinv_k into the diagonal block of X (lower, upper zero).
+__global__ void put_diag_kernel(float* X, int64_t ld, int64_t stride, int64_t k0, int nb, const float* dinv,
+                                int64_t dstride) {
+    const int b = blockIdx.y;
+    const float* D = dinv + (int64_t)b * dstride;
+    float* P = X + (int64_t)b * stride + k0 * ld + k0;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < nb * nb; idx += gridDim.x * blockDim.x) {
+        int i = idx / nb, j = idx - i * nb;
+        P[(int64_t)i * ld + j] = D[i * NB + j];
+    }
+}
+
+__global__ void fill_kernel(float* p, int64_t n, float v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// Copy the upper triangle onto the lower one (in place), per matrix.
+__global__ void mirror_upper_kernel(float* H, int64_t n, int64_t ld, int64_t stride) {
+    float* A = H + (int64_t)blockIdx.z * stride;
+    const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.y;
+    const int64_t j = (int64_t)blockIdx.x * 16 + threadIdx.x;
+    if (i < n && j < n && i > j) A[i * ld + j] = A[j * ld + i];
+}
+
+// Transpose the lower triangle into the upper one and zero the lower (in place):
+// turns a lower Cholesky factor L into L^T.
+__global__ void lower_to_upper_kernel(float* H, int64_t n, int64_t ld, int64_t stride) {
+    float* A = H + (int64_t)blockIdx.z * stride;
+    const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.y;
+    const int64_t j = (int64_t)blockIdx.x * 16 + threadIdx.x;
+    if (i < n && j < n && i < j) {
+        A[i * ld + j] = A[j * ld + i];
+        A[j * ld + i] = 0.0f;
+    }
+}
+
+static int fill(float* p, int64_t n, float v, hipStream_t st) {
+    if (n <= 0) return IC_OK;
+    int grid = (int)std::min<int64_t>(cdiv(n, 256), 65536);
+    hipLaunchKernelGGL(fill_kernel, dim3(grid), dim3(256), 0, st, p, n, v);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+static int64_t dinv_floats(int64_t batch, int64_t n) { return batch * cdiv(n, NB) * NB * NB; }
+
+// Lower Cholesky in place of `batch` matrices [n, n] (pitch ld, stride sH);
+// dinv receives every Dinv_k (batch x nblk x NB x NB).
+static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, int* info,
+                 hipStream_t st) {
+    const int64_t nblk = cdiv(n, NB);
+    const int64_t dstride = nblk * NB * NB;
+    for (int64_t kb = 0; kb < nblk; ++kb) {
+        const int64_t k0 = kb * NB;
+        const int nb = (int)std::min<int64_t>(NB, n - k0);
+        float* Dk = dinv + kb * NB * NB;
+        hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
+                           dstride, info);
+        IC_CHECK_LAUNCH();
+        const int64_t m = n - k0 - nb;
+        if (m <= 0) break;
+        float* A21 = H + (k0 + nb) * ld + k0;
+        // panel: A21 <- A21 * Dinv^T (in place: one tile column spans all nb columns)
+        GemmArgs p{m, nb, nb, 1.0f, 0.0f, A21, ld, sH, Dk, NB, dstride, A21, ld, sH, 0, 1, CMASK_FULL, KR_FULL, batch};
+        int rc = gemm_f32(p, st);
+        if (rc) return rc;
+        // trailing: A22 -= A21 A21^T (lower)
+        float* A22 = H + (k0 + nb) * ld + (k0 + nb);
+        GemmArgs s{m, m, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, A22, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch};
+        rc = gemm_f32(s, st);
+        if (rc) return rc;
+    }
+    return IC_OK;
+}
+
+// X = L^-1 (lower, upper zero) from L (lower, in H) and the Dinv blocks.
+static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const float* dinv,
+                 hipStream_t st) {
+    const int64_t nblk = cdiv(n, NB);
+    const int64_t dstride = nblk * NB * NB;
+    int rc = fill(X, batch * sH, 0.0f, st);
+    if (rc) return rc;
+    for (int64_t kb = 0; kb < nblk; ++kb) {
+        const int64_t k0 = kb * NB;
+        const int nb = (int)std::min<int64_t>(NB, n - k0);
+        const float* Dk = dinv + kb * NB * NB;
+        float* Xk = X + k0 * ld;   // row block k
+        if (k0 > 0) {
+            // X[k, :k] <- Dinv_k X[k, :k]   (in place, M = nb <= 128)
+            GemmArgs a{nb, k0, nb, 1.0f, 0.0f, Dk, NB, dstride, Xk, ld, sH, Xk, ld, sH, 0, 0, CMASK_FULL, KR_FULL,
+                       batch};
+            rc = gemm_f32(a, st);
+            if (rc) return rc;
+        }
+        hipLaunchKernelGGL(put_diag_kernel, dim3(16, (unsigned)batch), dim3(256), 0, st, X, ld, sH, k0, nb, dinv + kb * NB * NB,
+                           dstride);
+        IC_CHECK_LAUNCH();
+        const int64_t m = n - k0 - nb;
+        if (m <= 0) break;
+        // X[k+1:, :k+1] -= L[k+1:, k] X[k, :k+1]
+        GemmArgs c{m, k0 + nb, nb, -1.0f, 1.0f, L + (k0 + nb) * ld + k0, ld, sH, Xk, ld, sH, X + (k0 + nb) * ld, ld,
+                   sH, 0, 0, CMASK_FULL, KR_FULL, batch};
+        rc = gemm_f32(c, st);
+        if (rc) return rc;
+    }
+    return IC_OK;
+}
+
+}  // namespace icq
+
+using namespace icq;
+
+extern "C" int64_t ic_hessian_inverse_workspace_bytes(int64_t batch, int64_t n) {
+    return (batch * n * n + dinv_floats(batch, n)) * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damping, int method, int* info,
+                                  void* workspace, void* stream) {
+    IC_REQUIRE(H && info && workspace, "ic_hessian_inverse: null pointer");
+    IC_REQUIRE(n >= 0 && batch >= 0, "ic_hessian_inverse: bad size");
+    IC_REQUIRE(method == 0 || method == 1, "ic_hessian_inverse: method must be 0 (hinv) or 1 (cholesky)");
+    if (n == 0 || batch == 0) return IC_OK;
+    hipStream_t st = as_stream(stream);
+    const int64_t ld = n, sH = n * n;
+    float* X = reinterpret_cast<float*>(workspace);
+    float* dinv = X + batch * sH;
+    IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
+    hipLaunchKernelGGL(damp_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, n, ld, sH, damping);
+    IC_CHECK_LAUNCH();
+    int rc = potrf(H, batch, n, ld, sH, dinv, info, st);
+    if (rc) return rc;
+    rc = trtri(H, X, batch, n, ld, sH, dinv, st);
+    if (rc) return rc;
+    // H^-1 (upper triangle incl. diagonal) = X^T X  -> H
+    GemmArgs u{n, n, n, 1.0f, 0.0f, X, ld, sH, X, ld, sH, H, ld, sH, 1, 0, CMASK_UPPER, KR_FROM_MAXIJ, batch};
+    rc = gemm_f32(u, st);
+    if (rc) return rc;
+    dim3 tb(16, 16), tg((unsigned)cdiv(n, 16), (unsigned)cdiv(n, 16), (unsigned)batch);
+    hipLaunchKernelGGL(mirror_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
+    IC_CHECK_LAUNCH();
+    if (method == 1) {
+        // upper Cholesky factor of H^-1 (converter/gptq.py:91-110): L2 = chol(H^-1), return L2^T
+        rc = potrf(H, batch, n, ld, sH, dinv, info + batch, st);
+        if (rc) return rc;
+        hipLaunchKernelGGL(lower_to_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
+        IC_CHECK_LAUNCH();
+    }
+    return IC_OK;
+}
+
+extern "C" int ic_cholesky(float* H, int64_t batch, int64_t n, int* info, void* workspace, void* stream) {
+    IC_REQUIRE(H && info && workspace, "ic_cholesky: null pointer");
+    if (n == 0 || batch == 0) return IC_OK;
+    hipStream_t st = as_stream(stream);
+    IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
+    float* dinv = reinterpret_cast<float*>(workspace) + batch * n * n;
+    return potrf(H, batch, n, n, n * n, dinv, info, st);
+}

@@ -1,0 +1,266 @@
+// GPTQ / LDLQ column sweep and layer driver.
+//
+// Per block of nb <= 128 columns the reference (converter/rounding.py:37-103,
+// converter/ldlq.py:369-417) quantises column j for every row, normalises the
+// error by Hinv[j][j] and immediately updates the later columns of the block,
+// w_k <- w_k - RN(e_j * Hinv[j][k]); after the block the errors E [M, nb]
+// update all later columns at once, W[:, end:] -= E @ Hinv[blk, end:].
+//
+// Sweep kernel: the nb x nb Hinv block is staged in LDS; a row is owned by L
+// lanes, lane l holding columns l, l+L, l+2L, ... in registers.  At step j
+// the owning lane quantises w_j and the error is broadcast to the other lanes
+// of the row, which apply their updates in column order, so every w_k sees
+// exactly the reference's sequence of fp32 roundings (bit-exact given the
+// same Hinv).  Codes and errors are staged in LDS and stored coalesced.
+//
+// The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
+// order differs from MKL's sgemm, which is the only non-bit-exact step.
+#include "gemm.hpp"
+
+namespace icq {
+
+constexpr int SW_NB = 128;     // max columns per sweep block
+constexpr int SW_THREADS = 256;
+
+enum SweepMode : int {
+    SWEEP_GPTQ = 0,   // per-row scale (+zp), err / Hinv_jj, clamp +-100, NaN -> 0
+    SWEEP_LDLQ = 1,   // per-element scale (>= 1e-8), err * (1 / max(Hinv_jj, 1e-8)), no clamp
+};
+
+struct SweepArgs {
+    float* W; int64_t ldw;          // working weights (block columns start at col0)
+    int64_t rows;
+    int64_t col0; int nb;
+    int64_t gcol;                   // column stride between batched groups
+    const float* H; int64_t ldh;    // Hinv block top-left; group stride hg
+    int64_t hg;
+    const float* s;                 // GPTQ: per-row scale [rows]; LDLQ: per-element [rows, lds]
+    int64_t lds;
+    const float* zp;                // per-row zero-point (fp32) or null
+    float qmin, qmax;
+    int8_t* Q; int64_t ldq;         // codes, same column indexing as W
+    float* E; int64_t lde; int64_t eg;   // errors [rows, nb] per group (group stride eg)
+    int mode;
+};
+
+template <int L, int MODE>
+__global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
+    constexpr int R = SW_NB / L;              // registers (columns) per lane
+    constexpr int ROWS = SW_THREADS / L;      // rows per workgroup
+    __shared__ float Hs[SW_NB * SW_NB];
+    __shared__ float Es[ROWS * SW_NB];
+    __shared__ int8_t Qs[ROWS * SW_NB];
+    __shared__ float dinv[SW_NB];
+
+    const int g = blockIdx.y;
+    const int nb = a.nb;
+    const int64_t col0 = a.col0 + (int64_t)g * a.gcol;
+    const float* H = a.H + (int64_t)g * a.hg;
+    const int t = threadIdx.x;
+    const int lane = t % L, rl = t / L;
+    const int64_t row = (int64_t)blockIdx.x * ROWS + rl;
+    const bool rv = row < a.rows;
+
+    for (int idx = t; idx < nb * nb; idx += SW_THREADS) {
+        int i = idx / nb, j = idx - i * nb;
+        Hs[i * SW_NB + j] = H[(int64_t)i * a.ldh + j];
+    }
+    if (MODE == SWEEP_LDLQ) {
+        for (int j = t; j < nb; j += SW_THREADS) {
+            float d = H[(int64_t)j * a.ldh + j];
+            d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
+            dinv[j] = 1.0f / d;
+        }
+    }
+    __syncthreads();
+
+    float w[R];
+    const float* wrow = a.W + row * a.ldw + col0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int c = r * L + lane;
+        w[r] = (rv && c < nb) ? wrow[c] : 0.0f;
+    }
+    float s_row = 1.0f, z_row = 0.0f;
+    float sc[MODE == SWEEP_LDLQ ? R : 1];
+    if (MODE == SWEEP_GPTQ) {
+        if (rv) {
+            s_row = a.s[row];
+            if (a.zp) z_row = a.zp[row];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int c = r * L + lane;
+            float v = (rv && c < nb) ? a.s[row * a.lds + col0 + c] : 1.0f;
+            sc[r] = v > 1e-8f ? v : (v != v ? v : 1e-8f);
+        }
+    }
+    const bool has_zp = a.zp != nullptr;
+
+#pragma unroll
+    for (int r0 = 0; r0 < R; ++r0) {
+        for (int o = 0; o < L; ++o) {
+            const int j = r0 * L + o;
+            if (j >= nb) break;
+            // every lane evaluates its own column r0; only the owner's result is used
+            const float x = w[r0];
+            float q, e;
+            if (MODE == SWEEP_GPTQ) {
+                float y = x / s_row;
+                if (has_zp) y = y + z_row;
+                q = clampf(rhaz(y), a.qmin, a.qmax);
+                float deq = has_zp ? (q - z_row) * s_row : q * s_row;
+                e = (x - deq) / Hs[j * SW_NB + j];
+                e = clampf(e, -100.0f, 100.0f);
+                if (e != e) e = 0.0f;
+            } else {
+                const float scl = sc[MODE == SWEEP_LDLQ ? r0 : 0];
+                q = clampf(rhaz(x / scl), a.qmin, a.qmax);
+                // sign-flip correction (inert for positive scales)
+                float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
+                                            : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
+                float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
+                bool flip = ws * qs < 0.0f;
+                bool can = flip && (q > a.qmin);
+                if (flip && q == a.qmin) q = a.qmax;
+                if (can) q = -q;
+                q = clampf(q, a.qmin, a.qmax);
+                e = (x - q * scl) * dinv[j];
+            }
+            const float err = __shfl(e, o, L);   // broadcast from the owner lane of this row
+            if (lane == o) {
+                Qs[rl * SW_NB + j] = (int8_t)(int)q;
+                Es[rl * SW_NB + j] = e;
+            }
+#pragma unroll
+            for (int r = r0; r < R; ++r) {
+                const int c = r * L + lane;
+                if ((r > r0 || lane > o) && c < nb) w[r] = w[r] - err * Hs[j * SW_NB + c];
+            }
+        }
+    }
+    __syncthreads();
+    // coalesced stores of codes and errors
+    for (int idx = t; idx < ROWS * nb; idx += SW_THREADS) {
+        const int rr = idx / nb, c = idx - rr * nb;
+        const int64_t gr = (int64_t)blockIdx.x * ROWS + rr;
+        if (gr < a.rows) {
+            a.Q[gr * a.ldq + col0 + c] = Qs[rr * SW_NB + c];
+            a.E[(int64_t)g * a.eg + gr * a.lde + c] = Es[rr * SW_NB + c];
+        }
+    }
+}
+
+static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
+    IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
+    constexpr int L = 16;
+    const int64_t wgs = cdiv(a.rows, SW_THREADS / L);
+    if (a.mode == SWEEP_GPTQ)
+        hipLaunchKernelGGL((sweep_kernel<L, SWEEP_GPTQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
+                           st, a);
+    else
+        hipLaunchKernelGGL((sweep_kernel<L, SWEEP_LDLQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
+                           st, a);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+// Per-row GPTQ parameters from row min / max / absmax
+// (converter/gptq.py:254-317): fp32 scale, fp32 zero-point, and their
+// stored forms (fp16 scale bits, int8 zero-point).
+__global__ void gptq_params_kernel(const float* rmin, const float* rmax, const float* ramax, int64_t rows, int bits,
+                                   int asym, float* s32, float* z32, uint16_t* s16, int8_t* z8) {
+    for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
+        float s, z = 0.0f;
+        if (bits == 4 || asym) {
+            const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+            const float spread = bits == 4 ? 15.0f : 255.0f;
+            const float mn = rmin[r], mx = rmax[r];
+            s = clampf((mx - mn) / spread, 1e-5f, 65500.0f);
+            const float zraw = qmin - rhaz(mn / s);
+            const bool lo = zraw < qmin, hi = zraw > qmax;
+            if (lo) { float f = clampf(mx / spread, 1e-5f, 65500.0f); s = (s != s || s > f) ? s : f; }
+            if (hi) { float f = clampf(-mn / spread, 1e-5f, 65500.0f); s = (s != s || s > f) ? s : f; }
+            z = clampf(qmin - rhaz(mn / s), qmin, qmax);
+            if (mn == 0.0f && mx == 0.0f) z = 0.0f;
+            if (z8) z8[r] = (int8_t)(int)z;
+            if (z32) z32[r] = z;
+        } else {
+            s = clampf(ramax[r] / 127.0f, 1e-5f, 65500.0f);
+        }
+        s32[r] = s;
+        if (s16) s16[r] = f32_to_f16_bits(s);
+    }
+}
+
+// Whole-layer sweep for `groups` independent column groups of width gw
+// (groups == 1, gw == N: full 2-D Hessian; 3-D: one group per Hessian block).
+// Hinv of group g starts at Hinv + g * hg with pitch ldh.  E is scratch of
+// groups * rows * min(B,128) floats.
+static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
+                       int64_t ldh, int64_t hg, const float* s, int64_t lds, const float* zp, float qmin,
+                       float qmax, int B, int8_t* Q, int64_t ldq, float* E, int mode, hipStream_t st) {
+    IC_REQUIRE(B >= 1 && B <= SW_NB, "block size must be in [1, 128]");
+    for (int64_t b0 = 0; b0 < gw; b0 += B) {
+        const int nb = (int)std::min<int64_t>(B, gw - b0);
+        SweepArgs a{W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh, hg, s, lds, zp, qmin, qmax,
+                    Q, ldq, E, nb, rows * nb, mode};
+        int rc = launch_sweep(a, (int)groups, st);
+        if (rc) return rc;
+        const int64_t rest = gw - b0 - nb;
+        if (rest > 0) {
+            // W[:, b0+nb : gw] -= E @ Hinv[b0 : b0+nb, b0+nb : gw]   (per group)
+            GemmArgs ga{rows, rest, nb, -1.0f, 1.0f, E, nb, rows * nb, Hinv + b0 * ldh + b0 + nb, ldh, hg,
+                        W + b0 + nb, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups};
+            rc = gemm_f32(ga, st);
+            if (rc) return rc;
+        }
+    }
+    return IC_OK;
+}
+
+}  // namespace icq
+
+using namespace icq;
+
+extern "C" int ic_gptq_row_params(const float* rmin, const float* rmax, const float* ramax, int64_t rows, int bits,
+                                  int asym, float* s32, float* z32, uint16_t* s16, int8_t* z8, void* stream) {
+    IC_REQUIRE(s32, "ic_gptq_row_params: null scale output");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_gptq_row_params: bits must be 4 or 8");
+    IC_REQUIRE((bits == 8 && !asym) ? ramax != nullptr : (rmin && rmax), "ic_gptq_row_params: missing stats");
+    if (rows == 0) return IC_OK;
+    int grid = (int)std::min<int64_t>(cdiv(rows, 256), 4096);
+    hipLaunchKernelGGL(gptq_params_kernel, dim3(grid), dim3(256), 0, as_stream(stream), rmin, rmax, ramax, rows, bits,
+                       asym, s32, z32, s16, z8);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int64_t ic_gptq_workspace_bytes(int64_t rows, int64_t groups, int block) {
+    int64_t b = std::min<int64_t>(std::max(block, 1), SW_NB);
+    return groups * rows * b * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
+                                const float* s32, const float* z32, int bits, int block, int8_t* Q,
+                                void* workspace, void* stream) {
+    IC_REQUIRE(W && Hinv && s32 && Q && workspace, "ic_gptq_quantize: null pointer");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_gptq_quantize: bits must be 4 or 8");
+    IC_REQUIRE(groups >= 1 && gw >= 0 && rows >= 0, "ic_gptq_quantize: bad size");
+    if (rows == 0 || gw == 0) return IC_OK;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    const int64_t N = gw * groups;
+    return layer_sweep(W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
+                       reinterpret_cast<float*>(workspace), SWEEP_GPTQ, as_stream(stream));
+}
+
+extern "C" int ic_ldlq_quantize(float* W, int64_t rows, int64_t N, const float* Hinv, const float* scales,
+                                int bits, int block, int8_t* Q, void* workspace, void* stream) {
+    IC_REQUIRE(W && Hinv && scales && Q && workspace, "ic_ldlq_quantize: null pointer");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_ldlq_quantize: bits must be 4 or 8");
+    if (rows == 0 || N == 0) return IC_OK;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    return layer_sweep(W, N, rows, N, 1, Hinv, N, N * N, scales, N, nullptr, qmin, qmax, block, Q, N,
+                       reinterpret_cast<float*>(workspace), SWEEP_LDLQ, as_stream(stream));
+}

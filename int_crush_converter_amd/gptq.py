@@ -1,0 +1,184 @@
+"""GPTQ layer quantisation (API of ``converter/gptq.py``).
+
+``gptq_quantize_layer`` runs entirely on the GPU: row statistics and the
+per-row scale / zero-point (``ic_row_stats`` + ``ic_gptq_row_params``), the
+damped Hessian inverse (``ic_hessian_inverse``), the column sweep with its
+fp32-MFMA lazy trailing update (``ic_gptq_quantize``) and the error metrics
+(``ic_quant_error``).  Results are returned on the device of ``W``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+from .hessian import inverse_batch
+from .log import logger
+from .types import QuantizationResult
+from . import scales as _scales
+
+_HESSIAN_METHODS = {"hinv": "hinv", "cholesky": "cholesky"}
+
+SWEEP_MAX_BLOCK = 128
+
+
+def row_params(W: torch.Tensor, int_bits: int, asymmetric: bool):
+    """fp32 GPU W [M, N] -> (s32 [M], z32 [M] or None, s16 [M] fp16, z8 [M] int8 or None)
+    following converter/gptq.py:254-317."""
+    M, N = W.shape
+    dev = W.device
+    L = nat.lib()
+    asym = int_bits == 4 or asymmetric
+    rmin = torch.empty(M, dtype=torch.float32, device=dev)
+    rmax = torch.empty(M, dtype=torch.float32, device=dev)
+    ramax = torch.empty(M, dtype=torch.float32, device=dev)
+    nat.check(L.ic_row_stats(W.data_ptr(), M, N, N, rmin.data_ptr(), rmax.data_ptr(), ramax.data_ptr(),
+                             nat.stream()), "ic_row_stats")
+    s32 = torch.empty(M, dtype=torch.float32, device=dev)
+    s16 = torch.empty(M, dtype=torch.float16, device=dev)
+    z32 = torch.empty(M, dtype=torch.float32, device=dev) if asym else None
+    z8 = torch.empty(M, dtype=torch.int8, device=dev) if asym else None
+    nat.check(L.ic_gptq_row_params(rmin.data_ptr(), rmax.data_ptr(), ramax.data_ptr(), M, int_bits, int(asym),
+                                   s32.data_ptr(), nat.ptr(z32), s16.data_ptr(), nat.ptr(z8), nat.stream()),
+              "ic_gptq_row_params")
+    return s32, z32, s16, z8
+
+
+def quant_error(W: torch.Tensor, Q: torch.Tensor, scale: torch.Tensor, zp8: torch.Tensor | None):
+    """(mse, max_err) of (Q - zp) * scale against W, scale fp16 or fp32 [M]."""
+    M, N = W.shape
+    if W.numel() == 0:
+        return float("nan"), 0.0
+    out = torch.zeros(2, dtype=torch.float64, device=W.device)
+    mx = torch.zeros(1, dtype=torch.float32, device=W.device)
+    ws = nat.workspace(nat.lib().ic_quant_error_workspace_bytes(), W.device)
+    kind = 0 if scale.dtype == torch.float16 else 1
+    sc = scale.reshape(-1).contiguous() if kind == 0 else scale.reshape(-1).float().contiguous()
+    zp = None if zp8 is None else zp8.reshape(-1).to(torch.int8).contiguous()
+    nat.check(nat.lib().ic_quant_error(W.data_ptr(), M, N, N, Q.data_ptr(), N, sc.data_ptr(), kind, nat.ptr(zp),
+                                       out.data_ptr(), mx.data_ptr(), ws.data_ptr(), nat.stream()),
+              "ic_quant_error")
+    sumsq = out[0].item()
+    return sumsq / W.numel(), mx.item()
+
+
+def sweep(W_work: torch.Tensor, Hinv: torch.Tensor, s32: torch.Tensor, z32: torch.Tensor | None,
+          int_bits: int, block_size: int, groups: int = 1) -> torch.Tensor:
+    """Run the GPTQ sweep in place on W_work [M, groups*gw]; Hinv [gw, gw] or
+    [groups, gw, gw].  Returns int8 codes [M, groups*gw]."""
+    M, N = W_work.shape
+    gw = N // groups
+    Q = torch.empty(M, N, dtype=torch.int8, device=W_work.device)
+    blk = min(int(block_size), SWEEP_MAX_BLOCK)
+    ws = nat.workspace(nat.lib().ic_gptq_workspace_bytes(M, groups, blk), W_work.device)
+    nat.check(nat.lib().ic_gptq_quantize(W_work.data_ptr(), M, gw, groups, Hinv.data_ptr(), s32.data_ptr(),
+                                         nat.ptr(z32), int_bits, blk, Q.data_ptr(), ws.data_ptr(), nat.stream()),
+              "ic_gptq_quantize")
+    return Q
+
+
+def gptq_quantize_layer(
+    W: torch.Tensor,
+    hessian: torch.Tensor,
+    block_size: int = 128,
+    damping: float = 0.01,
+    int_bits: int = 4,
+    asymmetric: bool = False,
+    hessian_method: str = "hinv",
+    piso_scales: torch.Tensor | None = None,
+    piso_zero_points: torch.Tensor | None = None,
+) -> QuantizationResult:
+    """GPTQ with per-row scales (INT4 always asymmetric), 2-D or 3-D Hessian
+    (reference gptq.py:137-417).  ``block_size`` above 128 is run as 128-column
+    sweeps, which is the same update in exact arithmetic."""
+    if int_bits not in (4, 8):
+        raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
+    if W.dim() != 2:
+        raise ValueError(f"Expected 2D weight tensor, got {W.dim()}D")
+    if hessian_method not in _HESSIAN_METHODS:
+        raise ValueError(f"hessian_method must be one of {list(_HESSIAN_METHODS)}, got '{hessian_method}'")
+    if piso_scales is not None or piso_zero_points is not None:
+        raise NotImplementedError("PiSO scales are not supported by this build")
+    if isinstance(hessian, dict):
+        raise NotImplementedError("DLR Hessians are not supported by this build")
+
+    out_dev = W.device
+    Wg = nat.to_gpu(W).float().contiguous()
+    M, N = Wg.shape
+    Hg = nat.to_gpu(hessian)
+    fallbacks: list[str] = []
+    s32, z32, s16, z8 = row_params(Wg, int_bits, asymmetric)
+    W_work = Wg.clone()
+
+    if Hg.dim() == 3:
+        nblk, bs, _ = Hg.shape
+        full = N // bs
+        Q = torch.empty(M, N, dtype=torch.int8, device=Wg.device)
+        if full > 0:
+            Hinv = inverse_batch(Hg[:full].float(), damping, hessian_method, fallbacks)
+            Q[:, :full * bs] = sweep(W_work[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits,
+                                     block_size, groups=full)
+        if full * bs < N:
+            if full >= nblk:
+                raise ValueError(f"3-D Hessian with {nblk} blocks of {bs} does not cover {N} columns")
+            rem = N - full * bs
+            Hinv = inverse_batch(Hg[full, :rem, :rem].float(), damping, hessian_method, fallbacks)
+            Q[:, full * bs:] = sweep(W_work[:, full * bs:].contiguous(), Hinv, s32, z32, int_bits, block_size)
+    elif Hg.dim() == 2:
+        if tuple(Hg.shape) != (N, N):
+            raise ValueError(f"Hessian shape {hessian.shape} != ({N}, {N})")
+        Hinv = inverse_batch(Hg.float(), damping, hessian_method, fallbacks)
+        Q = sweep(W_work, Hinv, s32, z32, int_bits, block_size)
+    else:
+        raise ValueError(
+            f"Expected 2D tensor, 3D tensor, or DLR dict Hessian, got {type(hessian).__name__}")
+
+    logger.debug("GPTQ: HIP path, %dx%d, block_size=%d", M, N, block_size)
+    mse, max_err = quant_error(Wg, Q, s32, z8)
+    return QuantizationResult(
+        quantized_W=Q.to(out_dev),
+        scales=s16.reshape(M, 1).to(out_dev),
+        zero_points=None if z8 is None else z8.reshape(M, 1).to(out_dev),
+        mse=mse,
+        max_err=max_err,
+        method_used="gptq_hip",
+        fallbacks=fallbacks,
+    )
+
+
+def gptq_quantize_layer_rtn(
+    W: torch.Tensor,
+    int_bits: int = 4,
+    asymmetric: bool = False,
+    clipping_ratios: list[float] | None = None,
+    piso_scales: torch.Tensor | None = None,
+    piso_zero_points: torch.Tensor | None = None,
+) -> QuantizationResult:
+    """Round-to-nearest fallback used when no Hessian is available
+    (reference gptq.py:420-533)."""
+    if int_bits not in (4, 8):
+        raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
+    if piso_scales is not None or piso_zero_points is not None:
+        raise NotImplementedError("PiSO scales are not supported by this build")
+    out_dev = W.device
+    Wg = nat.to_gpu(W).float().contiguous()
+    N = Wg.shape[1]
+    zps = None
+    if asymmetric:
+        if int_bits == 8:
+            scales, zps = _scales.calculate_scales_int8_asymmetric(Wg, clipping_ratios=clipping_ratios)
+            q = _scales.quantize_weights_int8_asymmetric(Wg, scales, zps)
+        else:
+            scales, zps = _scales.calculate_scales_asymmetric(Wg, N, clipping_ratios=clipping_ratios)
+            q = _scales.quantize_weights_asymmetric(Wg, scales, zps, N)
+    elif int_bits == 8:
+        scales = _scales.calculate_scales_int8(Wg, clipping_ratios=clipping_ratios)
+        q = _scales.quantize_weights_int8(Wg, scales)
+    else:
+        scales = _scales.calculate_scales(Wg, N, clipping_ratios=clipping_ratios)
+        q = _scales.quantize_weights(Wg, scales, N)
+    mse, max_err = quant_error(Wg, q, scales, zps)
+    return QuantizationResult(
+        quantized_W=q.to(out_dev), scales=scales.to(out_dev),
+        zero_points=None if zps is None else zps.to(out_dev),
+        mse=mse, max_err=max_err, method_used="rtn", fallbacks=[])

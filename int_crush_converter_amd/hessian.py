@@ -1,0 +1,84 @@
+"""Damped Hessian inverse on the GPU (``ic_hessian_inverse``).
+
+Mirrors ``converter/gptq.py:91-121`` (``_prepare_hessian`` / ``_prepare_hinv``),
+``converter/rounding.py:19-34`` (``_invert_hessian``) and the block loop of
+``converter/ldlq.py:64-92``.  The Cholesky branch runs in the HIP library;
+when a pivot is not positive the reference falls back to ``torch.linalg.inv``
+and then ``pinv`` (with a ``UserWarning``): that rare branch is kept, on the
+GPU, for the affected matrices only.
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import torch
+
+from . import _native as nat
+from .config import DIAG_MEAN_FLOOR
+from .log import logger
+
+METHODS = {"hinv": 0, "cholesky": 1}
+
+
+def _damped(H: torch.Tensor, damping: float) -> torch.Tensor:
+    dm = H.diagonal().mean().clamp(min=DIAG_MEAN_FLOOR)
+    return H + damping * dm * torch.eye(H.shape[0], dtype=torch.float32, device=H.device)
+
+
+def _fallback_inverse(H_damped: torch.Tensor) -> torch.Tensor:
+    try:
+        return torch.linalg.inv(H_damped)
+    except torch.linalg.LinAlgError:
+        warnings.warn(
+            "Hessian is singular/ill-conditioned; falling back to pseudoinverse. "
+            "This may produce inaccurate quantization scales.",
+            stacklevel=4,
+        )
+        return torch.linalg.pinv(H_damped)
+
+
+def inverse_batch(H: torch.Tensor, damping: float, method: str = "hinv",
+                  fallbacks: list[str] | None = None) -> torch.Tensor:
+    """``H``: fp32 GPU tensor [n, n] or [batch, n, n] (not modified).  Returns
+    the damped inverse (method "hinv") or the upper Cholesky factor of the
+    damped inverse (method "cholesky") of every matrix, same shape."""
+    squeeze = H.dim() == 2
+    Hb = H.unsqueeze(0) if squeeze else H
+    batch, n, _ = Hb.shape
+    out = Hb.float().contiguous().clone()
+    if n == 0 or batch == 0:
+        return out[0] if squeeze else out
+    code = METHODS[method]
+    info = torch.zeros(2 * batch, dtype=torch.int32, device=out.device)
+    ws = nat.workspace(nat.lib().ic_hessian_inverse_workspace_bytes(batch, n), out.device)
+    nat.check(nat.lib().ic_hessian_inverse(out.data_ptr(), batch, n, float(damping), code, info.data_ptr(),
+                                           ws.data_ptr(), nat.stream()), "ic_hessian_inverse")
+    del ws
+    inf = info.tolist()
+    for b in range(batch):
+        chol_failed = inf[b] != 0
+        inv_chol_failed = code == 1 and inf[batch + b] != 0
+        if not (chol_failed or inv_chol_failed):
+            continue
+        Hd = _damped(Hb[b].float(), damping)
+        if chol_failed:
+            logger.debug("Cholesky of the damped Hessian failed at column %d; using inv", inf[b])
+            if fallbacks is not None:
+                fallbacks.append("hessian_inv_fallback")
+            Hi = _fallback_inverse(Hd)
+        else:
+            Hi = None
+        if code == 0:
+            out[b] = Hi
+            continue
+        if Hi is None:
+            # chol(H) worked but chol(H^-1) did not: return H^-1 itself (gptq.py:106-110)
+            Hi = inverse_batch(Hb[b], damping, "hinv")
+            out[b] = Hi
+            continue
+        try:
+            out[b] = torch.linalg.cholesky(Hi).T
+        except torch.linalg.LinAlgError:
+            out[b] = Hi
+    return out[0] if squeeze else out
