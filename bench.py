@@ -1,0 +1,237 @@
+"""Benchmark of the per-layer quantisation path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+A step is one pass of the per-layer path over one synthetic layer whose
+inputs are already resident in HBM: bf16 weights and the fp32 calibration
+Hessian in, packed INT4 codes + fp16 scales + int8 zero-points out
+(rotation of W, two-sided rotation of H, damping, Cholesky, inverse, GPTQ
+sweep with the fp32-MFMA lazy update, fp64 verification, packing).  Building
+H = X^T X / n from X is calibration and is outside the timed region.
+
+Prints one JSON line (the last line of stdout).  ``value`` is Mweights/s
+(out x in weights per second of wall time); ``roofline`` reports the
+dominant kernel phase measured with HIP events inside the timed region;
+``cpu_baseline`` times the CPU oracle (torch on the host cores, the
+reference's own algorithm) on one layer of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GPTQ-INT4 Mweights/s at 4096x12288 rot256; % of HBM / fp32-MFMA peak"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3
+
+WORKLOADS = {
+    # name: (kind, out, in, extra)
+    "gptq_int4_rot256_4096x12288": ("gptq", 4096, 12288, {"samples": 8192}),
+    "gptq_int4_rot256_3072x12288": ("gptq", 3072, 12288, {"samples": 8192}),
+    "gptq_int4_rot256_12288x3072": ("gptq", 12288, 3072, {"samples": 8192}),
+    "rtn_int8_asym_clip5_rot64_4096x4096": ("rtn8", 4096, 4096, {}),
+    "rtn_int4_rot256_64x256": ("rtn4", 64, 256, {}),
+    "ldlq_int4_it2_greedy5_rot256_4096x4096": ("ldlq", 4096, 4096, {}),
+}
+DEFAULT = "gptq_int4_rot256_4096x12288"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(kind, M, N, extra, seed=0):
+    import torch
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    W = (torch.randn(M, N, generator=g, device=dev) * 0.02)
+    H = None
+    if kind == "rtn8":
+        cols = torch.randperm(N, generator=g, device=dev)[: max(1, N // 100)]
+        W[:, cols] *= 20
+    if kind == "ldlq":
+        # Student-t(4) scaled to std 0.02; t = z / sqrt(chi2_4 / 4)
+        z = torch.randn(M, N, generator=g, device=dev)
+        chi = (torch.randn(M, N, 4, generator=g, device=dev) ** 2).sum(-1)
+        W = z / torch.sqrt(chi / 4) * (0.02 / math.sqrt(2))
+    W = W.to(torch.bfloat16 if kind != "rtn4" else torch.float32)
+    if kind == "gptq":
+        S = extra["samples"]
+        s = torch.exp(torch.randn(N, generator=g, device=dev))
+        H = torch.zeros(N, N, dtype=torch.float32, device=dev)
+        for r0 in range(0, S, 2048):     # X^T X / S in chunks of X rows
+            X = torch.randn(min(2048, S - r0), N, generator=g, device=dev) * s
+            H.addmm_(X.T, X)
+            del X
+        H /= S
+    torch.cuda.synchronize()
+    return W, H
+
+
+def gpu_step(kind, W, H):
+    from int_crush_converter_amd import layer as L
+    if kind == "gptq":
+        W_work, _ = L.prepare_weights(W, 256)
+        codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=256, block_size=128, damping=0.01, int_bits=4,
+                                      asymmetric=False, hessian_method="hinv", fallbacks=[])
+        return L.finish(W_work, codes, s16, z8, 4)
+    if kind == "rtn8":
+        W_work, _ = L.prepare_weights(W, 64)
+        codes, s16, z8, packed = L.rtn_codes(W_work, 8, True, [0.8, 0.85, 0.9, 0.95, 1.0])
+        return L.finish(W_work, codes, s16, z8, 8, packed=packed)
+    if kind == "rtn4":
+        W_work, _ = L.prepare_weights(W, 256)
+        codes, s16, z8, packed = L.rtn_codes(W_work, 4, False, None)
+        return L.finish(W_work, codes, s16, z8, 4, packed=packed)
+    if kind == "ldlq":
+        import warnings
+        from int_crush_converter_amd.ldlq import ldlq_quantize_layer
+        W_work, _ = L.prepare_weights(W, 256)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            r = ldlq_quantize_layer(W_work, None, 128, 0.01, 4, iterations=2, greedy_passes=5)
+        return L.finish(W_work, r.quantized_W, r.scales, None, 4)
+    raise ValueError(kind)
+
+
+def cpu_step(kind, W, H):
+    """The reference's CPU algorithm (oracle restatement) on the same layer."""
+    import torch
+    from oracle import torch_ref as ref
+    Wf = W.float()
+    Wf = Wf.masked_fill(Wf.abs() > 1000.0, 0.0)
+    if kind == "gptq":
+        Wr = ref.rotate_weights(Wf, 256)
+        Hr = ref.rotate_hessian(H, 256)
+        r = ref.gptq_quantize_layer(Wr, Hr, 128, 0.01, 4)
+        q, s, z = r.quantized_W, r.scales, r.zero_points
+    elif kind == "rtn8":
+        Wr = ref.rotate_weights(Wf, 64)
+        q, s, z = ref.rtn_layer(Wr, 8, True, [0.8, 0.85, 0.9, 0.95, 1.0])
+    elif kind == "rtn4":
+        Wr = ref.rotate_weights(Wf, 256)
+        q, s, z = ref.rtn_layer(Wr, 4, False, None)
+    else:
+        import warnings
+        Wr = ref.rotate_weights(Wf, 256)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            r = ref.ldlq_quantize_layer(Wr, None, 128, 0.01, 4, iterations=2, greedy_passes=5)
+        q, s, z = r.quantized_W, r.scales, None
+    d = (q.float() - (z.float() if z is not None else 0)) * s.float()
+    (Wr - d).double().pow(2).mean().item()
+    if kind != "rtn8":
+        ref.pack_int4(q)
+
+
+def roofline_from(prof):
+    """Dominant phase -> roofline object."""
+    mfma = {"gemm_trailing", "gemm_cholesky", "gemm_inverse", "greedy"}
+    name, ph = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    n = max(ph["launches"], 1)
+    avg_ms = ph["ms"] / n
+    if name in mfma:
+        achieved = (ph["flops"] / n) / (avg_ms * 1e-3) / 1e12 if avg_ms > 0 else 0.0
+        bound, peak, unit = "mfma", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+    else:
+        achieved = (ph["bytes"] / n) / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
+        bound, peak, unit = "hbm", PEAK_HBM_GBS, "GB/s"
+    return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                  "frac": round(achieved / peak, 4), "traffic": None}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build runs the per-layer path on a single MI355X "
+              "(layers shard across GPUs without communication; see the sharding notes).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from int_crush_converter_amd import _native as nat
+    kind, M, N, extra = WORKLOADS[args.workload]
+    log(f"[bench] workload {args.workload}: generating inputs")
+    W, H = make_inputs(kind, M, N, extra)
+    nat.lib()
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        gpu_step(kind, W, H)
+    torch.cuda.synchronize()
+    if not args.no_profile:
+        nat.profile_enable(True)
+    log(f"[bench] timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = gpu_step(kind, W, H)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    prof = None
+    if not args.no_profile:
+        prof = nat.profile_read()
+        nat.profile_enable(False)
+    weights = M * N
+    value = weights / (ms * 1e-3) / 1e6
+    log(f"[bench] {ms:.3f} ms/step, {value:.1f} Mweights/s, mse {out.mse:.3e}")
+
+    result = {
+        "metric": METRIC if args.workload == DEFAULT else f"{args.workload} Mweights/s",
+        "value": round(value, 3),
+        "unit": "Mweights/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,0.02^2) bf16 weights; H = X^T X / n, X rows N(0, diag(s^2)), "
+                "s ~ LogNormal(0,1)); random-init, no checkpoint",
+        "config": {"workload": args.workload, "out_features": M, "in_features": N,
+                   "layers_per_s": round(1e3 / ms, 4), "rot_size": 256 if kind != "rtn8" else 64,
+                   "block": 128, "damping": 0.01},
+    }
+    if prof is not None:
+        dom, roof = roofline_from(prof)
+        result["roofline"] = roof
+        result["roofline"]["kernel"] = dom
+        steps = args.steps
+        result["phases"] = {k: {"ms_per_step": round(v["ms"] / steps, 4), "launches_per_step": v["launches"] // steps,
+                                "TFLOP/s": round(v["flops"] / max(v["ms"], 1e-9) / 1e9, 3),
+                                "GB/s": round(v["bytes"] / max(v["ms"], 1e-9) / 1e6, 1)}
+                            for k, v in prof.items() if v["launches"]}
+    if not args.no_cpu_baseline:
+        threads = torch.get_num_threads()
+        log(f"[bench] CPU baseline (oracle, {threads} threads): 1 layer")
+        Wc = W.cpu()
+        Hc = H.cpu() if H is not None else None
+        c0 = time.perf_counter()
+        cpu_step(kind, Wc, Hc)
+        c1 = time.perf_counter()
+        result["cpu_baseline"] = {"value": round(weights / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
+                                  "cores": threads, "kind": "port",
+                                  "sample": f"1 layer of {args.workload} ({c1 - c0:.1f} s), torch CPU oracle "
+                                            "restating the reference's CPU path"}
+        log(f"[bench] CPU {c1 - c0:.2f} s")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

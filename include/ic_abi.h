@@ -47,11 +47,15 @@ const char* ic_last_error(void);
  * src is f32/bf16/f16 [rows, cols] (ld_src), dst is f32 [rows, cols_pad]
  * (ld_dst) with cols_pad = cols rounded up to a multiple of rot; the padding
  * is zero before rotation.  src may alias dst when dtype is f32 and
- * ld_src == ld_dst.  rot: power of 2 in [1, 4096].
+ * ld_src == ld_dst.  rot: power of 2 in [1, 4096] (1 = convert/pad only).
+ * When zero_above > 0, inputs with |w| > zero_above are replaced by 0 before
+ * rotating and their number is added to *n_zeroed (device uint64, may be
+ * NULL) - the outlier sanitising of converter/pipeline.py:527-537.
  * Replaces converter/rotation.py:95-125 (rotate_weights) and :128-153
  * (rotate_activations, same operation on a [-1, in] view). */
 int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
-                   float* dst, int64_t cols_pad, int64_t ld_dst, int rot, void* stream);
+                   float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
+                   unsigned long long* n_zeroed, void* stream);
 
 /* Two-sided rotation R^T H R of `batch` square fp32 matrices [n, n] stored
  * back to back with leading dimension ld (n multiple of rot), in place.
@@ -188,6 +192,56 @@ int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const f
  * Hinv [N, N]; W modified; Q int8 [rows, N]; workspace as for GPTQ. */
 int ic_ldlq_quantize(float* W, int64_t rows, int64_t N, const float* Hinv, const float* scales,
                      int bits, int block, int8_t* Q, void* workspace, void* stream);
+
+/* LDLQ initial per-element scales S[r, c] = max(absmax_r / (7 or 127), 1e-5)
+ * (no upper clamp) and the row vector srow (may be NULL).
+ * Replaces converter/ldlq.py:211-215. */
+int ic_ldlq_init_scales(const float* row_absmax, int64_t rows, int64_t cols, int bits, float* srow,
+                        float* S, void* stream);
+
+/* Non-finite scales -> 1e-8 (NaN, -inf) / 1e30 (+inf), then floor 1e-8
+ * (converter/ldlq.py:327-330, 499-502). */
+int ic_sanitize_scales(float* S, int64_t n, void* stream);
+
+/* sum((W - Q*S)^2) in fp64 into out_sumsq[0]; workspace 8192 bytes
+ * (converter/ldlq.py:518). */
+int ic_ldlq_mse(const float* W, const int8_t* Q, const float* S, int64_t n, double* out_sumsq,
+                void* workspace, void* stream);
+
+/* Iterative LDLQ scale update (converter/ldlq.py:553-599): where q != 0 and
+ * sign(w) == sign(q) with |w| > 1e-8: out = momentum*cur + (1-momentum) *
+ * clamp(|w|/|q|, lo, hi); where q != 0 otherwise: clamp(flat, lo, hi);
+ * else cur. */
+int ic_ldlq_update_scales(const float* W, const int8_t* Q, const float* cur, const float* flat,
+                          int64_t n, float momentum, float lo, float hi, float* out, void* stream);
+
+/* Per-row least-squares scale clamp(sum(q w) / max(sum(q q), 1e-8), min 1e-5)
+ * (converter/ldlq.py:227-231, 262-265). */
+int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64_t cols, float* out, void* stream);
+
+/* Full-rank greedy coordinate descent on the integer grid minimising
+ * tr((Q s - W) H (Q s - W)^T), `passes` sweeps over all columns, row scales
+ * srow, H [cols, cols] fp32; Q (int8 [rows, cols]) updated in place.
+ * Column blocks of 64 take their cross terms from one fp32-MFMA GEMM plus
+ * exact in-block corrections.  workspace: ic_greedy_workspace_bytes().
+ * Replaces converter/greedy.py:487-541 (greedy_local_search_pytorch) and
+ * 207-285 (greedy_local_search_triton). */
+int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols);
+int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
+              int passes, int bits, void* workspace, void* stream);
+
+/* ---------------------------------------------------------------- profiling */
+
+/* Launch profiler (no reference counterpart; measurement support).  While
+ * enabled, library launches are bracketed by HIP events on their stream and
+ * tagged with a phase: 0 trailing-update GEMM, 1 Cholesky GEMMs, 2 inverse
+ * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
+ * rotation, 7 RTN / pack / verify, 8 greedy, 9 other.  Enabling resets the
+ * record.  ic_profile_read synchronises the events and returns, per phase,
+ * the summed kernel time (ms), algorithmic flops and bytes, and the launch
+ * count (arrays of at least 10 entries). */
+int ic_profile_enable(int on);
+int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,10 @@ from .scales import (
     quantize_weights_int8_asymmetric,
 )
 from .config import INT4_SCALE_DIVISOR, INT8_SCALE_DIVISOR
+from .gptq import gptq_quantize_layer, gptq_quantize_layer_rtn
+from .ldlq import ldlq_quantize_layer
+from .calibration_io import load_calibration, build_name_map, get_hessian, get_per_channel_amax
+from .pipeline import quantize_model, should_skip
 from .types import QuantizationResult, QuantizeConfig, ProgressInfo, ProgressSummary, ProgressCallback
 
 __all__ = [
@@ -28,5 +32,8 @@ __all__ = [
     "calculate_scales_asymmetric", "quantize_weights_asymmetric",
     "calculate_scales_int8_asymmetric", "quantize_weights_int8_asymmetric",
     "INT4_SCALE_DIVISOR", "INT8_SCALE_DIVISOR",
+    "gptq_quantize_layer", "gptq_quantize_layer_rtn", "ldlq_quantize_layer",
+    "load_calibration", "build_name_map", "get_hessian", "get_per_channel_amax",
+    "quantize_model", "should_skip",
     "QuantizationResult", "QuantizeConfig", "ProgressInfo", "ProgressSummary", "ProgressCallback",
 ]

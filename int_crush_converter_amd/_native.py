@@ -34,7 +34,7 @@ _f32 = _c.c_float
 _SIGS = {
     "ic_abi_version": (_i32, []),
     "ic_last_error": (_c.c_char_p, []),
-    "ic_rotate_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _vp]),
+    "ic_rotate_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _f32, _vp, _vp]),
     "ic_rotate_hessian": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp]),
     "ic_row_stats": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "ic_rtn_scales": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _c.POINTER(_f32), _i32, _vp, _vp, _vp]),
@@ -51,7 +51,31 @@ _SIGS = {
     "ic_gptq_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "ic_gptq_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "ic_ldlq_quantize": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "ic_ldlq_init_scales": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "ic_sanitize_scales": (_i32, [_vp, _i64, _vp]),
+    "ic_ldlq_mse": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "ic_ldlq_update_scales": (_i32, [_vp, _vp, _vp, _vp, _i64, _f32, _f32, _f32, _vp, _vp]),
+    "ic_ls_scales": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "ic_greedy_workspace_bytes": (_i64, [_i64, _i64]),
+    "ic_greedy": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
+    "ic_profile_enable": (_i32, [_i32]),
+    "ic_profile_read": (_i32, [_vp, _vp, _vp, _vp, _i32]),
 }
+
+PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
+                "rotate_h", "rtn_pack_verify", "greedy", "other"]
+
+
+def profile_enable(on: bool) -> None:
+    check(lib().ic_profile_enable(int(on)), "ic_profile_enable")
+
+
+def profile_read() -> dict[str, dict]:
+    n = len(PROFILE_TAGS)
+    ms, fl, by = ((ctypes.c_double * n)() for _ in range(3))
+    la = (ctypes.c_int64 * n)()
+    check(lib().ic_profile_read(ms, fl, by, la, n), "ic_profile_read")
+    return {t: {"ms": ms[i], "flops": fl[i], "bytes": by[i], "launches": la[i]} for i, t in enumerate(PROFILE_TAGS)}
 
 
 def header_functions() -> list[str]:

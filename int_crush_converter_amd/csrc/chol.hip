@@ -19,6 +19,8 @@
 namespace icq {
 
 constexpr int NB = 128;
+
+static double dtri(double n) { return n * (n + 1) / 2; }
 constexpr int TP = NB + 1;   // LDS pitch of the diagonal tile
 
 __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
@@ -160,19 +162,24 @@ static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, flo
         const int64_t k0 = kb * NB;
         const int nb = (int)std::min<int64_t>(NB, n - k0);
         float* Dk = dinv + kb * NB * NB;
-        hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
-                           dstride, info);
-        IC_CHECK_LAUNCH();
+        {
+            ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
+            hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
+                               dstride, info);
+            IC_CHECK_LAUNCH();
+        }
         const int64_t m = n - k0 - nb;
         if (m <= 0) break;
         float* A21 = H + (k0 + nb) * ld + k0;
         // panel: A21 <- A21 * Dinv^T (in place: one tile column spans all nb columns)
-        GemmArgs p{m, nb, nb, 1.0f, 0.0f, A21, ld, sH, Dk, NB, dstride, A21, ld, sH, 0, 1, CMASK_FULL, KR_FULL, batch};
+        GemmArgs p{m, nb, nb, 1.0f, 0.0f, A21, ld, sH, Dk, NB, dstride, A21, ld, sH, 0, 1, CMASK_FULL, KR_FULL, batch,
+                   PT_GEMM_CHOL, (double)batch * m * nb * (nb + 1)};
         int rc = gemm_f32(p, st);
         if (rc) return rc;
         // trailing: A22 -= A21 A21^T (lower)
         float* A22 = H + (k0 + nb) * ld + (k0 + nb);
-        GemmArgs s{m, m, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, A22, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch};
+        GemmArgs s{m, m, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, A22, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch,
+                   PT_GEMM_CHOL, (double)batch * 2.0 * dtri((double)m) * nb};
         rc = gemm_f32(s, st);
         if (rc) return rc;
     }
@@ -194,7 +201,7 @@ static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld,
         if (k0 > 0) {
             // X[k, :k] <- Dinv_k X[k, :k]   (in place, M = nb <= 128)
             GemmArgs a{nb, k0, nb, 1.0f, 0.0f, Dk, NB, dstride, Xk, ld, sH, Xk, ld, sH, 0, 0, CMASK_FULL, KR_FULL,
-                       batch};
+                       batch, PT_GEMM_INV, (double)batch * k0 * nb * (nb + 1)};
             rc = gemm_f32(a, st);
             if (rc) return rc;
         }
@@ -205,7 +212,8 @@ static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld,
         if (m <= 0) break;
         // X[k+1:, :k+1] -= L[k+1:, k] X[k, :k+1]
         GemmArgs c{m, k0 + nb, nb, -1.0f, 1.0f, L + (k0 + nb) * ld + k0, ld, sH, Xk, ld, sH, X + (k0 + nb) * ld, ld,
-                   sH, 0, 0, CMASK_FULL, KR_FULL, batch};
+                   sH, 0, 0, CMASK_FULL, KR_FULL, batch, PT_GEMM_INV,
+                   (double)batch * m * (2.0 * k0 * nb + (double)nb * (nb + 1))};
         rc = gemm_f32(c, st);
         if (rc) return rc;
     }
@@ -238,7 +246,8 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     rc = trtri(H, X, batch, n, ld, sH, dinv, st);
     if (rc) return rc;
     // H^-1 (upper triangle incl. diagonal) = X^T X  -> H
-    GemmArgs u{n, n, n, 1.0f, 0.0f, X, ld, sH, X, ld, sH, H, ld, sH, 1, 0, CMASK_UPPER, KR_FROM_MAXIJ, batch};
+    GemmArgs u{n, n, n, 1.0f, 0.0f, X, ld, sH, X, ld, sH, H, ld, sH, 1, 0, CMASK_UPPER, KR_FROM_MAXIJ, batch,
+               PT_GEMM_INV, (double)batch * 2.0 * (double)n * (n + 1) * (n + 2) / 6.0};
     rc = gemm_f32(u, st);
     if (rc) return rc;
     dim3 tb(16, 16), tg((unsigned)cdiv(n, 16), (unsigned)cdiv(n, 16), (unsigned)batch);

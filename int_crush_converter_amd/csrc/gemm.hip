@@ -194,6 +194,9 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     int64_t tiles = tm * tn;
     if ((g.cmask == CMASK_LOWER || g.cmask == CMASK_UPPER) && tm == tn) tiles = tm * (tm + 1) / 2;
     IC_REQUIRE(tiles < (1LL << 31) && g.batch <= 65535, "gemm_f32: problem too large");
+    const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
+    const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
+    ProfScope prof_scope(st, g.tag, fl, by);
     hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)tiles, 1, (unsigned)g.batch), dim3(256), 0, st, g);
     IC_CHECK_LAUNCH();
     return IC_OK;

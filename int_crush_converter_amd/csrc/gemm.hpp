@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "prof.hpp"
 
 namespace icq {
 
@@ -28,6 +29,8 @@ struct GemmArgs {
     int transA, transB;
     int cmask, krange;
     int64_t batch;
+    int tag = PT_OTHER;        // profiler phase
+    double algo_flops = 0.0;   // algorithmic flops of the launch (0: 2*M*N*K*batch)
 };
 
 // Launches on `st`; returns IC_OK or an error code.  Safe in place (C aliases

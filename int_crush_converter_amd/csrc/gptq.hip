@@ -156,6 +156,8 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
     constexpr int L = 16;
     const int64_t wgs = cdiv(a.rows, SW_THREADS / L);
+    ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
+                 (double)groups * (a.rows * a.nb * 9.0 + 4.0 * a.nb * a.nb));
     if (a.mode == SWEEP_GPTQ)
         hipLaunchKernelGGL((sweep_kernel<L, SWEEP_GPTQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
                            st, a);
@@ -212,7 +214,7 @@ static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t 
         if (rest > 0) {
             // W[:, b0+nb : gw] -= E @ Hinv[b0 : b0+nb, b0+nb : gw]   (per group)
             GemmArgs ga{rows, rest, nb, -1.0f, 1.0f, E, nb, rows * nb, Hinv + b0 * ldh + b0 + nb, ldh, hg,
-                        W + b0 + nb, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups};
+                        W + b0 + nb, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
             rc = gemm_f32(ga, st);
             if (rc) return rc;
         }

@@ -1,0 +1,37 @@
+// Optional launch profiler: when enabled (ic_profile_enable), instrumented
+// launches are bracketed by HIP events on their stream and tagged with a
+// phase and the algorithmic flops / bytes they perform.  ic_profile_read()
+// synchronises the recorded events and returns per-phase totals.  Disabled,
+// a scope costs one branch.
+#pragma once
+
+#include "common.hpp"
+
+namespace icq {
+
+enum ProfTag : int {
+    PT_GEMM_TRAIL = 0,   // GPTQ / LDLQ lazy trailing update
+    PT_GEMM_CHOL = 1,    // potrf panel + SYRK
+    PT_GEMM_INV = 2,     // trtri + lauum
+    PT_DIAG = 3,         // nb x nb diagonal factor + inverse
+    PT_SWEEP = 4,        // GPTQ / LDLQ column sweep
+    PT_ROTATE = 5,       // weight rotation
+    PT_ROTATE_H = 6,     // two-sided Hessian rotation
+    PT_RTN = 7,          // scales / quantise / pack / verify
+    PT_GREEDY = 8,       // greedy block kernel + its cross-term GEMMs
+    PT_OTHER = 9,
+    PT_COUNT = 10,
+};
+
+bool prof_enabled();
+
+class ProfScope {
+public:
+    ProfScope(hipStream_t st, int tag, double flops, double bytes);
+    ~ProfScope();
+private:
+    hipStream_t st_;
+    int idx_ = -1;
+};
+
+}  // namespace icq

@@ -16,6 +16,7 @@
 // LDS kernel (any power of 2 up to 4096, and the column pass of R^T H R):
 // a [rot x TC] tile is staged in LDS and transformed stage by stage.
 #include "common.hpp"
+#include "prof.hpp"
 
 namespace icq {
 
@@ -36,10 +37,25 @@ __device__ __forceinline__ float bfly4_x(float v) {
     return s * 0.5f - p;
 }
 
+// Outlier sanitising on load (converter/pipeline.py:527-537): |w| > zero_above
+// (when zero_above > 0) becomes 0 before rotation; the count goes to *nz.
+__device__ __forceinline__ float sanitize(float v, float zero_above, unsigned& cnt) {
+    if (zero_above > 0.0f && fabsf(v) > zero_above) { ++cnt; return 0.0f; }
+    return v;
+}
+
+__device__ __forceinline__ void flush_count(unsigned cnt, unsigned long long* nz) {
+    if (!nz) return;
+    unsigned long long c = wave_sum((unsigned long long)cnt);
+    if ((threadIdx.x & 63) == 0 && c) atomicAdd(nz, c);
+}
+
 template <int ROT>
 __global__ __launch_bounds__(256) void rotate_rows_reg(
     const void* __restrict__ src, int dtype, int64_t rows, int64_t cols, int64_t ld_src,
-    float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst, int vec_ok) {
+    float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst, int vec_ok, float zero_above,
+    unsigned long long* nz) {
+    unsigned cnt = 0;
     const int64_t cpr = cols_pad >> 4;  // 16-column chunks per row
     const int64_t total = rows * cpr;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -80,6 +96,8 @@ __global__ __launch_bounds__(256) void rotate_rows_reg(
             for (int i = 0; i < 16; ++i)
                 v[i] = (c0 + i < cols) ? load_as_f32(src, dtype, base + i) : 0.0f;
         }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = sanitize(v[i], zero_above, cnt);
         // digit 0 (stride 1)
 #pragma unroll
         for (int a = 0; a < 4; ++a) bfly4(v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
@@ -105,17 +123,21 @@ __global__ __launch_bounds__(256) void rotate_rows_reg(
             for (int i = 0; i < 16; ++i) o[i] = v[i];
         }
     }
+    flush_count(cnt, nz);
 }
 
 // Convert + zero-pad copy into fp32 (used before the LDS kernel).
 __global__ void convert_pad_kernel(const void* __restrict__ src, int dtype, int64_t rows, int64_t cols,
-                                   int64_t ld_src, float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst) {
+                                   int64_t ld_src, float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst,
+                                   float zero_above, unsigned long long* nz) {
     const int64_t total = rows * cols_pad;
+    unsigned cnt = 0;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         int64_t r = i / cols_pad, c = i - r * cols_pad;
-        dst[r * ld_dst + c] = c < cols ? load_as_f32(src, dtype, r * ld_src + c) : 0.0f;
+        dst[r * ld_dst + c] = c < cols ? sanitize(load_as_f32(src, dtype, r * ld_src + c), zero_above, cnt) : 0.0f;
     }
+    flush_count(cnt, nz);
 }
 
 // In-place transform of tiles [rot along axis A] x [tc along axis B] of an
@@ -192,6 +214,8 @@ static int launch_lds(float* p, int rot, int64_t groups, int64_t nb, int64_t sa,
     int regular = is_pow4(rot) ? 1 : 0;
     float scale = regular ? 1.0f : (float)(1.0 / std::sqrt((double)rot));
     dim3 grid((unsigned)cdiv(nb, tc), (unsigned)groups, (unsigned)batch);
+    ProfScope prof_scope(st, PT_ROTATE_H, 2.0 * batch * groups * rot * nb * std::log2((double)rot),
+                 8.0 * batch * groups * rot * nb);
     hipLaunchKernelGGL(rotate_lds_kernel, grid, dim3(256), lds, st, p, rot, tc, nb, sa, sb, bstride,
                        regular, scale);
     IC_CHECK_LAUNCH();
@@ -203,7 +227,8 @@ static int launch_lds(float* p, int rot, int64_t groups, int64_t nb, int64_t sa,
 using namespace icq;
 
 extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
-                              float* dst, int64_t cols_pad, int64_t ld_dst, int rot, void* stream) {
+                              float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
+                              unsigned long long* n_zeroed, void* stream) {
     IC_REQUIRE(src && dst, "ic_rotate_rows: null pointer");
     IC_REQUIRE(src_dtype >= 0 && src_dtype <= 2, "ic_rotate_rows: bad dtype");
     IC_REQUIRE(rot >= 1 && rot <= 4096 && is_pow2(rot), "ic_rotate_rows: rot must be a power of 2 <= 4096");
@@ -219,19 +244,22 @@ extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int6
                       (ld_dst % 4 == 0);
         int64_t chunks = rows * (cols_pad / 16);
         int grid = grid_for(chunks, 256);
+        int stages = rot == 4 ? 1 : rot == 16 ? 2 : rot == 64 ? 3 : 4;
+        ProfScope prof_scope(st, src == (const void*)dst ? PT_ROTATE_H : PT_ROTATE, 2.0 * stages * rows * cols_pad,
+                     (double)rows * cols * esz + 4.0 * rows * cols_pad);
         switch (rot) {
-            case 4: hipLaunchKernelGGL(rotate_rows_reg<4>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok); break;
-            case 16: hipLaunchKernelGGL(rotate_rows_reg<16>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok); break;
-            case 64: hipLaunchKernelGGL(rotate_rows_reg<64>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok); break;
-            default: hipLaunchKernelGGL(rotate_rows_reg<256>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok); break;
+            case 4: hipLaunchKernelGGL(rotate_rows_reg<4>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
+            case 16: hipLaunchKernelGGL(rotate_rows_reg<16>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
+            case 64: hipLaunchKernelGGL(rotate_rows_reg<64>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
+            default: hipLaunchKernelGGL(rotate_rows_reg<256>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
         }
         IC_CHECK_LAUNCH();
         return IC_OK;
     }
     // generic: convert/pad into dst, then transform in place in LDS
-    if (!(src == (const void*)dst && cols == cols_pad)) {
+    if (!(src == (const void*)dst && cols == cols_pad && zero_above <= 0.0f)) {
         hipLaunchKernelGGL(convert_pad_kernel, dim3(grid_for(rows * cols_pad, 256)), dim3(256), 0, st, src,
-                           src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst);
+                           src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, zero_above, n_zeroed);
         IC_CHECK_LAUNCH();
     }
     if (rot == 1) return IC_OK;
@@ -246,7 +274,7 @@ extern "C" int ic_rotate_hessian(float* H, int64_t batch, int64_t n, int64_t ld,
     if (batch == 0 || n == 0 || rot == 1) return IC_OK;
     hipStream_t st = as_stream(stream);
     // rows: H <- H R; the batch is batch*n consecutive rows of pitch ld
-    int rc = ic_rotate_rows(H, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, stream);
+    int rc = ic_rotate_rows(H, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, 0.0f, nullptr, stream);
     if (rc) return rc;
     // columns: H <- R^T H; axis A = rows (stride ld), axis B = columns (stride 1)
     return launch_lds(H, rot, n / rot, n, ld, 1, batch, n * ld, st);

@@ -9,6 +9,7 @@
 // accumulated in fp64, so only candidates whose fp32 MSEs tie to within the
 // reference's own fp32 summation noise could be chosen differently.
 #include "common.hpp"
+#include "prof.hpp"
 
 namespace icq {
 
@@ -326,6 +327,7 @@ extern "C" int ic_rtn_quantize(const float* W, int64_t rows, int64_t cols, int64
     IC_REQUIRE(!codes || ld_q >= cols, "ic_rtn_quantize: bad ld_q");
     IC_REQUIRE(!packed || ld_p >= cdiv(cols, 2), "ic_rtn_quantize: bad ld_p");
     if (rows == 0 || cols == 0) return IC_OK;
+    ProfScope prof_scope(as_stream(stream), PT_RTN, 0.0, (double)rows * cols * (4 + (codes ? 1 : 0) + (packed ? 0.5 : 0)));
     hipLaunchKernelGGL(rtn_quant_kernel, dim3(elem_grid(rows * cdiv(cols, 16))), dim3(256), 0, as_stream(stream), W,
                        rows, cols, ld, bits, scale, scale_kind, zp, codes, ld_q, packed, ld_p);
     IC_CHECK_LAUNCH();
@@ -339,6 +341,7 @@ extern "C" int ic_pack_int4(const void* src, int src_kind, int64_t rows, int64_t
     hipStream_t st = as_stream(stream);
     IC_CHECK_HIP(hipMemsetAsync(flags, 0, 3 * sizeof(int32_t), st));
     if (rows == 0 || cols == 0) return IC_OK;
+    ProfScope prof_scope(st, PT_RTN, 0.0, (double)rows * cols * (src_kind == 0 ? 1.5 : 4.5));
     hipLaunchKernelGGL(pack_int4_kernel, dim3(elem_grid(rows * cdiv(cols, 2))), dim3(256), 0, st, src, src_kind, rows,
                        cols, ld_src, dst, ld_dst, flags);
     IC_CHECK_LAUNCH();
@@ -368,6 +371,7 @@ extern "C" int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_
     hipStream_t st = as_stream(stream);
     double* ps = reinterpret_cast<double*>(workspace);
     float* pm = reinterpret_cast<float*>(ps + QERR_BLOCKS);
+    ProfScope prof_scope(st, PT_RTN, 0.0, (double)rows * cols * 5.0);
     hipLaunchKernelGGL(quant_error_partial, dim3(QERR_BLOCKS), dim3(256), 0, st, W, rows, cols, ld, codes, ld_q,
                        scale, scale_kind, zp, ps, pm);
     IC_CHECK_LAUNCH();

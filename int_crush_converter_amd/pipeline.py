@@ -1,0 +1,300 @@
+"""``quantize_model``: safetensors in, quantised safetensors out (API of
+``converter/pipeline.py``).
+
+Same validation, output tensor names, dtypes and ``int_crush.*`` metadata as
+the reference for the methods this build implements (RTN, GPTQ, LDLQ with
+greedy search, ConvRot rotation).  Each layer goes to the GPU once: the
+per-layer step (``layer.py``) rotates, quantises, verifies and packs there;
+only the stored tensors come back to host memory.  Options that belong to
+other subsystems of the reference (PermuQuant, SmoothQuant / SmoothRot,
+SVD-absorbed, PiSO, DLR Hessians) raise ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import copy
+import json
+import os
+import time
+import warnings
+
+import torch
+from safetensors.torch import load_file, save_file
+
+from .calibration_io import build_name_map, get_hessian, is_dlr, load_calibration
+from .config import DEFAULT_SKIP_PATTERNS
+from .log import logger
+from .types import ProgressCallback, ProgressInfo, ProgressSummary, QuantizeConfig
+from . import layer as _layer
+
+
+def should_skip(name: str, skip_patterns: list[str]) -> bool:
+    """True when a (lower-cased) layer name contains any skip pattern."""
+    low = name.lower()
+    return any(p in low for p in skip_patterns)
+
+
+def _validate(config: QuantizeConfig) -> QuantizeConfig:
+    """Validation and implicit couplings of converter/pipeline.py:173-250."""
+    if config.quant_method not in ("rtn", "gptq", "ldlq"):
+        raise ValueError(f"quant_method must be 'rtn', 'gptq', or 'ldlq', got '{config.quant_method}'")
+    if config.quant_method == "gptq" and not config.calibration_path:
+        raise ValueError("GPTQ requires --calibration path to a .pt file")
+    if config.quant_method == "ldlq" and not config.calibration_path:
+        warnings.warn(
+            "LDLQ: no calibration data provided; will fall back to "
+            "H = W^T W / M (weight-only). This can perform worse than RTN. "
+            "Pass --calibration for best results.")
+    if config.rot_size > 0 and (config.rot_size & (config.rot_size - 1)) != 0:
+        raise ValueError(f"rot_size must be 0 (no rotation) or a power of 2, got {config.rot_size}")
+    if config.perm_group_size < 32 or (config.perm_group_size & (config.perm_group_size - 1)) != 0:
+        raise ValueError(f"perm_group_size must be a power of 2 >= 32, got {config.perm_group_size}")
+    if config.quant_group_size < 32 or (config.quant_group_size & (config.quant_group_size - 1)) != 0:
+        raise ValueError(f"quant_group_size must be a power of 2 >= 32, got {config.quant_group_size}")
+    if config.int_bits not in (4, 8):
+        raise ValueError(f"int_bits must be 4 or 8, got {config.int_bits}")
+    if config.smoothquant and config.int_bits == 4:
+        logger.warning("SmoothQuant is designed for W8A8 (INT8) quantization. With INT4 weight-only "
+                       "quantization, the benefit is limited. Consider using --int-bits 8 with --smoothquant.")
+    config = copy.copy(config)
+    if config.smoothrot and config.int_bits == 4 and not config.force_smoothrot_w4:
+        logger.warning("SmoothRot is automatically disabled at W4; use --force-smoothrot-w4 to override.")
+        config.smoothrot = False
+    if config.smoothquant and config.rot_size > 0:
+        config.smoothrot = True
+    if config.smoothrot:
+        if config.rot_size == 0:
+            raise ValueError("SmoothRot requires rot_size > 0")
+        config.smoothquant = True
+    if config.svd_rank < 0:
+        raise ValueError(f"svd_rank must be >= 0, got {config.svd_rank}")
+    if config.rot_size > 4096:
+        raise ValueError(f"rot_size {config.rot_size} exceeds the supported maximum 4096")
+    for flag, what in [(config.use_permuquant, "PermuQuant (--permuquant)"),
+                       (config.smoothquant, "SmoothQuant / SmoothRot (--smoothquant, --smoothrot)"),
+                       (config.svd_rank > 0, "SVD-absorbed (--svd-rank)"),
+                       (config.piso_scales, "PiSO (--piso)")]:
+        if flag:
+            raise NotImplementedError(f"{what} is not part of this build's quantization path")
+    return config
+
+
+def _metadata(config: QuantizeConfig, state_dict, skip_patterns) -> dict[str, str]:
+    """int_crush.* metadata (converter/pipeline.py:417-487)."""
+    is_int8 = config.int_bits == 8
+    method_base = "int_crush"
+    method = f"{method_base}_{config.quant_method}" if config.quant_method in ("gptq", "ldlq") else method_base
+    asym = config.asymmetric or (config.quant_method == "gptq" and not is_int8)
+    md = {
+        "int_crush.format_version": "3" if not is_int8 else "1",
+        "int_crush.method": method,
+        "int_crush.rot_size": str(config.rot_size),
+        "int_crush.scale_type": "per_row_asymmetric" if asym else "per_row",
+        "int_crush.hadamard_type": "regular",
+        "int_crush.packing_order": "native" if is_int8 else "little",
+    }
+    if config.exclude_patterns:
+        md["int_crush.exclude_patterns"] = ",".join(config.exclude_patterns)
+    if config.rot_size > 0:
+        padded = {}
+        for name, t in state_dict.items():
+            if t.dim() == 2 and not should_skip(name, skip_patterns) and t.shape[1] % config.rot_size:
+                padded[name] = str(t.shape[1])
+        if padded:
+            md["int_crush.padded_layers"] = ";".join(f"{k}={v}" for k, v in padded.items())
+    if config.quant_method == "gptq":
+        md["int_crush.gptq_block_size"] = str(config.gptq_block_size)
+        md["int_crush.damping_ratio"] = str(config.damping)
+    elif config.quant_method == "ldlq":
+        md["int_crush.ldlq_block_size"] = str(config.gptq_block_size)
+        md["int_crush.damping_ratio"] = str(config.damping)
+        md["int_crush.ldlq_iterations"] = str(config.ldlq_iterations)
+        if config.greedy_passes > 0:
+            md["int_crush.greedy_passes"] = str(config.greedy_passes)
+            md["int_crush.rank_threshold"] = str(config.rank_threshold)
+    return md
+
+
+def _comfy_tensor(name: str, config: QuantizeConfig, fmt: bool) -> tuple[str, torch.Tensor]:
+    prefix = name.rsplit(".weight", 1)[0]
+    data = {"format": "int8_tensorwise"} if fmt else {"per_row": True}
+    if config.rot_size > 0:
+        data["convrot"] = True
+        data["convrot_groupsize"] = config.rot_size
+    blob = json.dumps(data, separators=(",", ":")) if fmt else json.dumps(data)
+    return f"{prefix}.comfy_quant", torch.tensor(list(blob.encode("utf-8")), dtype=torch.uint8)
+
+
+def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, calibration, name_map,
+                   state: dict) -> _layer.LayerOutput:
+    """One layer of the pipeline loop on the GPU; ``state`` carries counters and
+    one-time warnings across layers."""
+    is_int8 = config.int_bits == 8
+    W_work, nz = _layer.prepare_weights(tensor, config.rot_size)
+    outliers = int(nz.item())
+    if outliers:
+        logger.warning("Zeroed %d outlier weight values in %s (|W| > %.0f)", outliers, name, 1000.0)
+    fallbacks: list[str] = []
+    packed = None
+    if config.quant_method in ("gptq", "ldlq"):
+        layer_name = name_map.get(name) if name_map else None
+        hessian = None
+        if layer_name is not None and calibration is not None:
+            hessian = get_hessian(calibration, layer_name, tensor.shape)
+        rot_h = 0
+        if hessian is not None:
+            md = calibration.get("metadata", {}) or {}
+            already = md.get("hessian_rotated", False)
+            cal_rot = md.get("rot_size", 0)
+            if already and cal_rot and int(cal_rot) != config.rot_size and not state.get("rot_warned"):
+                logger.warning("Calibration rot_size=%s != converter rot_size=%d. Hessian is in the wrong "
+                               "rotation space.", cal_rot, config.rot_size)
+                state["rot_warned"] = True
+            if is_dlr(hessian):
+                raise NotImplementedError("DLR Hessians are not supported by this build")
+            if not already and config.rot_size > 0:
+                rot_h = config.rot_size
+    if config.quant_method == "gptq":
+        if hessian is not None:
+            codes, s16, z8 = _layer.gptq_codes(
+                W_work, hessian, rotate_h=rot_h, block_size=config.gptq_block_size, damping=config.damping,
+                int_bits=config.int_bits, asymmetric=config.asymmetric, hessian_method=config.hessian_method,
+                fallbacks=fallbacks)
+            method = "gptq_hip"
+            state["gptq"] += 1
+        else:
+            codes, s16, z8, packed = _layer.rtn_codes(W_work, config.int_bits, config.asymmetric,
+                                                      config.clipping_ratios)
+            method = "rtn"
+            state["rtn_fallback"] += 1
+            logger.debug("No calibration data, using RTN fallback")
+    elif config.quant_method == "ldlq":
+        from .ldlq import ldlq_quantize_layer
+        H = None
+        if hessian is not None:
+            from .rotation import rotate_hessian_gpu
+            from . import _native as nat
+            H = nat.to_gpu(hessian).float()
+            if rot_h:
+                H = rotate_hessian_gpu(H, rot_h)
+        r = ldlq_quantize_layer(W_work, hessian=H, block_size=config.gptq_block_size, damping=config.damping,
+                                int_bits=config.int_bits, iterations=config.ldlq_iterations,
+                                greedy_passes=config.greedy_passes, rank_threshold=config.rank_threshold)
+        codes, s16, z8 = r.quantized_W, r.scales, r.zero_points
+        method = r.method_used
+        fallbacks.extend(r.fallbacks)
+        state["gptq"] += 1
+    else:
+        codes, s16, z8, packed = _layer.rtn_codes(W_work, config.int_bits, config.asymmetric,
+                                                  config.clipping_ratios)
+        method = "rtn"
+    out = _layer.finish(W_work, codes, s16, z8, config.int_bits, packed=packed, method=method,
+                        fallbacks=fallbacks, outliers=outliers)
+    if out.bad_scales:
+        logger.warning("Replaced bad scale values in %s (Inf/NaN/zero); quality may be degraded", name)
+    return out
+
+
+def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallback | None = None) -> None:
+    """Quantise every 2-D, non-skipped tensor of ``config.input_path`` and write
+    ``<output_dir>/model.safetensors`` (reference pipeline.py:150-1179)."""
+    skip_patterns = config.skip_patterns if config.skip_patterns is not None else DEFAULT_SKIP_PATTERNS
+    if config.exclude_patterns:
+        skip_patterns = list(skip_patterns) + config.exclude_patterns
+        logger.info("Excluding additional patterns: %s", config.exclude_patterns)
+    config = _validate(config)
+    is_int8 = config.int_bits == 8
+    if config.seed >= 0:
+        torch.manual_seed(config.seed)
+        if torch.cuda.is_available():
+            torch.cuda.manual_seed_all(config.seed)
+    os.makedirs(config.output_dir, exist_ok=True)
+
+    logger.info("Loading %s...", config.input_path)
+    state_dict = load_file(config.input_path)
+    logger.info("Loaded %d tensors", len(state_dict))
+
+    calibration, name_map = None, {}
+    if config.quant_method in ("gptq", "ldlq") and config.calibration_path:
+        logger.info("Loading calibration from %s...", config.calibration_path)
+        calibration = load_calibration(config.calibration_path)
+        cal_keys = list(calibration["hessians"].keys())
+        name_map = build_name_map(list(state_dict.keys()), cal_keys)
+        logger.info("Matched %d/%d calibration layers to model layers", len(name_map), len(cal_keys))
+
+    metadata = _metadata(config, state_dict, skip_patterns)
+    output: dict[str, torch.Tensor] = {}
+    state = {"gptq": 0, "rtn_fallback": 0}
+    skipped = quantized = 0
+    reports: list[dict] = []
+    total = sum(1 for n, t in state_dict.items() if not should_skip(n, skip_patterns) and t.dim() == 2)
+    t0 = time.monotonic() if progress_callback is not None else None
+
+    for name, tensor in state_dict.items():
+        if should_skip(name, skip_patterns) or tensor.dim() != 2:
+            output[name] = tensor
+            skipped += 1
+            continue
+        logger.info("Quantizing %s (%s)...", name, tensor.shape)
+        out = quantize_layer(name, tensor, config, calibration, name_map, state)
+        logger.debug("MSE=%.6f  max_err=%.4f", out.mse, out.max_err)
+        if config.quality_report_path is not None:
+            fb = list(out.fallbacks) + (["scale_repair"] if out.bad_scales else [])
+            reports.append({
+                "name": name, "method": out.method, "mse": out.mse, "max_err": out.max_err,
+                "scale_range": [out.scales.min().item(), out.scales.max().item()],
+                "fallbacks": fb, "shape": list(tensor.shape), "smoothquant": False, "smoothrot": False,
+                "smooth_source": None, "svd_rank": 0,
+            })
+        output[name] = out.stored.cpu()
+        output[f"{name}_scale"] = out.scales.cpu()
+        if out.zero_points is not None:
+            output[f"{name}_zp"] = out.zero_points.cpu()
+        if is_int8 and config.comfy_int8_fast:
+            k, v = _comfy_tensor(name, config, fmt=False)
+            output[k] = v
+        if is_int8 and config.comfy_compat:
+            k, v = _comfy_tensor(name, config, fmt=True)
+            output[k] = v
+        quantized += 1
+        if progress_callback is not None:
+            elapsed = time.monotonic() - t0
+            remaining = elapsed / quantized * (total - quantized) if quantized > 1 else 0.0
+            progress_callback(ProgressInfo(
+                current_layer=quantized, total_layers=total, layer_name=name, layer_shape=tuple(tensor.shape),
+                elapsed_seconds=elapsed, estimated_remaining_seconds=max(remaining, 0.0), method=out.method,
+                mse=out.mse))
+        if name.endswith(".weight"):
+            bias = name[: -len(".weight")] + ".bias"
+            if bias in state_dict:
+                output[bias] = state_dict[bias]
+
+    output = {k: v.contiguous() for k, v in output.items()}
+    path = os.path.join(config.output_dir, "model.safetensors")
+    logger.info("Saving to %s...", path)
+    save_file(output, path, metadata=metadata)
+
+    in_gb = sum(t.numel() * t.element_size() for t in state_dict.values()) / (1024 ** 3)
+    out_gb = sum(t.numel() * t.element_size() for t in output.values()) / (1024 ** 3)
+    ratio = in_gb / out_gb if out_gb else 0.0
+    logger.info("Done! Quantized %d layers, skipped %d layers", quantized, skipped)
+    if config.quant_method in ("gptq", "ldlq"):
+        logger.info("%s: %d layers, RTN fallback: %d layers", config.quant_method.upper(), state["gptq"],
+                    state["rtn_fallback"])
+    logger.info("Input size: %.2f GB", in_gb)
+    logger.info("Output size: %.2f GB", out_gb)
+    logger.info("Compression ratio: %.2fx", ratio)
+    if progress_callback is not None:
+        progress_callback(ProgressSummary(
+            total_layers=quantized, skipped_layers=skipped, permuted_layers=0, gptq_layers=state["gptq"],
+            rtn_fallback_layers=state["rtn_fallback"], smoothquant_layers=0, svd_layers=0,
+            elapsed_seconds=time.monotonic() - t0, input_size_gb=round(in_gb, 2), output_size_gb=round(out_gb, 2),
+            compression_ratio=round(ratio, 2)))
+    if config.quality_report_path is not None:
+        report = {"layers": reports, "summary": {
+            "total_layers": quantized + skipped, "quantized": quantized, "skipped": skipped,
+            "input_gb": round(in_gb, 2), "output_gb": round(out_gb, 2), "compression_ratio": round(ratio, 2)}}
+        os.makedirs(os.path.dirname(os.path.abspath(config.quality_report_path)), exist_ok=True)
+        with open(config.quality_report_path, "w") as f:
+            json.dump(report, f, indent=2)
+        logger.info("Quality report written to %s", config.quality_report_path)

@@ -70,16 +70,20 @@ def _check_rot(rot_size: int) -> None:
         raise ValueError(f"rot_size {rot_size} exceeds the supported maximum 4096")
 
 
-def rotate_rows_gpu(W: torch.Tensor, rot_size: int) -> torch.Tensor:
+def rotate_rows_gpu(W: torch.Tensor, rot_size: int, zero_above: float = 0.0,
+                    n_zeroed: torch.Tensor | None = None) -> torch.Tensor:
     """Rotate the rows of a 2-D GPU tensor (f32/bf16/f16) into a fresh fp32
-    [rows, cols_pad] GPU tensor.  Internal fast path used by the pipeline."""
+    [rows, cols_pad] GPU tensor (rot_size 1 = convert only).  With
+    zero_above > 0, |w| > zero_above is zeroed first and counted into the
+    int64 GPU tensor ``n_zeroed``.  Internal fast path used by the pipeline."""
     W = W.contiguous()
     rows, cols = W.shape
     cols_pad = -(-cols // rot_size) * rot_size
     out = torch.empty(rows, cols_pad, dtype=torch.float32, device=W.device)
     L = nat.lib()
     nat.check(L.ic_rotate_rows(W.data_ptr(), nat.dtype_code(W), rows, cols, cols, out.data_ptr(),
-                               cols_pad, cols_pad, rot_size, nat.stream()), "ic_rotate_rows")
+                               cols_pad, cols_pad, rot_size, float(zero_above), nat.ptr(n_zeroed), nat.stream()),
+              "ic_rotate_rows")
     return out
 
 

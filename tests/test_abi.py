@@ -43,7 +43,7 @@ def test_argument_validation_without_gpu(libicq):
     """Bad arguments are rejected on the host before any HIP call."""
     nat.load(require_gpu=False)
     L = nat._lib
-    rc = L.ic_rotate_rows(None, 0, 4, 16, 16, None, 16, 16, 16, None)
+    rc = L.ic_rotate_rows(None, 0, 4, 16, 16, None, 16, 16, 16, 0.0, None, None)
     assert rc == -1 and b"null" in L.ic_last_error()
-    rc = L.ic_rotate_rows(1, 0, 4, 16, 16, 1, 16, 16, 12, None)
+    rc = L.ic_rotate_rows(1, 0, 4, 16, 16, 1, 16, 16, 12, 0.0, None, None)
     assert rc == -1 and b"power of 2" in L.ic_last_error()

@@ -1,0 +1,160 @@
+"""End-to-end ``quantize_model`` on the GPU: output names, dtypes, shapes and
+metadata against the reference's golden pipeline files, stored bytes and
+scales against the oracle, GPTQ / LDLQ runs with calibration files,
+progress events and the quality report."""
+
+from __future__ import annotations
+
+import json
+import os
+import warnings
+
+import pytest
+import torch
+from safetensors import safe_open
+from safetensors.torch import load_file, save_file
+
+from oracle import torch_ref as ref
+from tests.conftest import lognormal_hessian
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(tmp_path, state, **kw):
+    from int_crush_converter_amd.pipeline import quantize_model
+    from int_crush_converter_amd.types import QuantizeConfig
+    src = str(tmp_path / "in.safetensors")
+    save_file(state, src)
+    out = str(tmp_path / "out")
+    events = []
+    quantize_model(QuantizeConfig(input_path=src, output_dir=out, **kw), progress_callback=events.append)
+    path = os.path.join(out, "model.safetensors")
+    with safe_open(path, framework="pt") as f:
+        md = f.metadata()
+    return load_file(path), md, events
+
+
+@pytest.mark.parametrize("tag", ["pipe_rtn4", "pipe_rtn8a"])
+def test_pipeline_matches_reference_golden(gpu_dev, golden, tmp_path, tag):
+    t, meta = golden
+    state = {k[len("pipe_in/"):]: v for k, v in t.items() if k.startswith("pipe_in/")}
+    res, md, _ = _run(tmp_path, state, **meta[tag]["config"])
+    want = {k[len(tag) + 1:]: v for k, v in t.items() if k.startswith(tag + "/")}
+    assert md == meta[tag]["metadata"]
+    assert set(res) == set(want)
+    for k, v in want.items():
+        assert res[k].dtype == v.dtype and res[k].shape == v.shape, k
+        if k.endswith("_scale") or k.endswith("_zp") or "norm" in k or k.endswith(".bias"):
+            assert torch.equal(res[k], v), k
+        else:
+            agree = (res[k] == v).float().mean().item()
+            assert agree >= 0.9999, (k, agree)
+
+
+def test_pipeline_rtn_bytes_vs_oracle(gpu_dev, tmp_path):
+    g = torch.Generator().manual_seed(3)
+    state = {"blk.0.fc.weight": (torch.randn(96, 512, generator=g) * 0.02).to(torch.bfloat16),
+             "blk.0.fc2.weight": torch.randn(32, 300, generator=g) * 0.05}
+    res, md, ev = _run(tmp_path, state, rot_size=256, int_bits=4)
+    for name, W in state.items():
+        Wr = ref.rotate_weights(W.float(), 256)
+        # bytes follow from the rotated weights: compare against codes of the GPU rotation
+        from int_crush_converter_amd.rotation import rotate_weights
+        Wg = rotate_weights(W.float().to(gpu_dev), 256).cpu()
+        assert torch.allclose(Wg, Wr, atol=1e-6)
+        s = ref.scales_int4_sym(Wg, Wg.shape[1])
+        q = ref.quant_int4_sym(Wg, s, Wg.shape[1])
+        assert torch.equal(res[f"{name}_scale"], s)
+        assert torch.equal(res[name], ref.pack_int4(q))
+    assert [type(e).__name__ for e in ev] == ["ProgressInfo", "ProgressInfo", "ProgressSummary"]
+    assert ev[0].current_layer == 1 and ev[1].total_layers == 2
+
+
+def test_pipeline_outlier_zeroing(gpu_dev, tmp_path):
+    W = torch.randn(16, 64) * 0.02
+    W[3, 5] = 5000.0
+    W[7, 9] = float("inf")
+    res, _, _ = _run(tmp_path, {"a.weight": W}, rot_size=0, int_bits=8)
+    Wz = W.masked_fill(W.abs() > 1000, 0.0)
+    s = ref.scales_int8_sym(Wz)
+    assert torch.equal(res["a.weight_scale"], s)
+    assert torch.equal(res["a.weight"], ref.quant_int8_sym(Wz, s))
+
+
+def _calib(tmp_path, hessians, rotated=False, rot=0):
+    path = str(tmp_path / "cal.pt")
+    torch.save({"hessians": hessians, "shapes": {k: list(v.shape) for k, v in hessians.items()},
+                "layer_types": {k: "linear" for k in hessians},
+                "metadata": {"num_samples": 256, "hessian_rotated": rotated, "rot_size": rot}}, path)
+    return path
+
+
+def test_pipeline_gptq_with_calibration(gpu_dev, tmp_path):
+    g = torch.Generator().manual_seed(5)
+    state = {"layers.0.attn.qkv.weight": torch.randn(64, 512, generator=g) * 0.02,
+             "layers.0.mlp.up.weight": torch.randn(48, 256, generator=g) * 0.02,
+             "layers.0.nocal.weight": torch.randn(16, 256, generator=g) * 0.02}
+    hs = {"layers.0.attn.qkv": lognormal_hessian(512, 700, 1),
+          "layers.0.mlp.up": torch.stack([lognormal_hessian(256, 400, 2)])}
+    cal = _calib(tmp_path, hs)
+    res, md, ev = _run(tmp_path, state, rot_size=256, quant_method="gptq", calibration_path=cal,
+                       quality_report_path=str(tmp_path / "rep.json"))
+    assert md["int_crush.method"] == "int_crush_gptq" and md["int_crush.scale_type"] == "per_row_asymmetric"
+    for name, W in state.items():
+        assert res[name].dtype == torch.uint8 and res[name].shape == (W.shape[0], W.shape[1] // 2)
+        assert res[f"{name}_scale"].dtype == torch.float16 and res[f"{name}_zp"].dtype == torch.int8
+    # the calibrated layers against the oracle
+    for name, key in [("layers.0.attn.qkv.weight", "layers.0.attn.qkv"), ("layers.0.mlp.up.weight", "layers.0.mlp.up")]:
+        Wr = ref.rotate_weights(state[name], 256)
+        Hr = ref.rotate_hessian(hs[key], 256)
+        r = ref.gptq_quantize_layer(Wr, Hr, 128, 0.01, 4)
+        assert torch.equal(res[f"{name}_scale"], r.scales)
+        q = ref.unpack_int4(res[name], Wr.shape[1])
+        assert (q == r.quantized_W).float().mean().item() >= 0.999
+    assert [e.method for e in ev[:-1]] == ["gptq_hip", "gptq_hip", "rtn"]
+    assert ev[-1].gptq_layers == 2 and ev[-1].rtn_fallback_layers == 1
+    rep = json.load(open(tmp_path / "rep.json"))
+    assert len(rep["layers"]) == 3 and rep["summary"]["quantized"] == 3
+
+
+def test_pipeline_ldlq_weight_only(gpu_dev, tmp_path):
+    g = torch.Generator().manual_seed(6)
+    state = {"l.0.w.weight": torch.randn(64, 256, generator=g) * 0.02}
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        res, md, ev = _run(tmp_path, state, rot_size=256, quant_method="ldlq", ldlq_iterations=2, greedy_passes=2)
+    assert md["int_crush.method"] == "int_crush_ldlq" and md["int_crush.greedy_passes"] == "2"
+    assert "l.0.w.weight_zp" not in res and res["l.0.w.weight"].shape == (64, 128)
+    Wr = ref.rotate_weights(state["l.0.w.weight"], 256)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        r = ref.ldlq_quantize_layer(Wr, None, 128, 0.01, 4, iterations=2, greedy_passes=2)
+    q = ref.unpack_int4(res["l.0.w.weight"], 256)
+    assert (q == r.quantized_W).float().mean().item() >= 0.98
+
+
+def test_pipeline_callback_abort_leaves_no_output(gpu_dev, tmp_path):
+    from int_crush_converter_amd.pipeline import quantize_model
+    from int_crush_converter_amd.types import QuantizeConfig
+    src = str(tmp_path / "in.safetensors")
+    save_file({"a.weight": torch.randn(8, 32)}, src)
+
+    def boom(info):
+        raise RuntimeError("stop")
+
+    with pytest.raises(RuntimeError, match="stop"):
+        quantize_model(QuantizeConfig(input_path=src, output_dir=str(tmp_path / "o"), rot_size=0),
+                       progress_callback=boom)
+    assert not os.path.exists(tmp_path / "o" / "model.safetensors")
+
+
+def test_cli_end_to_end(gpu_dev, tmp_path):
+    from int_crush_converter_amd.cli import main
+    src = str(tmp_path / "in.safetensors")
+    save_file({"b.0.q.weight": torch.randn(16, 256) * 0.02, "b.0.q.bias": torch.randn(16)}, src)
+    main(["-i", src, "-o", str(tmp_path / "cli"), "--rot-size", "64", "--int-bits", "8", "--asymmetric",
+          "--clipping-ratios", "0.9,1.0", "--comfy-compat", "--no-progress", "-q"])
+    res = load_file(str(tmp_path / "cli" / "model.safetensors"))
+    assert set(res) == {"b.0.q.weight", "b.0.q.weight_scale", "b.0.q.weight_zp", "b.0.q.bias", "b.0.q.comfy_quant"}
+    assert json.loads(bytes(res["b.0.q.comfy_quant"].tolist()).decode()) == {
+        "format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 64}

@@ -1,0 +1,136 @@
+"""Host-side logic on the CPU (no GPU calls): validation and error
+conventions, the metadata contract, calibration parsing, skip rules and the
+CLI flag surface."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from int_crush_converter_amd import calibration_io as cio
+from int_crush_converter_amd.config import DEFAULT_SKIP_PATTERNS
+from int_crush_converter_amd.pipeline import _metadata, _validate, should_skip
+from int_crush_converter_amd.types import QuantizeConfig
+
+
+def cfg(**kw):
+    return QuantizeConfig(input_path="x", output_dir="y", **kw)
+
+
+def test_config_defaults_match_reference():
+    c = cfg()
+    assert (c.rot_size, c.int_bits, c.quant_method, c.gptq_block_size, c.damping, c.hessian_method) == \
+        (256, 4, "rtn", 128, 0.01, "hinv")
+    assert (c.ldlq_iterations, c.greedy_passes, c.rank_threshold, c.seed) == (1, 0, 0.01, 42)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(quant_method="awq"), "quant_method must be"),
+    (dict(quant_method="gptq"), "GPTQ requires --calibration"),
+    (dict(rot_size=12), "rot_size must be 0"),
+    (dict(perm_group_size=16), "perm_group_size must be"),
+    (dict(quant_group_size=100), "quant_group_size must be"),
+    (dict(int_bits=3), "int_bits must be 4 or 8"),
+    (dict(svd_rank=-1), "svd_rank must be"),
+    (dict(smoothrot=True, rot_size=0, int_bits=8), "SmoothRot requires rot_size"),
+])
+def test_validation_errors(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        _validate(cfg(**kw))
+
+
+@pytest.mark.parametrize("kw", [dict(use_permuquant=True), dict(smoothquant=True, int_bits=8),
+                                dict(svd_rank=16), dict(piso_scales=True)])
+def test_unsupported_features_raise(kw):
+    with pytest.raises(NotImplementedError):
+        _validate(cfg(**kw))
+
+
+def test_should_skip_default_patterns():
+    assert should_skip("model.embed_tokens.weight", DEFAULT_SKIP_PATTERNS)
+    assert should_skip("blocks.3.NORM1.weight", DEFAULT_SKIP_PATTERNS)
+    assert should_skip("final.proj_out.weight", DEFAULT_SKIP_PATTERNS)
+    assert not should_skip("blocks.3.attn.qkv.weight", DEFAULT_SKIP_PATTERNS)
+
+
+def _sd():
+    return {"blocks.0.attn.qkv.weight": torch.zeros(4, 300), "blocks.0.norm.weight": torch.zeros(300),
+            "blocks.0.mlp.up.weight": torch.zeros(4, 512)}
+
+
+def test_metadata_configs():
+    """The output contract of the five benchmark configurations."""
+    sd = {"a.weight": torch.zeros(2, 256)}
+    assert _metadata(cfg(rot_size=256, int_bits=4), sd, DEFAULT_SKIP_PATTERNS) == {
+        "int_crush.format_version": "3", "int_crush.method": "int_crush", "int_crush.rot_size": "256",
+        "int_crush.scale_type": "per_row", "int_crush.hadamard_type": "regular", "int_crush.packing_order": "little"}
+    assert _metadata(cfg(rot_size=64, int_bits=8, asymmetric=True, clipping_ratios=[0.9]), sd,
+                     DEFAULT_SKIP_PATTERNS) == {
+        "int_crush.format_version": "1", "int_crush.method": "int_crush", "int_crush.rot_size": "64",
+        "int_crush.scale_type": "per_row_asymmetric", "int_crush.hadamard_type": "regular",
+        "int_crush.packing_order": "native"}
+    assert _metadata(cfg(rot_size=256, quant_method="gptq", calibration_path="c"), sd, DEFAULT_SKIP_PATTERNS) == {
+        "int_crush.format_version": "3", "int_crush.method": "int_crush_gptq", "int_crush.rot_size": "256",
+        "int_crush.scale_type": "per_row_asymmetric", "int_crush.hadamard_type": "regular",
+        "int_crush.packing_order": "little", "int_crush.gptq_block_size": "128", "int_crush.damping_ratio": "0.01"}
+    assert _metadata(cfg(rot_size=256, quant_method="ldlq", ldlq_iterations=2, greedy_passes=5), sd,
+                     DEFAULT_SKIP_PATTERNS) == {
+        "int_crush.format_version": "3", "int_crush.method": "int_crush_ldlq", "int_crush.rot_size": "256",
+        "int_crush.scale_type": "per_row", "int_crush.hadamard_type": "regular", "int_crush.packing_order": "little",
+        "int_crush.ldlq_block_size": "128", "int_crush.damping_ratio": "0.01", "int_crush.ldlq_iterations": "2",
+        "int_crush.greedy_passes": "5", "int_crush.rank_threshold": "0.01"}
+
+
+def test_metadata_padded_and_excluded():
+    md = _metadata(cfg(rot_size=256, exclude_patterns=["mlp"]), _sd(), DEFAULT_SKIP_PATTERNS + ["mlp"])
+    assert md["int_crush.padded_layers"] == "blocks.0.attn.qkv.weight=300"
+    assert md["int_crush.exclude_patterns"] == "mlp"
+
+
+def test_calibration_formats(tmp_path):
+    full = torch.eye(6)
+    blocks = torch.stack([torch.eye(4), torch.eye(4)])
+    lst = [torch.eye(4), torch.eye(2)]
+    bad = torch.eye(6)
+    bad[0, 0] = float("nan")
+    cal = {"hessians": {"a": full, "b": blocks, "c": lst, "d": bad, "e": torch.eye(5)},
+           "shapes": {}, "layer_types": {}}
+    assert torch.equal(cio.get_hessian(cal, "a", (3, 6)), full)
+    assert cio.get_hessian(cal, "b", (3, 8)).shape == (2, 4, 4)
+    assert cio.get_hessian(cal, "b", (3, 9)) is None             # wrong block count
+    h = cio.get_hessian(cal, "c", (3, 6))
+    assert h.shape == (2, 4, 4) and h[1, 2:, 2:].abs().sum() == 0
+    assert cio.get_hessian(cal, "d", (3, 6)) is None             # non-finite
+    assert cio.get_hessian(cal, "e", (3, 6)) is None             # shape mismatch
+    assert cio.get_hessian(cal, "zz", (3, 6)) is None
+    path = tmp_path / "c.pt"
+    torch.save(cal, path)
+    assert set(cio.load_calibration(str(path))["hessians"]) == set(cal["hessians"])
+    torch.save({"hessians": {}}, tmp_path / "bad.pt")
+    with pytest.raises(KeyError):
+        cio.load_calibration(str(tmp_path / "bad.pt"))
+    with pytest.raises(ValueError):
+        cio.load_calibration(str(tmp_path / "missing.pt"))
+
+
+def test_build_name_map():
+    m = cio.build_name_map(["a.b.weight", "a.c.weight", "a.b.bias", "x"], ["a.b", "q"])
+    assert m == {"a.b.weight": "a.b"}
+
+
+def test_cli_flags_parse():
+    from int_crush_converter_amd.cli import build_parser
+    a = build_parser().parse_args(["-i", "in", "-o", "out", "--rot-size", "256", "--quant-method", "gptq", "-c",
+                                   "cal.pt", "--gptq-block-size", "64", "--damping", "0.02", "--hessian-method",
+                                   "cholesky", "--ldlq-iterations", "2", "--greedy-passes", "5",
+                                   "--clipping-ratios", "0.9,1.0", "--int-bits", "8", "--asymmetric"])
+    assert (a.rot_size, a.quant_method, a.calibration, a.gptq_block_size, a.damping, a.hessian_method) == \
+        (256, "gptq", "cal.pt", 64, 0.02, "cholesky")
+    assert (a.ldlq_iterations, a.greedy_passes, a.clipping_ratios, a.int_bits, a.asymmetric) == \
+        (2, 5, "0.9,1.0", 8, True)
+
+
+def test_cli_rejects_bad_rot(capsys):
+    from int_crush_converter_amd.cli import main
+    with pytest.raises(SystemExit):
+        main(["-i", "a", "-o", "b", "--rot-size", "12", "-q"])
