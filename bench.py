@@ -133,9 +133,14 @@ def cpu_step(kind, W, H):
 
 
 def roofline_from(prof):
-    """Dominant phase -> roofline object."""
-    mfma = {"gemm_trailing", "gemm_cholesky", "gemm_inverse", "greedy"}
-    name, ph = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    """Dominant kernel (most summed time over the timed steps) -> roofline.
+    achieved = algorithmic work per launch / average launch duration."""
+    from int_crush_converter_amd._native import PROFILE_KERNELS
+    kernels = {}
+    for kname, phases in PROFILE_KERNELS.items():
+        kernels[kname] = {k: sum(prof[p][k] for p in phases) for k in ("ms", "flops", "bytes", "launches")}
+    name, ph = max(kernels.items(), key=lambda kv: kv[1]["ms"])
+    mfma = {"gemm_f32_kernel"}
     n = max(ph["launches"], 1)
     avg_ms = ph["ms"] / n
     if name in mfma:

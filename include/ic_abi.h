@@ -236,10 +236,11 @@ int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int6
  * enabled, library launches are bracketed by HIP events on their stream and
  * tagged with a phase: 0 trailing-update GEMM, 1 Cholesky GEMMs, 2 inverse
  * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
- * rotation, 7 RTN / pack / verify, 8 greedy, 9 other.  Enabling resets the
- * record.  ic_profile_read synchronises the events and returns, per phase,
- * the summed kernel time (ms), algorithmic flops and bytes, and the launch
- * count (arrays of at least 10 entries). */
+ * rotation, 7 RTN / pack / verify, 8 greedy block kernel, 9 other, 10 greedy
+ * cross-term GEMMs.  Enabling resets the record.  ic_profile_read
+ * synchronises the events and returns, per phase, the summed kernel time
+ * (ms), algorithmic flops and bytes, and the launch count (arrays of at least
+ * 11 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

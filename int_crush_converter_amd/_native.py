@@ -63,7 +63,15 @@ _SIGS = {
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
-                "rotate_h", "rtn_pack_verify", "greedy", "other"]
+                "rotate_h", "rtn_pack_verify", "greedy", "other", "gemm_greedy"]
+
+# kernel -> the profiler phases its launches are tagged with
+PROFILE_KERNELS = {
+    "gemm_f32_kernel": ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy"],
+    "potrf_diag_kernel": ["diag_factor"],
+    "sweep_kernel": ["sweep"],
+    "greedy_block_kernel": ["greedy"],
+}
 
 
 def profile_enable(on: bool) -> None:

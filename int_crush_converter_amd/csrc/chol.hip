@@ -21,7 +21,6 @@ namespace icq {
 constexpr int NB = 128;
 
 static double dtri(double n) { return n * (n + 1) / 2; }
-constexpr int TP = NB + 1;   // LDS pitch of the diagonal tile
 
 __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
     float* A = H + (int64_t)blockIdx.x * stride;
@@ -43,65 +42,117 @@ __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, flo
 // upper part of the block set to 0) and write Dinv = L_kk^-1 (lower, upper 0)
 // to dinv (pitch NB).  info[b] gets the 1-based column of the first
 // non-positive pivot (LAPACK convention) if it is still 0.
+//
+// 256 threads as a 16 x 16 grid; thread (ty, tx) keeps the 8 x 8 tile at
+// rows 8ty.., columns 8tx.. of both L and X = L^-1 in registers.  Column j of
+// the Cholesky (and row k of the inverse) is published through LDS once per
+// step, double-buffered so one barrier per step suffices.  Rank-1 updates are
+// unconditional: factors of rows / columns that must not change are zero.
+// A partial block (nb < 128) is padded with the identity.
 __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
                                                          float* dinv, int64_t dstride, int* info) {
-    __shared__ float T[NB * TP];
-    __shared__ float X[NB * TP];
-    __shared__ int bad;
+    __shared__ float colL[2][NB];
+    __shared__ float rowX[2][NB];
     const int b = blockIdx.x;
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
     const int t = threadIdx.x;
-    if (t == 0) bad = 0;
-    for (int idx = t; idx < nb * nb; idx += blockDim.x) {
-        int i = idx / nb, j = idx - i * nb;
-        T[i * TP + j] = j <= i ? A[(int64_t)i * ld + j] : 0.0f;
-    }
-    __syncthreads();
-    // right-looking unblocked Cholesky
-    for (int j = 0; j < nb; ++j) {
-        float d = T[j * TP + j];
-        if (!(d > 0.0f)) {           // non-positive or NaN pivot
-            if (t == 0 && bad == 0) bad = j + 1;
-            d = 1.0f;
+    const int tx = t & 15, ty = t >> 4;
+    const int r0 = ty * 8, c0 = tx * 8;
+    float a[8][8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int r = r0 + p, c = c0 + q;
+            float v = 0.0f;
+            if (c <= r) v = (r < nb) ? A[(int64_t)r * ld + c] : (r == c ? 1.0f : 0.0f);
+            a[p][q] = v;
         }
-        const float ljj = sqrtf(d);
-        __syncthreads();
-        if (t == 0) T[j * TP + j] = ljj;
-        for (int i = j + 1 + t; i < nb; i += blockDim.x) T[i * TP + j] = T[i * TP + j] / ljj;
-        __syncthreads();
-        const int m = nb - j - 1;                 // trailing size
-        // columns l = j+1.., rows i >= l; thread -> (column, row parity)
-        for (int c = t; c < m * 2; c += blockDim.x) {
-            const int l = j + 1 + (c >> 1);
-            const float llj = T[l * TP + j];
-            for (int i = l + (c & 1); i < nb; i += 2) T[i * TP + l] = T[i * TP + l] - T[i * TP + j] * llj;
+    int bad = 0;
+    int buf = 0;
+    // ---- Cholesky, right-looking, one column per step
+    for (int jb = 0; jb < 16; ++jb) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int j = jb * 8 + jj;
+            if (tx == jb) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) colL[buf][r0 + p] = a[p][jj];
+            }
+            __syncthreads();
+            float d = colL[buf][j];
+            if (!(d > 0.0f)) {
+                if (!bad) bad = j + 1;
+                d = 1.0f;
+            }
+            const float ljj = sqrtf(d);
+            const float rinv = 1.0f / ljj;
+            float li[8], lc[8];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > j) ? colL[buf][r0 + p] * rinv : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) lc[q] = (c0 + q > j) ? colL[buf][c0 + q] * rinv : 0.0f;
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) a[p][q] = a[p][q] - li[p] * lc[q];
+            if (tx == jb) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    const int r = r0 + p;
+                    if (r > j) a[p][jj] = li[p];
+                    else if (r == j) a[p][jj] = ljj;
+                }
+            }
+            buf ^= 1;
         }
-        __syncthreads();
     }
-    // X = L^-1: for k, X[k,:] = R[k,:] / L[k][k], R[i,:] -= L[i][k] X[k,:] (i > k)
-    for (int idx = t; idx < nb * nb; idx += blockDim.x) {
-        int i = idx / nb, j = idx - i * nb;
-        X[i * TP + j] = i == j ? 1.0f : 0.0f;
-    }
-    __syncthreads();
-    for (int k = 0; k < nb; ++k) {
-        const float lkk = T[k * TP + k];
-        for (int j = t; j <= k; j += blockDim.x) X[k * TP + j] = X[k * TP + j] / lkk;
-        __syncthreads();
-        const int m = nb - k - 1;
-        for (int c = t; c < m * (k + 1); c += blockDim.x) {
-            const int i = k + 1 + c / (k + 1), j = c % (k + 1);
-            X[i * TP + j] = X[i * TP + j] - T[i * TP + k] * X[k * TP + j];
+    // ---- X = L^-1, right-looking on L X = I: row k final = R[k,:] / L[k][k]
+    float x[8][8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[p][q] = (r0 + p == c0 + q) ? 1.0f : 0.0f;
+    for (int kb = 0; kb < 16; ++kb) {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const int k = kb * 8 + kk;
+            if (tx == kb) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) colL[buf][r0 + p] = a[p][kk];
+            }
+            if (ty == kb) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) rowX[buf][c0 + q] = x[kk][q];
+            }
+            __syncthreads();
+            const float rk = 1.0f / colL[buf][k];
+            float li[8], xk[8];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > k) ? colL[buf][r0 + p] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) xk[q] = rowX[buf][c0 + q] * rk;
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[p][q] = x[p][q] - li[p] * xk[q];
+            if (ty == kb) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[kk][q] = xk[q];
+            }
+            buf ^= 1;
         }
-        __syncthreads();
     }
     float* D = dinv + (int64_t)b * dstride;
-    for (int idx = t; idx < NB * NB; idx += blockDim.x) {
-        int i = idx / NB, j = idx - i * NB;
-        bool in = i < nb && j < nb;
-        if (in) A[(int64_t)i * ld + j] = j <= i ? T[i * TP + j] : 0.0f;
-        D[idx] = (in && j <= i) ? X[i * TP + j] : 0.0f;
-    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int r = r0 + p, c = c0 + q;
+            const bool in = r < nb && c < nb;
+            if (in) A[(int64_t)r * ld + c] = c <= r ? a[p][q] : 0.0f;
+            D[r * NB + c] = (in && c <= r) ? x[p][q] : 0.0f;
+        }
     if (t == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
 }
 

@@ -50,7 +50,8 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     __shared__ float Hs[SW_NB * SW_NB];
     __shared__ float Es[ROWS * SW_NB];
     __shared__ int8_t Qs[ROWS * SW_NB];
-    __shared__ float dinv[SW_NB];
+    __shared__ float dinv[SW_NB];             // GPTQ: RN(1 / Hinv_jj); LDLQ: 1 / max(Hinv_jj, 1e-8)
+    __shared__ int dok[SW_NB];                // GPTQ: Hinv_jj inside the fast-division domain
 
     const int g = blockIdx.y;
     const int nb = a.nb;
@@ -65,12 +66,11 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         int i = idx / nb, j = idx - i * nb;
         Hs[i * SW_NB + j] = H[(int64_t)i * a.ldh + j];
     }
-    if (MODE == SWEEP_LDLQ) {
-        for (int j = t; j < nb; j += SW_THREADS) {
-            float d = H[(int64_t)j * a.ldh + j];
-            d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
-            dinv[j] = 1.0f / d;
-        }
+    for (int j = t; j < nb; j += SW_THREADS) {
+        float d = H[(int64_t)j * a.ldh + j];
+        if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
+        dinv[j] = 1.0f / d;
+        dok[j] = div_b_ok(d) ? 1 : 0;
     }
     __syncthreads();
 
@@ -83,50 +83,63 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     }
     float s_row = 1.0f, z_row = 0.0f;
     float sc[MODE == SWEEP_LDLQ ? R : 1];
+    float scr[MODE == SWEEP_LDLQ ? R : 1];
     if (MODE == SWEEP_GPTQ) {
         if (rv) {
             s_row = a.s[row];
             if (a.zp) z_row = a.zp[row];
         }
+        sc[0] = s_row;
+        scr[0] = 1.0f / s_row;
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int c = r * L + lane;
             float v = (rv && c < nb) ? a.s[row * a.lds + col0 + c] : 1.0f;
-            sc[r] = v > 1e-8f ? v : (v != v ? v : 1e-8f);
+            v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
+            sc[r] = v;
+            scr[r] = 1.0f / v;
         }
     }
     const bool has_zp = a.zp != nullptr;
 
+    // Columns j = r0*L + o.  Updates are unconditional on registers r >= r0:
+    // for the owner and lower lanes the register of column r0 is already
+    // quantised and never read again, so the extra updates are dead values.
 #pragma unroll
     for (int r0 = 0; r0 < R; ++r0) {
+        const float s_el = sc[MODE == SWEEP_LDLQ ? r0 : 0];
+        const float s_rc = scr[MODE == SWEEP_LDLQ ? r0 : 0];
+        const bool s_ok = div_b_ok(s_el);
         for (int o = 0; o < L; ++o) {
             const int j = r0 * L + o;
             if (j >= nb) break;
-            // every lane evaluates its own column r0; only the owner's result is used
+            float h[R];
+#pragma unroll
+            for (int r = r0; r < R; ++r) h[r] = Hs[j * SW_NB + r * L + lane];
             const float x = w[r0];
             float q, e;
             if (MODE == SWEEP_GPTQ) {
-                float y = x / s_row;
+                float y = div_rn(x, s_el, s_rc, s_ok);
                 if (has_zp) y = y + z_row;
                 q = clampf(rhaz(y), a.qmin, a.qmax);
-                float deq = has_zp ? (q - z_row) * s_row : q * s_row;
-                e = (x - deq) / Hs[j * SW_NB + j];
+                const float deq = has_zp ? (q - z_row) * s_el : q * s_el;
+                // h[r0] on the owner lane is Hinv[j][j]
+                e = div_rn(x - deq, h[r0], dinv[j], dok[j] != 0);
                 e = clampf(e, -100.0f, 100.0f);
                 if (e != e) e = 0.0f;
             } else {
-                const float scl = sc[MODE == SWEEP_LDLQ ? r0 : 0];
-                q = clampf(rhaz(x / scl), a.qmin, a.qmax);
+                q = clampf(rhaz(div_rn(x, s_el, s_rc, s_ok)), a.qmin, a.qmax);
                 // sign-flip correction (inert for positive scales)
-                float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
-                                            : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
-                float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
-                bool flip = ws * qs < 0.0f;
-                bool can = flip && (q > a.qmin);
+                const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
+                                                  : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
+                const float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
+                const bool flip = ws * qs < 0.0f;
+                const bool can = flip && (q > a.qmin);
                 if (flip && q == a.qmin) q = a.qmax;
                 if (can) q = -q;
                 q = clampf(q, a.qmin, a.qmax);
-                e = (x - q * scl) * dinv[j];
+                e = (x - q * s_el) * dinv[j];
             }
             const float err = __shfl(e, o, L);   // broadcast from the owner lane of this row
             if (lane == o) {
@@ -134,10 +147,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 Es[rl * SW_NB + j] = e;
             }
 #pragma unroll
-            for (int r = r0; r < R; ++r) {
-                const int c = r * L + lane;
-                if ((r > r0 || lane > o) && c < nb) w[r] = w[r] - err * Hs[j * SW_NB + c];
-            }
+            for (int r = r0; r < R; ++r) w[r] = w[r] - err * h[r];
         }
     }
     __syncthreads();

@@ -55,12 +55,14 @@ __global__ __launch_bounds__(256) void ldlq_mse_kernel(const float* W, const int
     if (threadIdx.x == 0) part[blockIdx.x] = sh[0] + sh[1] + sh[2] + sh[3];
 }
 
-__global__ void sum_parts_kernel(const double* part, int n, double* out) {
-    if (threadIdx.x == 0) {
-        double a = 0.0;
-        for (int i = 0; i < n; ++i) a += part[i];
-        *out = a;
-    }
+__global__ __launch_bounds__(256) void sum_parts_kernel(const double* part, int n, double* out) {
+    double a = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) a += part[i];
+    __shared__ double sh[4];
+    a = wave_sum(a);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) *out = (sh[0] + sh[1]) + (sh[2] + sh[3]);
 }
 
 // converter/ldlq.py:553-599
@@ -212,7 +214,7 @@ extern "C" int ic_ldlq_mse(const float* W, const int8_t* Q, const float* S, int6
     double* part = reinterpret_cast<double*>(workspace);
     hipLaunchKernelGGL(ldlq_mse_kernel, dim3(1024), dim3(256), 0, st, W, Q, S, n, part);
     IC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(sum_parts_kernel, dim3(1), dim3(64), 0, st, part, 1024, out_sumsq);
+    hipLaunchKernelGGL(sum_parts_kernel, dim3(1), dim3(256), 0, st, part, 1024, out_sumsq);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }
@@ -256,7 +258,7 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
             const int nb = (int)std::min<int64_t>(GB, cols - j0);
             // cross[:, 0:nb] = err @ H[j0:j0+nb, :]^T
             GemmArgs g{rows, nb, cols, 1.0f, 0.0f, err, cols, 0, H + j0 * cols, cols, 0, cross, GB, 0, 0, 1,
-                       CMASK_FULL, KR_FULL, 1, PT_GREEDY};
+                       CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
             int rc = gemm_f32(g, st);
             if (rc) return rc;
             const int rpb = 256 / GL;

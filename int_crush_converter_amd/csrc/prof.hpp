@@ -20,7 +20,8 @@ enum ProfTag : int {
     PT_RTN = 7,          // scales / quantise / pack / verify
     PT_GREEDY = 8,       // greedy block kernel + its cross-term GEMMs
     PT_OTHER = 9,
-    PT_COUNT = 10,
+    PT_GEMM_GREEDY = 10, // greedy cross-term GEMMs
+    PT_COUNT = 11,
 };
 
 bool prof_enabled();

@@ -269,14 +269,21 @@ __global__ __launch_bounds__(256) void quant_error_partial(const float* __restri
     }
 }
 
-__global__ void quant_error_final(const double* part_sum, const float* part_max, int n, double* out_sum,
-                                  float* out_max) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        double a = 0.0;
-        float m = 0.0f;
-        for (int i = 0; i < n; ++i) { a += part_sum[i]; m = nmax(m, part_max[i]); }
-        *out_sum = a;
-        *out_max = m;
+// One workgroup: fixed-order tree reduction of the partials (deterministic).
+__global__ __launch_bounds__(256) void quant_error_final(const double* part_sum, const float* part_max, int n,
+                                                         double* out_sum, float* out_max) {
+    double a = 0.0;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) { a += part_sum[i]; m = nmax(m, part_max[i]); }
+    __shared__ double ss[4];
+    __shared__ float sm[4];
+    a = wave_sum(a);
+    m = wave_nmax(m);
+    if ((threadIdx.x & 63) == 0) { ss[threadIdx.x >> 6] = a; sm[threadIdx.x >> 6] = m; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        *out_sum = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+        *out_max = nmax(nmax(sm[0], sm[1]), nmax(sm[2], sm[3]));
     }
 }
 
@@ -375,7 +382,7 @@ extern "C" int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_
     hipLaunchKernelGGL(quant_error_partial, dim3(QERR_BLOCKS), dim3(256), 0, st, W, rows, cols, ld, codes, ld_q,
                        scale, scale_kind, zp, ps, pm);
     IC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(quant_error_final, dim3(1), dim3(64), 0, st, ps, pm, QERR_BLOCKS, out_sumsq, out_maxabs);
+    hipLaunchKernelGGL(quant_error_final, dim3(1), dim3(256), 0, st, ps, pm, QERR_BLOCKS, out_sumsq, out_maxabs);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

@@ -102,7 +102,9 @@ def test_pipeline_gptq_with_calibration(gpu_dev, tmp_path):
     assert md["int_crush.method"] == "int_crush_gptq" and md["int_crush.scale_type"] == "per_row_asymmetric"
     for name, W in state.items():
         assert res[name].dtype == torch.uint8 and res[name].shape == (W.shape[0], W.shape[1] // 2)
-        assert res[f"{name}_scale"].dtype == torch.float16 and res[f"{name}_zp"].dtype == torch.int8
+        assert res[f"{name}_scale"].dtype == torch.float16
+    # GPTQ INT4 is always asymmetric; the uncalibrated layer falls back to symmetric RTN (no _zp)
+    assert res["layers.0.attn.qkv.weight_zp"].dtype == torch.int8 and "layers.0.nocal.weight_zp" not in res
     # the calibrated layers against the oracle
     for name, key in [("layers.0.attn.qkv.weight", "layers.0.attn.qkv"), ("layers.0.mlp.up.weight", "layers.0.mlp.up")]:
         Wr = ref.rotate_weights(state[name], 256)
