@@ -49,10 +49,18 @@ __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, flo
 // step, double-buffered so one barrier per step suffices.  Rank-1 updates are
 // unconditional: factors of rows / columns that must not change are zero.
 // A partial block (nb < 128) is padded with the identity.
+// 8 consecutive LDS floats (32-byte aligned) as two 16-byte reads.
+__device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
                                                          float* dinv, int64_t dstride, int* info) {
-    __shared__ float colL[2][NB];
-    __shared__ float rowX[2][NB];
+    __shared__ __attribute__((aligned(16))) float colL[2][NB];
+    __shared__ __attribute__((aligned(16))) float rowX[2][NB];
     const int b = blockIdx.x;
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
     const int t = threadIdx.x;
@@ -88,10 +96,12 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
             const float ljj = sqrtf(d);
             const float rinv = 1.0f / ljj;
             float li[8], lc[8];
+            load8(&colL[buf][r0], li);
+            load8(&colL[buf][c0], lc);
 #pragma unroll
-            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > j) ? colL[buf][r0 + p] * rinv : 0.0f;
+            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > j) ? li[p] * rinv : 0.0f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) lc[q] = (c0 + q > j) ? colL[buf][c0 + q] * rinv : 0.0f;
+            for (int q = 0; q < 8; ++q) lc[q] = (c0 + q > j) ? lc[q] * rinv : 0.0f;
 #pragma unroll
             for (int p = 0; p < 8; ++p)
 #pragma unroll
@@ -128,10 +138,12 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
             __syncthreads();
             const float rk = 1.0f / colL[buf][k];
             float li[8], xk[8];
+            load8(&colL[buf][r0], li);
+            load8(&rowX[buf][c0], xk);
 #pragma unroll
-            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > k) ? colL[buf][r0 + p] : 0.0f;
+            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > k) ? li[p] : 0.0f;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) xk[q] = rowX[buf][c0 + q] * rk;
+            for (int q = 0; q < 8; ++q) xk[q] = xk[q] * rk;
 #pragma unroll
             for (int p = 0; p < 8; ++p)
 #pragma unroll

@@ -66,9 +66,11 @@ __device__ __forceinline__ float rhaz(float x) {
 __device__ __forceinline__ bool div_b_ok(float b) {
     return b >= 0x1p-30f && b < 0x1p31f;
 }
-__device__ __forceinline__ float div_rn(float a, float b, float y, bool b_ok) {
+// `needed` = false marks a lane whose result is discarded: it skips the
+// domain test so that it cannot force the slow path on the wave.
+__device__ __forceinline__ float div_rn(float a, float b, float y, bool b_ok, bool needed = true) {
     const float aa = fabsf(a);
-    const bool ok = b_ok && ((aa >= 0x1p-60f && aa < 0x1p61f) || aa == 0.0f);
+    const bool ok = !needed || (b_ok && ((aa >= 0x1p-60f && aa < 0x1p61f) || aa == 0.0f));
     if (__builtin_expect(!ok, 0)) return a / b;
     const float q0 = a * y;
     const float r = __builtin_fmaf(-q0, b, a);

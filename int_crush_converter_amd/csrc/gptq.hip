@@ -111,6 +111,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         const float s_el = sc[MODE == SWEEP_LDLQ ? r0 : 0];
         const float s_rc = scr[MODE == SWEEP_LDLQ ? r0 : 0];
         const bool s_ok = div_b_ok(s_el);
+#pragma nounroll
         for (int o = 0; o < L; ++o) {
             const int j = r0 * L + o;
             if (j >= nb) break;
@@ -118,18 +119,19 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 #pragma unroll
             for (int r = r0; r < R; ++r) h[r] = Hs[j * SW_NB + r * L + lane];
             const float x = w[r0];
+            const bool own = lane == o;
             float q, e;
             if (MODE == SWEEP_GPTQ) {
-                float y = div_rn(x, s_el, s_rc, s_ok);
+                float y = div_rn(x, s_el, s_rc, s_ok, own);
                 if (has_zp) y = y + z_row;
                 q = clampf(rhaz(y), a.qmin, a.qmax);
                 const float deq = has_zp ? (q - z_row) * s_el : q * s_el;
                 // h[r0] on the owner lane is Hinv[j][j]
-                e = div_rn(x - deq, h[r0], dinv[j], dok[j] != 0);
+                e = div_rn(x - deq, h[r0], dinv[j], dok[j] != 0, own);
                 e = clampf(e, -100.0f, 100.0f);
                 if (e != e) e = 0.0f;
             } else {
-                q = clampf(rhaz(div_rn(x, s_el, s_rc, s_ok)), a.qmin, a.qmax);
+                q = clampf(rhaz(div_rn(x, s_el, s_rc, s_ok, own)), a.qmin, a.qmax);
                 // sign-flip correction (inert for positive scales)
                 const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
                                                   : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 e = (x - q * s_el) * dinv[j];
             }
             const float err = __shfl(e, o, L);   // broadcast from the owner lane of this row
-            if (lane == o) {
+            if (own) {
                 Qs[rl * SW_NB + j] = (int8_t)(int)q;
                 Es[rl * SW_NB + j] = e;
             }
