@@ -1,10 +1,14 @@
 // fp32 GEMM on the CDNA4 matrix cores (v_mfma_f32_16x16x4_f32).
 //
-// Workgroup tile 128x128, K staged 16 at a time through double-buffered LDS;
-// 4 waves in a 2x2 arrangement, each owning a 64x64 sub-tile held as 4x4
-// MFMA 16x16 accumulators (64 VGPRs).  Per 4-wide k step a wave issues 16
-// MFMAs (512 cycles of matrix-core time) against 8 LDS reads, so LDS is far
-// from the bound; global traffic per tile step is 16 KB, served by L2.
+// Workgroup tile 128x128, K staged 32 at a time through LDS; 4 waves in a
+// 2x2 arrangement, each owning a 64x64 sub-tile held as 4x4 MFMA 16x16
+// accumulators (64 AGPR/VGPRs).  Per stage a wave issues 128 MFMAs (4096
+// cycles of matrix-core time) against 64 LDS reads; the next stage's global
+// loads are issued right after the LDS write of the current one, so their
+// latency hides behind a full stage of MFMAs.  Interior tiles use 16-byte
+// global loads; edge tiles take a bounds-checked path.  Work-group ids are
+// remapped so that each XCD (ids congruent mod 8) owns a contiguous run of
+// tiles that share A rows / B columns in its own L2.
 //
 // MFMA 16x16x4 f32 operand layout (lane l of 64):
 //   A: A[i = l%16][k = l/16]      B: B[k = l/16][j = l%16]
@@ -15,8 +19,9 @@ namespace icq {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
-constexpr int PITCH = BM + 16;   // LDS row pitch (floats): rows k, k+1.. land 16 banks apart
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int PITCH = BM + 16;   // LDS row pitch (floats): k-rows land 16 banks apart
+constexpr int NXCD = 8;
 
 struct TileRange { int64_t i0, j0, klo, khi; bool skip; };
 
@@ -27,13 +32,11 @@ __device__ __forceinline__ int64_t isqrt_floor(int64_t x) {
     return r;
 }
 
-// Map the linear block id to a tile.  Triangular masks enumerate only tiles
-// that touch the kept triangle (square grids); for KR_FROM_MAXIJ the upper
-// tiles are enumerated by increasing column block so that long-K tiles start
-// first.
-__device__ TileRange tile_of(const GemmArgs& g) {
+// Linear tile id -> tile.  Triangular masks enumerate only tiles that touch
+// the kept triangle (square grids); for KR_FROM_MAXIJ the upper tiles are
+// enumerated by increasing column block so that long-K tiles start first.
+__device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
     const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
-    const int64_t id = blockIdx.x;
     int64_t ti, tj;
     if (g.cmask == CMASK_LOWER && tm == tn) {
         int64_t r = (isqrt_floor(8 * id + 1) - 1) / 2;   // id -> (r, c), c <= r
@@ -53,77 +56,82 @@ __device__ TileRange tile_of(const GemmArgs& g) {
     if (g.krange == KR_FROM_MAXIJ) t.klo = t.i0 > t.j0 ? t.i0 : t.j0;
     else if (g.krange == KR_FROM_J) t.klo = t.j0;
     else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + BM);
-    t.klo = (t.klo / BK) * BK;
+    t.klo = (t.klo / 4) * 4;
     if (t.klo > g.K) t.klo = g.K;
     return t;
 }
 
-// Registers staged from global memory for one K step: 8 floats of A and 8 of B.
-struct Stage { float a[8]; float b[8]; };
+// Registers staged from global memory for one K stage: 16 floats of A, 16 of B.
+struct Stage { float4 a[4]; float4 b[4]; };
 
 __device__ __forceinline__ float ldg(const float* p, int64_t r, int64_t c, int64_t ld, int64_t R, int64_t Cc) {
     return (r < R && c < Cc) ? p[r * ld + c] : 0.0f;
 }
 
-// op(A) tile [BM x BK] at (i0, k0); op(B) tile [BK x BN] at (k0, j0).
-// Thread t covers 2 groups of 4 consecutive elements along the contiguous axis.
-__device__ __forceinline__ void load_stage(const GemmArgs& g, const float* A, const float* B, int64_t i0,
-                                           int64_t j0, int64_t k0, int64_t khi, Stage& s) {
+// Operand tiles: op(A) [BM x BK] at (i0, k0), op(B) [BK x BN] at (k0, j0).
+// "Row-contiguous" layouts (A not transposed, B transposed) are read as
+// 128 rows x 8 float4 of k; the others as 32 k-rows x 32 float4.
+// Thread t, slot p (0..3): idx = t + 256 p.
+__device__ __forceinline__ void rc_coords(int idx, int& r, int& kq) { r = idx >> 3; kq = (idx & 7) * 4; }
+__device__ __forceinline__ void kc_coords(int idx, int& kr, int& cq) { kr = idx >> 5; cq = (idx & 31) * 4; }
+
+__device__ __forceinline__ float4 ldg4(const float* p, int64_t r, int64_t c, int64_t ld, int64_t R, int64_t Cc,
+                                       bool fast) {
+    if (fast) return *reinterpret_cast<const float4*>(p + r * ld + c);
+    return make_float4(ldg(p, r, c, ld, R, Cc), ldg(p, r, c + 1, ld, R, Cc), ldg(p, r, c + 2, ld, R, Cc),
+                       ldg(p, r, c + 3, ld, R, Cc));
+}
+
+__device__ __forceinline__ void load_stage(const GemmArgs& g, const float* A, const float* B, const TileRange& tr,
+                                           int64_t k0, bool fast, Stage& s) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = t + p * 256;   // 0..511
-        if (!g.transA) {               // A[i][k]: 128 rows x 4 quads of k
-            int r = idx >> 2, kq = (idx & 3) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s.a[p * 4 + c] = ldg(A, i0 + r, k0 + kq + c, g.lda, g.M, khi);
-        } else {                       // A[k][i]: 16 k rows x 32 quads of i
-            int kr = idx >> 5, iq = (idx & 31) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s.a[p * 4 + c] = ldg(A, k0 + kr, i0 + iq + c, g.lda, khi, g.M);
-        }
-        if (!g.transB) {               // B[k][j]: 16 k rows x 32 quads of j
-            int kr = idx >> 5, jq = (idx & 31) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s.b[p * 4 + c] = ldg(B, k0 + kr, j0 + jq + c, g.ldb, khi, g.N);
-        } else {                       // B[j][k]: 128 j rows x 4 quads of k
-            int r = idx >> 2, kq = (idx & 3) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s.b[p * 4 + c] = ldg(B, j0 + r, k0 + kq + c, g.ldb, g.N, khi);
-        }
+    for (int p = 0; p < 4; ++p) {
+        const int idx = t + p * 256;
+        int r, q;
+        if (!g.transA) { rc_coords(idx, r, q); s.a[p] = ldg4(A, tr.i0 + r, k0 + q, g.lda, g.M, tr.khi, fast); }
+        else { kc_coords(idx, r, q); s.a[p] = ldg4(A, k0 + r, tr.i0 + q, g.lda, tr.khi, g.M, fast); }
+        if (!g.transB) { kc_coords(idx, r, q); s.b[p] = ldg4(B, k0 + r, tr.j0 + q, g.ldb, tr.khi, g.N, fast); }
+        else { rc_coords(idx, r, q); s.b[p] = ldg4(B, tr.j0 + r, k0 + q, g.ldb, g.N, tr.khi, fast); }
     }
 }
 
+// LDS holds As[k][i] and Bs[k][j] (k-major, pitch PITCH).
 __device__ __forceinline__ void store_stage(const GemmArgs& g, const Stage& s, float* As, float* Bs) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < 4; ++p) {
         const int idx = t + p * 256;
+        int r, q;
         if (!g.transA) {
-            int r = idx >> 2, kq = (idx & 3) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) As[(kq + c) * PITCH + r] = s.a[p * 4 + c];
+            rc_coords(idx, r, q);
+            As[(q + 0) * PITCH + r] = s.a[p].x; As[(q + 1) * PITCH + r] = s.a[p].y;
+            As[(q + 2) * PITCH + r] = s.a[p].z; As[(q + 3) * PITCH + r] = s.a[p].w;
         } else {
-            int kr = idx >> 5, iq = (idx & 31) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) As[kr * PITCH + iq + c] = s.a[p * 4 + c];
+            kc_coords(idx, r, q);
+            *reinterpret_cast<float4*>(&As[r * PITCH + q]) = s.a[p];
         }
         if (!g.transB) {
-            int kr = idx >> 5, jq = (idx & 31) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) Bs[kr * PITCH + jq + c] = s.b[p * 4 + c];
+            kc_coords(idx, r, q);
+            *reinterpret_cast<float4*>(&Bs[r * PITCH + q]) = s.b[p];
         } else {
-            int r = idx >> 2, kq = (idx & 3) * 4;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) Bs[(kq + c) * PITCH + r] = s.b[p * 4 + c];
+            rc_coords(idx, r, q);
+            Bs[(q + 0) * PITCH + r] = s.b[p].x; Bs[(q + 1) * PITCH + r] = s.b[p].y;
+            Bs[(q + 2) * PITCH + r] = s.b[p].z; Bs[(q + 3) * PITCH + r] = s.b[p].w;
         }
     }
 }
 
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
-    __shared__ float As[2][BK * PITCH];
-    __shared__ float Bs[2][BK * PITCH];
-    const TileRange tr = tile_of(g);
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap, int aligned) {
+    __shared__ __attribute__((aligned(16))) float As[BK * PITCH];
+    __shared__ __attribute__((aligned(16))) float Bs[BK * PITCH];
+    int64_t id = blockIdx.x;
+    if (remap) {   // XCD-contiguous tile runs
+        const int64_t per = (ntiles + NXCD - 1) / NXCD;
+        id = (id % NXCD) * per + id / NXCD;
+        if (id >= ntiles) return;
+    }
+    const TileRange tr = tile_of(g, id);
     if (tr.skip) return;
     const int64_t z = blockIdx.z;
     const float* A = g.A + z * g.sA;
@@ -138,38 +146,46 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    const bool interior = aligned && tr.i0 + BM <= g.M && tr.j0 + BN <= g.N;
     Stage st;
-    int buf = 0;
-    if (tr.klo < tr.khi) {
-        load_stage(g, A, B, tr.i0, tr.j0, tr.klo, tr.khi, st);
-        store_stage(g, st, As[0], Bs[0]);
-    }
-    __syncthreads();
-    for (int64_t k0 = tr.klo; k0 < tr.khi; k0 += BK) {
-        const bool more = k0 + BK < tr.khi;
-        if (more) load_stage(g, A, B, tr.i0, tr.j0, k0 + BK, tr.khi, st);
-        const float* as = As[buf];
-        const float* bs = Bs[buf];
+    int64_t k0 = tr.klo;
+    if (k0 < tr.khi) load_stage(g, A, B, tr, k0, interior && k0 + BK <= tr.khi, st);
+    for (; k0 < tr.khi; k0 += BK) {
+        __syncthreads();                       // previous stage's LDS reads are done
+        store_stage(g, st, As, Bs);
+        __syncthreads();
+        const int64_t kn = k0 + BK;
+        if (kn < tr.khi) load_stage(g, A, B, tr, kn, interior && kn + BK <= tr.khi, st);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 4) {
             const int kr = kk + (lane >> 4);
             float av[4], bv[4];
 #pragma unroll
-            for (int a = 0; a < 4; ++a) av[a] = as[kr * PITCH + wi + a * 16 + (lane & 15)];
+            for (int a = 0; a < 4; ++a) av[a] = As[kr * PITCH + wi + a * 16 + (lane & 15)];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) bv[b] = bs[kr * PITCH + wj + b * 16 + (lane & 15)];
+            for (int b = 0; b < 4; ++b) bv[b] = Bs[kr * PITCH + wj + b * 16 + (lane & 15)];
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
                 for (int b = 0; b < 4; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
-        if (more) store_stage(g, st, As[buf ^ 1], Bs[buf ^ 1]);
-        __syncthreads();
-        buf ^= 1;
     }
 
-    // epilogue
+    // epilogue: all C loads are issued before any store so their latency overlaps
+    float cold[4][4][4];
+    if (g.beta != 0.0f) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int64_t i = tr.i0 + wi + a * 16 + 4 * (lane >> 4) + v;
+                    const int64_t j = tr.j0 + wj + b * 16 + (lane & 15);
+                    cold[a][b][v] = (i < g.M && j < g.N) ? C[i * g.ldc + j] : 0.0f;
+                }
+    }
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -182,9 +198,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
                 if (g.cmask == CMASK_LOWER && i < j) continue;
                 if (g.cmask == CMASK_UPPER && i > j) continue;
                 float r = g.alpha * acc[a][b][v];
-                float* cp = C + i * g.ldc + j;
-                if (g.beta != 0.0f) r = r + g.beta * (*cp);
-                *cp = r;
+                if (g.beta != 0.0f) r = r + g.beta * cold[a][b][v];
+                C[i * g.ldc + j] = r;
             }
 }
 
@@ -192,12 +207,20 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return IC_OK;
     const int64_t tm = cdiv(g.M, BM), tn = cdiv(g.N, BN);
     int64_t tiles = tm * tn;
-    if ((g.cmask == CMASK_LOWER || g.cmask == CMASK_UPPER) && tm == tn) tiles = tm * (tm + 1) / 2;
-    IC_REQUIRE(tiles < (1LL << 31) && g.batch <= 65535, "gemm_f32: problem too large");
+    const bool tri = (g.cmask == CMASK_LOWER || g.cmask == CMASK_UPPER) && tm == tn;
+    if (tri) tiles = tm * (tm + 1) / 2;
+    IC_REQUIRE(tiles < (1LL << 30) && g.batch <= 65535, "gemm_f32: problem too large");
+    // 16-byte loads need 16-byte aligned bases and leading dimensions
+    const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
+                         g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;
+    // triangular enumerations keep their own (long-K-first) order
+    const int remap = (!tri && tiles >= 2 * NXCD) ? 1 : 0;
+    const int64_t grid = remap ? cdiv(tiles, NXCD) * NXCD : tiles;
     const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
     const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
     ProfScope prof_scope(st, g.tag, fl, by);
-    hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)tiles, 1, (unsigned)g.batch), dim3(256), 0, st, g);
+    hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)grid, 1, (unsigned)g.batch), dim3(256), 0, st, g, tiles, remap,
+                       (int)aligned);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }
