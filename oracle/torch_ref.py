@@ -12,7 +12,7 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 baseline.  The product package never imports it.
 
 Parity pinning (how each function is checked against something other than
-itself; see tests/test_oracle_*.py):
+itself; see tests/test_oracle.py):
   * hadamard_regular / hadamard_sylvester: closed form (involution, entries
     +-2^-k, Kronecker structure), reference KATs of tests/test_rotation.py.
   * rotate_weights / rotate_hessian: brute-force dense R, norm and trace
