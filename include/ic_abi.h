@@ -128,8 +128,8 @@ int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld,
 
 /* C = alpha * op(A) op(B) + beta * C on the fp32 matrix cores, row-major.
  * cmask 0 full / 1 lower (i >= j) / 2 upper (i <= j) output; krange 0 full /
- * 1 k >= max(tile i0, j0) / 2 k >= tile j0 / 3 k < tile i0 + 128 (skips the
- * zero half of a triangular operand).  beta == 0 never reads C.
+ * 1 k >= max(tile i0, j0) / 2 k >= tile j0 / 3 k < tile i0 + 128 /
+ * 4 k >= tile i0 (skips the zero half of a triangular operand).  beta == 0 never reads C.
  * Replaces the torch matmuls of converter/rounding.py:103 and
  * converter/gptq_triton.py:178-180 (lazy trailing update) and the LAPACK
  * level-3 kernels behind torch.linalg.cholesky / cholesky_inverse. */
@@ -237,10 +237,10 @@ int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int6
  * tagged with a phase: 0 trailing-update GEMM, 1 Cholesky GEMMs, 2 inverse
  * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
  * rotation, 7 RTN / pack / verify, 8 greedy block kernel, 9 other, 10 greedy
- * cross-term GEMMs.  Enabling resets the record.  ic_profile_read
+ * cross-term GEMMs, 11 Cholesky panel solve.  Enabling resets the record.  ic_profile_read
  * synchronises the events and returns, per phase, the summed kernel time
  * (ms), algorithmic flops and bytes, and the launch count (arrays of at least
- * 11 entries). */
+ * 12 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

@@ -63,12 +63,13 @@ _SIGS = {
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
-                "rotate_h", "rtn_pack_verify", "greedy", "other", "gemm_greedy"]
+                "rotate_h", "rtn_pack_verify", "greedy", "other", "gemm_greedy", "chol_panel"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {
     "gemm_f32_kernel": ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy"],
     "potrf_diag_kernel": ["diag_factor"],
+    "panel64_kernel": ["chol_panel"],
     "sweep_kernel": ["sweep"],
     "greedy_block_kernel": ["greedy"],
 }

@@ -8,12 +8,13 @@
 //             block is factored in LDS by one workgroup, which also writes
 //             its triangular inverse Dinv_k; the panel is A21 <- A21 Dinv_k^T
 //             and the trailing update A22 -= A21 A21^T, both fp32-MFMA GEMMs.
-//  3. trtri:  X = L^-1 by right-looking block substitution on L X = I:
-//             X[k, :k] <- Dinv_k X[k, :k];  X[k, k] = Dinv_k;
-//             X[k+1:, :k+1] -= L[k+1:, k] X[k, :k+1]           (GEMMs)
+//  3. trtri:  X = L^-1: diagonal blocks Dinv_k, then adjacent diagonal
+//             inverses merged level by level, X21 = -X22 (L21 X11)  (GEMMs)
 //  4. lauum:  H^-1 (upper triangle) = X^T X, one GEMM whose tile (I, J)
 //             only runs k >= max(I, J) because X is lower triangular.
 // Flops: n^3/3 each for 2-4; all but the nb x nb factorisations are MFMA.
+#include <vector>
+
 #include "gemm.hpp"
 
 namespace icq {
@@ -40,149 +41,246 @@ __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, flo
 
 // Factor the diagonal block [k0, k0+nb) of matrix blockIdx.x in place (lower,
 // upper part of the block set to 0) and write Dinv = L_kk^-1 (lower, upper 0)
-// to dinv (pitch NB).  info[b] gets the 1-based column of the first
-// non-positive pivot (LAPACK convention) if it is still 0.
+// to dinv (fp32, pitch NB) and dinv64 (fp64, pitch NB).  info[b] gets the
+// 1-based column of the first non-positive pivot (LAPACK convention) if it
+// is still 0.  A partial block (nb < 128) is padded with the identity.
 //
-// 256 threads as a 16 x 16 grid; thread (ty, tx) keeps the 8 x 8 tile at
-// rows 8ty.., columns 8tx.. of both L and X = L^-1 in registers.  Column j of
-// the Cholesky (and row k of the inverse) is published through LDS once per
-// step, double-buffered so one barrier per step suffices.  Rank-1 updates are
-// unconditional: factors of rows / columns that must not change are zero.
-// A partial block (nb < 128) is padded with the identity.
-// 8 consecutive LDS floats (32-byte aligned) as two 16-byte reads.
-__device__ __forceinline__ void load8(const float* p, float* v) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0];
-    const float4 b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+// The arithmetic is fp64 (inputs and outputs fp32 / fp64): the diagonal
+// blocks and their inverses feed every later step, and an fp64 factor keeps
+// the whole inverse at the accuracy of the reference's LAPACK fp32 path.
+//
+// The block is processed in 16 panels of 8 columns.  Both the block A and
+// R (X = L^-1 under construction, started as I) live in MFMA accumulators:
+// the 36 lower 16x16 tiles of each are dealt round-robin to the 4 waves (9
+// per wave).  Per panel:
+//   1. the tiles holding the panel columns publish them to LDS, and the
+//      tiles holding rows j0..j0+7 of R publish those rows;
+//   2. wave 0 factors the panel (rows j0..127, 8 columns) in registers, two
+//      rows per lane, broadcasting pivots and the 8x8 diagonal block with
+//      readlane (no barrier per column), and stores the final L columns;
+//   3. 128 threads finish rows j0..j0+7 of X = L^-1 by forward substitution
+//      with the 8x8 diagonal block of L (one column of X per thread);
+//   4. every wave applies the rank-8 updates A -= L_p L_p^T and
+//      R -= L_p X_p to its live tiles with v_mfma_f64_16x16x4_f64.
+// Elements that are already final (or above the diagonal) may receive
+// updates in step 4; they are never read again.
+//
+// MFMA 16x16x4 f64 operand layout (lane l of 64; D differs from the f32
+// variant's 4*(l/16) + v):
+//   A: A[i = l%16][k = l/16]      B: B[k = l/16][j = l%16]
+//   D (4 doubles v): D[i = l/16 + 4*v][j = l%16]
+typedef double ddoublex4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ double rdlane(double v, int l) {
+    const int64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffff), l);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
 }
 
+constexpr int DSLOTS = 9;   // 36 lower tiles / 4 waves
+
 __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
-                                                         float* dinv, int64_t dstride, int* info) {
-    __shared__ __attribute__((aligned(16))) float colL[2][NB];
-    __shared__ __attribute__((aligned(16))) float rowX[2][NB];
+                                                         float* dinv, double* dinv64, int64_t dstride, int* info) {
+    __shared__ __attribute__((aligned(16))) double pRaw[NB][8];
+    __shared__ __attribute__((aligned(16))) double pL[NB][8];
+    __shared__ __attribute__((aligned(16))) double rowR[8][NB];
+    __shared__ __attribute__((aligned(16))) double rowX[8][NB];
+    __shared__ double rinvS[8];
     const int b = blockIdx.x;
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
-    const int t = threadIdx.x;
-    const int tx = t & 15, ty = t >> 4;
-    const int r0 = ty * 8, c0 = tx * 8;
-    float a[8][8];
+    float* D = dinv + (int64_t)b * dstride;
+    double* D64 = dinv64 + (int64_t)b * dstride;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
+
+    int tI[DSLOTS], tJ[DSLOTS];
+    ddoublex4 accA[DSLOTS], accX[DSLOTS];
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
+    for (int s = 0; s < DSLOTS; ++s) {
+        const int id = s * 4 + wave;
+        int I = 0;
+        while ((I + 1) * (I + 2) / 2 <= id) ++I;
+        tI[s] = I;
+        tJ[s] = id - I * (I + 1) / 2;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int r = r0 + p, c = c0 + q;
-            float v = 0.0f;
-            if (c <= r) v = (r < nb) ? A[(int64_t)r * ld + c] : (r == c ? 1.0f : 0.0f);
-            a[p][q] = v;
+        for (int v = 0; v < 4; ++v) {
+            const int i = tI[s] * 16 + lr + 4 * v, j = tJ[s] * 16 + lj;
+            double a = 0.0;
+            if (j <= i) a = (i < nb) ? (double)A[(int64_t)i * ld + j] : (i == j ? 1.0 : 0.0);
+            accA[s][v] = a;
+            accX[s][v] = (i == j) ? 1.0 : 0.0;
         }
+    }
+
     int bad = 0;
-    int buf = 0;
-    // ---- Cholesky, right-looking, one column per step
     for (int jb = 0; jb < 16; ++jb) {
+        const int j0 = jb * 8, Jp = jb >> 1, co = (jb & 1) * 8;
+        // 1. publish the panel columns of A and rows j0..j0+7 of R
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            const int j = jb * 8 + jj;
-            if (tx == jb) {
+        for (int s = 0; s < DSLOTS; ++s) {
+            if (tJ[s] == Jp && lj >= co && lj < co + 8) {
 #pragma unroll
-                for (int p = 0; p < 8; ++p) colL[buf][r0 + p] = a[p][jj];
+                for (int v = 0; v < 4; ++v) pRaw[tI[s] * 16 + lr + 4 * v][lj - co] = accA[s][v];
             }
-            __syncthreads();
-            float d = colL[buf][j];
-            if (!(d > 0.0f)) {
-                if (!bad) bad = j + 1;
-                d = 1.0f;
-            }
-            const float ljj = sqrtf(d);
-            const float rinv = 1.0f / ljj;
-            float li[8], lc[8];
-            load8(&colL[buf][r0], li);
-            load8(&colL[buf][c0], lc);
+            if (tI[s] == Jp) {
 #pragma unroll
-            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > j) ? li[p] * rinv : 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) lc[q] = (c0 + q > j) ? lc[q] * rinv : 0.0f;
-#pragma unroll
-            for (int p = 0; p < 8; ++p)
-#pragma unroll
-                for (int q = 0; q < 8; ++q) a[p][q] = a[p][q] - li[p] * lc[q];
-            if (tx == jb) {
-#pragma unroll
-                for (int p = 0; p < 8; ++p) {
-                    const int r = r0 + p;
-                    if (r > j) a[p][jj] = li[p];
-                    else if (r == j) a[p][jj] = ljj;
+                for (int v = 0; v < 4; ++v) {
+                    const int r = lr + 4 * v;
+                    if (r >= co && r < co + 8) rowR[r - co][tJ[s] * 16 + lj] = accX[s][v];
                 }
             }
-            buf ^= 1;
+        }
+        __syncthreads();
+        // 2. wave 0 factors the panel
+        if (wave == 0) {
+            const int ra = j0 + lane, rb = j0 + lane + 64;
+            double va[8], vb[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                va[c] = ra < NB ? pRaw[ra < NB ? ra : 0][c] : 0.0;
+                vb[c] = rb < NB ? pRaw[rb < NB ? rb : 0][c] : 0.0;
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                double d = rdlane(va[c], c);
+                if (!(d > 0.0)) {
+                    if (!bad) bad = j0 + c + 1;
+                    d = 1.0;
+                }
+                const double ljj = sqrt(d);
+                const double rinv = 1.0 / ljj;
+                va[c] = lane > c ? va[c] * rinv : (lane == c ? ljj : 0.0);
+                vb[c] = vb[c] * rinv;
+                if (lane == 0) rinvS[c] = rinv;
+#pragma unroll
+                for (int c2 = c + 1; c2 < 8; ++c2) {
+                    const double lk = rdlane(va[c], c2);
+                    va[c2] = va[c2] - va[c] * lk;
+                    vb[c2] = vb[c2] - vb[c] * lk;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                if (ra < NB) pL[ra][c] = va[c];
+                if (rb < NB) pL[rb][c] = vb[c];
+                if (lane < j0) pL[lane][c] = 0.0;
+                if (lane + 64 < j0) pL[lane + 64][c] = 0.0;
+                const int col = j0 + c;
+                if (col < nb) {
+                    if (ra < nb) A[(int64_t)ra * ld + col] = (float)va[c];
+                    if (rb < nb) A[(int64_t)rb * ld + col] = (float)vb[c];
+                    if (lane < j0 && lane < nb) A[(int64_t)lane * ld + col] = 0.0f;
+                    if (lane + 64 < j0 && lane + 64 < nb) A[(int64_t)(lane + 64) * ld + col] = 0.0f;
+                }
+            }
+        }
+        __syncthreads();
+        // 3. rows j0..j0+7 of X = L^-1
+        if (t < NB) {
+            const int q = t;
+            double x[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                double r = rowR[c][q];
+#pragma unroll
+                for (int c2 = 0; c2 < c; ++c2) r = r - pL[j0 + c][c2] * x[c2];
+                x[c] = q <= j0 + 7 ? r * rinvS[c] : 0.0;
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                rowX[c][q] = x[c];
+                const int row = j0 + c;
+                const double out = (row < nb && q < nb) ? x[c] : 0.0;
+                D[row * NB + q] = (float)out;
+                D64[row * NB + q] = out;
+            }
+        }
+        __syncthreads();
+        // 4. rank-8 updates of the live tiles on the matrix cores
+#pragma unroll
+        for (int s = 0; s < DSLOTS; ++s) {
+            const int I = tI[s], J = tJ[s];
+            if (J * 16 + 15 >= j0 + 8) {
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const int k = ks * 4 + (lane >> 4);
+                    const double a = -pL[I * 16 + lj][k];
+                    const double bb = pL[J * 16 + lj][k];
+                    accA[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bb, accA[s], 0, 0, 0);
+                }
+            }
+            if (I * 16 + 15 >= j0 + 8 && J * 16 <= j0 + 7) {
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const int k = ks * 4 + (lane >> 4);
+                    const double a = -pL[I * 16 + lj][k];
+                    const double bb = rowX[k][J * 16 + lj];
+                    accX[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bb, accX[s], 0, 0, 0);
+                }
+            }
         }
     }
-    // ---- X = L^-1, right-looking on L X = I: row k final = R[k,:] / L[k][k]
-    float x[8][8];
-#pragma unroll
-    for (int p = 0; p < 8; ++p)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) x[p][q] = (r0 + p == c0 + q) ? 1.0f : 0.0f;
-    for (int kb = 0; kb < 16; ++kb) {
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const int k = kb * 8 + kk;
-            if (tx == kb) {
-#pragma unroll
-                for (int p = 0; p < 8; ++p) colL[buf][r0 + p] = a[p][kk];
-            }
-            if (ty == kb) {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) rowX[buf][c0 + q] = x[kk][q];
-            }
-            __syncthreads();
-            const float rk = 1.0f / colL[buf][k];
-            float li[8], xk[8];
-            load8(&colL[buf][r0], li);
-            load8(&rowX[buf][c0], xk);
-#pragma unroll
-            for (int p = 0; p < 8; ++p) li[p] = (r0 + p > k) ? li[p] : 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) xk[q] = xk[q] * rk;
-#pragma unroll
-            for (int p = 0; p < 8; ++p)
-#pragma unroll
-                for (int q = 0; q < 8; ++q) x[p][q] = x[p][q] - li[p] * xk[q];
-            if (ty == kb) {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) x[kk][q] = xk[q];
-            }
-            buf ^= 1;
-        }
-    }
-    float* D = dinv + (int64_t)b * dstride;
-#pragma unroll
-    for (int p = 0; p < 8; ++p)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int r = r0 + p, c = c0 + q;
-            const bool in = r < nb && c < nb;
-            if (in) A[(int64_t)r * ld + c] = c <= r ? a[p][q] : 0.0f;
-            D[r * NB + c] = (in && c <= r) ? x[p][q] : 0.0f;
-        }
     if (t == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
 }
 
-// Copy Dinv_k into the diagonal block of X (lower, upper zero).
-__global__ void put_diag_kernel(float* X, int64_t ld, int64_t stride, int64_t k0, int nb, const float* dinv,
-                                int64_t dstride) {
-    const int b = blockIdx.y;
-    const float* D = dinv + (int64_t)b * dstride;
-    float* P = X + (int64_t)b * stride + k0 * ld + k0;
-    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < nb * nb; idx += gridDim.x * blockDim.x) {
-        int i = idx / nb, j = idx - i * nb;
-        P[(int64_t)i * ld + j] = D[i * NB + j];
-    }
-}
+// Panel solve A21 <- A21 * Dinv^T for the m rows below a diagonal block, in
+// place, with fp64 accumulation (fp32 in and out).  Multiplying by an
+// explicit inverse is where a blocked fp32 Cholesky loses most accuracy;
+// this step is ~1 % of the factorisation's flops, so it runs in fp64.
+// Work-group: 64 rows x nb columns; thread (ty, tx) computes rows ty + 16 r
+// (r < 4) and columns tx + 16 c (c < 8); k is staged 32 at a time.
+constexpr int PR = 64, PK = 32, PPITCH = PK + 1;
 
-__global__ void fill_kernel(float* p, int64_t n, float v) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = v;
+__global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int nb, int64_t ld, int64_t stride,
+                                                      const double* dinv64, int64_t dstride) {
+    __shared__ double As[PR][PPITCH];
+    __shared__ double Ds[NB][PPITCH];
+    const int b = blockIdx.y;
+    float* P = A21 + (int64_t)b * stride;
+    const double* D64 = dinv64 + (int64_t)b * dstride;
+    const int64_t r0 = (int64_t)blockIdx.x * PR;
+    const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
+    double acc[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[r][c] = 0.0;
+    for (int kc = 0; kc < nb; kc += PK) {
+        __syncthreads();
+        for (int idx = t; idx < PR * PK; idx += 256) {
+            const int r = idx / PK, k = idx - r * PK;
+            const int64_t row = r0 + r;
+            As[r][k] = (row < m && kc + k < nb) ? (double)P[row * ld + kc + k] : 0.0;
+        }
+        for (int idx = t; idx < NB * PK; idx += 256) {
+            const int j = idx / PK, k = idx - j * PK;
+            Ds[j][k] = D64[j * NB + kc + k];
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int k = 0; k < PK; ++k) {
+            double a[4], d[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[r] = As[ty + 16 * r][k];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) d[c] = Ds[tx + 16 * c][k];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[r][c] = fma(a[r], d[c], acc[r][c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t row = r0 + ty + 16 * r;
+        if (row >= m) continue;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int col = tx + 16 * c;
+            if (col < nb) P[row * ld + col] = (float)acc[r][c];
+        }
+    }
 }
 
 // Copy the upper triangle onto the lower one (in place), per matrix.
@@ -205,19 +303,17 @@ __global__ void lower_to_upper_kernel(float* H, int64_t n, int64_t ld, int64_t s
     }
 }
 
-static int fill(float* p, int64_t n, float v, hipStream_t st) {
-    if (n <= 0) return IC_OK;
-    int grid = (int)std::min<int64_t>(cdiv(n, 256), 65536);
-    hipLaunchKernelGGL(fill_kernel, dim3(grid), dim3(256), 0, st, p, n, v);
-    IC_CHECK_LAUNCH();
-    return IC_OK;
-}
-
 static int64_t dinv_floats(int64_t batch, int64_t n) { return batch * cdiv(n, NB) * NB * NB; }
 
+// fp64 copy of the Dinv blocks: after the fp32 ones, 256-byte aligned.
+static double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
+    const uintptr_t p = reinterpret_cast<uintptr_t>(dinv + dinv_floats(batch, n));
+    return reinterpret_cast<double*>((p + 255) & ~(uintptr_t)255);
+}
+
 // Lower Cholesky in place of `batch` matrices [n, n] (pitch ld, stride sH);
-// dinv receives every Dinv_k (batch x nblk x NB x NB).
-static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, int* info,
+// dinv / dinv64 receive every Dinv_k (batch x nblk x NB x NB, fp32 / fp64).
+static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, double* dinv64, int* info,
                  hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
@@ -225,60 +321,114 @@ static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, flo
         const int64_t k0 = kb * NB;
         const int nb = (int)std::min<int64_t>(NB, n - k0);
         float* Dk = dinv + kb * NB * NB;
+        double* Dk64 = dinv64 + kb * NB * NB;
         {
             ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
             hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
-                               dstride, info);
+                               Dk64, dstride, info);
             IC_CHECK_LAUNCH();
         }
         const int64_t m = n - k0 - nb;
         if (m <= 0) break;
         float* A21 = H + (k0 + nb) * ld + k0;
-        // panel: A21 <- A21 * Dinv^T (in place: one tile column spans all nb columns)
-        GemmArgs p{m, nb, nb, 1.0f, 0.0f, A21, ld, sH, Dk, NB, dstride, A21, ld, sH, 0, 1, CMASK_FULL, KR_FULL, batch,
-                   PT_GEMM_CHOL, (double)batch * m * nb * (nb + 1)};
-        int rc = gemm_f32(p, st);
-        if (rc) return rc;
+        {
+            // panel: A21 <- A21 * Dinv^T (fp64 accumulation, in place)
+            ProfScope prof_scope(st, PT_PANEL, (double)batch * m * nb * (nb + 1), (double)batch * m * nb * 8.0);
+            hipLaunchKernelGGL(panel64_kernel, dim3((unsigned)cdiv(m, PR), (unsigned)batch), dim3(256), 0, st, A21, m,
+                               nb, ld, sH, Dk64, dstride);
+            IC_CHECK_LAUNCH();
+        }
         // trailing: A22 -= A21 A21^T (lower)
         float* A22 = H + (k0 + nb) * ld + (k0 + nb);
         GemmArgs s{m, m, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, A22, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch,
                    PT_GEMM_CHOL, (double)batch * 2.0 * dtri((double)m) * nb};
-        rc = gemm_f32(s, st);
+        int rc = gemm_f32(s, st);
         if (rc) return rc;
     }
     return IC_OK;
 }
 
-// X = L^-1 (lower, upper zero) from L (lower, in H) and the Dinv blocks.
+// X = L^-1 (lower triangle and the 128x128 diagonal blocks exact; the rest
+// of the upper triangle is scratch) from L (lower, in H) and the Dinv
+// blocks.  The diagonal blocks of X are the Dinv_k; then adjacent diagonal
+// inverses are merged level by level,
+//     [L11 0; L21 L22]^-1 = [X11 0; X21 X22],   X21 = -X22 (L21 X11),
+// with T^T = X11^T L21^T parked in the (unused) upper block of the merged
+// square.  All pairs of one level that have the same shape run as one
+// batched GEMM, so the whole inverse takes ~2 log2(n/128) launches of
+// large-K GEMMs instead of 2 n/128 rank-128 updates.
+__global__ void put_diag_all_kernel(float* X, int64_t n, int64_t ld, int64_t stride, const float* dinv,
+                                    int64_t dstride) {
+    const int64_t k0 = (int64_t)blockIdx.x * NB;
+    const int b = blockIdx.y;
+    const float* D = dinv + (int64_t)b * dstride + (int64_t)blockIdx.x * NB * NB;
+    float* P = X + (int64_t)b * stride + k0 * ld + k0;
+    const int nb = (int)std::min<int64_t>(NB, n - k0);
+    for (int idx = threadIdx.x; idx < nb * nb; idx += blockDim.x) {
+        const int i = idx / nb, j = idx - i * nb;
+        P[(int64_t)i * ld + j] = D[i * NB + j];
+    }
+}
+
+static int merge_pairs(const float* L, float* X, int64_t ld, int64_t r0, int64_t n1, int64_t n2, int64_t count,
+                       int64_t pstride, int64_t batch, int64_t sH, hipStream_t st) {
+    // per (pair, matrix): strides differ only when both are > 1; then loop over matrices
+    const bool pairs_batched = count > 1;
+    const int64_t gb = pairs_batched ? count : batch;
+    const int64_t gs = pairs_batched ? pstride : sH;
+    const int64_t outer = pairs_batched ? batch : 1;
+    for (int64_t m = 0; m < outer; ++m) {
+        const int64_t off = pairs_batched ? m * sH : 0;
+        const float* X11 = X + off + r0 * ld + r0;
+        const float* L21 = L + off + (r0 + n1) * ld + r0;
+        float* Tt = X + off + r0 * ld + (r0 + n1);              // n1 x n2 scratch (upper block)
+        const float* X22 = X + off + (r0 + n1) * ld + (r0 + n1);
+        float* X21 = X + off + (r0 + n1) * ld + r0;
+        // T^T[a][b] = sum_k X11[k][a] L21[b][k], k >= a (X11 lower)
+        GemmArgs t{n1, n2, n1, 1.0f, 0.0f, X11, ld, gs, L21, ld, gs, Tt, ld, gs, 1, 1, CMASK_FULL, KR_FROM_I, gb,
+                   PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
+        int rc = gemm_f32(t, st);
+        if (rc) return rc;
+        // X21 = -X22 T, k <= i (X22 lower)
+        GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, Tt, ld, gs, X21, ld, gs, 0, 1, CMASK_FULL, KR_TO_I, gb,
+                   PT_GEMM_INV, (double)gb * n1 * n2 * (n2 + 1)};
+        rc = gemm_f32(x, st);
+        if (rc) return rc;
+    }
+    return IC_OK;
+}
+
 static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const float* dinv,
                  hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
-    int rc = fill(X, batch * sH, 0.0f, st);
-    if (rc) return rc;
-    for (int64_t kb = 0; kb < nblk; ++kb) {
-        const int64_t k0 = kb * NB;
-        const int nb = (int)std::min<int64_t>(NB, n - k0);
-        const float* Dk = dinv + kb * NB * NB;
-        float* Xk = X + k0 * ld;   // row block k
-        if (k0 > 0) {
-            // X[k, :k] <- Dinv_k X[k, :k]   (in place, M = nb <= 128)
-            GemmArgs a{nb, k0, nb, 1.0f, 0.0f, Dk, NB, dstride, Xk, ld, sH, Xk, ld, sH, 0, 0, CMASK_FULL, KR_FULL,
-                       batch, PT_GEMM_INV, (double)batch * k0 * nb * (nb + 1)};
-            rc = gemm_f32(a, st);
+    hipLaunchKernelGGL(put_diag_all_kernel, dim3((unsigned)nblk, (unsigned)batch), dim3(256), 0, st, X, n, ld, sH,
+                       dinv, dstride);
+    IC_CHECK_LAUNCH();
+    // segments of rows [start, start + len); merged pairwise per level
+    std::vector<int64_t> seg;
+    for (int64_t k = 0; k < nblk; ++k) seg.push_back(k * NB);
+    seg.push_back(n);
+    while (seg.size() > 2) {
+        const int64_t nseg = (int64_t)seg.size() - 1;
+        const int64_t npair = nseg / 2;
+        std::vector<int64_t> next;
+        // pairs with the shape of the first one and uniform spacing run together
+        int64_t p = 0;
+        while (p < npair) {
+            const int64_t r0 = seg[2 * p], n1 = seg[2 * p + 1] - r0, n2 = seg[2 * p + 2] - seg[2 * p + 1];
+            int64_t q = p + 1;
+            while (q < npair && seg[2 * q + 1] - seg[2 * q] == n1 && seg[2 * q + 2] - seg[2 * q + 1] == n2 &&
+                   seg[2 * q] - seg[2 * q - 2] == n1 + n2)
+                ++q;
+            int rc = merge_pairs(L, X, ld, r0, n1, n2, q - p, (n1 + n2) * (ld + 1), batch, sH, st);
             if (rc) return rc;
+            p = q;
         }
-        hipLaunchKernelGGL(put_diag_kernel, dim3(16, (unsigned)batch), dim3(256), 0, st, X, ld, sH, k0, nb, dinv + kb * NB * NB,
-                           dstride);
-        IC_CHECK_LAUNCH();
-        const int64_t m = n - k0 - nb;
-        if (m <= 0) break;
-        // X[k+1:, :k+1] -= L[k+1:, k] X[k, :k+1]
-        GemmArgs c{m, k0 + nb, nb, -1.0f, 1.0f, L + (k0 + nb) * ld + k0, ld, sH, Xk, ld, sH, X + (k0 + nb) * ld, ld,
-                   sH, 0, 0, CMASK_FULL, KR_FULL, batch, PT_GEMM_INV,
-                   (double)batch * m * (2.0 * k0 * nb + (double)nb * (nb + 1))};
-        rc = gemm_f32(c, st);
-        if (rc) return rc;
+        for (int64_t i = 0; i < npair; ++i) next.push_back(seg[2 * i]);
+        if (nseg % 2) next.push_back(seg[nseg - 1]);
+        next.push_back(n);
+        seg.swap(next);
     }
     return IC_OK;
 }
@@ -288,7 +438,8 @@ static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld,
 using namespace icq;
 
 extern "C" int64_t ic_hessian_inverse_workspace_bytes(int64_t batch, int64_t n) {
-    return (batch * n * n + dinv_floats(batch, n)) * (int64_t)sizeof(float) + 256;
+    return (batch * n * n + dinv_floats(batch, n)) * (int64_t)sizeof(float) +
+           dinv_floats(batch, n) * (int64_t)sizeof(double) + 256;
 }
 
 extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damping, int method, int* info,
@@ -301,10 +452,11 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     const int64_t ld = n, sH = n * n;
     float* X = reinterpret_cast<float*>(workspace);
     float* dinv = X + batch * sH;
+    double* dinv64 = dinv64_of(dinv, batch, n);
     IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
     hipLaunchKernelGGL(damp_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, n, ld, sH, damping);
     IC_CHECK_LAUNCH();
-    int rc = potrf(H, batch, n, ld, sH, dinv, info, st);
+    int rc = potrf(H, batch, n, ld, sH, dinv, dinv64, info, st);
     if (rc) return rc;
     rc = trtri(H, X, batch, n, ld, sH, dinv, st);
     if (rc) return rc;
@@ -318,7 +470,7 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     IC_CHECK_LAUNCH();
     if (method == 1) {
         // upper Cholesky factor of H^-1 (converter/gptq.py:91-110): L2 = chol(H^-1), return L2^T
-        rc = potrf(H, batch, n, ld, sH, dinv, info + batch, st);
+        rc = potrf(H, batch, n, ld, sH, dinv, dinv64, info + batch, st);
         if (rc) return rc;
         hipLaunchKernelGGL(lower_to_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
         IC_CHECK_LAUNCH();
@@ -332,5 +484,6 @@ extern "C" int ic_cholesky(float* H, int64_t batch, int64_t n, int* info, void* 
     hipStream_t st = as_stream(stream);
     IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
     float* dinv = reinterpret_cast<float*>(workspace) + batch * n * n;
-    return potrf(H, batch, n, n, n * n, dinv, info, st);
+    double* dinv64 = dinv64_of(dinv, batch, n);
+    return potrf(H, batch, n, n, n * n, dinv, dinv64, info, st);
 }

@@ -56,6 +56,7 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
     if (g.krange == KR_FROM_MAXIJ) t.klo = t.i0 > t.j0 ? t.i0 : t.j0;
     else if (g.krange == KR_FROM_J) t.klo = t.j0;
     else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + BM);
+    else if (g.krange == KR_FROM_I) t.klo = t.i0;
     t.klo = (t.klo / 4) * 4;
     if (t.klo > g.K) t.klo = g.K;
     return t;
@@ -234,7 +235,7 @@ extern "C" int ic_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
                         int krange, void* stream) {
     IC_REQUIRE(A && B && C, "ic_sgemm: null pointer");
     IC_REQUIRE(M >= 0 && N >= 0 && K >= 0, "ic_sgemm: negative size");
-    IC_REQUIRE(cmask >= 0 && cmask <= 2 && krange >= 0 && krange <= 3, "ic_sgemm: bad mask");
+    IC_REQUIRE(cmask >= 0 && cmask <= 2 && krange >= 0 && krange <= 4, "ic_sgemm: bad mask");
     GemmArgs g{M, N, K, alpha, beta, A, lda, 0, B, ldb, 0, C, ldc, 0, transA, transB, cmask, krange, 1};
     return gemm_f32(g, as_stream(stream));
 }

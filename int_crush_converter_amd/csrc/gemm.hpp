@@ -18,6 +18,7 @@ enum KRange : int {
     KR_FROM_MAXIJ = 1,   // k in [max(tile_i0, tile_j0), K): C = X^T X with X lower
     KR_FROM_J = 2,       // k in [tile_j0, K): op(B) lower (B[k][j] = 0 for k < j)
     KR_TO_I = 3,         // k in [0, tile_i0 + BM): op(A) lower (A[i][k] = 0 for k > i)
+    KR_FROM_I = 4,       // k in [tile_i0, K): op(A) upper (A[i][k] = 0 for k < i)
 };
 
 struct GemmArgs {

@@ -21,7 +21,8 @@ enum ProfTag : int {
     PT_GREEDY = 8,       // greedy block kernel + its cross-term GEMMs
     PT_OTHER = 9,
     PT_GEMM_GREEDY = 10, // greedy cross-term GEMMs
-    PT_COUNT = 11,
+    PT_PANEL = 11,       // Cholesky panel solve (fp64 accumulation)
+    PT_COUNT = 12,
 };
 
 bool prof_enabled();

@@ -8,7 +8,9 @@ Bars (see the module docstrings of oracle/torch_ref.py):
     fp32 error (same algorithm family, different rounding order).
   * Sweep of one block given the same Hinv: codes bit-exact.
   * Whole layer: scales / zero-points bit-exact; codes agree on >= 99.9 %
-    at these sizes, tr(dW H dW^T) within 1e-3 relative.  (At N >= 6144 the
+    at these sizes; tr(dW H dW^T) within the 1e-2 fp32 noise band of these
+    small cases (the 1e-3 bar is asserted at N = 2048, where it is above
+    the noise).  (At N >= 6144 the
     reference disagrees with itself by ~0.7 % between MKL thread counts; the
     large-size bars live in tests/test_gpu_gptq_large.py.)
 """
@@ -176,7 +178,12 @@ def test_gptq_layer_golden(gpu_dev, golden, case):
     z = t.get(f"{case}.zp")
     p_ref = _proxy(W, t[f"{case}.q"], t[f"{case}.scales"], z, Hd)
     p_got = _proxy(W, q, r.scales.cpu(), z, Hd)
-    assert abs(p_got / p_ref - 1) <= 1e-3
+    # These cases are small (<= 64 x 512) and ill-conditioned, so a handful of
+    # codes decide the proxy: random symmetric perturbations of Hinv at
+    # 3e-5 / 6e-5 relative (LAPACK's own fp32 error here is 3e-5) move it by
+    # up to 3.9e-3 / 5.5e-3 and flip up to 0.9 % / 2.4 % of the codes.  The
+    # 1e-3 bar is asserted at N = 2048 in test_gpu_gptq_large.py.
+    assert abs(p_got / p_ref - 1) <= 1e-2
     assert r.mse == pytest.approx(m["mse"], rel=1e-2)
 
 
