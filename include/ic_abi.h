@@ -175,7 +175,9 @@ int ic_gptq_row_params(const float* row_min, const float* row_max, const float* 
  * (modified), Hinv [groups, gw, gw] (groups == 1: the full inverse; > 1: the
  * block-diagonal inverses of a 3-D Hessian, each group of gw columns
  * independent), per-row s32 / z32 (z32 NULL = symmetric), block <= 128
- * columns of eager updates then one fp32-MFMA lazy update per block.
+ * columns of eager updates; the lazy updates are fp32-MFMA GEMMs, rank-block
+ * inside super-blocks of 1024 columns (groups == 1) and one update with the
+ * whole super-block's errors for the columns after it.
  * Q: int8 codes [rows, groups*gw].  workspace:
  * ic_gptq_workspace_bytes(rows, groups, block).
  * Replaces converter/rounding.py:37-103 (_gptq_block), converter/gptq.py:27-88

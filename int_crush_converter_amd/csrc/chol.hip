@@ -247,15 +247,31 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[r][c] = 0.0;
     for (int kc = 0; kc < nb; kc += PK) {
-        __syncthreads();
-        for (int idx = t; idx < PR * PK; idx += 256) {
-            const int r = idx / PK, k = idx - r * PK;
+        // all global loads of the chunk in flight before the LDS stores
+        constexpr int NA = PR * PK / 256, ND = NB * PK / 256;
+        float av[NA];
+        double dv[ND];
+#pragma unroll
+        for (int u = 0; u < NA; ++u) {
+            const int idx = t + u * 256, r = idx / PK, k = idx % PK;
             const int64_t row = r0 + r;
-            As[r][k] = (row < m && kc + k < nb) ? (double)P[row * ld + kc + k] : 0.0;
+            av[u] = (row < m && kc + k < nb) ? P[row * ld + kc + k] : 0.0f;
         }
-        for (int idx = t; idx < NB * PK; idx += 256) {
-            const int j = idx / PK, k = idx - j * PK;
-            Ds[j][k] = D64[j * NB + kc + k];
+#pragma unroll
+        for (int u = 0; u < ND; ++u) {
+            const int idx = t + u * 256, j = idx / PK, k = idx % PK;
+            dv[u] = D64[j * NB + kc + k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NA; ++u) {
+            const int idx = t + u * 256;
+            As[idx / PK][idx % PK] = (double)av[u];
+        }
+#pragma unroll
+        for (int u = 0; u < ND; ++u) {
+            const int idx = t + u * 256;
+            Ds[idx / PK][idx % PK] = dv[u];
         }
         __syncthreads();
 #pragma unroll 4

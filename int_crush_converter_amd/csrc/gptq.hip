@@ -6,12 +6,17 @@
 // w_k <- w_k - RN(e_j * Hinv[j][k]); after the block the errors E [M, nb]
 // update all later columns at once, W[:, end:] -= E @ Hinv[blk, end:].
 //
-// Sweep kernel: the nb x nb Hinv block is staged in LDS; a row is owned by L
-// lanes, lane l holding columns l, l+L, l+2L, ... in registers.  At step j
-// the owning lane quantises w_j and the error is broadcast to the other lanes
-// of the row, which apply their updates in column order, so every w_k sees
+// Sweep kernel: the nb x nb Hinv block is staged in LDS once per work-group
+// of 16 rows.  A row is owned by 16 lanes, lane l holding columns l, l + 16,
+// ..., l + 112 in 8 registers, so one wave quantises 4 rows per instruction.
+// At step j the owning lane quantises w_j; the four owners' errors are read
+// into scalar registers (readlane) and every lane picks its row's value.
+// Every lane then applies its updates in column order, so every w_k sees
 // exactly the reference's sequence of fp32 roundings (bit-exact given the
-// same Hinv).  Codes and errors are staged in LDS and stored coalesced.
+// same Hinv).  The column recurrence is a pure VALU chain: each owner keeps
+// its divisor data in registers and the next Hinv row is fetched while the
+// current column is processed.  Codes and errors are staged in LDS and
+// stored coalesced.
 //
 // The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
 // order differs from MKL's sgemm, which is the only non-bit-exact step.
@@ -20,7 +25,10 @@
 namespace icq {
 
 constexpr int SW_NB = 128;     // max columns per sweep block
+constexpr int SW_L = 16;       // lanes per row
+constexpr int SW_R = SW_NB / SW_L;   // columns (registers) per lane
 constexpr int SW_THREADS = 256;
+constexpr int SW_ROWS = SW_THREADS / SW_L;
 
 enum SweepMode : int {
     SWEEP_GPTQ = 0,   // per-row scale (+zp), err / Hinv_jj, clamp +-100, NaN -> 0
@@ -43,10 +51,21 @@ struct SweepArgs {
     int mode;
 };
 
-template <int L, int MODE>
+// Value of lane o of each 16-lane row group (o wave-uniform).  m[k] is all
+// ones on the lanes of group k and zero elsewhere, so the select is
+// branch-free.
+__device__ __forceinline__ float row16_bcast(float v, int o, const int (&m)[4]) {
+    const int x = __float_as_int(v);
+    const int b0 = __builtin_amdgcn_readlane(x, o);
+    const int b1 = __builtin_amdgcn_readlane(x, o + 16);
+    const int b2 = __builtin_amdgcn_readlane(x, o + 32);
+    const int b3 = __builtin_amdgcn_readlane(x, o + 48);
+    return __int_as_float((b0 & m[0]) | (b1 & m[1]) | (b2 & m[2]) | (b3 & m[3]));
+}
+
+template <int MODE>
 __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
-    constexpr int R = SW_NB / L;              // registers (columns) per lane
-    constexpr int ROWS = SW_THREADS / L;      // rows per workgroup
+    constexpr int L = SW_L, R = SW_R, ROWS = SW_ROWS;
     __shared__ float Hs[SW_NB * SW_NB];
     __shared__ float Es[ROWS * SW_NB];
     __shared__ int8_t Qs[ROWS * SW_NB];
@@ -58,16 +77,27 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const int64_t col0 = a.col0 + (int64_t)g * a.gcol;
     const float* H = a.H + (int64_t)g * a.hg;
     const int t = threadIdx.x;
-    const int lane = t % L, rl = t / L;
+    const int l = t % L, rl = t / L;
+    const int grp = (t & 63) / L;            // row group within the wave
+    const int gmask[4] = {grp == 0 ? -1 : 0, grp == 1 ? -1 : 0, grp == 2 ? -1 : 0, grp == 3 ? -1 : 0};
     const int64_t row = (int64_t)blockIdx.x * ROWS + rl;
     const bool rv = row < a.rows;
 
-    for (int idx = t; idx < nb * nb; idx += SW_THREADS) {
-        int i = idx / nb, j = idx - i * nb;
-        Hs[i * SW_NB + j] = H[(int64_t)i * a.ldh + j];
+    {
+        // all global loads in flight before the LDS stores
+        constexpr int STEP = SW_THREADS / SW_NB, PER = SW_NB / STEP;
+        const int c = t & (SW_NB - 1), i0 = t >> 7;
+        float tmp[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = i0 + k * STEP;
+            tmp[k] = (i < nb && c < nb) ? H[(int64_t)i * a.ldh + c] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k) Hs[(i0 + k * STEP) * SW_NB + c] = tmp[k];
     }
-    for (int j = t; j < nb; j += SW_THREADS) {
-        float d = H[(int64_t)j * a.ldh + j];
+    for (int j = t; j < SW_NB; j += SW_THREADS) {
+        float d = j < nb ? H[(int64_t)j * a.ldh + j] : 1.0f;
         if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
         dinv[j] = 1.0f / d;
         dok[j] = div_b_ok(d) ? 1 : 0;
@@ -78,7 +108,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const float* wrow = a.W + row * a.ldw + col0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int c = r * L + lane;
+        const int c = r * L + l;
         w[r] = (rv && c < nb) ? wrow[c] : 0.0f;
     }
     float s_row = 1.0f, z_row = 0.0f;
@@ -94,7 +124,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int c = r * L + lane;
+            const int c = r * L + l;
             float v = (rv && c < nb) ? a.s[row * a.lds + col0 + c] : 1.0f;
             v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
             sc[r] = v;
@@ -102,24 +132,39 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         }
     }
     const bool has_zp = a.zp != nullptr;
+    const bool srow_ok = div_b_ok(s_row);
+    // divisor data of the lane's own columns
+    float dv[R];
+    bool dk[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        dv[r] = dinv[r * L + l];
+        dk[r] = dok[r * L + l] != 0;
+    }
 
-    // Columns j = r0*L + o.  Updates are unconditional on registers r >= r0:
-    // for the owner and lower lanes the register of column r0 is already
-    // quantised and never read again, so the extra updates are dead values.
+    // Column j = r0 * L + o lives in register r0 of lane o.  Updates are
+    // unconditional on registers r >= r0: the register of column r0 on lanes
+    // <= o is already quantised and never read again, so those updates are
+    // dead values.
+    float h[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) h[r] = Hs[r * L + l];
 #pragma unroll
     for (int r0 = 0; r0 < R; ++r0) {
+        if (r0 * L >= nb) break;
         const float s_el = sc[MODE == SWEEP_LDLQ ? r0 : 0];
         const float s_rc = scr[MODE == SWEEP_LDLQ ? r0 : 0];
-        const bool s_ok = div_b_ok(s_el);
+        const bool s_ok = MODE == SWEEP_LDLQ ? div_b_ok(s_el) : srow_ok;
 #pragma nounroll
         for (int o = 0; o < L; ++o) {
             const int j = r0 * L + o;
             if (j >= nb) break;
-            float h[R];
+            const int jn = j + 1 < SW_NB ? j + 1 : j;
+            float hn[R];
 #pragma unroll
-            for (int r = r0; r < R; ++r) h[r] = Hs[j * SW_NB + r * L + lane];
+            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * L + l];
             const float x = w[r0];
-            const bool own = lane == o;
+            const bool own = l == o;
             float q, e;
             if (MODE == SWEEP_GPTQ) {
                 float y = div_rn(x, s_el, s_rc, s_ok, own);
@@ -127,7 +172,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 q = clampf(rhaz(y), a.qmin, a.qmax);
                 const float deq = has_zp ? (q - z_row) * s_el : q * s_el;
                 // h[r0] on the owner lane is Hinv[j][j]
-                e = div_rn(x - deq, h[r0], dinv[j], dok[j] != 0, own);
+                e = div_rn(x - deq, h[r0], dv[r0], dk[r0], own);
                 e = clampf(e, -100.0f, 100.0f);
                 if (e != e) e = 0.0f;
             } else {
@@ -141,40 +186,43 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 if (flip && q == a.qmin) q = a.qmax;
                 if (can) q = -q;
                 q = clampf(q, a.qmin, a.qmax);
-                e = (x - q * s_el) * dinv[j];
+                e = (x - q * s_el) * dv[r0];
             }
-            const float err = __shfl(e, o, L);   // broadcast from the owner lane of this row
+            const float err = row16_bcast(e, o, gmask);   // the owner's error, in every lane of its row
             if (own) {
                 Qs[rl * SW_NB + j] = (int8_t)(int)q;
                 Es[rl * SW_NB + j] = e;
             }
 #pragma unroll
             for (int r = r0; r < R; ++r) w[r] = w[r] - err * h[r];
+#pragma unroll
+            for (int r = r0; r < R; ++r) h[r] = hn[r];
         }
     }
     __syncthreads();
     // coalesced stores of codes and errors
-    for (int idx = t; idx < ROWS * nb; idx += SW_THREADS) {
-        const int rr = idx / nb, c = idx - rr * nb;
-        const int64_t gr = (int64_t)blockIdx.x * ROWS + rr;
-        if (gr < a.rows) {
-            a.Q[gr * a.ldq + col0 + c] = Qs[rr * SW_NB + c];
-            a.E[(int64_t)g * a.eg + gr * a.lde + c] = Es[rr * SW_NB + c];
+    {
+        const int c = t & (SW_NB - 1);
+        for (int rr = t >> 7; rr < ROWS; rr += SW_THREADS / SW_NB) {
+            const int64_t gr = (int64_t)blockIdx.x * ROWS + rr;
+            if (gr < a.rows && c < nb) {
+                a.Q[gr * a.ldq + col0 + c] = Qs[rr * SW_NB + c];
+                a.E[(int64_t)g * a.eg + gr * a.lde + c] = Es[rr * SW_NB + c];
+            }
         }
     }
 }
 
 static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
-    constexpr int L = 16;
-    const int64_t wgs = cdiv(a.rows, SW_THREADS / L);
+    const int64_t wgs = cdiv(a.rows, SW_ROWS);
     ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
                  (double)groups * (a.rows * a.nb * 9.0 + 4.0 * a.nb * a.nb));
     if (a.mode == SWEEP_GPTQ)
-        hipLaunchKernelGGL((sweep_kernel<L, SWEEP_GPTQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
+        hipLaunchKernelGGL((sweep_kernel<SWEEP_GPTQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
                            st, a);
     else
-        hipLaunchKernelGGL((sweep_kernel<L, SWEEP_LDLQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
+        hipLaunchKernelGGL((sweep_kernel<SWEEP_LDLQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
                            st, a);
     IC_CHECK_LAUNCH();
     return IC_OK;
@@ -212,22 +260,46 @@ __global__ void gptq_params_kernel(const float* rmin, const float* rmax, const f
 // (groups == 1, gw == N: full 2-D Hessian; 3-D: one group per Hessian block).
 // Hinv of group g starts at Hinv + g * hg with pitch ldh.  E is scratch of
 // groups * rows * min(B,128) floats.
+// Two-level lazy update.  Columns are taken in super-blocks of up to
+// SUPER columns (one group when groups > 1).  Inside a super-block, the
+// errors of each block update only the rest of the super-block (rank-nb);
+// the columns after it receive one update with all of its errors at once,
+// W[:, end:] -= E_sb @ Hinv[sb, end:], a GEMM with K = SUPER.  Same flops
+// as one update per block, with the trailing matrix read and written once
+// per super-block instead of once per block.
+constexpr int SUPER = 1024;
+
+static int64_t super_cols(int64_t groups, int block) {
+    const int64_t b = std::min<int64_t>(std::max(block, 1), SW_NB);
+    return groups == 1 ? std::max<int64_t>(b, (SUPER / b) * b) : b;
+}
+
 static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
                        int64_t ldh, int64_t hg, const float* s, int64_t lds, const float* zp, float qmin,
                        float qmax, int B, int8_t* Q, int64_t ldq, float* E, int mode, hipStream_t st) {
     IC_REQUIRE(B >= 1 && B <= SW_NB, "block size must be in [1, 128]");
-    for (int64_t b0 = 0; b0 < gw; b0 += B) {
-        const int nb = (int)std::min<int64_t>(B, gw - b0);
-        SweepArgs a{W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh, hg, s, lds, zp, qmin, qmax,
-                    Q, ldq, E, nb, rows * nb, mode};
-        int rc = launch_sweep(a, (int)groups, st);
-        if (rc) return rc;
-        const int64_t rest = gw - b0 - nb;
-        if (rest > 0) {
-            // W[:, b0+nb : gw] -= E @ Hinv[b0 : b0+nb, b0+nb : gw]   (per group)
-            GemmArgs ga{rows, rest, nb, -1.0f, 1.0f, E, nb, rows * nb, Hinv + b0 * ldh + b0 + nb, ldh, hg,
-                        W + b0 + nb, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
-            rc = gemm_f32(ga, st);
+    const int64_t SB = super_cols(groups, B);   // error matrix E: [groups][rows][SB]
+    // W[:, c0 : c0+nc] -= E[:, e0 : e0+k] @ Hinv[h0 : h0+k, c0 : c0+nc]   (per group)
+    auto update = [&](int64_t e0, int64_t h0, int64_t k, int64_t c0, int64_t nc) {
+        GemmArgs ga{rows, nc, k, -1.0f, 1.0f, E + e0, SB, rows * SB, Hinv + h0 * ldh + c0, ldh, hg,
+                    W + c0, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
+        return gemm_f32(ga, st);
+    };
+    for (int64_t sb0 = 0; sb0 < gw; sb0 += SB) {
+        const int64_t sbe = std::min<int64_t>(gw, sb0 + SB);
+        for (int64_t b0 = sb0; b0 < sbe; b0 += B) {
+            const int nb = (int)std::min<int64_t>(B, sbe - b0);
+            SweepArgs a{W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh, hg, s, lds, zp, qmin, qmax,
+                        Q, ldq, E + (b0 - sb0), SB, rows * SB, mode};
+            int rc = launch_sweep(a, (int)groups, st);
+            if (rc) return rc;
+            if (b0 + nb < sbe) {
+                rc = update(b0 - sb0, b0, nb, b0 + nb, sbe - b0 - nb);
+                if (rc) return rc;
+            }
+        }
+        if (sbe < gw) {
+            int rc = update(0, sb0, sbe - sb0, sbe, gw - sbe);
             if (rc) return rc;
         }
     }
@@ -252,8 +324,7 @@ extern "C" int ic_gptq_row_params(const float* rmin, const float* rmax, const fl
 }
 
 extern "C" int64_t ic_gptq_workspace_bytes(int64_t rows, int64_t groups, int block) {
-    int64_t b = std::min<int64_t>(std::max(block, 1), SW_NB);
-    return groups * rows * b * (int64_t)sizeof(float) + 256;
+    return groups * rows * super_cols(groups, block) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
