@@ -369,8 +369,8 @@ static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, flo
 // blocks.  The diagonal blocks of X are the Dinv_k; then adjacent diagonal
 // inverses are merged level by level,
 //     [L11 0; L21 L22]^-1 = [X11 0; X21 X22],   X21 = -X22 (L21 X11),
-// with T^T = X11^T L21^T parked in the (unused) upper block of the merged
-// square.  All pairs of one level that have the same shape run as one
+// with T (or T^T when the halves differ in size) parked in the unused
+// upper block of the merged square.  All pairs of one level that have the same shape run as one
 // batched GEMM, so the whole inverse takes ~2 log2(n/128) launches of
 // large-K GEMMs instead of 2 n/128 rank-128 updates.
 __global__ void put_diag_all_kernel(float* X, int64_t n, int64_t ld, int64_t stride, const float* dinv,
@@ -397,19 +397,29 @@ static int merge_pairs(const float* L, float* X, int64_t ld, int64_t r0, int64_t
         const int64_t off = pairs_batched ? m * sH : 0;
         const float* X11 = X + off + r0 * ld + r0;
         const float* L21 = L + off + (r0 + n1) * ld + r0;
-        float* Tt = X + off + r0 * ld + (r0 + n1);              // n1 x n2 scratch (upper block)
+        float* U = X + off + r0 * ld + (r0 + n1);               // n1 x n2 scratch (upper block)
         const float* X22 = X + off + (r0 + n1) * ld + (r0 + n1);
         float* X21 = X + off + (r0 + n1) * ld + r0;
-        // T^T[a][b] = sum_k X11[k][a] L21[b][k], k >= a (X11 lower)
-        GemmArgs t{n1, n2, n1, 1.0f, 0.0f, X11, ld, gs, L21, ld, gs, Tt, ld, gs, 1, 1, CMASK_FULL, KR_FROM_I, gb,
-                   PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
-        int rc = gemm_f32(t, st);
-        if (rc) return rc;
-        // X21 = -X22 T, k <= i (X22 lower)
-        GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, Tt, ld, gs, X21, ld, gs, 0, 1, CMASK_FULL, KR_TO_I, gb,
-                   PT_GEMM_INV, (double)gb * n1 * n2 * (n2 + 1)};
-        rc = gemm_f32(x, st);
-        if (rc) return rc;
+        int rc;
+        if (n1 == n2) {
+            // T = L21 X11 (n2 x n1) in the square scratch block; k >= j (X11 lower)
+            GemmArgs t{n2, n1, n1, 1.0f, 0.0f, L21, ld, gs, X11, ld, gs, U, ld, gs, 0, 0, CMASK_FULL, KR_FROM_J, gb,
+                       PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
+            if ((rc = gemm_f32(t, st))) return rc;
+            // X21 = -X22 T; k <= i (X22 lower)
+            GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, U, ld, gs, X21, ld, gs, 0, 0, CMASK_FULL, KR_TO_I, gb,
+                       PT_GEMM_INV, (double)gb * n1 * n2 * (n2 + 1)};
+            if ((rc = gemm_f32(x, st))) return rc;
+        } else {
+            // T^T[a][b] = sum_k X11[k][a] L21[b][k], k >= a (X11 lower), stored n1 x n2
+            GemmArgs t{n1, n2, n1, 1.0f, 0.0f, X11, ld, gs, L21, ld, gs, U, ld, gs, 1, 1, CMASK_FULL, KR_FROM_I, gb,
+                       PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
+            if ((rc = gemm_f32(t, st))) return rc;
+            // X21 = -X22 T, k <= i (X22 lower)
+            GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, U, ld, gs, X21, ld, gs, 0, 1, CMASK_FULL, KR_TO_I, gb,
+                       PT_GEMM_INV, (double)gb * n1 * n2 * (n2 + 1)};
+            if ((rc = gemm_f32(x, st))) return rc;
+        }
     }
     return IC_OK;
 }

@@ -46,6 +46,8 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
         tj = r; ti = id - r * (r + 1) / 2;
     } else {
         ti = id / tn; tj = id - ti * tn;
+        // K range grows with the tile row: start the long tiles first
+        if (g.krange == KR_TO_I) ti = tm - 1 - ti;
     }
     TileRange t;
     t.i0 = ti * BM; t.j0 = tj * BN;
