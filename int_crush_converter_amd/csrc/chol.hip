@@ -397,21 +397,25 @@ static int merge_pairs(const float* L, float* X, int64_t ld, int64_t r0, int64_t
         const int64_t off = pairs_batched ? m * sH : 0;
         const float* X11 = X + off + r0 * ld + r0;
         const float* L21 = L + off + (r0 + n1) * ld + r0;
-        float* U = X + off + r0 * ld + (r0 + n1);               // n1 x n2 scratch (upper block)
         const float* X22 = X + off + (r0 + n1) * ld + (r0 + n1);
         float* X21 = X + off + (r0 + n1) * ld + r0;
         int rc;
-        if (n1 == n2) {
-            // T = L21 X11 (n2 x n1) in the square scratch block; k >= j (X11 lower)
-            GemmArgs t{n2, n1, n1, 1.0f, 0.0f, L21, ld, gs, X11, ld, gs, U, ld, gs, 0, 0, CMASK_FULL, KR_FROM_J, gb,
+        if (n2 <= n1 && n2 % NB == 0) {
+            // T = L21 X11 (n2 x n1) in the upper triangle of the merged square:
+            // rows r0 .. r0+n2, columns r0+n2 .. r0+n2+n1 (strictly above the
+            // diagonal blocks, since n2 is a whole number of blocks; X11 is
+            // read only on and below its diagonal blocks)
+            float* T = X + off + r0 * ld + (r0 + n2);
+            GemmArgs t{n2, n1, n1, 1.0f, 0.0f, L21, ld, gs, X11, ld, gs, T, ld, gs, 0, 0, CMASK_FULL, KR_FROM_J, gb,
                        PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
             if ((rc = gemm_f32(t, st))) return rc;
             // X21 = -X22 T; k <= i (X22 lower)
-            GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, U, ld, gs, X21, ld, gs, 0, 0, CMASK_FULL, KR_TO_I, gb,
+            GemmArgs x{n2, n1, n2, -1.0f, 0.0f, X22, ld, gs, T, ld, gs, X21, ld, gs, 0, 0, CMASK_FULL, KR_TO_I, gb,
                        PT_GEMM_INV, (double)gb * n1 * n2 * (n2 + 1)};
             if ((rc = gemm_f32(x, st))) return rc;
         } else {
             // T^T[a][b] = sum_k X11[k][a] L21[b][k], k >= a (X11 lower), stored n1 x n2
+            float* U = X + off + r0 * ld + (r0 + n1);
             GemmArgs t{n1, n2, n1, 1.0f, 0.0f, X11, ld, gs, L21, ld, gs, U, ld, gs, 1, 1, CMASK_FULL, KR_FROM_I, gb,
                        PT_GEMM_INV, (double)gb * n2 * n1 * (n1 + 1)};
             if ((rc = gemm_f32(t, st))) return rc;
