@@ -2,13 +2,19 @@
 //
 // Workgroup tile 128x128, K staged 32 at a time through LDS; 4 waves in a
 // 2x2 arrangement, each owning a 64x64 sub-tile held as 4x4 MFMA 16x16
-// accumulators (64 AGPR/VGPRs).  Per stage a wave issues 128 MFMAs (4096
-// cycles of matrix-core time) against 64 LDS reads; the next stage's global
-// loads are issued right after the LDS write of the current one, so their
-// latency hides behind a full stage of MFMAs.  Interior tiles use 16-byte
-// global loads; edge tiles take a bounds-checked path.  Work-group ids are
-// remapped so that each XCD (ids congruent mod 8) owns a contiguous run of
-// tiles that share A rows / B columns in its own L2.
+// accumulators.  Per stage a wave issues 128 MFMAs (4096 cycles of
+// matrix-core time) against 64 LDS reads; the next stage's global loads are
+// issued before the current stage's MFMAs so their latency hides behind
+// them.  Work-group ids are remapped so that each XCD (ids congruent mod 8)
+// owns a contiguous run of tiles that share A rows / B columns in its L2.
+//
+// Each operand is staged in LDS in its memory order, so every global load
+// and LDS store is a 16-byte vector: a row-major operand tile (A, or B^T)
+// as 128 rows x 32 k at pitch 36 floats, a k-major one (A^T, or B) as 32 k
+// rows x 128 at pitch 144.  Both pitches make the MFMA operand reads (16
+// consecutive rows or columns per k) free of bank conflicts.  The transposes
+// are template parameters, and problems made of whole tiles and whole K
+// stages run a kernel instance without bounds checks.
 //
 // MFMA 16x16x4 f32 operand layout (lane l of 64):
 //   A: A[i = l%16][k = l/16]      B: B[k = l/16][j = l%16]
@@ -20,7 +26,9 @@ namespace icq {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int PITCH = BM + 16;   // LDS row pitch (floats): k-rows land 16 banks apart
+constexpr int PR = BK + 4;        // pitch of a row-major operand tile [128][32]
+constexpr int PKM = BM + 16;      // pitch of a k-major operand tile [32][128]
+constexpr int TILE_F = BM * PR > BK * PKM ? BM * PR : BK * PKM;   // floats per operand tile
 constexpr int NXCD = 8;
 
 struct TileRange { int64_t i0, j0, klo, khi; bool skip; };
@@ -64,70 +72,138 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
     return t;
 }
 
-// Registers staged from global memory for one K stage: 16 floats of A, 16 of B.
-struct Stage { float4 a[4]; float4 b[4]; };
+// One operand's share of a stage: 4 float4 per thread (kept in named
+// registers so that no unrolled index can push them to scratch).
+struct Quad { floatx4 v0, v1, v2, v3; };
 
-__device__ __forceinline__ float ldg(const float* p, int64_t r, int64_t c, int64_t ld, int64_t R, int64_t Cc) {
-    return (r < R && c < Cc) ? p[r * ld + c] : 0.0f;
-}
+// A row-major tile (ROWMAJ: element (r, k) at p[r * ld + k]) is read as 128
+// rows x 8 float4 of k; a k-major one (element (k, c) at p[k * ld + c]) as 32
+// k-rows x 32 float4.  Thread t, slot s: idx = t + 256 s.
+template <bool ROWMAJ>
+struct OperandLoader {
+    const float* p;     // this thread's slot-0 element at the current stage
+    int64_t step;       // pointer advance per stage
+    int64_t slot;       // pointer distance between slots
+    int r, c;           // slot-0 coordinates in the tile: (row, k) or (k, col)
 
-// Operand tiles: op(A) [BM x BK] at (i0, k0), op(B) [BK x BN] at (k0, j0).
-// "Row-contiguous" layouts (A not transposed, B transposed) are read as
-// 128 rows x 8 float4 of k; the others as 32 k-rows x 32 float4.
-// Thread t, slot p (0..3): idx = t + 256 p.
-__device__ __forceinline__ void rc_coords(int idx, int& r, int& kq) { r = idx >> 3; kq = (idx & 7) * 4; }
-__device__ __forceinline__ void kc_coords(int idx, int& kr, int& cq) { kr = idx >> 5; cq = (idx & 31) * 4; }
-
-__device__ __forceinline__ float4 ldg4(const float* p, int64_t r, int64_t c, int64_t ld, int64_t R, int64_t Cc,
-                                       bool fast) {
-    if (fast) return *reinterpret_cast<const float4*>(p + r * ld + c);
-    return make_float4(ldg(p, r, c, ld, R, Cc), ldg(p, r, c + 1, ld, R, Cc), ldg(p, r, c + 2, ld, R, Cc),
-                       ldg(p, r, c + 3, ld, R, Cc));
-}
-
-__device__ __forceinline__ void load_stage(const GemmArgs& g, const float* A, const float* B, const TileRange& tr,
-                                           int64_t k0, bool fast, Stage& s) {
-    const int t = threadIdx.x;
+    __device__ __forceinline__ void init(const float* base, int64_t ld, int64_t m0, int64_t k0) {
+        const int t = threadIdx.x;
+        if (ROWMAJ) {
+            r = t >> 3; c = (t & 7) * 4;
+            p = base + (m0 + r) * ld + k0 + c;
+            step = BK; slot = 32 * ld;
+        } else {
+            r = t >> 5; c = (t & 31) * 4;
+            p = base + (k0 + r) * ld + m0 + c;
+            step = (int64_t)BK * ld; slot = 8 * ld;
+        }
+    }
+    __device__ __forceinline__ void load_fast(Quad& q) const {
+        q.v0 = *reinterpret_cast<const floatx4*>(p);
+        q.v1 = *reinterpret_cast<const floatx4*>(p + slot);
+        q.v2 = *reinterpret_cast<const floatx4*>(p + 2 * slot);
+        q.v3 = *reinterpret_cast<const floatx4*>(p + 3 * slot);
+    }
+    // Element (m, k) exists when m < mlim and k < klim; m0 / k0 are the
+    // tile's / stage's origins.
+    __device__ __forceinline__ floatx4 get_checked(int s, int64_t m0, int64_t k0, int64_t mlim, int64_t klim,
+                                                  int64_t ld, const float* base) const {
+        float e[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int idx = t + p * 256;
-        int r, q;
-        if (!g.transA) { rc_coords(idx, r, q); s.a[p] = ldg4(A, tr.i0 + r, k0 + q, g.lda, g.M, tr.khi, fast); }
-        else { kc_coords(idx, r, q); s.a[p] = ldg4(A, k0 + r, tr.i0 + q, g.lda, tr.khi, g.M, fast); }
-        if (!g.transB) { kc_coords(idx, r, q); s.b[p] = ldg4(B, k0 + r, tr.j0 + q, g.ldb, tr.khi, g.N, fast); }
-        else { rc_coords(idx, r, q); s.b[p] = ldg4(B, tr.j0 + r, k0 + q, g.ldb, g.N, tr.khi, fast); }
+        for (int u = 0; u < 4; ++u) {
+            int64_t m, k;
+            if (ROWMAJ) { m = m0 + r + 32 * s; k = k0 + c + u; }
+            else { k = k0 + r + 8 * s; m = m0 + c + u; }
+            e[u] = (m < mlim && k < klim) ? base[ROWMAJ ? m * ld + k : k * ld + m] : 0.0f;
+        }
+        return floatx4{e[0], e[1], e[2], e[3]};
+    }
+    __device__ __forceinline__ void load_checked(Quad& q, int64_t m0, int64_t k0, int64_t mlim, int64_t klim,
+                                                 int64_t ld, const float* base) const {
+        q.v0 = get_checked(0, m0, k0, mlim, klim, ld, base);
+        q.v1 = get_checked(1, m0, k0, mlim, klim, ld, base);
+        q.v2 = get_checked(2, m0, k0, mlim, klim, ld, base);
+        q.v3 = get_checked(3, m0, k0, mlim, klim, ld, base);
+    }
+    __device__ __forceinline__ floatx4* at(float* tile, int s) const {
+        return ROWMAJ ? reinterpret_cast<floatx4*>(&tile[(r + 32 * s) * PR + c])
+                      : reinterpret_cast<floatx4*>(&tile[(r + 8 * s) * PKM + c]);
+    }
+    __device__ __forceinline__ void store_lds(const Quad& q, float* tile) const {
+        *at(tile, 0) = q.v0;
+        *at(tile, 1) = q.v1;
+        *at(tile, 2) = q.v2;
+        *at(tile, 3) = q.v3;
+    }
+};
+
+// LDS offset of operand element (m, k) of a tile: row-major tiles are
+// m-major at pitch PR, k-major tiles k-major at pitch PKM.
+template <bool ROWMAJ>
+__device__ __forceinline__ int lds_at(int m, int k) { return ROWMAJ ? m * PR + k : k * PKM + m; }
+
+template <int TA, int TB>
+__device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int wi, int wj, int lane,
+                                          floatx4 (&acc)[4][4]) {
+    constexpr bool AR = TA == 0, BR = TB == 1;   // row-major staging
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 4) {
+        const int kr = kk + (lane >> 4);
+        float av[4], bv[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) av[a] = As[lds_at<AR>(wi + a * 16 + (lane & 15), kr)];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bv[b] = Bs[lds_at<BR>(wj + b * 16 + (lane & 15), kr)];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
     }
 }
 
-// LDS holds As[k][i] and Bs[k][j] (k-major, pitch PITCH).
-__device__ __forceinline__ void store_stage(const GemmArgs& g, const Stage& s, float* As, float* Bs) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int idx = t + p * 256;
-        int r, q;
-        if (!g.transA) {
-            rc_coords(idx, r, q);
-            As[(q + 0) * PITCH + r] = s.a[p].x; As[(q + 1) * PITCH + r] = s.a[p].y;
-            As[(q + 2) * PITCH + r] = s.a[p].z; As[(q + 3) * PITCH + r] = s.a[p].w;
-        } else {
-            kc_coords(idx, r, q);
-            *reinterpret_cast<float4*>(&As[r * PITCH + q]) = s.a[p];
-        }
-        if (!g.transB) {
-            kc_coords(idx, r, q);
-            *reinterpret_cast<float4*>(&Bs[r * PITCH + q]) = s.b[p];
-        } else {
-            rc_coords(idx, r, q);
-            Bs[(q + 0) * PITCH + r] = s.b[p].x; Bs[(q + 1) * PITCH + r] = s.b[p].y;
-            Bs[(q + 2) * PITCH + r] = s.b[p].z; Bs[(q + 3) * PITCH + r] = s.b[p].w;
-        }
+template <int TA, int TB, bool CHECK>
+__device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, const float* B, const TileRange& tr,
+                                          float* lds, floatx4 (&acc)[4][4]) {
+    constexpr bool AR = TA == 0, BR = TB == 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
+    OperandLoader<AR> la;
+    OperandLoader<BR> lb;
+    la.init(A, g.lda, tr.i0, tr.klo);
+    lb.init(B, g.ldb, tr.j0, tr.klo);
+    Quad va, vb;
+    float* As = lds;
+    float* Bs = lds + TILE_F;
+#define ICQ_LOAD_STAGE(K0)                                                 \
+    do {                                                                   \
+        if (CHECK) {                                                       \
+            la.load_checked(va, tr.i0, (K0), g.M, tr.khi, g.lda, A);       \
+            lb.load_checked(vb, tr.j0, (K0), g.N, tr.khi, g.ldb, B);       \
+        } else {                                                           \
+            la.load_fast(va);                                              \
+            lb.load_fast(vb);                                              \
+        }                                                                  \
+        la.p += la.step;                                                   \
+        lb.p += lb.step;                                                   \
+    } while (0)
+    int64_t k0 = tr.klo;
+    if (k0 >= tr.khi) return;
+    ICQ_LOAD_STAGE(k0);
+    for (; k0 < tr.khi; k0 += BK) {
+        __syncthreads();                       // previous stage's LDS reads are done
+        la.store_lds(va, As);
+        lb.store_lds(vb, Bs);
+        __syncthreads();
+        if (k0 + BK < tr.khi) ICQ_LOAD_STAGE(k0 + BK);
+        mma_stage<TA, TB>(As, Bs, wi, wj, lane, acc);
     }
+#undef ICQ_LOAD_STAGE
 }
 
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap, int aligned) {
-    __shared__ __attribute__((aligned(16))) float As[BK * PITCH];
-    __shared__ __attribute__((aligned(16))) float Bs[BK * PITCH];
+template <int TA, int TB, bool CHECK>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap) {
+    __shared__ __attribute__((aligned(16))) float lds[2 * TILE_F];
     int64_t id = blockIdx.x;
     if (remap) {   // XCD-contiguous tile runs
         const int64_t per = (ntiles + NXCD - 1) / NXCD;
@@ -141,40 +217,19 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
     const float* B = g.B + z * g.sB;
     float* C = g.C + z * g.sC;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
     floatx4 acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const bool interior = aligned && tr.i0 + BM <= g.M && tr.j0 + BN <= g.N;
-    Stage st;
-    int64_t k0 = tr.klo;
-    if (k0 < tr.khi) load_stage(g, A, B, tr, k0, interior && k0 + BK <= tr.khi, st);
-    for (; k0 < tr.khi; k0 += BK) {
-        __syncthreads();                       // previous stage's LDS reads are done
-        store_stage(g, st, As, Bs);
-        __syncthreads();
-        const int64_t kn = k0 + BK;
-        if (kn < tr.khi) load_stage(g, A, B, tr, kn, interior && kn + BK <= tr.khi, st);
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 4) {
-            const int kr = kk + (lane >> 4);
-            float av[4], bv[4];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) av[a] = As[kr * PITCH + wi + a * 16 + (lane & 15)];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) bv[b] = Bs[kr * PITCH + wj + b * 16 + (lane & 15)];
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
-        }
-    }
+    main_loop<TA, TB, CHECK>(g, A, B, tr, lds, acc);
 
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
+    const int64_t ib = tr.i0 + wi + 4 * (lane >> 4), jb = tr.j0 + wj + (lane & 15);
+    float* Cb = C + ib * g.ldc + jb;
+    const bool full = !CHECK && g.cmask == CMASK_FULL;
     // epilogue: all C loads are issued before any store so their latency overlaps
     float cold[4][4][4];
     if (g.beta != 0.0f) {
@@ -184,9 +239,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int64_t i = tr.i0 + wi + a * 16 + 4 * (lane >> 4) + v;
-                    const int64_t j = tr.j0 + wj + b * 16 + (lane & 15);
-                    cold[a][b][v] = (i < g.M && j < g.N) ? C[i * g.ldc + j] : 0.0f;
+                    const int64_t i = ib + a * 16 + v, j = jb + b * 16;
+                    cold[a][b][v] = (full || (i < g.M && j < g.N)) ? Cb[(int64_t)(a * 16 + v) * g.ldc + b * 16] : 0.0f;
                 }
     }
 #pragma unroll
@@ -195,14 +249,15 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int64_t i = tr.i0 + wi + a * 16 + 4 * (lane >> 4) + v;
-                const int64_t j = tr.j0 + wj + b * 16 + (lane & 15);
-                if (i >= g.M || j >= g.N) continue;
-                if (g.cmask == CMASK_LOWER && i < j) continue;
-                if (g.cmask == CMASK_UPPER && i > j) continue;
+                const int64_t i = ib + a * 16 + v, j = jb + b * 16;
+                if (!full) {
+                    if (i >= g.M || j >= g.N) continue;
+                    if (g.cmask == CMASK_LOWER && i < j) continue;
+                    if (g.cmask == CMASK_UPPER && i > j) continue;
+                }
                 float r = g.alpha * acc[a][b][v];
                 if (g.beta != 0.0f) r = r + g.beta * cold[a][b][v];
-                C[i * g.ldc + j] = r;
+                Cb[(int64_t)(a * 16 + v) * g.ldc + b * 16] = r;
             }
 }
 
@@ -222,8 +277,19 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
     const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
     ProfScope prof_scope(st, g.tag, fl, by);
-    hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)grid, 1, (unsigned)g.batch), dim3(256), 0, st, g, tiles, remap,
-                       (int)aligned);
+    const dim3 gd((unsigned)grid, 1, (unsigned)g.batch);
+    // whole tiles and whole K stages everywhere: the kernel without bounds checks
+    const bool exact = aligned && g.M % BM == 0 && g.N % BN == 0 && g.K % BK == 0;
+#define ICQ_GEMM_LAUNCH(TA, TB)                                                                                  \
+    do {                                                                                                        \
+        if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false>), gd, dim3(256), 0, st, g, tiles, remap);  \
+        else hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, true>), gd, dim3(256), 0, st, g, tiles, remap);         \
+    } while (0)
+    if (!g.transA && !g.transB) ICQ_GEMM_LAUNCH(0, 0);
+    else if (!g.transA) ICQ_GEMM_LAUNCH(0, 1);
+    else if (!g.transB) ICQ_GEMM_LAUNCH(1, 0);
+    else ICQ_GEMM_LAUNCH(1, 1);
+#undef ICQ_GEMM_LAUNCH
     IC_CHECK_LAUNCH();
     return IC_OK;
 }
