@@ -148,16 +148,20 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
                     if (!bad) bad = j0 + c + 1;
                     d = 1.0;
                 }
-                const double ljj = sqrt(d);
-                const double rinv = 1.0 / ljj;
+                // 1/sqrt(d) from the hardware estimate and two Newton steps
+                // (relative error far below fp32's), then sqrt(d) = d / sqrt(d)
+                double rinv = __builtin_amdgcn_rsq(d);
+                rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
+                rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
+                const double ljj = d * rinv;
                 va[c] = lane > c ? va[c] * rinv : (lane == c ? ljj : 0.0);
                 vb[c] = vb[c] * rinv;
                 if (lane == 0) rinvS[c] = rinv;
 #pragma unroll
                 for (int c2 = c + 1; c2 < 8; ++c2) {
                     const double lk = rdlane(va[c], c2);
-                    va[c2] = va[c2] - va[c] * lk;
-                    vb[c2] = vb[c2] - vb[c] * lk;
+                    va[c2] = fma(-va[c], lk, va[c2]);
+                    vb[c2] = fma(-vb[c], lk, vb[c2]);
                 }
             }
 #pragma unroll
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
             for (int c = 0; c < 8; ++c) {
                 double r = rowR[c][q];
 #pragma unroll
-                for (int c2 = 0; c2 < c; ++c2) r = r - pL[j0 + c][c2] * x[c2];
+                for (int c2 = 0; c2 < c; ++c2) r = fma(-pL[j0 + c][c2], x[c2], r);
                 x[c] = q <= j0 + 7 ? r * rinvS[c] : 0.0;
             }
 #pragma unroll
@@ -329,37 +333,63 @@ static double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
 
 // Lower Cholesky in place of `batch` matrices [n, n] (pitch ld, stride sH);
 // dinv / dinv64 receive every Dinv_k (batch x nblk x NB x NB, fp32 / fp64).
+//
+// Two-level right-looking: columns are taken in super-blocks of up to
+// SUPER_NB columns.  After each block's panel, only the rest of the
+// super-block's columns are updated (rank-NB); after the super-block, the
+// trailing matrix beyond it gets one SYRK with K = SUPER_NB.  Same flops as
+// one SYRK per block, with the trailing matrix read and written once per
+// super-block.
+constexpr int64_t SUPER_NB = 1024;
+
 static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, double* dinv64, int* info,
                  hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
-    for (int64_t kb = 0; kb < nblk; ++kb) {
-        const int64_t k0 = kb * NB;
-        const int nb = (int)std::min<int64_t>(NB, n - k0);
-        float* Dk = dinv + kb * NB * NB;
-        double* Dk64 = dinv64 + kb * NB * NB;
-        {
-            ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
-            hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
-                               Dk64, dstride, info);
-            IC_CHECK_LAUNCH();
+    for (int64_t s0 = 0; s0 < n; s0 += SUPER_NB) {
+        const int64_t s1 = std::min<int64_t>(n, s0 + SUPER_NB);
+        for (int64_t k0 = s0; k0 < s1; k0 += NB) {
+            const int64_t kb = k0 / NB;
+            const int nb = (int)std::min<int64_t>(NB, n - k0);
+            float* Dk = dinv + kb * NB * NB;
+            double* Dk64 = dinv64 + kb * NB * NB;
+            {
+                ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
+                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
+                                   Dk64, dstride, info);
+                IC_CHECK_LAUNCH();
+            }
+            const int64_t k1 = k0 + nb;
+            const int64_t m = n - k1;
+            if (m <= 0) break;
+            float* A21 = H + k1 * ld + k0;
+            {
+                // panel: A21 <- A21 * Dinv^T (fp64 accumulation, in place)
+                ProfScope prof_scope(st, PT_PANEL, (double)batch * m * nb * (nb + 1), (double)batch * m * nb * 8.0);
+                hipLaunchKernelGGL(panel64_kernel, dim3((unsigned)cdiv(m, PR), (unsigned)batch), dim3(256), 0, st,
+                                   A21, m, nb, ld, sH, Dk64, dstride);
+                IC_CHECK_LAUNCH();
+            }
+            // rest of the super-block: A[k1:, k1:s1] -= A21 A21[:s1-k1]^T (lower in its top square)
+            const int64_t w = s1 - k1;
+            if (w > 0) {
+                GemmArgs g{m, w, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, H + k1 * ld + k1, ld, sH, 0, 1,
+                           CMASK_LOWER, KR_FULL, batch, PT_GEMM_CHOL,
+                           (double)batch * 2.0 * (dtri((double)w) + (double)(m - w) * w) * nb};
+                int rc = gemm_f32(g, st);
+                if (rc) return rc;
+            }
         }
-        const int64_t m = n - k0 - nb;
-        if (m <= 0) break;
-        float* A21 = H + (k0 + nb) * ld + k0;
-        {
-            // panel: A21 <- A21 * Dinv^T (fp64 accumulation, in place)
-            ProfScope prof_scope(st, PT_PANEL, (double)batch * m * nb * (nb + 1), (double)batch * m * nb * 8.0);
-            hipLaunchKernelGGL(panel64_kernel, dim3((unsigned)cdiv(m, PR), (unsigned)batch), dim3(256), 0, st, A21, m,
-                               nb, ld, sH, Dk64, dstride);
-            IC_CHECK_LAUNCH();
+        // beyond the super-block: A[s1:, s1:] -= L[s1:, s0:s1] L[s1:, s0:s1]^T (lower)
+        const int64_t m = n - s1;
+        if (m > 0) {
+            const float* P = H + s1 * ld + s0;
+            const int64_t k = s1 - s0;
+            GemmArgs g{m, m, k, -1.0f, 1.0f, P, ld, sH, P, ld, sH, H + s1 * ld + s1, ld, sH, 0, 1, CMASK_LOWER,
+                       KR_FULL, batch, PT_GEMM_CHOL, (double)batch * 2.0 * dtri((double)m) * k};
+            int rc = gemm_f32(g, st);
+            if (rc) return rc;
         }
-        // trailing: A22 -= A21 A21^T (lower)
-        float* A22 = H + (k0 + nb) * ld + (k0 + nb);
-        GemmArgs s{m, m, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, A22, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch,
-                   PT_GEMM_CHOL, (double)batch * 2.0 * dtri((double)m) * nb};
-        int rc = gemm_f32(s, st);
-        if (rc) return rc;
     }
     return IC_OK;
 }
