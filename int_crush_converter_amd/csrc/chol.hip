@@ -229,27 +229,30 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
 }
 
 // Panel solve A21 <- A21 * Dinv^T for the m rows below a diagonal block, in
-// place, with fp64 accumulation (fp32 in and out).  Multiplying by an
-// explicit inverse is where a blocked fp32 Cholesky loses most accuracy;
-// this step is ~1 % of the factorisation's flops, so it runs in fp64.
-// Work-group: 64 rows x nb columns; thread (ty, tx) computes rows ty + 16 r
-// (r < 4) and columns tx + 16 c (c < 8); k is staged 32 at a time.
-constexpr int PR = 64, PK = 32, PPITCH = PK + 1;
+// place, with fp64 products and accumulation (fp32 in and out).  Multiplying
+// by an explicit inverse is where a blocked fp32 Cholesky loses most
+// accuracy; this step is ~1 % of the factorisation's flops, so it runs on
+// the fp64 matrix cores (v_mfma_f64_16x16x4_f64).
+// Work-group: 64 rows, wave w owning the 16-row strip 16 w .. 16 w + 15 as 8
+// accumulator tiles of 16 columns.  k is staged 32 at a time; a column tile
+// J only takes the k-steps with k <= 16 J + 15 (Dinv is lower triangular).
+constexpr int PR = 64, PK = 32;
+constexpr int PA = PK + 1;   // As pitch (floats)
+constexpr int PD = PK + 2;   // Ds pitch (doubles)
 
 __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int nb, int64_t ld, int64_t stride,
                                                       const double* dinv64, int64_t dstride) {
-    __shared__ double As[PR][PPITCH];
-    __shared__ double Ds[NB][PPITCH];
+    __shared__ float As[PR * PA];
+    __shared__ double Ds[NB * PD];
     const int b = blockIdx.y;
     float* P = A21 + (int64_t)b * stride;
     const double* D64 = dinv64 + (int64_t)b * dstride;
     const int64_t r0 = (int64_t)blockIdx.x * PR;
-    const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
-    double acc[4][8];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    ddoublex4 acc[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[r][c] = 0.0;
+    for (int J = 0; J < 8; ++J) acc[J] = ddoublex4{0.0, 0.0, 0.0, 0.0};
     for (int kc = 0; kc < nb; kc += PK) {
         // all global loads of the chunk in flight before the LDS stores
         constexpr int NA = PR * PK / 256, ND = NB * PK / 256;
@@ -270,37 +273,34 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
 #pragma unroll
         for (int u = 0; u < NA; ++u) {
             const int idx = t + u * 256;
-            As[idx / PK][idx % PK] = (double)av[u];
+            As[(idx / PK) * PA + idx % PK] = av[u];
         }
 #pragma unroll
         for (int u = 0; u < ND; ++u) {
             const int idx = t + u * 256;
-            Ds[idx / PK][idx % PK] = dv[u];
+            Ds[(idx / PK) * PD + idx % PK] = dv[u];
         }
         __syncthreads();
-#pragma unroll 4
-        for (int k = 0; k < PK; ++k) {
-            double a[4], d[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[r] = As[ty + 16 * r][k];
+        for (int ks = 0; ks < PK / 4; ++ks) {
+            const int k = ks * 4 + lk;
+            const double a = (double)As[(wave * 16 + li) * PA + k];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) d[c] = Ds[tx + 16 * c][k];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) acc[r][c] = fma(a[r], d[c], acc[r][c]);
+            for (int J = 0; J < 8; ++J) {
+                if (J * 16 + 15 < kc + ks * 4) continue;   // Dinv[j][k] = 0 for k > j
+                const double bb = Ds[(J * 16 + li) * PD + k];
+                acc[J] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bb, acc[J], 0, 0, 0);
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t row = r0 + ty + 16 * r;
-        if (row >= m) continue;
+    for (int J = 0; J < 8; ++J)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int col = tx + 16 * c;
-            if (col < nb) P[row * ld + col] = (float)acc[r][c];
+        for (int v = 0; v < 4; ++v) {
+            const int64_t row = r0 + wave * 16 + lk + 4 * v;
+            const int col = J * 16 + li;
+            if (row < m && col < nb) P[row * ld + col] = (float)acc[J][v];
         }
-    }
 }
 
 // Copy the upper triangle onto the lower one (in place), per matrix.
