@@ -20,21 +20,29 @@
 
 namespace icq {
 
+// s * 0.5 is exact, so fma(s, 0.5, -x) is the reference's RN(S/2 - x).
 __device__ __forceinline__ void bfly4(float& a, float& b, float& c, float& d) {
-    float s = (a + b) + (c + d);
-    float h = s * 0.5f;
-    float na = h - d, nb = h - c, nc = h - b, nd = h - a;
+    const float s = (a + b) + (c + d);
+    const float na = __builtin_fmaf(s, 0.5f, -d), nb = __builtin_fmaf(s, 0.5f, -c);
+    const float nc = __builtin_fmaf(s, 0.5f, -b), nd = __builtin_fmaf(s, 0.5f, -a);
     a = na; b = nb; c = nc; d = nd;
 }
 
-// One radix-4 stage across the 4 lanes selected by xor masks m1, m2 (partner
-// of digit value d is 3-d = d ^ 3, i.e. xor (m1|m2)).
-template <int M1, int M2>
-__device__ __forceinline__ float bfly4_x(float v) {
-    float a = v + __shfl_xor(v, M1, 64);
-    float s = a + __shfl_xor(a, M2, 64);
-    float p = __shfl_xor(v, M1 | M2, 64);
-    return s * 0.5f - p;
+// One radix-4 stage across the 4 lanes of a quad (the digit value is the
+// lane's position in the quad; the partner of digit d is 3 - d = d ^ 3).
+// DPP quad permutations keep the exchange in the VALU.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int QP_XOR1 = 0xB1;   // quad_perm(1,0,3,2)
+constexpr int QP_XOR2 = 0x4E;   // quad_perm(2,3,0,1)
+constexpr int QP_XOR3 = 0x1B;   // quad_perm(3,2,1,0)
+
+__device__ __forceinline__ float bfly4_quad(float v) {
+    const float a = v + dpp<QP_XOR1>(v);            // (x0 + x1) or (x2 + x3)
+    const float s = a + dpp<QP_XOR2>(a);            // (x0 + x1) + (x2 + x3)
+    return __builtin_fmaf(s, 0.5f, -dpp<QP_XOR3>(v));
 }
 
 // Outlier sanitising on load (converter/pipeline.py:527-537): |w| > zero_above
@@ -44,86 +52,179 @@ __device__ __forceinline__ float sanitize(float v, float zero_above, unsigned& c
     return v;
 }
 
+// Same, for a lane's whole register block: the outlier count is taken per
+// wave from the comparison masks (one scalar popcount per element).
+template <int K>
+__device__ __forceinline__ void sanitize_block(float (&v)[K], float zero_above, unsigned& cnt) {
+    if (!(zero_above > 0.0f)) return;
+    unsigned wc = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        const bool out = fabsf(v[i]) > zero_above;
+        wc += (unsigned)__popcll(__ballot(out));
+        v[i] = out ? 0.0f : v[i];
+    }
+    if ((threadIdx.x & 63) == 0) cnt += wc;   // counted once per wave
+}
+
 __device__ __forceinline__ void flush_count(unsigned cnt, unsigned long long* nz) {
     if (!nz) return;
     unsigned long long c = wave_sum((unsigned long long)cnt);
     if ((threadIdx.x & 63) == 0 && c) atomicAdd(nz, c);
 }
 
-template <int ROT>
-__global__ __launch_bounds__(256) void rotate_rows_reg(
-    const void* __restrict__ src, int dtype, int64_t rows, int64_t cols, int64_t ld_src,
-    float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst, int vec_ok, float zero_above,
-    unsigned long long* nz) {
-    unsigned cnt = 0;
-    const int64_t cpr = cols_pad >> 4;  // 16-column chunks per row
-    const int64_t total = rows * cpr;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += stride) {
-        const int64_t r = g / cpr;
-        const int64_t c0 = (g - r * cpr) << 4;
-        float v[16];
-        const int64_t base = r * ld_src + c0;
-        if (vec_ok && c0 + 16 <= cols) {
-            if (dtype == IC_DTYPE_F32) {
-                const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(src) + base);
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int uintx4_t __attribute__((ext_vector_type(4)));
+
+// 16 consecutive source elements -> fp32 (FAST: 16-byte loads, no bounds).
+template <int DT, bool FAST>
+__device__ __forceinline__ void load16(const void* src, int64_t base, int64_t c0, int64_t cols, float (&v)[16]) {
+    if (FAST) {
+        if (DT == IC_DTYPE_F32) {
+            const floatx4_t* p = reinterpret_cast<const floatx4_t*>(reinterpret_cast<const float*>(src) + base);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float4 t = p[i];
-                    v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-                }
-            } else {
-                const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(src) + base);
+            for (int i = 0; i < 4; ++i) {
+                const floatx4_t t = p[i];
+                v[4 * i] = t[0]; v[4 * i + 1] = t[1]; v[4 * i + 2] = t[2]; v[4 * i + 3] = t[3];
+            }
+        } else {
+            const uintx4_t* p = reinterpret_cast<const uintx4_t*>(reinterpret_cast<const uint16_t*>(src) + base);
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    uint4 t = p[i];
-                    uint32_t w[4] = {t.x, t.y, t.z, t.w};
+            for (int i = 0; i < 2; ++i) {
+                const uintx4_t t = p[i];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        uint16_t lo = (uint16_t)(w[k] & 0xffffu), hi = (uint16_t)(w[k] >> 16);
-                        if (dtype == IC_DTYPE_BF16) {
-                            v[8 * i + 2 * k] = __uint_as_float(uint32_t(lo) << 16);
-                            v[8 * i + 2 * k + 1] = __uint_as_float(uint32_t(hi) << 16);
-                        } else {
-                            v[8 * i + 2 * k] = f16_bits_to_f32(lo);
-                            v[8 * i + 2 * k + 1] = f16_bits_to_f32(hi);
-                        }
+                for (int k = 0; k < 4; ++k) {
+                    if (DT == IC_DTYPE_BF16) {
+                        v[8 * i + 2 * k] = __uint_as_float(t[k] << 16);
+                        v[8 * i + 2 * k + 1] = __uint_as_float(t[k] & 0xffff0000u);
+                    } else {
+                        v[8 * i + 2 * k] = f16_bits_to_f32((uint16_t)(t[k] & 0xffffu));
+                        v[8 * i + 2 * k + 1] = f16_bits_to_f32((uint16_t)(t[k] >> 16));
                     }
                 }
             }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = (c0 + i < cols) ? load_as_f32(src, DT, base + i) : 0.0f;
+    }
+}
+
+// Rotation of groups of ROT in {4, 16, 64, 256} columns, entirely in
+// registers and DPP.  FAST: 16-byte aligned rows made of whole 16-column
+// chunks (no bounds checks); DT: the source dtype.  A lane holds NCH chunks of 16 consecutive columns:
+// base-4 digits 0 and 1 of the in-group index are the register index inside
+// a chunk; for ROT >= 64 digit 2 is the lane's position in its quad; for
+// ROT = 256 digit 3 is the chunk (the quad's lane j holds columns
+// 16 j + 64 m, m < 4, of its 256-column group).  Item = one thread's
+// chunks; threads 4q .. 4q+3 cover one 64- (or 256-) column group.
+template <int ROT, int DT, bool FAST>
+__global__ __launch_bounds__(256) void rotate_rows_reg(
+    const void* __restrict__ src, int64_t rows, int64_t cols, int64_t ld_src,
+    float* __restrict__ dst, int64_t cols_pad, int64_t ld_dst, float zero_above,
+    unsigned long long* nz) {
+    constexpr int NCH = ROT == 256 ? 4 : 1;
+    unsigned cnt = 0;
+    // per row: units of 16 columns per thread (256 per quad for ROT = 256)
+    const uint32_t upr = (uint32_t)(ROT == 256 ? cols_pad / 256 : cols_pad / 16);
+    const uint32_t total = (uint32_t)rows * upr * (ROT == 256 ? 4u : 1u);   // threads' items
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < total; g += stride) {
+        uint32_t r, c0;
+        if (ROT == 256) {
+            const uint32_t u = g >> 2;
+            r = u / upr;
+            c0 = (u - r * upr) * 256 + 16 * (g & 3);
         } else {
+            r = g / upr;
+            c0 = (g - r * upr) * 16;
+        }
+        float v[NCH][16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                v[i] = (c0 + i < cols) ? load_as_f32(src, dtype, base + i) : 0.0f;
+        for (int m = 0; m < NCH; ++m) {
+            const int64_t cm = (int64_t)c0 + 64 * m;
+            load16<DT, FAST>(src, (int64_t)r * ld_src + cm, cm, cols, v[m]);
+            sanitize_block(v[m], zero_above, cnt);
+            // digit 0 (stride 1), digit 1 (stride 4)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) bfly4(v[m][4 * a], v[m][4 * a + 1], v[m][4 * a + 2], v[m][4 * a + 3]);
+            if (ROT >= 16) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) bfly4(v[m][b], v[m][b + 4], v[m][b + 8], v[m][b + 12]);
+            }
+            // digit 2 (the quad)
+            if (ROT >= 64) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[m][i] = bfly4_quad(v[m][i]);
+            }
+        }
+        // digit 3 (the chunks)
+        if (ROT == 256) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) bfly4(v[0][i], v[1 % NCH][i], v[2 % NCH][i], v[3 % NCH][i]);
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = sanitize(v[i], zero_above, cnt);
-        // digit 0 (stride 1)
+        for (int m = 0; m < NCH; ++m) {
+            float* o = dst + (int64_t)r * ld_dst + c0 + 64 * m;
+            if (FAST) {
+                floatx4_t* q = reinterpret_cast<floatx4_t*>(o);
 #pragma unroll
-        for (int a = 0; a < 4; ++a) bfly4(v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
-        if (ROT >= 16) {
+                for (int i = 0; i < 4; ++i)
+                    q[i] = floatx4_t{v[m][4 * i], v[m][4 * i + 1], v[m][4 * i + 2], v[m][4 * i + 3]};
+            } else {
 #pragma unroll
-            for (int b = 0; b < 4; ++b) bfly4(v[b], v[b + 4], v[b + 8], v[b + 12]);
-        }
-        if (ROT >= 64) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bfly4_x<1, 2>(v[i]);
-        }
-        if (ROT >= 256) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bfly4_x<4, 8>(v[i]);
-        }
-        float* o = dst + r * ld_dst + c0;
-        if (vec_ok) {
-            float4* q = reinterpret_cast<float4*>(o);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[i] = v[i];
+                for (int i = 0; i < 16; ++i) o[i] = v[m][i];
+            }
         }
     }
     flush_count(cnt, nz);
+}
+
+// Column pass of R^T H R for groups of 256 rows: in place on fp32 [n, n]
+// matrices.  Work-group: one 256-row group x 64 columns; thread (c, q)
+// (c = t % 64 the column, q = t / 64 the wave) loads rows 64 q .. 64 q + 63 of
+// its column (a wave reads 64 consecutive floats of a row per load), applies
+// digits 0-2 of the row index in registers, and hands digit 3 (the wave)
+// through LDS: after one exchange thread (c, q) finishes rows 16 q + i +
+// 64 m (i < 16, m < 4).  Same stages, in the same order, as the row kernel.
+constexpr int CP_COLS = 64;
+constexpr int CP_PITCH = CP_COLS + 1;
+
+__global__ __launch_bounds__(256) void rotate_cols256_kernel(float* __restrict__ H, int64_t n, int64_t ld,
+                                                             int64_t bstride) {
+    __shared__ float tile[256 * CP_PITCH];
+    float* P = H + (int64_t)blockIdx.z * bstride + (int64_t)blockIdx.y * 256 * ld + (int64_t)blockIdx.x * CP_COLS;
+    const int t = threadIdx.x, c = t & 63, q = t >> 6;
+    const bool cv = (int64_t)blockIdx.x * CP_COLS + c < n;
+    float v[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) v[i] = cv ? P[(int64_t)(64 * q + i) * ld + c] : 0.0f;
+    // digit 0 (stride 1), digit 1 (stride 4), digit 2 (stride 16)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) bfly4(v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bfly4(v[16 * h + b], v[16 * h + b + 4], v[16 * h + b + 8], v[16 * h + b + 12]);
+#pragma unroll
+    for (int b = 0; b < 16; ++b) bfly4(v[b], v[b + 16], v[b + 32], v[b + 48]);
+#pragma unroll
+    for (int i = 0; i < 64; ++i) tile[(64 * q + i) * CP_PITCH + c] = v[i];
+    __syncthreads();
+    // digit 3 (stride 64): rows r, r+64, r+128, r+192 for r = 16 q + i
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 16 * q + i;
+        float x0 = tile[r * CP_PITCH + c], x1 = tile[(r + 64) * CP_PITCH + c];
+        float x2 = tile[(r + 128) * CP_PITCH + c], x3 = tile[(r + 192) * CP_PITCH + c];
+        bfly4(x0, x1, x2, x3);
+        if (cv) {
+            P[(int64_t)r * ld + c] = x0;
+            P[(int64_t)(r + 64) * ld + c] = x1;
+            P[(int64_t)(r + 128) * ld + c] = x2;
+            P[(int64_t)(r + 192) * ld + c] = x3;
+        }
+    }
 }
 
 // Convert + zero-pad copy into fp32 (used before the LDS kernel).
@@ -238,21 +339,34 @@ extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int6
                "ic_rotate_rows: in-place needs f32 and equal ld");
     if (rows == 0 || cols_pad == 0) return IC_OK;
     hipStream_t st = as_stream(stream);
-    if (rot >= 4 && rot <= 256 && is_pow4(rot) && cols_pad % 16 == 0) {
+    if (rot >= 4 && rot <= 256 && is_pow4(rot) && cols_pad % 16 == 0 && rows * (cols_pad / 16) < (1LL << 31)) {
         size_t esz = src_dtype == IC_DTYPE_F32 ? 4 : 2;
         bool vec_ok = ((uintptr_t)src % 16 == 0) && ((ld_src * esz) % 16 == 0) && ((uintptr_t)dst % 16 == 0) &&
                       (ld_dst % 4 == 0);
-        int64_t chunks = rows * (cols_pad / 16);
-        int grid = grid_for(chunks, 256);
+        int64_t chunks = rows * (cols_pad / 16);   // one 16-column chunk per thread and pass
+        // rot 256: a few items per thread (8 work-groups of 256 per CU)
+        int grid = rot == 256 ? (int)std::min<int64_t>(grid_for(chunks / 4, 256), 2048) : grid_for(chunks, 256);
         int stages = rot == 4 ? 1 : rot == 16 ? 2 : rot == 64 ? 3 : 4;
         ProfScope prof_scope(st, src == (const void*)dst ? PT_ROTATE_H : PT_ROTATE, 2.0 * stages * rows * cols_pad,
                      (double)rows * cols * esz + 4.0 * rows * cols_pad);
+        const bool fast = vec_ok && cols % 16 == 0;
+#define ICQ_ROT_LAUNCH(R, D, F)                                                                               \
+    hipLaunchKernelGGL((rotate_rows_reg<R, D, F>), dim3(grid), dim3(256), 0, st, src, rows, cols, ld_src, dst, \
+                       cols_pad, ld_dst, zero_above, n_zeroed)
+#define ICQ_ROT_DT(R)                                                                                          \
+    do {                                                                                                       \
+        if (src_dtype == IC_DTYPE_F32) { if (fast) ICQ_ROT_LAUNCH(R, IC_DTYPE_F32, true); else ICQ_ROT_LAUNCH(R, IC_DTYPE_F32, false); } \
+        else if (src_dtype == IC_DTYPE_BF16) { if (fast) ICQ_ROT_LAUNCH(R, IC_DTYPE_BF16, true); else ICQ_ROT_LAUNCH(R, IC_DTYPE_BF16, false); } \
+        else { if (fast) ICQ_ROT_LAUNCH(R, IC_DTYPE_F16, true); else ICQ_ROT_LAUNCH(R, IC_DTYPE_F16, false); } \
+    } while (0)
         switch (rot) {
-            case 4: hipLaunchKernelGGL(rotate_rows_reg<4>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
-            case 16: hipLaunchKernelGGL(rotate_rows_reg<16>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
-            case 64: hipLaunchKernelGGL(rotate_rows_reg<64>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
-            default: hipLaunchKernelGGL(rotate_rows_reg<256>, dim3(grid), dim3(256), 0, st, src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, (int)vec_ok, zero_above, n_zeroed); break;
+            case 4: ICQ_ROT_DT(4); break;
+            case 16: ICQ_ROT_DT(16); break;
+            case 64: ICQ_ROT_DT(64); break;
+            default: ICQ_ROT_DT(256); break;
         }
+#undef ICQ_ROT_DT
+#undef ICQ_ROT_LAUNCH
         IC_CHECK_LAUNCH();
         return IC_OK;
     }
@@ -276,6 +390,14 @@ extern "C" int ic_rotate_hessian(float* H, int64_t batch, int64_t n, int64_t ld,
     // rows: H <- H R; the batch is batch*n consecutive rows of pitch ld
     int rc = ic_rotate_rows(H, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, 0.0f, nullptr, stream);
     if (rc) return rc;
-    // columns: H <- R^T H; axis A = rows (stride ld), axis B = columns (stride 1)
+    // columns: H <- R^T H
+    if (rot == 256) {
+        ProfScope prof_scope(st, PT_ROTATE_H, 2.0 * 4 * batch * n * n, 8.0 * batch * n * n);
+        dim3 grid((unsigned)cdiv(n, CP_COLS), (unsigned)(n / 256), (unsigned)batch);
+        hipLaunchKernelGGL(rotate_cols256_kernel, grid, dim3(256), 0, st, H, n, ld, n * ld);
+        IC_CHECK_LAUNCH();
+        return IC_OK;
+    }
+    // axis A = rows (stride ld), axis B = columns (stride 1)
     return launch_lds(H, rot, n / rot, n, ld, 1, batch, n * ld, st);
 }

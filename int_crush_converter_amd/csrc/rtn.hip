@@ -221,6 +221,52 @@ __global__ __launch_bounds__(256) void pack_int4_kernel(const void* __restrict__
     if (__any(hi)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 2, 1); }
 }
 
+// Packing of int8 codes, 32 per thread (16-byte loads and stores), for rows
+// of whole 32-code units with 16-byte aligned rows.  Per 32-bit word of 4
+// codes: nibbles (w & 0x0F0F0F0F) fold into 2 bytes; a code lies in
+// [-8, 7] iff its bits 3..7 are equal, i.e. ((w ^ (w << 1)) & 0xF0F0F0F0)
+// is zero.  A thread that sees an out-of-range code re-checks its 32 codes
+// one by one to set the < -8 / > 7 flags like the scalar kernel.
+typedef unsigned int pk_uintx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned pack_word_pair(unsigned w0, unsigned w1) {
+    const unsigned l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+    const unsigned p0 = l0 | (l0 >> 4), p1 = l1 | (l1 >> 4);
+    return (p0 & 0xFFu) | ((p0 >> 8) & 0xFF00u) | ((p1 & 0xFFu) << 16) | ((p1 << 8) & 0xFF000000u);
+}
+
+__global__ __launch_bounds__(256) void pack_int4_vec_kernel(const int8_t* __restrict__ src, uint32_t rows,
+                                                            uint32_t upr, int64_t ld_src, uint8_t* __restrict__ dst,
+                                                            int64_t ld_dst, int32_t* flags) {
+    const uint32_t total = rows * upr;
+    int lo = 0, hi = 0;
+    for (uint32_t u = blockIdx.x * blockDim.x + threadIdx.x; u < total; u += gridDim.x * blockDim.x) {
+        const uint32_t r = u / upr, c0 = (u - r * upr) * 32;
+        const pk_uintx4* p = reinterpret_cast<const pk_uintx4*>(src + (int64_t)r * ld_src + c0);
+        const pk_uintx4 a = p[0], b = p[1];
+        unsigned bad = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bad |= ((a[k] ^ (a[k] << 1)) | (b[k] ^ (b[k] << 1))) & 0xF0F0F0F0u;
+        if (bad) {
+            const int8_t* q = src + (int64_t)r * ld_src + c0;
+            for (int i = 0; i < 32; ++i) {
+                lo |= q[i] < -8;
+                hi |= q[i] > 7;
+            }
+        }
+        if (dst) {
+            pk_uintx4 o;
+            o[0] = pack_word_pair(a[0], a[1]);
+            o[1] = pack_word_pair(a[2], a[3]);
+            o[2] = pack_word_pair(b[0], b[1]);
+            o[3] = pack_word_pair(b[2], b[3]);
+            *reinterpret_cast<pk_uintx4*>(dst + (int64_t)r * ld_dst + c0 / 2) = o;
+        }
+    }
+    if (__any(lo)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 1, 1); }
+    if (__any(hi)) { if ((threadIdx.x & 63) == 0) atomicOr(flags + 2, 1); }
+}
+
 __global__ void unpack_int4_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t k, int64_t ld_src,
                                    int8_t* __restrict__ dst, int64_t ld_dst) {
     const int64_t total = rows * k;
@@ -349,8 +395,17 @@ extern "C" int ic_pack_int4(const void* src, int src_kind, int64_t rows, int64_t
     IC_CHECK_HIP(hipMemsetAsync(flags, 0, 3 * sizeof(int32_t), st));
     if (rows == 0 || cols == 0) return IC_OK;
     ProfScope prof_scope(st, PT_RTN, 0.0, (double)rows * cols * (src_kind == 0 ? 1.5 : 4.5));
-    hipLaunchKernelGGL(pack_int4_kernel, dim3(elem_grid(rows * cdiv(cols, 2))), dim3(256), 0, st, src, src_kind, rows,
-                       cols, ld_src, dst, ld_dst, flags);
+    const bool vec = src_kind == 0 && cols % 32 == 0 && ld_src % 16 == 0 && (uintptr_t)src % 16 == 0 &&
+                     (!dst || (ld_dst % 16 == 0 && (uintptr_t)dst % 16 == 0)) && rows * (cols / 32) < (1LL << 31);
+    if (vec) {
+        const int64_t units = rows * (cols / 32);
+        const int grid = (int)std::min<int64_t>(cdiv(units, 256), 4096);
+        hipLaunchKernelGGL(pack_int4_vec_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<const int8_t*>(src),
+                           (uint32_t)rows, (uint32_t)(cols / 32), ld_src, dst, ld_dst, flags);
+    } else {
+        hipLaunchKernelGGL(pack_int4_kernel, dim3(elem_grid(rows * cdiv(cols, 2))), dim3(256), 0, st, src, src_kind,
+                           rows, cols, ld_src, dst, ld_dst, flags);
+    }
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

@@ -144,7 +144,7 @@ def test_rtn_extreme_values(gpu_dev):
     assert torch.equal(S.calculate_scales(W.to(gpu_dev)).cpu(), ref.scales_int4_sym(W, 128))
 
 
-@pytest.mark.parametrize("shape", [(7,), (4, 33), (3, 5, 16), (1, 1)])
+@pytest.mark.parametrize("shape", [(7,), (4, 33), (3, 5, 16), (1, 1), (64, 256), (33, 12288), (2, 3, 64)])
 def test_pack_unpack_bit_exact(gpu_dev, shape):
     from int_crush_converter_amd.packing import pack_int4, unpack_int4
     g = torch.Generator().manual_seed(1)
@@ -166,6 +166,21 @@ def test_pack_validation(gpu_dev):
     # float input is truncated like .to(torch.int8)
     f = torch.tensor([-7.5, 3.7, 0.2, -0.9], device=gpu_dev)
     assert torch.equal(pack_int4(f).cpu(), ref.pack_int4(f.cpu().to(torch.int8)))
+
+
+@pytest.mark.parametrize("bad,err", [(8, "above"), (-9, "below"), (127, "above"), (-128, "below")])
+def test_pack_validation_vector_path(gpu_dev, bad, err):
+    """Whole 32-code rows take the vectorised packer; its range flags must
+    match the scalar rules for every position of a bad code."""
+    from int_crush_converter_amd.packing import pack_int4, INT4PackingError
+    g = torch.Generator().manual_seed(2)
+    v = torch.randint(-8, 8, (16, 64), generator=g, dtype=torch.int8)
+    for pos in [(0, 0), (5, 31), (15, 63), (7, 33)]:
+        w = v.clone()
+        w[pos] = bad
+        with pytest.raises(INT4PackingError):
+            pack_int4(w.to(gpu_dev))
+    assert torch.equal(pack_int4(v.to(gpu_dev)).cpu(), ref.pack_int4(v))
 
 
 def test_quant_error_matches_oracle(gpu_dev):
