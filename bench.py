@@ -132,7 +132,22 @@ def cpu_step(kind, W, H):
         ref.pack_int4(q)
 
 
-def roofline_from(prof):
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    FETCH_SIZE / WRITE_SIZE counter runs (profiles/gemm_traffic.json), already
+    scaled by what the same counters read for a plain copy; None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("workload") != workload or rec.get("kernel") != kernel:
+        return None
+    return rec.get("traffic_bytes_per_launch")
+
+
+def roofline_from(prof, workload):
     """Dominant kernel (most summed time over the timed steps) -> roofline.
     achieved = algorithmic work per launch / average launch duration."""
     from int_crush_converter_amd._native import PROFILE_KERNELS
@@ -150,7 +165,7 @@ def roofline_from(prof):
         achieved = (ph["bytes"] / n) / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
         bound, peak, unit = "hbm", PEAK_HBM_GBS, "GB/s"
     return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                  "frac": round(achieved / peak, 4), "traffic": None}
+                  "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, name)}
 
 
 def main():
@@ -161,6 +176,8 @@ def main():
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB fp32 device copy (3 times), the reference for HBM counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build runs the per-layer path on a single MI355X "
@@ -169,6 +186,15 @@ def main():
 
     import torch
     from int_crush_converter_amd import _native as nat
+    if args.copy_calibration:
+        a = torch.ones(64 << 20, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": True, "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
+                          "launches": 3}), flush=True)
+        return
     kind, M, N, extra = WORKLOADS[args.workload]
     log(f"[bench] workload {args.workload}: generating inputs")
     W, H = make_inputs(kind, M, N, extra)
@@ -221,7 +247,7 @@ def main():
                    "block": 128, "damping": 0.01},
     }
     if prof is not None:
-        dom, roof = roofline_from(prof)
+        dom, roof = roofline_from(prof, args.workload)
         result["roofline"] = roof
         result["roofline"]["kernel"] = dom
         steps = prof_steps
