@@ -57,13 +57,18 @@ __global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, flo
 //      tiles holding rows j0..j0+7 of R publish those rows;
 //   2. wave 0 factors the panel (rows j0..127, 8 columns) in registers, two
 //      rows per lane, broadcasting pivots and the 8x8 diagonal block with
-//      readlane (no barrier per column), and stores the final L columns;
-//   3. 128 threads finish rows j0..j0+7 of X = L^-1 by forward substitution
-//      with the 8x8 diagonal block of L (one column of X per thread);
-//   4. every wave applies the rank-8 updates A -= L_p L_p^T and
-//      R -= L_p X_p to its live tiles with v_mfma_f64_16x16x4_f64.
+//      readlane (no barrier per column), and puts the final L columns into
+//      an fp32 image of L in LDS and, in fp64, into the step-4 operands;
+//   3. meanwhile wave 1 finishes the rows of X = L^-1 of the previous panel
+//      by forward substitution with that panel's 8x8 diagonal block (two
+//      columns of X per lane) and stores them to Dinv / Dinv64 (whole rows:
+//      coalesced) - X runs one panel behind A, which never reads it;
+//   4. every wave applies the rank-8 updates A -= L_p L_p^T (this panel) and
+//      R -= L_p X_p (the previous panel) to its live tiles with
+//      v_mfma_f64_16x16x4_f64.
 // Elements that are already final (or above the diagonal) may receive
-// updates in step 4; they are never read again.
+// updates in step 4; they are never read again.  At the end the block
+// writes the image of L row by row.
 //
 // MFMA 16x16x4 f64 operand layout (lane l of 64; D differs from the f32
 // variant's 4*(l/16) + v):
@@ -80,66 +85,100 @@ __device__ __forceinline__ double rdlane(double v, int l) {
 
 constexpr int DSLOTS = 9;   // 36 lower tiles / 4 waves
 
-__global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
-                                                         float* dinv, double* dinv64, int64_t dstride, int* info) {
-    __shared__ __attribute__((aligned(16))) double pRaw[NB][8];
-    __shared__ __attribute__((aligned(16))) double pL[NB][8];
-    __shared__ __attribute__((aligned(16))) double rowR[8][NB];
-    __shared__ __attribute__((aligned(16))) double rowX[8][NB];
-    __shared__ double rinvS[8];
-    const int b = blockIdx.x;
-    float* A = H + (int64_t)b * stride + k0 * ld + k0;
-    float* D = dinv + (int64_t)b * dstride;
-    double* D64 = dinv64 + (int64_t)b * dstride;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
+// Lower 16x16 tile `id`, row-major over the lower triangle of the 8x8 tile
+// grid: tile row and tile column.  Wave W owns the tiles id = 4 s + W.
+constexpr int tri_row(int id) {
+    int I = 0;
+    while ((I + 1) * (I + 2) / 2 <= id) ++I;
+    return I;
+}
+constexpr int tri_col(int id) { return id - tri_row(id) * (tri_row(id) + 1) / 2; }
 
-    int tI[DSLOTS], tJ[DSLOTS];
+// Panel-local k (0..7) is stored at kperm(k), so that the two k values a
+// lane feeds to the two MFMA steps of a panel, lr and lr + 4, are adjacent.
+__device__ __forceinline__ constexpr int kperm(int k) { return (k & 3) * 2 + (k >> 2); }
+
+// Rows of 8 doubles are padded to DP = 9, so that a wave's 64 row-wise
+// accesses spread over the LDS banks (a 64-byte pitch would put them on 4).
+// Arrays indexed by a row of the block have a spare row NB, where accesses
+// for rows past the block are clamped (so they need no branch).
+constexpr int DP = 9, RP = 17;
+
+struct DiagShared {
+    double pRaw[NB + 1][RP];   // the panel's tile column of A (16 columns; row NB stays 0)
+    double pL[2][NB + 1][DP];  // final L columns of the last two panels, at kperm
+    double dL[2][8][8];        // the 8x8 diagonal blocks of L of the last two panels
+    double rinv[2][8];         // and their pivots' reciprocal square roots
+    double rowR[8][NB];        // rows of R of the panel whose X rows are due
+    double rowXt[NB][DP];      // final rows of X = L^-1 of that panel, transposed, at kperm
+    float Lfin[NB + 1][NB + 1];   // L as it is finalised, zero above the diagonal
+};
+
+// The body of potrf_diag_kernel for wave W; every tile coordinate is a
+// compile-time constant, so the accumulators and the per-panel operand
+// registers are indexed statically.  Iteration it factors panel it (wave 0)
+// and finishes the rows of X of panel it - 1 (wave 1) at the same time: the
+// factorisation of A never reads X, so X runs one panel behind.
+template <int W>
+__device__ __forceinline__ void potrf_diag_wave(DiagShared& sh, const float* A, int64_t ld, int nb, float* D,
+                                                double* D64, int lane, int& bad) {
+    const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
     ddoublex4 accA[DSLOTS], accX[DSLOTS];
+    // All 36 loads in flight at once: addresses are clamped into the block
+    // (every load is in bounds, no branch) and values outside it replaced.
+    float raw[DSLOTS][4];
 #pragma unroll
-    for (int s = 0; s < DSLOTS; ++s) {
-        const int id = s * 4 + wave;
-        int I = 0;
-        while ((I + 1) * (I + 2) / 2 <= id) ++I;
-        tI[s] = I;
-        tJ[s] = id - I * (I + 1) / 2;
+    for (int s = 0; s < DSLOTS; ++s)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int i = tI[s] * 16 + lr + 4 * v, j = tJ[s] * 16 + lj;
-            double a = 0.0;
-            if (j <= i) a = (i < nb) ? (double)A[(int64_t)i * ld + j] : (i == j ? 1.0 : 0.0);
-            accA[s][v] = a;
-            accX[s][v] = (i == j) ? 1.0 : 0.0;
+            const int i = tri_row(4 * s + W) * 16 + lr + 4 * v, j = tri_col(4 * s + W) * 16 + lj;
+            const int ic = i < nb ? i : nb - 1, jc = j < nb ? j : nb - 1;
+            raw[s][v] = A[(int64_t)ic * ld + jc];
         }
-    }
+#pragma unroll
+    for (int s = 0; s < DSLOTS; ++s)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = tri_row(4 * s + W) * 16 + lr + 4 * v, j = tri_col(4 * s + W) * 16 + lj;
+            const double pad = (i == j) ? 1.0 : 0.0;
+            accA[s][v] = j > i ? 0.0 : (i < nb ? (double)raw[s][v] : pad);
+            accX[s][v] = pad;
+        }
 
-    int bad = 0;
-    for (int jb = 0; jb < 16; ++jb) {
-        const int j0 = jb * 8, Jp = jb >> 1, co = (jb & 1) * 8;
-        // 1. publish the panel columns of A and rows j0..j0+7 of R
+    for (int it = 0; it <= 16; ++it) {
+        // panel it of A (it < 16) and panel it - 1 of X (it >= 1)
+        const int j0 = it * 8, Jp = it >> 1, co = (it & 1) * 8, pb = it & 1;
+        const int x0 = j0 - 8, Jx = (it - 1) >> 1, cx = ((it - 1) & 1) * 8, xbuf = pb ^ 1;
+        // 1. publish the tile column of A that holds the panel (all 16
+        //    columns) and rows x0..x0+7 of R
 #pragma unroll
         for (int s = 0; s < DSLOTS; ++s) {
-            if (tJ[s] == Jp && lj >= co && lj < co + 8) {
+            const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
+            if (it < 16 && J == Jp) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) pRaw[tI[s] * 16 + lr + 4 * v][lj - co] = accA[s][v];
+                for (int v = 0; v < 4; ++v) sh.pRaw[I * 16 + lr + 4 * v][lj] = accA[s][v];
             }
-            if (tI[s] == Jp) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int r = lr + 4 * v;
-                    if (r >= co && r < co + 8) rowR[r - co][tJ[s] * 16 + lj] = accX[s][v];
+            if (it >= 1 && I == Jx) {
+                if (cx == 0) {
+                    sh.rowR[lr][J * 16 + lj] = accX[s][0];
+                    sh.rowR[lr + 4][J * 16 + lj] = accX[s][1];
+                } else {
+                    sh.rowR[lr][J * 16 + lj] = accX[s][2];
+                    sh.rowR[lr + 4][J * 16 + lj] = accX[s][3];
                 }
             }
         }
         __syncthreads();
-        // 2. wave 0 factors the panel
-        if (wave == 0) {
+        if (W == 0 && it < 16) {
+            // 2. wave 0 factors panel it (rows j0..127), two rows per lane;
+            //    rows past the block read the zero row NB
             const int ra = j0 + lane, rb = j0 + lane + 64;
-            double va[8], vb[8];
+            const int rac = ra < NB ? ra : NB, rbc = rb < NB ? rb : NB;
+            double va[8], vb[8], rinvv[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                va[c] = ra < NB ? pRaw[ra < NB ? ra : 0][c] : 0.0;
-                vb[c] = rb < NB ? pRaw[rb < NB ? rb : 0][c] : 0.0;
+                va[c] = sh.pRaw[rac][co + c];
+                vb[c] = sh.pRaw[rbc][co + c];
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
@@ -156,7 +195,7 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
                 const double ljj = d * rinv;
                 va[c] = lane > c ? va[c] * rinv : (lane == c ? ljj : 0.0);
                 vb[c] = vb[c] * rinv;
-                if (lane == 0) rinvS[c] = rinv;
+                rinvv[c] = rinv;
 #pragma unroll
                 for (int c2 = c + 1; c2 < 8; ++c2) {
                     const double lk = rdlane(va[c], c2);
@@ -164,68 +203,137 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, i
                     vb[c2] = fma(-vb[c], lk, vb[c2]);
                 }
             }
+            // the panel's L columns: fp64 operands for step 3, its 8x8
+            // diagonal block and pivots for the rows of X, and the fp32 image
+            // of L (rows past the block go to the spare row NB).  Rows of pL
+            // above the panel keep older values: they only reach elements
+            // that are final already, which are never read again.
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                if (ra < NB) pL[ra][c] = va[c];
-                if (rb < NB) pL[rb][c] = vb[c];
-                if (lane < j0) pL[lane][c] = 0.0;
-                if (lane + 64 < j0) pL[lane + 64][c] = 0.0;
-                const int col = j0 + c;
-                if (col < nb) {
-                    if (ra < nb) A[(int64_t)ra * ld + col] = (float)va[c];
-                    if (rb < nb) A[(int64_t)rb * ld + col] = (float)vb[c];
-                    if (lane < j0 && lane < nb) A[(int64_t)lane * ld + col] = 0.0f;
-                    if (lane + 64 < j0 && lane + 64 < nb) A[(int64_t)(lane + 64) * ld + col] = 0.0f;
+                sh.pL[pb][rac][kperm(c)] = va[c];
+                sh.pL[pb][rbc][kperm(c)] = vb[c];
+                sh.Lfin[rac][j0 + c] = (float)va[c];
+                sh.Lfin[rbc][j0 + c] = (float)vb[c];
+            }
+            if (lane < 8) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) sh.dL[pb][lane][c] = va[c];
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) sh.rinv[pb][c] = rinvv[c];
+            }
+        }
+        if (W == 1 && it >= 1) {
+            // 2'. wave 1: rows x0..x0+7 of X = L^-1 by forward substitution
+            //     with panel it - 1's diagonal block, two columns per lane;
+            //     stored to Dinv / Dinv64 as whole rows (coalesced)
+            const int qa = lane, qb = lane + 64;
+            double xa[8], xb[8], l[8][8], ri[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                xa[c] = sh.rowR[c][qa];
+                xb[c] = sh.rowR[c][qb];
+                ri[c] = sh.rinv[xbuf][c];
+#pragma unroll
+                for (int c2 = 0; c2 < c; ++c2) l[c][c2] = sh.dL[xbuf][c][c2];
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+#pragma unroll
+                for (int c2 = 0; c2 < c; ++c2) {
+                    xa[c] = fma(-l[c][c2], xa[c2], xa[c]);
+                    xb[c] = fma(-l[c][c2], xb[c2], xb[c]);
                 }
+                xa[c] = qa <= x0 + 7 ? xa[c] * ri[c] : 0.0;
+                xb[c] = qb <= x0 + 7 ? xb[c] * ri[c] : 0.0;
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                sh.rowXt[qa][kperm(c)] = xa[c];
+                sh.rowXt[qb][kperm(c)] = xb[c];
+                const int row = x0 + c;
+                const double oa = (row < nb && qa < nb) ? xa[c] : 0.0;
+                const double ob = (row < nb && qb < nb) ? xb[c] : 0.0;
+                D[row * NB + qa] = (float)oa;
+                D[row * NB + qb] = (float)ob;
+                D64[row * NB + qa] = oa;
+                D64[row * NB + qb] = ob;
             }
         }
         __syncthreads();
-        // 3. rows j0..j0+7 of X = L^-1
-        if (t < NB) {
-            const int q = t;
-            double x[8];
+        // 3. rank-8 updates on the matrix cores, operands from registers:
+        //    A -= L_p L_p^T for panel it (live tiles: J*16+15 >= j0+8) and
+        //    R -= L_x X_x for panel it - 1 (rows below it, columns up to it),
+        //    opL[r][ks] = L[16 r + lj][panel col 4 ks + lr] (0 above the panel),
+        //    opX[r][ks] = X[panel row 4 ks + lr][16 r + lj].
+        //    Elements that are already final receive updates too; they are
+        //    never read again (their final values went to Lfin and Dinv).
+        if (it < 16) {
+            double opL[8][2];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                double r = rowR[c][q];
-#pragma unroll
-                for (int c2 = 0; c2 < c; ++c2) r = fma(-pL[j0 + c][c2], x[c2], r);
-                x[c] = q <= j0 + 7 ? r * rinvS[c] : 0.0;
+            for (int r = 0; r < 8; ++r) {
+                opL[r][0] = sh.pL[pb][r * 16 + lj][2 * lr];
+                opL[r][1] = sh.pL[pb][r * 16 + lj][2 * lr + 1];
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                rowX[c][q] = x[c];
-                const int row = j0 + c;
-                const double out = (row < nb && q < nb) ? x[c] : 0.0;
-                D[row * NB + q] = (float)out;
-                D64[row * NB + q] = out;
-            }
-        }
-        __syncthreads();
-        // 4. rank-8 updates of the live tiles on the matrix cores
+            for (int s = 0; s < DSLOTS; ++s) {
+                const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
+                if (J * 16 + 15 >= j0 + 8) {
 #pragma unroll
-        for (int s = 0; s < DSLOTS; ++s) {
-            const int I = tI[s], J = tJ[s];
-            if (J * 16 + 15 >= j0 + 8) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const int k = ks * 4 + (lane >> 4);
-                    const double a = -pL[I * 16 + lj][k];
-                    const double bb = pL[J * 16 + lj][k];
-                    accA[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bb, accA[s], 0, 0, 0);
+                    for (int ks = 0; ks < 2; ++ks)
+                        accA[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opL[I][ks], opL[J][ks], accA[s], 0, 0, 0);
                 }
             }
-            if (I * 16 + 15 >= j0 + 8 && J * 16 <= j0 + 7) {
+        }
+        if (it >= 1 && it < 16) {
+            double opM[8][2], opX[8][2];
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const int k = ks * 4 + (lane >> 4);
-                    const double a = -pL[I * 16 + lj][k];
-                    const double bb = rowX[k][J * 16 + lj];
-                    accX[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, bb, accX[s], 0, 0, 0);
+            for (int r = 0; r < 8; ++r) {
+                opM[r][0] = sh.pL[xbuf][r * 16 + lj][2 * lr];
+                opM[r][1] = sh.pL[xbuf][r * 16 + lj][2 * lr + 1];
+                opX[r][0] = sh.rowXt[r * 16 + lj][2 * lr];
+                opX[r][1] = sh.rowXt[r * 16 + lj][2 * lr + 1];
+            }
+#pragma unroll
+            for (int s = 0; s < DSLOTS; ++s) {
+                const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
+                if (I * 16 + 15 >= x0 + 8 && J * 16 <= x0 + 7) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        accX[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opM[I][ks], opX[J][ks], accX[s], 0, 0, 0);
                 }
             }
         }
     }
-    if (t == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
+}
+
+__global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
+                                                         float* dinv, double* dinv64, int64_t dstride, int* info) {
+    __shared__ __attribute__((aligned(16))) DiagShared sh;
+    const int b = blockIdx.x;
+    float* A = H + (int64_t)b * stride + k0 * ld + k0;
+    float* D = dinv + (int64_t)b * dstride;
+    double* D64 = dinv64 + (int64_t)b * dstride;
+    const int lane = threadIdx.x & 63;
+    // uniform in the wave; each wave runs the same loop (two barriers per panel)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Lfin starts at 0 (its upper part is never written) and so does the
+    // spare row of pRaw; the first barrier inside the loop orders this
+    for (int idx = threadIdx.x; idx < (NB + 1) * (NB + 1); idx += 256) (&sh.Lfin[0][0])[idx] = 0.0f;
+    if (threadIdx.x < RP) sh.pRaw[NB][threadIdx.x] = 0.0;
+    int bad = 0;
+    if (wave == 0) potrf_diag_wave<0>(sh, A, ld, nb, D, D64, lane, bad);
+    else if (wave == 1) potrf_diag_wave<1>(sh, A, ld, nb, D, D64, lane, bad);
+    else if (wave == 2) potrf_diag_wave<2>(sh, A, ld, nb, D, D64, lane, bad);
+    else potrf_diag_wave<3>(sh, A, ld, nb, D, D64, lane, bad);
+    __syncthreads();
+    // write L (its upper part is 0 in Lfin), row-coalesced
+    for (int idx = threadIdx.x; idx < NB * NB; idx += 256) {
+        const int i = idx >> 7, j = idx & (NB - 1);
+        if (i < nb && j < nb) A[(int64_t)i * ld + j] = sh.Lfin[i][j];
+    }
+    if (threadIdx.x == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
 }
 
 // Panel solve A21 <- A21 * Dinv^T for the m rows below a diagonal block, in
