@@ -6,7 +6,8 @@
 // matrix-core time) against 64 LDS reads; the next stage's global loads are
 // issued before the current stage's MFMAs so their latency hides behind
 // them.  Work-group ids are remapped so that each XCD (ids congruent mod 8)
-// owns a contiguous run of tiles that share A rows / B columns in its L2.
+// owns a balanced set of tile rows and runs 8x8 blocks of tiles at a time,
+// which share A rows / B columns in its L2.
 //
 // Each operand is staged in LDS in its memory order, so every global load
 // and LDS store is a 16-byte vector: a row-major operand tile (A, or B^T)
@@ -40,6 +41,23 @@ __device__ __forceinline__ int64_t isqrt_floor(int64_t x) {
     return r;
 }
 
+// The tile (ti, tj) with its K range.
+__device__ __forceinline__ TileRange tile_range(const GemmArgs& g, int64_t ti, int64_t tj) {
+    TileRange t;
+    t.i0 = ti * BM; t.j0 = tj * BN;
+    t.skip = false;
+    if (g.cmask == CMASK_LOWER && t.i0 + BM - 1 < t.j0) t.skip = true;
+    if (g.cmask == CMASK_UPPER && t.j0 + BN - 1 < t.i0) t.skip = true;
+    t.klo = 0; t.khi = g.K;
+    if (g.krange == KR_FROM_MAXIJ) t.klo = t.i0 > t.j0 ? t.i0 : t.j0;
+    else if (g.krange == KR_FROM_J) t.klo = t.j0;
+    else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + BM);
+    else if (g.krange == KR_FROM_I) t.klo = t.i0;
+    t.klo = (t.klo / 4) * 4;
+    if (t.klo > g.K) t.klo = g.K;
+    return t;
+}
+
 // Linear tile id -> tile.  Triangular masks enumerate only tiles that touch
 // the kept triangle (square grids); for KR_FROM_MAXIJ the upper tiles are
 // enumerated by increasing column block so that long-K tiles start first.
@@ -57,19 +75,44 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
         // K range grows with the tile row: start the long tiles first
         if (g.krange == KR_TO_I) ti = tm - 1 - ti;
     }
-    TileRange t;
-    t.i0 = ti * BM; t.j0 = tj * BN;
-    t.skip = false;
-    if (g.cmask == CMASK_LOWER && t.i0 + BM - 1 < t.j0) t.skip = true;
-    if (g.cmask == CMASK_UPPER && t.j0 + BN - 1 < t.i0) t.skip = true;
-    t.klo = 0; t.khi = g.K;
-    if (g.krange == KR_FROM_MAXIJ) t.klo = t.i0 > t.j0 ? t.i0 : t.j0;
-    else if (g.krange == KR_FROM_J) t.klo = t.j0;
-    else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + BM);
-    else if (g.krange == KR_FROM_I) t.klo = t.i0;
-    t.klo = (t.klo / 4) * 4;
-    if (t.klo > g.K) t.klo = g.K;
-    return t;
+    return tile_range(g, ti, tj);
+}
+
+// Work-group b -> tile for rectangular grids with at least NXCD tile rows.
+// The hardware deals work-groups to the XCDs round-robin (b mod NXCD), then
+// to the 4 shader engines of the XCD round-robin (its l-th group to engine
+// l mod 4); only inside an engine does a group take whichever CU frees
+// first.  XCD x owns the tile rows of a snake order (round q hands rows
+// NXCD q .. NXCD q + 7 to XCDs 0..7, reversed in odd rounds), which
+// balances per-row work that grows or shrinks with the row.  Inside the
+// XCD, uniform or column-dependent work walks groups of NXCD rows column by
+// column (the 64 tiles an XCD runs at once form an 8x8 block, 16 operand
+// panels in its L2); row-dependent work (KR_TO_I, KR_FROM_I) walks rows
+// one after another, longest first, so that every engine gets every 4th
+// tile of every row.  False: no tile.
+__device__ __forceinline__ bool xcd_tile(const GemmArgs& g, int64_t b, TileRange& t) {
+    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    const int x = (int)(b % NXCD);
+    const int64_t l = b / NXCD;
+    const int64_t full = tm / NXCD, rem = tm - full * NXCD;
+    const int lastpos = (full & 1) ? (NXCD - 1 - x) : x;
+    const int64_t nr = full + (lastpos < rem ? 1 : 0);   // tile rows of XCD x
+    if (l >= nr * tn) return false;
+    int64_t q, tj;                                       // q: round = row index within XCD x
+    if (g.krange == KR_TO_I || g.krange == KR_FROM_I) {
+        q = l / tn;
+        tj = l - q * tn;
+        if (g.krange == KR_TO_I) q = nr - 1 - q;         // K grows with the row: last rows first
+    } else {
+        const int64_t g0 = (l / (NXCD * tn)) * NXCD;    // first row (of XCD x) of l's group
+        const int64_t G = min((int64_t)NXCD, nr - g0);
+        const int64_t w = l - g0 * tn;
+        tj = w / G;
+        q = g0 + (w - tj * G);
+    }
+    const int64_t ti = q * NXCD + ((q & 1) ? (NXCD - 1 - x) : x);
+    t = tile_range(g, ti, tj);
+    return true;
 }
 
 // One operand's share of a stage: 4 float4 per thread (kept in named
@@ -204,13 +247,13 @@ __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, con
 template <int TA, int TB, bool CHECK>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap) {
     __shared__ __attribute__((aligned(16))) float lds[2 * TILE_F];
-    int64_t id = blockIdx.x;
-    if (remap) {   // XCD-contiguous tile runs
-        const int64_t per = (ntiles + NXCD - 1) / NXCD;
-        id = (id % NXCD) * per + id / NXCD;
-        if (id >= ntiles) return;
+    TileRange tr;
+    if (remap) {
+        if (!xcd_tile(g, blockIdx.x, tr)) return;
+    } else {
+        if ((int64_t)blockIdx.x >= ntiles) return;
+        tr = tile_of(g, blockIdx.x);
     }
-    const TileRange tr = tile_of(g, id);
     if (tr.skip) return;
     const int64_t z = blockIdx.z;
     const float* A = g.A + z * g.sA;
@@ -271,9 +314,11 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     // 16-byte loads need 16-byte aligned bases and leading dimensions
     const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
                          g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;
-    // triangular enumerations keep their own (long-K-first) order
-    const int remap = (!tri && tiles >= 2 * NXCD) ? 1 : 0;
-    const int64_t grid = remap ? cdiv(tiles, NXCD) * NXCD : tiles;
+    // triangular enumerations keep their own (long-K-first) order; other
+    // grids with at least NXCD tile rows use the XCD row assignment
+    const int remap = (!tri && tm >= NXCD) ? 1 : 0;
+    const int64_t grid = remap ? cdiv(tm, NXCD) * tn * NXCD : tiles;
+    IC_REQUIRE(grid < (1LL << 23), "gemm_f32: problem too large");
     const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
     const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
     ProfScope prof_scope(st, g.tag, fl, by);
