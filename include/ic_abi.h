@@ -57,10 +57,12 @@ int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, i
                    float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
                    unsigned long long* n_zeroed, void* stream);
 
-/* Two-sided rotation R^T H R of `batch` square fp32 matrices [n, n] stored
- * back to back with leading dimension ld (n multiple of rot), in place.
+/* Two-sided rotation H <- R^T src R of `batch` square fp32 matrices [n, n]
+ * stored back to back with leading dimension ld (n multiple of rot); src has
+ * the same layout and may be H itself (in place).
  * Replaces converter/rotation.py:156-248 (rotate_hessian, after padding). */
-int ic_rotate_hessian(float* H, int64_t batch, int64_t n, int64_t ld, int rot, void* stream);
+int ic_rotate_hessian(const float* src, float* H, int64_t batch, int64_t n, int64_t ld, int rot,
+                      void* stream);
 
 /* Per-row min / max / max-abs of an fp32 matrix; NaN propagates like
  * torch.amin/amax.  Any output pointer may be NULL.
@@ -142,7 +144,11 @@ int ic_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alph
 /* In place on `batch` dense fp32 matrices [n, n] (back to back):
  *   H <- H + fp32(damping) * max(mean(diag H), 1e-6) * I;  L = chol(H);
  *   method 0 ("hinv"):     H <- H^-1 = L^-T L^-1 (full symmetric);
- *   method 1 ("cholesky"): H <- chol(H^-1)^T (upper; lower part zero).
+ *   method 1 ("cholesky"): H <- chol(H^-1)^T (upper; lower part zero);
+ *   method 2 ("hinv", upper triangle): as method 0 on and above the
+ *            diagonal, the strictly lower part left holding finite scratch
+ *            values (for callers that read only rows j, columns >= j, as
+ *            the GPTQ / LDLQ sweeps and lazy updates do).
  * info: device int32[2*batch]; info[b] > 0 is the 1-based column of the
  * first non-positive pivot of chol(H_b) (then H_b is not a valid result and
  * the caller falls back like converter/rounding.py:19-34); info[batch+b]

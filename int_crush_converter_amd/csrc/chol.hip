@@ -614,7 +614,8 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
                                   void* workspace, void* stream) {
     IC_REQUIRE(H && info && workspace, "ic_hessian_inverse: null pointer");
     IC_REQUIRE(n >= 0 && batch >= 0, "ic_hessian_inverse: bad size");
-    IC_REQUIRE(method == 0 || method == 1, "ic_hessian_inverse: method must be 0 (hinv) or 1 (cholesky)");
+    IC_REQUIRE(method >= 0 && method <= 2,
+               "ic_hessian_inverse: method must be 0 (hinv), 1 (cholesky) or 2 (hinv, upper triangle)");
     if (n == 0 || batch == 0) return IC_OK;
     hipStream_t st = as_stream(stream);
     const int64_t ld = n, sH = n * n;
@@ -634,6 +635,7 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     rc = gemm_f32(u, st);
     if (rc) return rc;
     dim3 tb(16, 16), tg((unsigned)cdiv(n, 16), (unsigned)cdiv(n, 16), (unsigned)batch);
+    if (method == 2) return IC_OK;   // the lower part keeps L: finite, never read by such callers
     hipLaunchKernelGGL(mirror_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
     IC_CHECK_LAUNCH();
     if (method == 1) {

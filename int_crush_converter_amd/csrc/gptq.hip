@@ -7,16 +7,15 @@
 // update all later columns at once, W[:, end:] -= E @ Hinv[blk, end:].
 //
 // Sweep kernel: the nb x nb Hinv block is staged in LDS once per work-group
-// of 16 rows.  A row is owned by 16 lanes, lane l holding columns l, l + 16,
-// ..., l + 112 in 8 registers, so one wave quantises 4 rows per instruction.
-// At step j the owning lane quantises w_j; the four owners' errors are read
-// into scalar registers (readlane) and every lane picks its row's value.
-// Every lane then applies its updates in column order, so every w_k sees
-// exactly the reference's sequence of fp32 roundings (bit-exact given the
-// same Hinv).  The column recurrence is a pure VALU chain: each owner keeps
-// its divisor data in registers and the next Hinv row is fetched while the
-// current column is processed.  Codes and errors are staged in LDS and
-// stored coalesced.
+// of 16 rows, one row per wave (16 waves: 4 per SIMD, which hide each
+// other's latency).  Lane l holds columns l and l + 64 of its row.  At step
+// j the owner's value is read into a scalar register (readlane) and every
+// lane quantises it, so the error is already uniform and the division's
+// domain test is a scalar branch; every lane then applies its updates in
+// column order, so every w_k sees exactly the reference's sequence of fp32
+// roundings (bit-exact given the same Hinv).  The next Hinv row and the next
+// pivot data are fetched while the current column is processed.  A lane
+// owns the codes and errors of its two columns and stores them at the end.
 //
 // The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
 // order differs from MKL's sgemm, which is the only non-bit-exact step.
@@ -25,10 +24,9 @@
 namespace icq {
 
 constexpr int SW_NB = 128;     // max columns per sweep block
-constexpr int SW_L = 16;       // lanes per row
-constexpr int SW_R = SW_NB / SW_L;   // columns (registers) per lane
-constexpr int SW_THREADS = 256;
-constexpr int SW_ROWS = SW_THREADS / SW_L;
+constexpr int SW_R = SW_NB / 64;   // columns (registers) per lane
+constexpr int SW_ROWS = 16;    // rows (waves) per work-group
+constexpr int SW_THREADS = SW_ROWS * 64;
 
 enum SweepMode : int {
     SWEEP_GPTQ = 0,   // per-row scale (+zp), err / Hinv_jj, clamp +-100, NaN -> 0
@@ -51,24 +49,15 @@ struct SweepArgs {
     int mode;
 };
 
-// Value of lane o of each 16-lane row group (o wave-uniform).  m[k] is all
-// ones on the lanes of group k and zero elsewhere, so the select is
-// branch-free.
-__device__ __forceinline__ float row16_bcast(float v, int o, const int (&m)[4]) {
-    const int x = __float_as_int(v);
-    const int b0 = __builtin_amdgcn_readlane(x, o);
-    const int b1 = __builtin_amdgcn_readlane(x, o + 16);
-    const int b2 = __builtin_amdgcn_readlane(x, o + 32);
-    const int b3 = __builtin_amdgcn_readlane(x, o + 48);
-    return __int_as_float((b0 & m[0]) | (b1 & m[1]) | (b2 & m[2]) | (b3 & m[3]));
+__device__ __forceinline__ float rdlanef(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 template <int MODE>
 __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
-    constexpr int L = SW_L, R = SW_R, ROWS = SW_ROWS;
+    constexpr int R = SW_R;
     __shared__ float Hs[SW_NB * SW_NB];
-    __shared__ float Es[ROWS * SW_NB];
-    __shared__ int8_t Qs[ROWS * SW_NB];
+    __shared__ float hjj[SW_NB];              // Hinv_jj
     __shared__ float dinv[SW_NB];             // GPTQ: RN(1 / Hinv_jj); LDLQ: 1 / max(Hinv_jj, 1e-8)
     __shared__ int dok[SW_NB];                // GPTQ: Hinv_jj inside the fast-division domain
 
@@ -76,17 +65,12 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const int nb = a.nb;
     const int64_t col0 = a.col0 + (int64_t)g * a.gcol;
     const float* H = a.H + (int64_t)g * a.hg;
-    const int t = threadIdx.x;
-    const int l = t % L, rl = t / L;
-    const int grp = (t & 63) / L;            // row group within the wave
-    const int gmask[4] = {grp == 0 ? -1 : 0, grp == 1 ? -1 : 0, grp == 2 ? -1 : 0, grp == 3 ? -1 : 0};
-    const int64_t row = (int64_t)blockIdx.x * ROWS + rl;
-    const bool rv = row < a.rows;
-
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     {
         // all global loads in flight before the LDS stores
         constexpr int STEP = SW_THREADS / SW_NB, PER = SW_NB / STEP;
-        const int c = t & (SW_NB - 1), i0 = t >> 7;
+        const int c = t & (SW_NB - 1), i0 = t / SW_NB;
         float tmp[PER];
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
@@ -96,87 +80,84 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 #pragma unroll
         for (int k = 0; k < PER; ++k) Hs[(i0 + k * STEP) * SW_NB + c] = tmp[k];
     }
-    for (int j = t; j < SW_NB; j += SW_THREADS) {
-        float d = j < nb ? H[(int64_t)j * a.ldh + j] : 1.0f;
+    if (t < SW_NB) {
+        const int j = t;
+        const float hd = j < nb ? H[(int64_t)j * a.ldh + j] : 1.0f;
+        float d = hd;
         if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
+        hjj[j] = hd;
         dinv[j] = 1.0f / d;
         dok[j] = div_b_ok(d) ? 1 : 0;
     }
     __syncthreads();
+    const int64_t row = (int64_t)blockIdx.x * SW_ROWS + wave;
+    if (row >= a.rows) return;
 
     float w[R];
     const float* wrow = a.W + row * a.ldw + col0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int c = r * L + l;
-        w[r] = (rv && c < nb) ? wrow[c] : 0.0f;
+        const int c = r * 64 + lane;
+        w[r] = c < nb ? wrow[c] : 0.0f;
     }
     float s_row = 1.0f, z_row = 0.0f;
     float sc[MODE == SWEEP_LDLQ ? R : 1];
     float scr[MODE == SWEEP_LDLQ ? R : 1];
     if (MODE == SWEEP_GPTQ) {
-        if (rv) {
-            s_row = a.s[row];
-            if (a.zp) z_row = a.zp[row];
-        }
-        sc[0] = s_row;
-        scr[0] = 1.0f / s_row;
+        s_row = a.s[row];
+        if (a.zp) z_row = a.zp[row];
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int c = r * L + l;
-            float v = (rv && c < nb) ? a.s[row * a.lds + col0 + c] : 1.0f;
+            const int c = r * 64 + lane;
+            float v = c < nb ? a.s[row * a.lds + col0 + c] : 1.0f;
             v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
             sc[r] = v;
             scr[r] = 1.0f / v;
         }
     }
+    const float s_rrow = 1.0f / s_row;
     const bool has_zp = a.zp != nullptr;
     const bool srow_ok = div_b_ok(s_row);
-    // divisor data of the lane's own columns
-    float dv[R];
-    bool dk[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        dv[r] = dinv[r * L + l];
-        dk[r] = dok[r * L + l] != 0;
-    }
 
-    // Column j = r0 * L + o lives in register r0 of lane o.  Updates are
-    // unconditional on registers r >= r0: the register of column r0 on lanes
+    // Column j = 64 r0 + o lives in register r0 of lane o.  Updates are
+    // unconditional on registers r >= r0: the register of column j on lanes
     // <= o is already quantised and never read again, so those updates are
     // dead values.
+    float qv[R], ev[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) qv[r] = ev[r] = 0.0f;
     float h[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) h[r] = Hs[r * L + l];
+    for (int r = 0; r < R; ++r) h[r] = Hs[r * 64 + lane];
+    float hd = hjj[0], dvj = dinv[0];
+    bool dkj = dok[0] != 0;
 #pragma unroll
     for (int r0 = 0; r0 < R; ++r0) {
-        if (r0 * L >= nb) break;
-        const float s_el = sc[MODE == SWEEP_LDLQ ? r0 : 0];
-        const float s_rc = scr[MODE == SWEEP_LDLQ ? r0 : 0];
-        const bool s_ok = MODE == SWEEP_LDLQ ? div_b_ok(s_el) : srow_ok;
+        if (r0 * 64 >= nb) break;
 #pragma nounroll
-        for (int o = 0; o < L; ++o) {
-            const int j = r0 * L + o;
+        for (int o = 0; o < 64; ++o) {
+            const int j = r0 * 64 + o;
             if (j >= nb) break;
             const int jn = j + 1 < SW_NB ? j + 1 : j;
             float hn[R];
 #pragma unroll
-            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * L + l];
-            const float x = w[r0];
-            const bool own = l == o;
+            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * 64 + lane];
+            const float hdn = hjj[jn], dvn = dinv[jn];
+            const bool dkn = dok[jn] != 0;
+            const float x = rdlanef(w[r0], o);   // the owner's value, in every lane
             float q, e;
             if (MODE == SWEEP_GPTQ) {
-                float y = div_rn(x, s_el, s_rc, s_ok, own);
+                float y = div_rn(x, s_row, s_rrow, srow_ok);
                 if (has_zp) y = y + z_row;
                 q = clampf(rhaz(y), a.qmin, a.qmax);
-                const float deq = has_zp ? (q - z_row) * s_el : q * s_el;
-                // h[r0] on the owner lane is Hinv[j][j]
-                e = div_rn(x - deq, h[r0], dv[r0], dk[r0], own);
+                const float deq = has_zp ? (q - z_row) * s_row : q * s_row;
+                e = div_rn(x - deq, hd, dvj, dkj);
                 e = clampf(e, -100.0f, 100.0f);
                 if (e != e) e = 0.0f;
             } else {
-                q = clampf(rhaz(div_rn(x, s_el, s_rc, s_ok, own)), a.qmin, a.qmax);
+                const float s_el = rdlanef(sc[r0], o), s_rc = rdlanef(scr[r0], o);
+                q = clampf(rhaz(div_rn(x, s_el, s_rc, div_b_ok(s_el))), a.qmin, a.qmax);
                 // sign-flip correction (inert for positive scales)
                 const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
                                                   : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
@@ -186,29 +167,27 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 if (flip && q == a.qmin) q = a.qmax;
                 if (can) q = -q;
                 q = clampf(q, a.qmin, a.qmax);
-                e = (x - q * s_el) * dv[r0];
+                e = (x - q * s_el) * dvj;
             }
-            const float err = row16_bcast(e, o, gmask);   // the owner's error, in every lane of its row
-            if (own) {
-                Qs[rl * SW_NB + j] = (int8_t)(int)q;
-                Es[rl * SW_NB + j] = e;
-            }
+            const bool own = lane == o;
+            qv[r0] = own ? q : qv[r0];
+            ev[r0] = own ? e : ev[r0];
 #pragma unroll
-            for (int r = r0; r < R; ++r) w[r] = w[r] - err * h[r];
+            for (int r = r0; r < R; ++r) w[r] = w[r] - e * h[r];
 #pragma unroll
             for (int r = r0; r < R; ++r) h[r] = hn[r];
+            hd = hdn;
+            dvj = dvn;
+            dkj = dkn;
         }
     }
-    __syncthreads();
-    // coalesced stores of codes and errors
-    {
-        const int c = t & (SW_NB - 1);
-        for (int rr = t >> 7; rr < ROWS; rr += SW_THREADS / SW_NB) {
-            const int64_t gr = (int64_t)blockIdx.x * ROWS + rr;
-            if (gr < a.rows && c < nb) {
-                a.Q[gr * a.ldq + col0 + c] = Qs[rr * SW_NB + c];
-                a.E[(int64_t)g * a.eg + gr * a.lde + c] = Es[rr * SW_NB + c];
-            }
+    // codes and errors of the lane's own columns (coalesced per row)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int c = r * 64 + lane;
+        if (c < nb) {
+            a.Q[row * a.ldq + col0 + c] = (int8_t)(int)qv[r];
+            a.E[(int64_t)g * a.eg + row * a.lde + c] = ev[r];
         }
     }
 }

@@ -327,9 +327,10 @@ static int launch_lds(float* p, int rot, int64_t groups, int64_t nb, int64_t sa,
 
 using namespace icq;
 
-extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
-                              float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
-                              unsigned long long* n_zeroed, void* stream) {
+// Row rotation; `tag` is the profiler phase (weights or the Hessian's row pass).
+static int rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src, float* dst,
+                       int64_t cols_pad, int64_t ld_dst, int rot, float zero_above, unsigned long long* n_zeroed,
+                       void* stream, int tag) {
     IC_REQUIRE(src && dst, "ic_rotate_rows: null pointer");
     IC_REQUIRE(src_dtype >= 0 && src_dtype <= 2, "ic_rotate_rows: bad dtype");
     IC_REQUIRE(rot >= 1 && rot <= 4096 && is_pow2(rot), "ic_rotate_rows: rot must be a power of 2 <= 4096");
@@ -347,7 +348,7 @@ extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int6
         // rot 256: a few items per thread (8 work-groups of 256 per CU)
         int grid = rot == 256 ? (int)std::min<int64_t>(grid_for(chunks / 4, 256), 2048) : grid_for(chunks, 256);
         int stages = rot == 4 ? 1 : rot == 16 ? 2 : rot == 64 ? 3 : 4;
-        ProfScope prof_scope(st, src == (const void*)dst ? PT_ROTATE_H : PT_ROTATE, 2.0 * stages * rows * cols_pad,
+        ProfScope prof_scope(st, tag, 2.0 * stages * rows * cols_pad,
                      (double)rows * cols * esz + 4.0 * rows * cols_pad);
         const bool fast = vec_ok && cols % 16 == 0;
 #define ICQ_ROT_LAUNCH(R, D, F)                                                                               \
@@ -381,14 +382,29 @@ extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int6
     return launch_lds(dst, rot, cols_pad / rot, rows, 1, ld_dst, 1, 0, st);
 }
 
-extern "C" int ic_rotate_hessian(float* H, int64_t batch, int64_t n, int64_t ld, int rot, void* stream) {
-    IC_REQUIRE(H, "ic_rotate_hessian: null pointer");
+extern "C" int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                              float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
+                              unsigned long long* n_zeroed, void* stream) {
+    return rotate_rows(src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, rot, zero_above, n_zeroed,
+                       stream, PT_ROTATE);
+}
+
+extern "C" int ic_rotate_hessian(const float* src, float* H, int64_t batch, int64_t n, int64_t ld, int rot,
+                                 void* stream) {
+    IC_REQUIRE(src && H, "ic_rotate_hessian: null pointer");
     IC_REQUIRE(rot >= 1 && rot <= 4096 && is_pow2(rot), "ic_rotate_hessian: rot must be a power of 2 <= 4096");
     IC_REQUIRE(n % rot == 0 && ld >= n, "ic_rotate_hessian: n must be a multiple of rot");
-    if (batch == 0 || n == 0 || rot == 1) return IC_OK;
+    if (batch == 0 || n == 0) return IC_OK;
     hipStream_t st = as_stream(stream);
-    // rows: H <- H R; the batch is batch*n consecutive rows of pitch ld
-    int rc = ic_rotate_rows(H, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, 0.0f, nullptr, stream);
+    if (rot == 1) {
+        if (src != H)
+            IC_CHECK_HIP(hipMemcpy2DAsync(H, ld * sizeof(float), src, ld * sizeof(float), n * sizeof(float),
+                                          batch * n, hipMemcpyDeviceToDevice, st));
+        return IC_OK;
+    }
+    // rows: H <- src R (the copy out of src is this pass); the batch is
+    // batch*n consecutive rows of pitch ld
+    int rc = rotate_rows(src, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, 0.0f, nullptr, stream, PT_ROTATE_H);
     if (rc) return rc;
     // columns: H <- R^T H
     if (rot == 256) {

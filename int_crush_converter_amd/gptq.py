@@ -115,19 +115,25 @@ def gptq_quantize_layer(
         full = N // bs
         Q = torch.empty(M, N, dtype=torch.int8, device=Wg.device)
         if full > 0:
-            Hinv = inverse_batch(Hg[:full].float(), damping, hessian_method, fallbacks)
+            Hinv = inverse_batch(Hg[:full].float(), damping, hessian_method, fallbacks, upper_only=True)
             Q[:, :full * bs] = sweep(W_work[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits,
                                      block_size, groups=full)
         if full * bs < N:
             if full >= nblk:
                 raise ValueError(f"3-D Hessian with {nblk} blocks of {bs} does not cover {N} columns")
             rem = N - full * bs
-            Hinv = inverse_batch(Hg[full, :rem, :rem].float(), damping, hessian_method, fallbacks)
+            Hinv = inverse_batch(Hg[full, :rem, :rem].float(), damping, hessian_method, fallbacks, upper_only=True)
             Q[:, full * bs:] = sweep(W_work[:, full * bs:].contiguous(), Hinv, s32, z32, int_bits, block_size)
     elif Hg.dim() == 2:
         if tuple(Hg.shape) != (N, N):
             raise ValueError(f"Hessian shape {hessian.shape} != ({N}, {N})")
-        Hinv = inverse_batch(Hg.float(), damping, hessian_method, fallbacks)
+        Hf = Hg.float().contiguous()
+        if Hf.data_ptr() != hessian.data_ptr():
+            # our own copy (moved to the GPU or converted): invert it in place
+            Hinv = inverse_batch(Hf, damping, hessian_method, fallbacks, inplace=True,
+                                 restore=lambda: nat.to_gpu(hessian).float().contiguous(), upper_only=True)
+        else:
+            Hinv = inverse_batch(Hf, damping, hessian_method, fallbacks, upper_only=True)
         Q = sweep(W_work, Hinv, s32, z32, int_bits, block_size)
     else:
         raise ValueError(

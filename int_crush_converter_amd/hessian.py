@@ -39,29 +39,49 @@ def _fallback_inverse(H_damped: torch.Tensor) -> torch.Tensor:
 
 
 def inverse_batch(H: torch.Tensor, damping: float, method: str = "hinv",
-                  fallbacks: list[str] | None = None) -> torch.Tensor:
-    """``H``: fp32 GPU tensor [n, n] or [batch, n, n] (not modified).  Returns
-    the damped inverse (method "hinv") or the upper Cholesky factor of the
-    damped inverse (method "cholesky") of every matrix, same shape."""
+                  fallbacks: list[str] | None = None, *, inplace: bool = False, restore=None,
+                  upper_only: bool = False) -> torch.Tensor:
+    """``H``: fp32 GPU tensor [n, n] or [batch, n, n].  Returns the damped
+    inverse (method "hinv") or the upper Cholesky factor of the damped
+    inverse (method "cholesky") of every matrix, same shape.
+
+    ``H`` is not modified unless ``inplace`` (a contiguous fp32 tensor the
+    caller owns, which then holds the result); an in-place call needs
+    ``restore()``, which returns the original ``H`` again for the fallback
+    chain when a Cholesky factorisation fails.  ``upper_only`` (method
+    "hinv"): only the entries on and above the diagonal are the inverse's,
+    the rest are finite scratch values - for callers that read rows j from
+    column j on, as the GPTQ / LDLQ sweeps do."""
     squeeze = H.dim() == 2
     Hb = H.unsqueeze(0) if squeeze else H
     batch, n, _ = Hb.shape
-    out = Hb.float().contiguous().clone()
+    if inplace:
+        if restore is None or Hb.dtype != torch.float32 or not Hb.is_contiguous():
+            raise ValueError("inverse_batch: inplace needs a contiguous fp32 tensor and restore()")
+        out = Hb
+    else:
+        out = Hb.float().contiguous().clone()
     if n == 0 or batch == 0:
         return out[0] if squeeze else out
     code = METHODS[method]
+    if upper_only and code == 0:
+        code = 2
     info = torch.zeros(2 * batch, dtype=torch.int32, device=out.device)
     ws = nat.workspace(nat.lib().ic_hessian_inverse_workspace_bytes(batch, n), out.device)
     nat.check(nat.lib().ic_hessian_inverse(out.data_ptr(), batch, n, float(damping), code, info.data_ptr(),
                                            ws.data_ptr(), nat.stream()), "ic_hessian_inverse")
     del ws
     inf = info.tolist()
+    orig = None
     for b in range(batch):
         chol_failed = inf[b] != 0
         inv_chol_failed = code == 1 and inf[batch + b] != 0
         if not (chol_failed or inv_chol_failed):
             continue
-        Hd = _damped(Hb[b].float(), damping)
+        if inplace and orig is None:
+            orig = restore()
+            orig = orig.unsqueeze(0) if squeeze else orig
+        Hd = _damped((orig if inplace else Hb)[b].float(), damping)
         if chol_failed:
             logger.debug("Cholesky of the damped Hessian failed at column %d; using inv", inf[b])
             if fallbacks is not None:
@@ -74,7 +94,7 @@ def inverse_batch(H: torch.Tensor, damping: float, method: str = "hinv",
             continue
         if Hi is None:
             # chol(H) worked but chol(H^-1) did not: return H^-1 itself (gptq.py:106-110)
-            Hi = inverse_batch(Hb[b], damping, "hinv")
+            Hi = inverse_batch((orig if inplace else Hb)[b], damping, "hinv")
             out[b] = Hi
             continue
         try:

@@ -66,9 +66,18 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
                int_bits: int, asymmetric: bool, hessian_method: str, fallbacks: list[str]):
     """GPTQ on a rotated W_work with a (raw or rotated) 2-D / 3-D Hessian."""
     M, N = W_work.shape
-    Hg = nat.to_gpu(H).float()
-    if rotate_h > 0:
-        Hg = rotate_hessian_gpu(Hg, rotate_h)
+    Hsrc = nat.to_gpu(H).float()
+    Hg = rotate_hessian_gpu(Hsrc, rotate_h) if rotate_h > 0 else Hsrc
+    # a Hessian this function created (rotated, or copied to the GPU / fp32)
+    # is inverted in place; the fallback chain rebuilds it from the caller's
+    # untouched one
+    own = Hg.data_ptr() != H.data_ptr() and Hg.is_contiguous()
+
+    def restore():
+        src = nat.to_gpu(H).float()
+        return rotate_hessian_gpu(src, rotate_h) if rotate_h > 0 else src
+
+    inv_kw = dict(inplace=True, restore=restore, upper_only=True) if own else dict(upper_only=True)
     s32, z32, s16, z8 = row_params(W_work, int_bits, asymmetric)
     Ww = W_work.clone()
     if Hg.dim() == 3:
@@ -76,16 +85,16 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
         full = N // bs
         Q = torch.empty(M, N, dtype=torch.int8, device=W_work.device)
         if full:
-            Hinv = inverse_batch(Hg[:full], damping, hessian_method, fallbacks)
+            Hinv = inverse_batch(Hg[:full], damping, hessian_method, fallbacks, upper_only=True)
             Q[:, :full * bs] = sweep(Ww[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits, block_size, full)
         if full * bs < N:
             rem = N - full * bs
-            Hinv = inverse_batch(Hg[full, :rem, :rem], damping, hessian_method, fallbacks)
+            Hinv = inverse_batch(Hg[full, :rem, :rem], damping, hessian_method, fallbacks, upper_only=True)
             Q[:, full * bs:] = sweep(Ww[:, full * bs:].contiguous(), Hinv, s32, z32, int_bits, block_size)
     else:
         if tuple(Hg.shape) != (N, N):
             raise ValueError(f"Hessian shape {tuple(Hg.shape)} != ({N}, {N})")
-        Hinv = inverse_batch(Hg, damping, hessian_method, fallbacks)
+        Hinv = inverse_batch(Hg, damping, hessian_method, fallbacks, **inv_kw)
         Q = sweep(Ww, Hinv, s32, z32, int_bits, block_size)
     return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
 

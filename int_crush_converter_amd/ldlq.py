@@ -174,18 +174,19 @@ def ldlq_quantize_layer(
             Hinv = torch.zeros(N, N, dtype=torch.float32, device=Wg.device)
             full = min(N // bs, nblk)
             if full:
-                inv = inverse_batch(Hg[:full], damping, "hinv", fallbacks)
+                inv = inverse_batch(Hg[:full], damping, "hinv", fallbacks, upper_only=True)
                 for b in range(full):
                     Hinv[b * bs:(b + 1) * bs, b * bs:(b + 1) * bs] = inv[b]
             if full * bs < N and full < nblk:
                 rem = N - full * bs
-                Hinv[full * bs:, full * bs:] = inverse_batch(Hg[full, :rem, :rem], damping, "hinv", fallbacks)
+                Hinv[full * bs:, full * bs:] = inverse_batch(Hg[full, :rem, :rem], damping, "hinv", fallbacks,
+                                                            upper_only=True)
             if greedy_passes > 0:
                 raise ValueError("greedy search needs a 2-D Hessian (block-diagonal 3-D given)")
         elif Hg.dim() == 2:
             if tuple(Hg.shape) != (N, N):
                 raise ValueError(f"Hessian shape {tuple(hessian.shape)} != ({N}, {N})")
-            Hinv = inverse_batch(Hg, damping, "hinv", fallbacks)
+            Hinv = inverse_batch(Hg, damping, "hinv", fallbacks, upper_only=True)
             H_greedy = Hg
         else:
             raise ValueError(f"Expected 2D tensor, 3D tensor, or DLR dict Hessian, got {hessian.dim()}D")
@@ -198,7 +199,7 @@ def ldlq_quantize_layer(
         if not bool(torch.isfinite(H).all().item()):
             logger.warning("LDLQ: Hessian has inf/nan, falling back to RTN")
             return _hessian_nan_rtn(Wg, int_bits, out_dev)
-        Hinv = inverse_batch(H, damping, "hinv", fallbacks)
+        Hinv = inverse_batch(H, damping, "hinv", fallbacks, upper_only=True)
         H_greedy = _damp_only(H, damping)
 
     ramax = _row_absmax(Wg)

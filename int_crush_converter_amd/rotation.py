@@ -116,21 +116,16 @@ def rotate_hessian_gpu(H: torch.Tensor, rot_size: int) -> torch.Tensor:
     """R^T H R of a 2-D or 3-D fp32 GPU Hessian (padded first for 2-D); a new
     tensor.  Internal fast path used by the GPTQ/LDLQ drivers."""
     H = H.float().contiguous()
-    if H.dim() == 2:
-        n = H.shape[0]
-        if n % rot_size:
-            p = rot_size - n % rot_size
-            H = F.pad(H, (0, p, 0, p))
-        else:
-            H = H.clone()
-        batch, n = 1, H.shape[0]
+    if H.dim() == 2 and H.shape[0] % rot_size:
+        p = rot_size - H.shape[0] % rot_size
+        src = out = F.pad(H, (0, p, 0, p))          # a new tensor: rotated in place
     else:
-        batch, n = H.shape[0], H.shape[1]
-        H = H.clone()
-    if H.numel():
-        nat.check(nat.lib().ic_rotate_hessian(H.data_ptr(), batch, n, n, rot_size, nat.stream()),
-                  "ic_rotate_hessian")
-    return H
+        src, out = H, torch.empty_like(H)          # the first pass reads H and writes out
+    batch, n = (1, out.shape[0]) if out.dim() == 2 else (out.shape[0], out.shape[1])
+    if out.numel():
+        nat.check(nat.lib().ic_rotate_hessian(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size,
+                                              nat.stream()), "ic_rotate_hessian")
+    return out
 
 
 def rotate_hessian(H, rot_size: int):

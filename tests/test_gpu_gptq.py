@@ -105,6 +105,50 @@ def test_hessian_cholesky_method(gpu_dev):
     assert torch.allclose(got, want, atol=2e-3 * want.abs().max().item())
 
 
+@pytest.mark.parametrize("n", [200, 1024])
+def test_hessian_inverse_upper_only_in_place(gpu_dev, n):
+    # method 2 / inplace: the same upper triangle, bit for bit, as the full
+    # out-of-place inverse; the lower part finite; the input consumed
+    from int_crush_converter_amd.hessian import inverse_batch
+    H = lognormal_hessian(n, n + 100, 7).to(gpu_dev)
+    full = inverse_batch(H, 0.01, "hinv")
+    work = H.clone()
+    calls = []
+    got = inverse_batch(work, 0.01, "hinv", inplace=True, restore=lambda: calls.append(1) or H.clone(),
+                        upper_only=True)
+    assert got.data_ptr() == work.data_ptr() and not calls
+    iu = torch.triu_indices(n, n, device=gpu_dev)
+    assert torch.equal(got[iu[0], iu[1]], full[iu[0], iu[1]])
+    assert torch.isfinite(got).all()
+
+
+def test_hessian_in_place_fallback_uses_restore(gpu_dev):
+    from int_crush_converter_amd.hessian import inverse_batch
+    H = torch.zeros(8, 8)
+    H[0, 0] = -1.0
+    work = H.to(gpu_dev)
+    fb = []
+    got = inverse_batch(work, 0.01, "hinv", fb, inplace=True, restore=lambda: H.to(gpu_dev)).cpu()
+    assert fb == ["hessian_inv_fallback"]
+    assert torch.allclose(got, torch.linalg.inv(ref.damp(H, 0.01)), atol=1e-5)
+
+
+def test_rotate_hessian_out_of_place(gpu_dev):
+    from int_crush_converter_amd.rotation import rotate_hessian_gpu
+    H = lognormal_hessian(512, 600, 5).to(gpu_dev)
+    H0 = H.clone()
+    got = rotate_hessian_gpu(H, 256)
+    assert torch.equal(H, H0) and got.data_ptr() != H.data_ptr()
+    want = ref.rotate_hessian(H0.cpu(), 256)
+    assert torch.allclose(got.cpu(), want, atol=2e-6 * want.abs().max().item(), rtol=0)
+    # src == dst through the C ABI (what the padded path does): the same bits
+    from int_crush_converter_amd import _native as nat
+    inplace = H0.clone()
+    nat.check(nat.lib().ic_rotate_hessian(inplace.data_ptr(), inplace.data_ptr(), 1, 512, 512, 256,
+                                          nat.stream()), "ic_rotate_hessian")
+    assert torch.equal(inplace, got)
+
+
 def test_hessian_singular_falls_back(gpu_dev):
     from int_crush_converter_amd.hessian import inverse_batch
     H = torch.zeros(8, 8)
