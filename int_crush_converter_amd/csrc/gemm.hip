@@ -185,23 +185,50 @@ struct OperandLoader {
 template <bool ROWMAJ>
 __device__ __forceinline__ int lds_at(int m, int k) { return ROWMAJ ? m * PR + k : k * PKM + m; }
 
+// One BK stage of a wave's 64x64 sub-tile; MFMA step s of a group of 16 k
+// feeds k = 4 s + l / 16 from lane l.  When both operands are staged k-major
+// (A^T B: the LAUUM), each permutes its rows (A) or columns (B) inside the
+// wave's 64 - fragment a / b at MFMA row / column m is row 4 m + a / column
+// 4 m + b - so one 16-byte LDS read gives a lane all four fragments of one
+// step (WIDE).  Otherwise each fragment value is one 4-byte read, which
+// measured faster there.
+//   row of accumulator (a, v) at lane l:  wi + 16 a + 4 (l/16) + v,  WIDE: wi + 4 (4 (l/16) + v) + a
+//   column of (b) at lane l:              wj + 16 b + l%16,          WIDE: wj + 4 (l%16) + b
 template <int TA, int TB>
 __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int wi, int wj, int lane,
                                           floatx4 (&acc)[4][4]) {
     constexpr bool AR = TA == 0, BR = TB == 1;   // row-major staging
+    constexpr bool WIDE = !AR && !BR;
+    const int m = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 4) {
-        const int kr = kk + (lane >> 4);
-        float av[4], bv[4];
+    for (int kq = 0; kq < BK; kq += 16) {
+        floatx4 af[4], bf[4];   // af[a][s], bf[b][s]
 #pragma unroll
-        for (int a = 0; a < 4; ++a) av[a] = As[lds_at<AR>(wi + a * 16 + (lane & 15), kr)];
+        for (int s = 0; s < 4; ++s) {
+            const int k = kq + 4 * s + g;
+            if (WIDE) {
+                const floatx4 ta = *reinterpret_cast<const floatx4*>(&As[k * PKM + wi + 4 * m]);
+                const floatx4 tb = *reinterpret_cast<const floatx4*>(&Bs[k * PKM + wj + 4 * m]);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) bv[b] = Bs[lds_at<BR>(wj + b * 16 + (lane & 15), kr)];
+                for (int x = 0; x < 4; ++x) {
+                    af[x][s] = ta[x];
+                    bf[x][s] = tb[x];
+                }
+            } else {
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+                for (int x = 0; x < 4; ++x) {
+                    af[x][s] = As[lds_at<AR>(wi + 16 * x + m, k)];
+                    bf[x][s] = Bs[lds_at<BR>(wj + 16 * x + m, k)];
+                }
+            }
+        }
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
     }
 }
 
@@ -268,12 +295,41 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
 
     main_loop<TA, TB, CHECK>(g, A, B, tr, lds, acc);
 
+    constexpr bool WIDE = TA == 1 && TB == 0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
-    const int64_t ib = tr.i0 + wi + 4 * (lane >> 4), jb = tr.j0 + wj + (lane & 15);
-    float* Cb = C + ib * g.ldc + jb;
+    const int g4 = 4 * (lane >> 4), m = lane & 15;
+    // element (a, b, v) of the accumulators is C[row(a, v)][col(b)] (see mma_stage)
+    auto row_of = [&](int a, int v) -> int64_t { return tr.i0 + (WIDE ? wi + 4 * (g4 + v) + a : wi + 16 * a + g4 + v); };
+    auto col_of = [&](int b) -> int64_t { return tr.j0 + (WIDE ? wj + 4 * m + b : wj + 16 * b + m); };
     const bool full = !CHECK && g.cmask == CMASK_FULL;
-    // epilogue: all C loads are issued before any store so their latency overlaps
+    const bool c16 = (((uintptr_t)C) % 16 == 0) && (g.ldc % 4 == 0);
+    if (WIDE && full && c16) {
+        // the lane's four columns 4 m .. 4 m + 3 are adjacent: 16-byte loads and stores
+        const int64_t j0 = col_of(0);
+        floatx4 cold[4][4];
+        if (g.beta != 0.0f) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    cold[a][v] = *reinterpret_cast<const floatx4*>(&C[row_of(a, v) * g.ldc + j0]);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                floatx4 r;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    r[b] = g.alpha * acc[a][b][v];
+                    if (g.beta != 0.0f) r[b] = r[b] + g.beta * cold[a][v][b];
+                }
+                *reinterpret_cast<floatx4*>(&C[row_of(a, v) * g.ldc + j0]) = r;
+            }
+        return;
+    }
+    // general epilogue: all C loads are issued before any store so their latency overlaps
     float cold[4][4][4];
     if (g.beta != 0.0f) {
 #pragma unroll
@@ -282,8 +338,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int64_t i = ib + a * 16 + v, j = jb + b * 16;
-                    cold[a][b][v] = (full || (i < g.M && j < g.N)) ? Cb[(int64_t)(a * 16 + v) * g.ldc + b * 16] : 0.0f;
+                    const int64_t i = row_of(a, v), j = col_of(b);
+                    cold[a][b][v] = (full || (i < g.M && j < g.N)) ? C[i * g.ldc + j] : 0.0f;
                 }
     }
 #pragma unroll
@@ -292,7 +348,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int64_t i = ib + a * 16 + v, j = jb + b * 16;
+                const int64_t i = row_of(a, v), j = col_of(b);
                 if (!full) {
                     if (i >= g.M || j >= g.N) continue;
                     if (g.cmask == CMASK_LOWER && i < j) continue;
@@ -300,7 +356,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
                 }
                 float r = g.alpha * acc[a][b][v];
                 if (g.beta != 0.0f) r = r + g.beta * cold[a][b][v];
-                Cb[(int64_t)(a * 16 + v) * g.ldc + b * 16] = r;
+                C[i * g.ldc + j] = r;
             }
 }
 
