@@ -238,6 +238,40 @@ int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols);
 int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
               int passes, int bits, void* workspace, void* stream);
 
+/* The p largest eigenpairs of a symmetric positive semi-definite H [n, n]
+ * (fp32): seeded subspace iteration (`iters` steps of (H + mu I) Q with
+ * shifted-CholeskyQR3 orthonormalisation, mu = 1e-3 x a power-iteration
+ * estimate of the largest eigenvalue), then Rayleigh-Ritz with an fp64
+ * cyclic Jacobi eigensolver.  evals [p] fp32 in descending order; evecs
+ * [n, p] fp32, column i the eigenvector of evals[i].  2 <= p <= min(n, 4096),
+ * p even; with p == n, iters = 0 gives the full eigendecomposition.
+ * *sweeps (host, may be NULL) receives the Jacobi sweep count.
+ * Synchronous: returns after the stream has finished (the Jacobi sweeps test
+ * convergence on the host).  IC_ERR_RANGE if the orthonormalisation loses
+ * positive definiteness (the caller falls back to the full-rank search).
+ * workspace: ic_lowrank_workspace_bytes(n, p).
+ * Replaces converter/greedy.py:293-366 (_lowrank_decompose: torch.svd_lowrank
+ * with q = N/2, then torch.linalg.eigh); the rank cut and its refusal gates
+ * stay with the caller, as in greedy.py:330-341. */
+int64_t ic_lowrank_workspace_bytes(int64_t n, int64_t p);
+int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed, float* evals,
+                    float* evecs, int* sweeps, void* workspace, void* stream);
+
+/* Low-rank greedy search: the greedy of ic_greedy with the cross terms taken
+ * from Hk = U_k diag(s_k) U_k^T (U [cols, >= k] pitch ldu, s [k]) and the
+ * exact diagonal H_jj, i.e. cross_j = err . Hk[:, j] - err_j H_jj; after
+ * every pass but the last, the proxy sum((err @ H) * err) with the full H
+ * ends the search once it is >= 0.99 x the previous pass's (from the second
+ * pass on).  *passes_run (host, may be NULL) receives the passes made.
+ * Synchronous (one host read of the proxy per pass).
+ * workspace: ic_greedy_lowrank_workspace_bytes(rows, cols, k).
+ * Replaces converter/greedy.py:369-479 (greedy_lowrank_triton) and its
+ * kernel 99-199 (_greedy_lowrank_kernel). */
+int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k);
+int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float* H, const float* U, int64_t ldu,
+                      const float* s, int64_t k, int64_t rows, int64_t cols, int passes, int bits,
+                      int* passes_run, void* workspace, void* stream);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Launch profiler (no reference counterpart; measurement support).  While

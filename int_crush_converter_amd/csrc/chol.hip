@@ -15,7 +15,7 @@
 // Flops: n^3/3 each for 2-4; all but the nb x nb factorisations are MFMA.
 #include <vector>
 
-#include "gemm.hpp"
+#include "chol.hpp"
 
 namespace icq {
 
@@ -431,10 +431,10 @@ __global__ void lower_to_upper_kernel(float* H, int64_t n, int64_t ld, int64_t s
     }
 }
 
-static int64_t dinv_floats(int64_t batch, int64_t n) { return batch * cdiv(n, NB) * NB * NB; }
+int64_t dinv_floats(int64_t batch, int64_t n) { return batch * cdiv(n, NB) * NB * NB; }
 
 // fp64 copy of the Dinv blocks: after the fp32 ones, 256-byte aligned.
-static double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
+double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
     const uintptr_t p = reinterpret_cast<uintptr_t>(dinv + dinv_floats(batch, n));
     return reinterpret_cast<double*>((p + 255) & ~(uintptr_t)255);
 }
@@ -450,7 +450,7 @@ static double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
 // super-block.
 constexpr int64_t SUPER_NB = 1024;
 
-static int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, double* dinv64, int* info,
+int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, double* dinv64, int* info,
                  hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
@@ -566,7 +566,7 @@ static int merge_pairs(const float* L, float* X, int64_t ld, int64_t r0, int64_t
     return IC_OK;
 }
 
-static int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const float* dinv,
+int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const float* dinv,
                  hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;

@@ -124,10 +124,12 @@ __global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const floa
 // One 64-column block of a greedy pass.  GL lanes per row: lane l keeps the
 // changes d_j' of the columns j' = l (mod GL) and their share of the
 // correction sum; the candidate scan runs redundantly on all GL lanes.
+// H is the matrix of the cross terms (the Hessian, or its low-rank
+// truncation) and hd its exact diagonal H_jj (null: the diagonal of H).
 __global__ __launch_bounds__(256) void greedy_block_kernel(float* err, float* Qf, const float* srow, const float* H,
-                                                           int64_t ldh, const float* cross, int64_t rows,
-                                                           int64_t cols, int64_t j0, int nb, float qmin,
-                                                           float qmax) {
+                                                           int64_t ldh, const float* hd, const float* cross,
+                                                           int64_t rows, int64_t cols, int64_t j0, int nb,
+                                                           float qmin, float qmax) {
     __shared__ float Hs[GB * GB];
     const int t = threadIdx.x;
     for (int idx = t; idx < nb * nb; idx += blockDim.x) {
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(256) void greedy_block_kernel(float* err, float* Qf
         }
         part = part + __shfl_xor(part, 1, GL);
         part = part + __shfl_xor(part, 2, GL);
-        const float hjj = Hs[jl * GB + jl];
+        const float hjj = hd ? hd[j0 + jl] : Hs[jl * GB + jl];
         float e = 0.0f, qo = 0.0f, c = 0.0f;
         if (rv) {
             e = err[r * cols + j];
@@ -184,6 +186,56 @@ __global__ void to_int8_kernel(const float* Qf, int64_t n, float qmin, float qma
 }
 
 static int egrid(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, 256), 65536)); }
+
+// hd[j] = H[j][j]
+__global__ void diag_kernel(const float* H, int64_t n, float* hd) {
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x)
+        hd[j] = H[j * n + j];
+}
+
+// US[i][c] = U[i][c] * s[c]   (n x k, U pitch ldu)
+__global__ void scale_cols_kernel(const float* U, int64_t ldu, const float* s, int64_t n, int64_t k, float* US) {
+    const int64_t total = n * k;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = idx / k, c = idx - i * k;
+        US[idx] = U[i * ldu + c] * s[c];
+    }
+}
+
+// part[b] = sum over the block's share of err * EH (fp64), EH = err @ H
+__global__ void proxy_partial_kernel(const float* err, const float* EH, int64_t n, double* part) {
+    __shared__ double red[4];
+    double acc = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        acc += (double)err[i] * (double)EH[i];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+constexpr int PROXY_PARTS = 1024;
+
+// One greedy pass over all column blocks: cross terms from Hc (the full
+// Hessian or its truncation), exact diagonal hd (null: Hc's).
+static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* cross,
+                       int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
+    for (int64_t j0 = 0; j0 < cols; j0 += GB) {
+        const int nb = (int)std::min<int64_t>(GB, cols - j0);
+        // cross[:, 0:nb] = err @ Hc[j0:j0+nb, :]^T
+        GemmArgs g{rows, nb, cols, 1.0f, 0.0f, err, cols, 0, Hc + j0 * cols, cols, 0, cross, GB, 0, 0, 1,
+                   CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
+        int rc = gemm_f32(g, st);
+        if (rc) return rc;
+        const int rpb = 256 / GL;
+        ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)), (double)rows * nb * 16);
+        hipLaunchKernelGGL(greedy_block_kernel, dim3((unsigned)cdiv(rows, rpb)), dim3(256), 0, st, err, Qf, srow,
+                           Hc, cols, hd, cross, rows, cols, j0, nb, qmin, qmax);
+        IC_CHECK_LAUNCH();
+    }
+    return IC_OK;
+}
 
 }  // namespace icq
 
@@ -254,20 +306,74 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
     hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
     IC_CHECK_LAUNCH();
     for (int p = 0; p < passes; ++p) {
-        for (int64_t j0 = 0; j0 < cols; j0 += GB) {
-            const int nb = (int)std::min<int64_t>(GB, cols - j0);
-            // cross[:, 0:nb] = err @ H[j0:j0+nb, :]^T
-            GemmArgs g{rows, nb, cols, 1.0f, 0.0f, err, cols, 0, H + j0 * cols, cols, 0, cross, GB, 0, 0, 1,
-                       CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
-            int rc = gemm_f32(g, st);
-            if (rc) return rc;
-            const int rpb = 256 / GL;
-            ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)), (double)rows * nb * 16);
-            hipLaunchKernelGGL(greedy_block_kernel, dim3((unsigned)cdiv(rows, rpb)), dim3(256), 0, st, err, Qf, srow,
-                               H, cols, cross, rows, cols, j0, nb, qmin, qmax);
-            IC_CHECK_LAUNCH();
-        }
+        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, rows, cols, qmin, qmax, st);
+        if (rc) return rc;
     }
+    hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k) {
+    return (3 * rows * cols + rows * GB + cols * cols + cols * std::max<int64_t>(k, 1) + cols) *
+               (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
+}
+
+extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float* H, const float* U,
+                                 int64_t ldu, const float* s, int64_t k, int64_t rows, int64_t cols, int passes,
+                                 int bits, int* passes_run, void* workspace, void* stream) {
+    IC_REQUIRE(W && Q && srow && H && workspace && (k == 0 || (U && s)), "ic_greedy_lowrank: null pointer");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_greedy_lowrank: bits must be 4 or 8");
+    IC_REQUIRE(k >= 0 && k <= cols && ldu >= k, "ic_greedy_lowrank: bad rank");
+    if (passes_run) *passes_run = 0;
+    if (rows == 0 || cols == 0 || passes <= 0) return IC_OK;
+    hipStream_t st = as_stream(stream);
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    float* err = reinterpret_cast<float*>(workspace);
+    float* Qf = err + rows * cols;
+    float* EH = Qf + rows * cols;
+    float* cross = EH + rows * cols;
+    float* Hk = cross + rows * GB;
+    float* US = Hk + cols * cols;
+    float* hd = US + cols * std::max<int64_t>(k, 1);
+    double* part = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(hd + cols) + 255) & ~(uintptr_t)255);
+    // Hk = U_k diag(s_k) U_k^T
+    if (k == 0) {
+        IC_CHECK_HIP(hipMemsetAsync(Hk, 0, cols * cols * sizeof(float), st));
+    } else {
+        hipLaunchKernelGGL(scale_cols_kernel, dim3(egrid(cols * k)), dim3(256), 0, st, U, ldu, s, cols, k, US);
+        IC_CHECK_LAUNCH();
+        GemmArgs g{cols, cols, k, 1.0f, 0.0f, US, k, 0, U, ldu, 0, Hk, cols, 0, 0, 1, CMASK_FULL, KR_FULL, 1,
+                   PT_GEMM_GREEDY};
+        int rc = gemm_f32(g, st);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(diag_kernel, dim3(egrid(cols)), dim3(256), 0, st, H, cols, hd);
+    IC_CHECK_LAUNCH();
+    hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
+    IC_CHECK_LAUNCH();
+    double prev = 0.0;
+    int done = 0;
+    for (int p = 0; p < passes; ++p) {
+        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, rows, cols, qmin, qmax, st);
+        if (rc) return rc;
+        done = p + 1;
+        if (p + 1 == passes) break;   // a stall test after the last pass changes nothing
+        // proxy = sum((err @ H) * err) with the full Hessian
+        GemmArgs g{rows, cols, cols, 1.0f, 0.0f, err, cols, 0, H, cols, 0, EH, cols, 0, 0, 0, CMASK_FULL, KR_FULL,
+                   1, PT_GEMM_GREEDY};
+        if ((rc = gemm_f32(g, st))) return rc;
+        hipLaunchKernelGGL(proxy_partial_kernel, dim3(PROXY_PARTS), dim3(256), 0, st, err, EH, rows * cols, part);
+        IC_CHECK_LAUNCH();
+        double parts[PROXY_PARTS];
+        IC_CHECK_HIP(hipMemcpyAsync(parts, part, sizeof(parts), hipMemcpyDeviceToHost, st));
+        IC_CHECK_HIP(hipStreamSynchronize(st));
+        double proxy = 0.0;
+        for (int i = 0; i < PROXY_PARTS; ++i) proxy += parts[i];
+        if (p > 0 && proxy >= prev * 0.99) break;   // STALL_THRESHOLD (converter/config.py:128)
+        prev = proxy;
+    }
+    if (passes_run) *passes_run = done;
     hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
     IC_CHECK_LAUNCH();
     return IC_OK;

@@ -4,9 +4,10 @@ coordinate descent (API of ``converter/ldlq.py`` and ``converter/greedy.py``).
 All array work runs in the HIP library: ``WᵀW`` and the trailing updates on
 the fp32 matrix cores, the damped inverse (``ic_hessian_inverse``), the
 per-element-scale sweep (``ic_ldlq_quantize``), iteration MSE / scale update
-kernels, least-squares row scales and the full-rank greedy search
-(``ic_greedy``).  Host code only makes the scalar control decisions of the
-reference (convergence, divergence revert).
+kernels, least-squares row scales and the greedy search (``greedy.py``:
+full-rank ``ic_greedy`` or the eigen-truncated ``ic_greedy_lowrank``).
+Host code only makes the scalar control decisions of the reference
+(convergence, divergence revert, the greedy backend choice).
 """
 
 from __future__ import annotations
@@ -17,6 +18,7 @@ import warnings
 import torch
 
 from . import _native as nat
+from . import greedy as _greedy
 from .config import LDLQ_MSE_DIVERGENCE, LDLQ_SCALE_MOMENTUM, CONVERGENCE_EPS, CONVERGENCE_IMPROVEMENT_THRESHOLD
 from .gptq import quant_error, SWEEP_MAX_BLOCK
 from .hessian import inverse_batch
@@ -133,12 +135,8 @@ def _ls_scales(Q, W) -> torch.Tensor:
 def greedy_local_search(W: torch.Tensor, Q: torch.Tensor, srow: torch.Tensor, H: torch.Tensor, passes: int,
                         bits: int) -> torch.Tensor:
     """Full-rank greedy coordinate descent on int8 codes (returns new int8 codes)."""
-    M, N = W.shape
-    Qo = Q.clone()
-    ws = nat.workspace(_lib().ic_greedy_workspace_bytes(M, N), W.device)
-    nat.check(_lib().ic_greedy(W.data_ptr(), Qo.data_ptr(), srow.data_ptr(), H.contiguous().data_ptr(), M, N,
-                               passes, bits, ws.data_ptr(), nat.stream()), "ic_greedy")
-    return Qo
+    qmin, qmax = (-128, 127) if bits == 8 else (-8, 7)
+    return _greedy.greedy_local_search(W, Q, srow, H, passes, qmin, qmax)
 
 
 def ldlq_quantize_layer(
@@ -150,10 +148,15 @@ def ldlq_quantize_layer(
     iterations: int = 1,
     greedy_passes: int = 0,
     rank_threshold: float = 0.01,
+    *,
+    greedy_backend: str = "auto",
 ) -> QuantizationResult:
     """LDLQ with per-element scales (reference ldlq.py:95-279).  Without a
-    Hessian, H = WᵀW / M (weight-only).  The greedy search always takes the
-    full-rank path (exact cross terms)."""
+    Hessian, H = WᵀW / M (weight-only).  The greedy search follows the
+    reference's GPU backend choice (ldlq.py:602-647): the low-rank search
+    when the Hessian's effective rank at ``rank_threshold`` is at most
+    min(512, 0.3 N), else the full-rank one; ``greedy_backend="full"``
+    always takes the exact full-rank search (the reference's CPU path)."""
     if int_bits not in (4, 8):
         raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
     if W.dim() != 2:
@@ -214,7 +217,9 @@ def ldlq_quantize_layer(
     method = "ldlq_hip"
     if greedy_passes > 0:
         gs = _ls_scales(Q, Wg)
-        Q = greedy_local_search(Wg, Q, gs, H_greedy, greedy_passes, int_bits)
+        qmin, qmax = (-128, 127) if int_bits == 8 else (-8, 7)
+        Q = _greedy.greedy_search(Wg, Q, gs, H_greedy, greedy_passes, qmin, qmax, rank_threshold=rank_threshold,
+                                  backend=greedy_backend)
     fs = _ls_scales(Q, Wg)
     mse, max_err = quant_error(Wg, Q, fs, None)
     return QuantizationResult(quantized_W=Q.to(out_dev), scales=fs.to(torch.float16).reshape(M, 1).to(out_dev),

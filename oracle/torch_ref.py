@@ -25,6 +25,11 @@ itself; see tests/test_oracle.py):
   * gptq_block / ldlq_loop: brute-force column-by-column float32 numpy loop
     on tiny shapes; golden vectors from the reference (tests/golden/).
   * greedy_pytorch: coordinate-wise optimality by brute force; golden vectors.
+  * lowrank_decompose: planted spectra (H = V diag(l) V^T with known l) for
+    the rank count and both gates; eigen-equation residual.
+  * greedy_lowrank_loop: with the full eigendecomposition (k = N) it is the
+    exact greedy_pytorch; golden vectors of the reference's own low-rank
+    kernel and its full-rank v2 path (Triton interpreter, tests/golden/).
   * iterative LDLQ / final least-squares scales: golden vectors.
 """
 
@@ -42,6 +47,11 @@ DIAG_MEAN_FLOOR = 1e-6
 ERR_CLAMP = 100.0
 HINV_DIAG_FLOOR = 1e-8
 SCALE_FLOOR = 1e-8
+EIGENVALUE_FLOOR = 1e-12      # config.py:124
+STALL_THRESHOLD = 0.99        # config.py:128
+LOWRANK_MAX_RANK_FRAC = 0.3   # config.py:133
+LOWRANK_MAX_K = 512           # config.py:137
+GREEDY_COL_BLOCK = 64         # config.py:177
 
 
 # --------------------------------------------------------------------------
@@ -573,6 +583,81 @@ def greedy_pytorch(W, Q, S, H, passes, qmin, qmax):
     return Q.clamp(qmin, qmax).to(torch.int8)
 
 
+def lowrank_decompose(H, rank_threshold=0.01, max_rank_frac=0.3):
+    """greedy.py:293-366, the eigh branch (_lowrank_decompose_eigh, 344-366):
+    eigenvalues in descending order, keep those > threshold * max; refuse
+    (used = False) when max < EIGENVALUE_FLOOR or k > max_rank_frac * N or
+    k > LOWRANK_MAX_K.  The reference tries torch.svd_lowrank first, whose
+    randomised result equals this one up to its approximation error."""
+    N = H.shape[0]
+    ev, V = torch.linalg.eigh(H)
+    ev = ev.flip(0)
+    V = V.flip(1)
+    mx = ev[0].item()
+    if mx < EIGENVALUE_FLOOR:
+        return None, None, 0, False
+    mask = ev > mx * rank_threshold
+    k = int(mask.sum().item())
+    if k > max_rank_frac * N or k > LOWRANK_MAX_K:
+        # the svd branch (greedy.py:323-341) counts among its q = min(max(N // 2,
+        # 64), N) singular values only, so a refused k it reports is <= q
+        return None, None, min(k, min(max(N // 2, 64), N)), False
+    return ev[mask], V[:, mask], k, True
+
+
+def greedy_lowrank_loop(W, Q, S, H, s_k, U_k, passes, qmin, qmax, col_block=GREEDY_COL_BLOCK):
+    """greedy.py:400-479 with the kernel of greedy.py:99-199, vectorised over
+    rows.  err_lr = err @ U_k is kept up to date by rank-1 updates; the cross
+    term of column j is err_lr @ (s_k * U_k[j]) - err_j * H_jj; candidates
+    are scanned in grid order with a strict < from 1e30 (first minimum wins,
+    q_old kept if no cost is below 1e30).  After every pass the proxy
+    sum((err @ H) * err) stops the search once it is >= 0.99 x the previous
+    pass's (from the second pass on).  ``Q`` is float32 and mutated."""
+    M, N = W.shape
+    hd = torch.diag(H)
+    err = Q * S - W
+    err_lr = err @ U_k
+    su = U_k * s_k.unsqueeze(0)
+    prev = float("inf")
+    for p in range(passes):
+        for j0 in range(0, N, col_block):
+            for j in range(j0, min(j0 + col_block, N)):
+                cross = err_lr @ su[j] - err[:, j] * hd[j]
+                e = err[:, j]
+                sj = S[:, j].clamp(min=1e-8)
+                qo = Q[:, j]
+                best = torch.full((M,), 1e30)
+                bq = qo.clone()
+                for g in range(qmin, qmax + 1):
+                    ne = e + (g - qo) * sj
+                    cost = ne * ne * hd[j] + 2.0 * ne * cross
+                    better = cost < best
+                    best = torch.where(better, cost, best)
+                    bq = torch.where(better, torch.full_like(bq, float(g)), bq)
+                bq = bq.clamp(qmin, qmax)
+                d = (bq - qo) * sj
+                Q[:, j] = bq
+                err[:, j] = e + d
+                err_lr += d.unsqueeze(1) * U_k[j].unsqueeze(0)
+        proxy = (err @ H * err).sum().item()
+        if p > 0 and proxy >= prev * STALL_THRESHOLD:
+            break
+        prev = proxy
+    return Q.clamp(qmin, qmax).to(torch.int8)
+
+
+def greedy_gpu(W, Q, S, H, passes, qmin, qmax, rank_threshold=0.01):
+    """ldlq.py:602-647 on a GPU: the low-rank search when the Hessian's
+    effective rank is small enough (greedy.py:369-479), else the full-rank
+    search (greedy.py:207-285, whose cross terms equal greedy_pytorch's in
+    exact arithmetic).  Returns (codes, k, used_lowrank)."""
+    s_k, U_k, k, used = lowrank_decompose(H, rank_threshold, LOWRANK_MAX_RANK_FRAC)
+    Qf = Q.clone().float().contiguous()
+    if not used:
+        return greedy_pytorch(W, Qf, S, H, passes, qmin, qmax), k, False
+    return greedy_lowrank_loop(W, Qf, S, H, s_k, U_k, passes, qmin, qmax), k, True
+
+
 def ls_scales(Q, W):
     """Per-row least-squares scale (ldlq.py:227-231, 262-265)."""
     Qf = Q.float()
@@ -582,8 +667,10 @@ def ls_scales(Q, W):
 
 
 def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=4,
-                        iterations=1, greedy_passes=0, rank_threshold=0.01):
-    """ldlq.py:95-279 (2-D / 3-D / weight-only Hessians, PyTorch greedy)."""
+                        iterations=1, greedy_passes=0, rank_threshold=0.01, greedy_device="cpu"):
+    """ldlq.py:95-279 (2-D / 3-D / weight-only Hessians).  The greedy search
+    is the one ldlq.py:602-647 picks for tensors on ``greedy_device``: "cpu"
+    the PyTorch search, "gpu" the low-rank / full-rank choice."""
     from types import SimpleNamespace
     W = W.float()
     M, N = W.shape
@@ -620,8 +707,11 @@ def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=
         Q = ldlq_single_pass(W, Hinv, flat, block_size, qmin, qmax)
     if greedy_passes > 0:
         gs = ls_scales(Q, W)
-        Q = greedy_pytorch(W, Q.clone().float().contiguous(), gs.expand(M, N), H,
-                           greedy_passes, qmin, qmax)
+        if greedy_device == "gpu":
+            Q, _, _ = greedy_gpu(W, Q, gs.expand(M, N), H, greedy_passes, qmin, qmax, rank_threshold)
+        else:
+            Q = greedy_pytorch(W, Q.clone().float().contiguous(), gs.expand(M, N), H,
+                               greedy_passes, qmin, qmax)
     fs = ls_scales(Q, W)
     d = Q.float() * fs.float()
     return SimpleNamespace(quantized_W=Q, scales=fs.to(torch.float16), zero_points=None,

@@ -34,6 +34,17 @@ def golden():
     return tensors, meta
 
 
+@pytest.fixture(scope="session")
+def golden_greedy_gpu():
+    """Vectors of the reference's GPU greedy backends (low-rank kernel and
+    full-rank v2), written by tests/golden/make_golden.py --greedy-gpu."""
+    from safetensors.torch import load_file
+    tensors = load_file(os.path.join(GOLDEN_DIR, "golden_greedy_gpu.safetensors"))
+    with open(os.path.join(GOLDEN_DIR, "golden_greedy_gpu.json")) as f:
+        meta = json.load(f)
+    return tensors, meta
+
+
 @pytest.fixture
 def one_thread():
     """Pin torch to one intra-op thread (MKL rounding depends on blocking)."""

@@ -10,6 +10,15 @@ because they depend on fp32 LAPACK/BLAS rounding or fp32 reduction order:
 GPTQ / LDLQ / greedy codes, LDLQ iteration decisions, clipping-ratio choices
 and a small end-to-end pipeline file.  Every case is a small seeded input;
 the outputs are stored as ``.safetensors`` next to this script.
+
+    PYTHONPATH=/root/reference python tests/golden/make_golden.py --greedy-gpu
+
+writes ``golden_greedy_gpu.safetensors`` / ``.json`` instead: the
+reference's GPU greedy backends (the low-rank kernel of
+converter/greedy.py:99-199, 369-479 and the full-rank v2 path of
+greedy.py:207-285), run on CPU tensors under Triton's interpreter
+(TRITON_INTERPRET=1), with torch's global RNG seeded before each call
+because ``torch.svd_lowrank`` draws its test matrix from it.
 """
 
 from __future__ import annotations
@@ -18,6 +27,10 @@ import json
 import os
 import sys
 import tempfile
+
+GREEDY_GPU = "--greedy-gpu" in sys.argv
+if GREEDY_GPU:
+    os.environ["TRITON_INTERPRET"] = "1"   # must precede the first triton import
 
 import torch
 from safetensors.torch import save_file, load_file
@@ -166,8 +179,74 @@ def pipeline_cases(out: dict, meta: dict) -> None:
             out[f"pipe_in/{k}"] = v
 
 
+def greedy_gpu_cases(out: dict, meta: dict) -> None:
+    """Reference GPU greedy backends on seeded inputs.  Each case starts from
+    RTN codes of W and the per-row least-squares scales of those codes (what
+    ldlq.py:222-231 hands to the greedy search)."""
+    from converter.greedy import (greedy_lowrank_triton, greedy_local_search_triton,
+                                  _lowrank_decompose)
+
+    def lowrank_h(n, r, seed, damp):
+        g = torch.Generator().manual_seed(seed)
+        s = torch.exp(torch.randn(n, generator=g))
+        X = torch.randn(r, n, generator=g) * s
+        H = X.T @ X / r
+        if damp:
+            H = H + damp * H.diagonal().mean() * torch.eye(n)
+        return H
+
+    cases = [
+        # name, M, N, bits, passes, H recipe (rank, damping) or None = full rank
+        ("lr_a", 32, 256, 4, 3, (20, 0.0)),
+        ("lr_b", 48, 192, 4, 5, (48, 0.01)),
+        ("lr_c", 16, 128, 8, 2, (16, 0.0)),
+        ("lr_d", 64, 320, 4, 4, (60, 0.01)),
+        ("fr_a", 32, 128, 4, 2, None),
+    ]
+    for i, (name, M, N, bits, passes, hr) in enumerate(cases):
+        qmin, qmax = (-128, 127) if bits == 8 else (-8, 7)
+        W = weights(M, N, 600 + i)
+        H = lognormal_hessian(N, 4 * N, 700 + i) if hr is None else lowrank_h(N, hr[0], 700 + i, hr[1])
+        s0 = (W.abs().amax(dim=1, keepdim=True) / (qmax)).clamp(min=1e-5)
+        Q0 = (W / s0).round().clamp(qmin, qmax)
+        num = (Q0 * W).sum(dim=1, keepdim=True)
+        den = (Q0 * Q0).sum(dim=1, keepdim=True).clamp(min=1e-8)
+        sls = (num / den).clamp(min=1e-5)
+        S2 = sls.expand(M, N).contiguous()
+        torch.manual_seed(800 + i)
+        s_k, U_k, k, used = _lowrank_decompose(H, rank_threshold=0.01, max_rank_frac=0.3)
+        torch.manual_seed(800 + i)
+        if hr is None:
+            q = greedy_local_search_triton(W, Q0.clone(), S2, H, passes, qmin, qmax)
+            used_lr = False
+        else:
+            q, k2, used_lr = greedy_lowrank_triton(W, Q0.clone(), S2, H, passes, qmin, qmax,
+                                                   rank_threshold=0.01)
+            assert k2 == k
+        out[f"{name}.W"] = W
+        out[f"{name}.H"] = H.contiguous()
+        out[f"{name}.q0"] = Q0.to(torch.int8)
+        out[f"{name}.s"] = sls
+        out[f"{name}.q"] = q
+        if used:
+            out[f"{name}.s_k"] = s_k.contiguous()
+            out[f"{name}.U_k"] = U_k.contiguous()
+        meta[name] = dict(kind="greedy_gpu", bits=bits, passes=passes, k=int(k),
+                          lowrank=bool(used_lr), rank_threshold=0.01)
+
+
 def main() -> None:
     torch.set_num_threads(1)
+    if GREEDY_GPU:
+        out: dict[str, torch.Tensor] = {}
+        meta: dict = {}
+        greedy_gpu_cases(out, meta)
+        out = {k: v.contiguous() for k, v in out.items()}
+        save_file(out, os.path.join(HERE, "golden_greedy_gpu.safetensors"))
+        with open(os.path.join(HERE, "golden_greedy_gpu.json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
+        print(f"wrote {len(out)} tensors, {len(meta)} cases: {meta}")
+        return
     out: dict[str, torch.Tensor] = {}
     meta: dict = {}
     gptq_cases(out, meta)

@@ -50,9 +50,10 @@ def test_ldlq_golden(gpu_dev, golden, case):
     H = t.get(f"{case}.H")
     with warnings.catch_warnings():
         warnings.simplefilter("ignore")
+        # the golden vectors come from the reference's CPU path: exact (full-rank) greedy
         r = ldlq_quantize_layer(t[f"{case}.W"].to(gpu_dev), hessian=None if H is None else H.to(gpu_dev),
                                 block_size=m["block"], damping=0.01, int_bits=m["bits"], iterations=m["iters"],
-                                greedy_passes=m["greedy"])
+                                greedy_passes=m["greedy"], greedy_backend="full")
     q = r.quantized_W.cpu()
     agree = (q == t[f"{case}.q"]).float().mean().item()
     assert agree >= 0.99, agree

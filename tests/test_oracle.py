@@ -349,3 +349,87 @@ def test_greedy_coordinatewise_optimal():
             Qt = Q.clone()
             Qt[r, j] = v
             assert proxy(Qt) >= base - 1e-6 * abs(base)
+
+
+# --------------------------------------------------------------------------
+# Low-rank greedy (converter/greedy.py:99-199, 293-479) and the GPU dispatch
+# --------------------------------------------------------------------------
+
+def _planted(n, evals, seed):
+    g = torch.Generator().manual_seed(seed)
+    V, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+    return ((V * torch.as_tensor(evals, dtype=torch.float64)) @ V.T).float(), V
+
+
+def test_lowrank_decompose_planted_spectrum():
+    """Known spectrum: the count of eigenvalues above threshold x max, both
+    refusal gates, and the eigen-equation for the returned pairs."""
+    n = 100
+    ev = torch.cat([torch.linspace(10.0, 0.2, 25), torch.full((75,), 0.05)])
+    H, _ = _planted(n, ev, 1)
+    s_k, U_k, k, used = ref.lowrank_decompose(H, 0.01)
+    assert used and k == 25
+    assert torch.allclose(s_k, ev[:25], rtol=1e-4)
+    r = H @ U_k - U_k * s_k
+    assert r.abs().max() < 1e-4 * 10.0
+    # threshold above the 0.05 floor but k > 0.3 N once the floor counts
+    _, _, k2, used2 = ref.lowrank_decompose(H, 0.004)
+    assert k2 == 64 and not used2   # reported within svd_lowrank's q = 64 values
+    # LOWRANK_MAX_K gate (k <= 0.3 N but > 512 needs N > 1706: check the rule directly)
+    assert ref.LOWRANK_MAX_K == 512
+    # near-zero matrix
+    _, _, k3, used3 = ref.lowrank_decompose(torch.zeros(8, 8), 0.01)
+    assert k3 == 0 and not used3
+
+
+def test_greedy_lowrank_loop_full_basis_is_exact_greedy():
+    """With every eigenpair (k = N) the low-rank cross term is the exact one,
+    so one pass equals the reference's PyTorch greedy."""
+    g = torch.Generator().manual_seed(3)
+    M, N = 24, 80
+    W = torch.randn(M, N, generator=g) * 0.02
+    H = lognormal_hessian(N, 200, 5).double()
+    ev, V = torch.linalg.eigh(H)
+    H = H.float()
+    S = (W.abs().amax(dim=1, keepdim=True) / 7).expand(M, N).contiguous()
+    Q0 = ref.rhaz(W / S).clamp(-8, 7)
+    a = ref.greedy_lowrank_loop(W, Q0.clone(), S, H, ev.float(), V.float(), 1, -8, 7)
+    b = ref.greedy_pytorch(W, Q0.clone(), S, H, 1, -8, 7)
+    assert (a == b).float().mean().item() >= 0.995
+
+
+@pytest.mark.parametrize("case", ["lr_a", "lr_b", "lr_c", "lr_d"])
+def test_greedy_lowrank_loop_golden(golden_greedy_gpu, case):
+    """Given the reference's own eigenpairs, the oracle's loop reproduces the
+    reference's low-rank kernel bit for bit (codes, stall decisions)."""
+    t, meta = golden_greedy_gpu
+    m = meta[case]
+    qmin, qmax = (-128, 127) if m["bits"] == 8 else (-8, 7)
+    W, H, Q0, s = t[f"{case}.W"], t[f"{case}.H"], t[f"{case}.q0"], t[f"{case}.s"]
+    M, N = W.shape
+    q = ref.greedy_lowrank_loop(W, Q0.float(), s.expand(M, N), H, t[f"{case}.s_k"], t[f"{case}.U_k"],
+                                m["passes"], qmin, qmax)
+    assert torch.equal(q, t[f"{case}.q"])
+
+
+@pytest.mark.parametrize("case", ["lr_a", "lr_b", "lr_c", "lr_d", "fr_a"])
+def test_greedy_gpu_golden(golden_greedy_gpu, case):
+    """The oracle's GPU dispatch against the reference's low-rank kernel and
+    full-rank v2 path: same rank decision and k, the same truncated Hessian
+    U_k diag(s_k) U_k^T up to fp32 noise, codes agree.  The reference's
+    svd_lowrank basis and eigh's differ by ~1e-6 relative, which the greedy
+    feedback turns into up to ~0.2 % of flipped codes (lr_b)."""
+    t, meta = golden_greedy_gpu
+    m = meta[case]
+    qmin, qmax = (-128, 127) if m["bits"] == 8 else (-8, 7)
+    W, H, Q0, s = t[f"{case}.W"], t[f"{case}.H"], t[f"{case}.q0"], t[f"{case}.s"]
+    M, N = W.shape
+    q, k, used = ref.greedy_gpu(W, Q0.float(), s.expand(M, N), H, m["passes"], qmin, qmax)
+    assert k == m["k"] and used == m["lowrank"]
+    agree = (q == t[f"{case}.q"]).float().mean().item()
+    assert agree >= 0.998, agree
+    if used:
+        s_k, U_k, _, _ = ref.lowrank_decompose(H)
+        Hk = (U_k * s_k) @ U_k.T
+        Hg = (t[f"{case}.U_k"] * t[f"{case}.s_k"]) @ t[f"{case}.U_k"].T
+        assert ((Hk - Hg).norm() / Hg.norm()).item() < 1e-5
