@@ -29,6 +29,7 @@ extern "C" {
 #define IC_ERR_ARG (-1)
 #define IC_ERR_HIP (-2)
 #define IC_ERR_RANGE (-3)
+#define IC_LOWRANK_REFUSED 1   /* ic_lowrank_eigs: rank certified too high */
 
 #define IC_DTYPE_F32 0
 #define IC_DTYPE_BF16 1
@@ -245,7 +246,11 @@ int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int6
  * cyclic Jacobi eigensolver.  evals [p] fp32 in descending order; evecs
  * [n, p] fp32, column i the eigenvector of evals[i].  2 <= p <= min(n, 4096),
  * p even; with p == n, iters = 0 gives the full eigendecomposition.
- * *sweeps (host, may be NULL) receives the Jacobi sweep count.
+ * refuse_rel > 0 enables an early exit: after min(iters, 2) steps, if
+ * Q^T H Q - refuse_rel ||H||_F I is positive definite (Cholesky), then H has
+ * at least p eigenvalues above refuse_rel x its largest (interlacing, and
+ * lambda_max <= ||H||_F), and the call returns IC_LOWRANK_REFUSED without
+ * eigenpairs.  *sweeps (host, may be NULL) receives the Jacobi sweep count.
  * Synchronous: returns after the stream has finished (the Jacobi sweeps test
  * convergence on the host).  IC_ERR_RANGE if the orthonormalisation loses
  * positive definiteness (the caller falls back to the full-rank search).
@@ -254,8 +259,8 @@ int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int6
  * with q = N/2, then torch.linalg.eigh); the rank cut and its refusal gates
  * stay with the caller, as in greedy.py:330-341. */
 int64_t ic_lowrank_workspace_bytes(int64_t n, int64_t p);
-int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed, float* evals,
-                    float* evecs, int* sweeps, void* workspace, void* stream);
+int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed, float refuse_rel,
+                    float* evals, float* evecs, int* sweeps, void* workspace, void* stream);
 
 /* Low-rank greedy search: the greedy of ic_greedy with the cross terms taken
  * from Hk = U_k diag(s_k) U_k^T (U [cols, >= k] pitch ldu, s [k]) and the

@@ -59,7 +59,8 @@ _SIGS = {
     "ic_greedy_workspace_bytes": (_i64, [_i64, _i64]),
     "ic_greedy": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "ic_lowrank_workspace_bytes": (_i64, [_i64, _i64]),
-    "ic_lowrank_eigs": (_i32, [_vp, _i64, _i64, _i32, _c.c_ulonglong, _vp, _vp, _c.POINTER(_i32), _vp, _vp]),
+    "ic_lowrank_eigs": (_i32, [_vp, _i64, _i64, _i32, _c.c_ulonglong, _f32, _vp, _vp, _c.POINTER(_i32), _vp,
+                               _vp]),
     "ic_greedy_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "ic_greedy_lowrank": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32,
                                  _c.POINTER(_i32), _vp, _vp]),

@@ -13,7 +13,7 @@
 namespace icq {
 
 constexpr int GB = 64;          // greedy column block
-constexpr int GL = 4;           // lanes per row in the greedy block kernel
+constexpr int GL = 16;          // lanes per row in the greedy block kernel
 
 __device__ __forceinline__ float nclampmin(float x, float lo) { return x != x ? x : (x < lo ? lo : x); }
 
@@ -121,62 +121,158 @@ __global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const floa
     }
 }
 
-// One 64-column block of a greedy pass.  GL lanes per row: lane l keeps the
-// changes d_j' of the columns j' = l (mod GL) and their share of the
-// correction sum; the candidate scan runs redundantly on all GL lanes.
-// H is the matrix of the cross terms (the Hessian, or its low-rank
-// truncation) and hd its exact diagonal H_jj (null: the diagonal of H).
+// One 64-column block of a greedy pass for GROWS rows.  The block's err,
+// codes and cross terms are staged in LDS (all loads in flight at once), so
+// the column loop touches no global memory; at the end the new err and codes
+// and the changes d (D [rows, 64]) are written back.  C holds, for the
+// block's columns, err @ H[:, j] as of the start of the block.
+// GL lanes per row: lane l keeps the changes d_j' of the columns
+// j' = l (mod GL) and their share of the correction sum, and scans the
+// candidates g = qmin + l + GL m in increasing order; the lanes' best
+// (cost, g) pairs are then merged, the lower g winning a tie, which is the
+// sequential first-minimum scan.  H is the matrix of the cross terms (the
+// Hessian, or its low-rank truncation) and hd its exact diagonal H_jj (null:
+// the diagonal of H).
+constexpr int GROWS = 256 / GL;
+constexpr int GSTAGE = GROWS * GB / 256;   // staged elements per thread
+
+// Exchanges inside a 16-lane DPP row (one greedy row): rotations by 8 and 4
+// within the row, then quad swaps; after the four steps of a commutative,
+// associative merge every lane of the row holds the merge of all 16.
+template <int CTRL>
+__device__ __forceinline__ float rdpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124, DPP_QXOR2 = 0x4E, DPP_QXOR1 = 0xB1;
+static_assert(GL == 16, "the row exchanges assume one greedy row per 16-lane DPP row");
+
+__device__ __forceinline__ float row_sum16(float v) {
+    v = v + rdpp<DPP_ROR8>(v);
+    v = v + rdpp<DPP_ROR4>(v);
+    v = v + rdpp<DPP_QXOR2>(v);
+    return v + rdpp<DPP_QXOR1>(v);
+}
+
+// Merge (cost, g) pairs: the lower cost, on a tie the lower g (branch-free).
+template <int CTRL>
+__device__ __forceinline__ void argmin_step(float& best, float& bq) {
+    const float ob = rdpp<CTRL>(best), oq = rdpp<CTRL>(bq);
+    const bool take = (ob < best) | ((ob == best) & (oq < bq));
+    best = take ? ob : best;
+    bq = take ? oq : bq;
+}
+
+template <int NG>
 __global__ __launch_bounds__(256) void greedy_block_kernel(float* err, float* Qf, const float* srow, const float* H,
-                                                           int64_t ldh, const float* hd, const float* cross,
-                                                           int64_t rows, int64_t cols, int64_t j0, int nb,
-                                                           float qmin, float qmax) {
-    __shared__ float Hs[GB * GB];
+                                                           int64_t ldh, const float* hd, const float* C,
+                                                           int64_t ldc, float* D, int64_t rows, int64_t cols,
+                                                           int64_t j0, int nb, float qmin, float qmax) {
+    constexpr int HP = GB + 1;                 // pitch of the transposed H tile
+    __shared__ float HsT[GB * HP];             // HsT[j][j'] = H[j0 + j'][j0 + j]
+    __shared__ float Es[GROWS][GB + 1];
+    __shared__ float Qs[GROWS][GB + 1];
+    __shared__ float Cs[GROWS][GB + 1];
+    __shared__ float hds[GB];
     const int t = threadIdx.x;
-    for (int idx = t; idx < nb * nb; idx += blockDim.x) {
-        int a = idx / nb, b = idx - a * nb;
-        Hs[a * GB + b] = H[(j0 + a) * ldh + j0 + b];
+    const int64_t r0 = (int64_t)blockIdx.x * GROWS;
+    if (t < GB) hds[t] = t < nb ? (hd ? hd[j0 + t] : H[(j0 + t) * ldh + j0 + t]) : 1.0f;
+    {
+        float e[GSTAGE], q[GSTAGE], c[GSTAGE], h[GB * GB / 256];
+#pragma unroll
+        for (int k = 0; k < GSTAGE; ++k) {
+            const int idx = t + 256 * k, rr = idx / GB, cc = idx % GB;
+            const int64_t r = r0 + rr;
+            const bool ok = r < rows && cc < nb;
+            e[k] = ok ? err[r * cols + j0 + cc] : 0.0f;
+            q[k] = ok ? Qf[r * cols + j0 + cc] : 0.0f;
+            c[k] = ok ? C[r * ldc + cc] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < GB * GB / 256; ++k) {
+            const int idx = t + 256 * k, a = idx / GB, b = idx % GB;
+            h[k] = (a < nb && b < nb) ? H[(j0 + a) * ldh + j0 + b] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < GSTAGE; ++k) {
+            const int idx = t + 256 * k, rr = idx / GB, cc = idx % GB;
+            Es[rr][cc] = e[k];
+            Qs[rr][cc] = q[k];
+            Cs[rr][cc] = c[k];
+        }
+#pragma unroll
+        for (int k = 0; k < GB * GB / 256; ++k) {
+            const int idx = t + 256 * k, a = idx / GB, b = idx % GB;
+            HsT[b * HP + a] = h[k];
+        }
     }
     __syncthreads();
-    const int lane = t % GL;
-    const int64_t r = (int64_t)blockIdx.x * (blockDim.x / GL) + t / GL;
-    const bool rv = r < rows;
-    const float s = rv ? srow[r] : 1.0f;
+    const int lane = t % GL, rr = t / GL;
+    const int64_t r = r0 + rr;
+    const float s = r < rows ? srow[r] : 1.0f;
     float dl[GB / GL];
 #pragma unroll
     for (int i = 0; i < GB / GL; ++i) dl[i] = 0.0f;
+    // operands of column 0; each iteration fetches those of the next column
+    float hv[GB / GL];
+#pragma unroll
+    for (int i = 0; i < GB / GL; ++i) hv[i] = HsT[i * GL + lane];
+    float e = Es[rr][0], qo = Qs[rr][0], cc0 = Cs[rr][0], hjj = hds[0];
     for (int jl = 0; jl < nb; ++jl) {
-        const int64_t j = j0 + jl;
+        const int jn = jl + 1 < GB ? jl + 1 : jl;
+        float hn[GB / GL];
+#pragma unroll
+        for (int i = 0; i < GB / GL; ++i) hn[i] = HsT[jn * HP + i * GL + lane];
+        const float en = Es[rr][jn], qn = Qs[rr][jn], cn = Cs[rr][jn], hjn = hds[jn];
         // correction: sum over earlier block columns of d_j' * H[j', j]
+        // (branch-free; columns j' >= j add +0)
         float part = 0.0f;
 #pragma unroll
         for (int i = 0; i < GB / GL; ++i) {
-            const int jp = i * GL + lane;
-            if (jp < jl) part = part + dl[i] * Hs[jp * GB + jl];
+            const float pr = dl[i] * hv[i];
+            part = part + (i * GL + lane < jl ? pr : 0.0f);
         }
-        part = part + __shfl_xor(part, 1, GL);
-        part = part + __shfl_xor(part, 2, GL);
-        const float hjj = hd ? hd[j0 + jl] : Hs[jl * GB + jl];
-        float e = 0.0f, qo = 0.0f, c = 0.0f;
-        if (rv) {
-            e = err[r * cols + j];
-            qo = Qf[r * cols + j];
-            c = (cross[r * GB + jl] + part) - e * hjj;
-        }
+        part = row_sum16(part);
+        const float c = (cc0 + part) - e * hjj;
         float best = 1e30f, bq = qo;
-        for (float g = qmin; g <= qmax; g += 1.0f) {
+#pragma unroll
+        for (int m = 0; m < NG / GL; ++m) {
+            const float g = qmin + (float)(m * GL + lane);
             const float ne = e + (g - qo) * s;
             const float cost = ne * ne * hjj + 2.0f * ne * c;
-            if (cost < best) { best = cost; bq = g; }
+            const bool better = cost < best;
+            best = better ? cost : best;
+            bq = better ? g : bq;
         }
+        argmin_step<DPP_ROR8>(best, bq);
+        argmin_step<DPP_ROR4>(best, bq);
+        argmin_step<DPP_QXOR2>(best, bq);
+        argmin_step<DPP_QXOR1>(best, bq);
         bq = clampf(bq, qmin, qmax);
         const float d = (bq - qo) * s;
-        if (rv && lane == 0) {
-            Qf[r * cols + j] = bq;
-            err[r * cols + j] = e + d;
+        if (lane == 0) {   // column jl is not read again in this block; Cs[.][jl] now keeps d
+            Qs[rr][jl] = bq;
+            Es[rr][jl] = e + d;
+            Cs[rr][jl] = d;
         }
 #pragma unroll
-        for (int i = 0; i < GB / GL; ++i)
-            if (i * GL + lane == jl) dl[i] = d;
+        for (int i = 0; i < GB / GL; ++i) dl[i] = i * GL + lane == jl ? d : dl[i];
+#pragma unroll
+        for (int i = 0; i < GB / GL; ++i) hv[i] = hn[i];
+        e = en;
+        qo = qn;
+        cc0 = cn;
+        hjj = hjn;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < GSTAGE; ++k) {
+        const int idx = t + 256 * k, rr2 = idx / GB, c2 = idx % GB;
+        const int64_t r2 = r0 + rr2;
+        if (r2 < rows && c2 < nb) {
+            err[r2 * cols + j0 + c2] = Es[rr2][c2];
+            Qf[r2 * cols + j0 + c2] = Qs[rr2][c2];
+            D[r2 * GB + c2] = Cs[rr2][c2];
+        }
     }
 }
 
@@ -217,22 +313,44 @@ __global__ void proxy_partial_kernel(const float* err, const float* EH, int64_t 
 
 constexpr int PROXY_PARTS = 1024;
 
-// One greedy pass over all column blocks: cross terms from Hc (the full
-// Hessian or its truncation), exact diagonal hd (null: Hc's).
-static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* cross,
-                       int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
-    for (int64_t j0 = 0; j0 < cols; j0 += GB) {
-        const int nb = (int)std::min<int64_t>(GB, cols - j0);
-        // cross[:, 0:nb] = err @ Hc[j0:j0+nb, :]^T
-        GemmArgs g{rows, nb, cols, 1.0f, 0.0f, err, cols, 0, Hc + j0 * cols, cols, 0, cross, GB, 0, 0, 1,
-                   CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
+// Two-level pass.  Columns go in super-blocks of GSB: one GEMM gives the
+// cross terms of a whole super-block, C = err @ Hc[sb, :]^T (K = cols, full
+// tiles), and after each 64-column block its changes D update the rest of
+// the super-block, C[:, rest] += D @ Hc[blk, rest] (K = 64).  Cross terms of
+// later super-blocks come from the updated err.  Same sums as one GEMM per
+// block over all of err, in another fp32 order.
+constexpr int64_t GSB = 512;
+
+static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* C,
+                       float* D, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
+    for (int64_t s0 = 0; s0 < cols; s0 += GSB) {
+        const int64_t sw = std::min<int64_t>(GSB, cols - s0);
+        GemmArgs g{rows, sw, cols, 1.0f, 0.0f, err, cols, 0, Hc + s0 * cols, cols, 0, C, GSB, 0, 0, 1, CMASK_FULL,
+                   KR_FULL, 1, PT_GEMM_GREEDY};
         int rc = gemm_f32(g, st);
         if (rc) return rc;
-        const int rpb = 256 / GL;
-        ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)), (double)rows * nb * 16);
-        hipLaunchKernelGGL(greedy_block_kernel, dim3((unsigned)cdiv(rows, rpb)), dim3(256), 0, st, err, Qf, srow,
-                           Hc, cols, hd, cross, rows, cols, j0, nb, qmin, qmax);
-        IC_CHECK_LAUNCH();
+        for (int64_t j0 = s0; j0 < s0 + sw; j0 += GB) {
+            const int nb = (int)std::min<int64_t>(GB, s0 + sw - j0);
+            {
+                ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)),
+                                     (double)rows * nb * 20);
+                if (qmax - qmin + 1.0f == 16.0f)
+                    hipLaunchKernelGGL(greedy_block_kernel<16>, dim3((unsigned)cdiv(rows, GROWS)), dim3(256), 0, st,
+                                       err, Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin,
+                                       qmax);
+                else
+                    hipLaunchKernelGGL(greedy_block_kernel<256>, dim3((unsigned)cdiv(rows, GROWS)), dim3(256), 0, st,
+                                       err, Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin,
+                                       qmax);
+                IC_CHECK_LAUNCH();
+            }
+            const int64_t rest = s0 + sw - (j0 + nb);
+            if (rest > 0) {
+                GemmArgs u{rows, rest, nb, 1.0f, 1.0f, D, GB, 0, Hc + j0 * cols + j0 + nb, cols, 0,
+                           C + (j0 + nb - s0), GSB, 0, 0, 0, CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
+                if ((rc = gemm_f32(u, st))) return rc;
+            }
+        }
     }
     return IC_OK;
 }
@@ -290,7 +408,7 @@ extern "C" int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64
 }
 
 extern "C" int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols) {
-    return (2 * rows * cols + rows * GB) * (int64_t)sizeof(float) + 256;
+    return (2 * rows * cols + rows * (GSB + GB)) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
@@ -306,7 +424,7 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
     hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
     IC_CHECK_LAUNCH();
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, cross + rows * GSB, rows, cols, qmin, qmax, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
@@ -315,7 +433,7 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
 }
 
 extern "C" int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k) {
-    return (3 * rows * cols + rows * GB + cols * cols + cols * std::max<int64_t>(k, 1) + cols) *
+    return (3 * rows * cols + rows * (GSB + GB) + cols * cols + cols * std::max<int64_t>(k, 1) + cols) *
                (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
 }
 
@@ -333,7 +451,8 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     float* Qf = err + rows * cols;
     float* EH = Qf + rows * cols;
     float* cross = EH + rows * cols;
-    float* Hk = cross + rows * GB;
+    float* D = cross + rows * GSB;
+    float* Hk = D + rows * GB;
     float* US = Hk + cols * cols;
     float* hd = US + cols * std::max<int64_t>(k, 1);
     double* part = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(hd + cols) + 255) & ~(uintptr_t)255);
@@ -355,7 +474,7 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     double prev = 0.0;
     int done = 0;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, D, rows, cols, qmin, qmax, st);
         if (rc) return rc;
         done = p + 1;
         if (p + 1 == passes) break;   // a stall test after the last pass changes nothing

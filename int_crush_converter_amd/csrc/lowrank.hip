@@ -77,6 +77,32 @@ __global__ void normalize_kernel(const float* y, float* x, int64_t n, double rel
     if (threadIdx.x == 0) out[0] = rel * nrm;
 }
 
+// part[b] = sum of squares over the block's grid-stride share (fp64)
+__global__ void sumsq_kernel(const float* x, int64_t n, double* part) {
+    __shared__ double red[4];
+    double acc = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const double v = x[i];
+        acc += v * v;
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// T[i][i] -= rel * sqrt(sum part[0..n))  (one work-group; fixed order)
+__global__ void sub_frob_diag_kernel(float* T, int64_t p, const double* part, int n, double rel) {
+    __shared__ double shift;
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int i = 0; i < n; ++i) acc += part[i];
+        shift = rel * sqrt(acc);
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < p; i += blockDim.x) T[i * p + i] = (float)((double)T[i * p + i] - shift);
+}
+
 // Y += mu * Q  (mu read from device memory)
 __global__ void axpy_dev_kernel(float* Y, const float* Q, int64_t n, const double* mu) {
     const float m = (float)mu[0];
@@ -264,12 +290,13 @@ static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Workspace carve-up (every piece 256-byte aligned).
 struct LrWork {
-    float *Y, *Q, *G, *X, *dinv, *T, *Vs, *x, *y;
+    float *Y, *Q, *G, *X, *dinv, *T, *Vs, *x, *y, *Gp;
     double *dinv64, *A0, *A1, *V0, *V1, *part, *scal;
     int* info;
 };
 
 constexpr int LR_PARTS = 1024;   // partial sums of the reductions
+constexpr int GRAM_SPLIT = 8;    // K chunks of the p x p Gram matrices (K = n)
 
 static size_t lr_layout(int64_t n, int64_t p, char* base, LrWork* w) {
     size_t off = 0;
@@ -287,6 +314,7 @@ static size_t lr_layout(int64_t n, int64_t p, char* base, LrWork* w) {
     t.T = (float*)take(pp4);
     t.Vs = (float*)take(pp4);
     t.x = (float*)take((size_t)n * 4);
+    t.Gp = (float*)take((size_t)GRAM_SPLIT * pp4);
     t.y = (float*)take((size_t)n * 4);
     t.dinv = (float*)take((size_t)dinv_floats(1, p) * 4 + (size_t)dinv_floats(1, p) * 8 + 512);
     t.A0 = (double*)take(pp8);
@@ -303,11 +331,42 @@ static size_t lr_layout(int64_t n, int64_t p, char* base, LrWork* w) {
     return off + 256;
 }
 
+// G[i][j] = sum over the S partials (fixed order), lower triangle
+__global__ void sum_partials_kernel(const float* Gp, int S, int64_t pp, float* G) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pp; i += (int64_t)gridDim.x * blockDim.x) {
+        float acc = Gp[i];
+        for (int s = 1; s < S; ++s) acc = acc + Gp[s * pp + i];
+        G[i] = acc;
+    }
+}
+
+// G = A^T B (p x p, part `cmask`; A, B [n, p]) with K = n cut into up to
+// GRAM_SPLIT chunks of a batched GEMM: the p x p output alone has too few
+// tiles to fill the chip.
+static int gram(const float* A, const float* B, int64_t n, int64_t p, float* G, const LrWork& w, int cmask,
+                hipStream_t st) {
+    const int64_t kc = cdiv(cdiv(n, GRAM_SPLIT), 32) * 32;
+    const int S = (int)cdiv(n, kc);
+    const int64_t pp = p * p;
+    int rc;
+    if (S > 1) {
+        GemmArgs g{p, p, kc, 1.0f, 0.0f, A, p, kc * p, B, p, kc * p, w.Gp, p, pp, 1, 0, cmask, KR_FULL, S - 1,
+                   PT_OTHER};
+        if ((rc = gemm_f32(g, st))) return rc;
+    }
+    const int64_t k0 = (S - 1) * kc;
+    GemmArgs g{p, p, n - k0, 1.0f, 0.0f, A + k0 * p, p, 0, B + k0 * p, p, 0, w.Gp + (S - 1) * pp, p, 0, 1, 0, cmask,
+               KR_FULL, 1, PT_OTHER};
+    if ((rc = gemm_f32(g, st))) return rc;
+    hipLaunchKernelGGL(sum_partials_kernel, dim3(egrid_lr(pp)), dim3(256), 0, st, w.Gp, S, pp, G);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
 // One CholeskyQR pass: Q = Y R^-1 with R^T R = Y^T Y + shift_rel tr(Y^T Y) I.
 static int cholqr_pass(const float* Y, float* Q, int64_t n, int64_t p, float shift_rel, const LrWork& w,
                        hipStream_t st) {
-    GemmArgs g{p, p, n, 1.0f, 0.0f, Y, p, 0, Y, p, 0, w.G, p, 0, 1, 0, CMASK_LOWER, KR_FULL, 1, PT_OTHER};
-    int rc = gemm_f32(g, st);
+    int rc = gram(Y, Y, n, p, w.G, w, CMASK_LOWER, st);
     if (rc) return rc;
     if (shift_rel > 0.0f) {
         hipLaunchKernelGGL(shift_diag_kernel, dim3(1), dim3(256), 0, st, w.G, p, shift_rel);
@@ -322,9 +381,19 @@ static int cholqr_pass(const float* Y, float* Q, int64_t n, int64_t p, float shi
     return gemm_f32(q, st);
 }
 
-// Shifted CholeskyQR3 of Y (overwritten) into Q.
-static int orth(float* Y, float* Q, int64_t n, int64_t p, const LrWork& w, hipStream_t st) {
-    int rc = cholqr_pass(Y, Q, n, p, 1e-5f, w, st);
+// Shifted CholeskyQR3 of Y (overwritten) into Q; `well_conditioned` (a
+// Gaussian start, cond ~ (1 + sqrt(p/n)) / (1 - sqrt(p/n))) skips the
+// shifted pass: plain CholeskyQR2.
+static int orth(float* Y, float* Q, int64_t n, int64_t p, const LrWork& w, hipStream_t st,
+                bool well_conditioned = false) {
+    int rc;
+    if (well_conditioned) {
+        rc = cholqr_pass(Y, Q, n, p, 0.0f, w, st);
+        if (!rc) rc = cholqr_pass(Q, Y, n, p, 0.0f, w, st);
+        if (!rc) IC_CHECK_HIP(hipMemcpyAsync(Q, Y, (size_t)n * p * sizeof(float), hipMemcpyDeviceToDevice, st));
+        return rc;
+    }
+    rc = cholqr_pass(Y, Q, n, p, 1e-5f, w, st);
     if (!rc) rc = cholqr_pass(Q, Y, n, p, 0.0f, w, st);
     if (!rc) rc = cholqr_pass(Y, Q, n, p, 0.0f, w, st);
     return rc;
@@ -341,16 +410,18 @@ extern "C" int64_t ic_lowrank_workspace_bytes(int64_t n, int64_t p) {
     return (int64_t)lr_layout(n, p, nullptr, nullptr);
 }
 
-extern "C" int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed, float* evals,
-                               float* evecs, int* sweeps_out, void* workspace, void* stream) {
+extern "C" int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed,
+                               float refuse_rel, float* evals, float* evecs, int* sweeps_out, void* workspace,
+                               void* stream) {
     IC_REQUIRE(H && evals && evecs && workspace, "ic_lowrank_eigs: null pointer");
     IC_REQUIRE(n >= 2 && p >= 2 && p <= n && p % 2 == 0, "ic_lowrank_eigs: need 2 <= p <= n, p even");
     IC_REQUIRE(p <= 4096 && iters >= 0 && iters <= 64, "ic_lowrank_eigs: p <= 4096, 0 <= iters <= 64");
+    IC_REQUIRE(refuse_rel >= 0.0f, "ic_lowrank_eigs: refuse_rel must be >= 0");
     hipStream_t st = as_stream(stream);
     LrWork w;
     char* base = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(workspace) + 255) & ~(uintptr_t)255);
     lr_layout(n, p, base, &w);
-    IC_CHECK_HIP(hipMemsetAsync(w.info, 0, sizeof(int), st));
+    IC_CHECK_HIP(hipMemsetAsync(w.info, 0, 2 * sizeof(int), st));
     const int64_t np = n * p;
     // mu = 1e-3 lambda_max estimate (power iteration from a seeded vector)
     constexpr int POWER_STEPS = 16;
@@ -366,23 +437,39 @@ extern "C" int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, 
     }
     hipLaunchKernelGGL(randn_kernel, dim3(egrid_lr(np)), dim3(256), 0, st, w.Y, np, (uint64_t)seed);
     IC_CHECK_LAUNCH();
-    int rc = orth(w.Y, w.Q, n, p, w, st);
+    int rc = orth(w.Y, w.Q, n, p, w, st, /*well_conditioned=*/true);
     if (rc) return rc;
-    for (int it = 0; it < iters; ++it) {
-        // Y = H Q + mu Q
+    const int test_it = refuse_rel > 0.0f ? std::min(iters, 2) : -1;
+    for (int it = 0;; ++it) {
+        // Y = H Q
         GemmArgs g{n, p, n, 1.0f, 0.0f, H, n, 0, w.Q, p, 0, w.Y, p, 0, 0, 0, CMASK_FULL, KR_FULL, 1, PT_OTHER};
         if ((rc = gemm_f32(g, st))) return rc;
+        if (it == test_it) {
+            // Refusal certificate: if T - refuse_rel ||H||_F I is positive definite,
+            // every Ritz value exceeds refuse_rel ||H||_F >= refuse_rel lambda_max,
+            // and by interlacing so do the p largest eigenvalues of H.
+            if ((rc = gram(w.Q, w.Y, n, p, w.T, w, CMASK_LOWER, st))) return rc;
+            hipLaunchKernelGGL(sumsq_kernel, dim3(LR_PARTS), dim3(256), 0, st, H, n * n, w.part);
+            IC_CHECK_LAUNCH();
+            hipLaunchKernelGGL(sub_frob_diag_kernel, dim3(1), dim3(256), 0, st, w.T, p, w.part, LR_PARTS,
+                               (double)refuse_rel);
+            IC_CHECK_LAUNCH();
+            if ((rc = potrf(w.T, 1, p, p, p * p, w.dinv, w.dinv64, w.info + 1, st))) return rc;
+            int pd_info = 0;
+            IC_CHECK_HIP(hipMemcpyAsync(&pd_info, w.info + 1, sizeof(int), hipMemcpyDeviceToHost, st));
+            IC_CHECK_HIP(hipStreamSynchronize(st));
+            if (pd_info == 0) {
+                if (sweeps_out) *sweeps_out = 0;
+                return IC_LOWRANK_REFUSED;
+            }
+        }
+        if (it == iters) break;
         hipLaunchKernelGGL(axpy_dev_kernel, dim3(egrid_lr(np)), dim3(256), 0, st, w.Y, w.Q, np, w.scal);
         IC_CHECK_LAUNCH();
         if ((rc = orth(w.Y, w.Q, n, p, w, st))) return rc;
     }
     // Rayleigh-Ritz: T = Q^T (H Q)
-    {
-        GemmArgs g{n, p, n, 1.0f, 0.0f, H, n, 0, w.Q, p, 0, w.Y, p, 0, 0, 0, CMASK_FULL, KR_FULL, 1, PT_OTHER};
-        if ((rc = gemm_f32(g, st))) return rc;
-        GemmArgs t{p, p, n, 1.0f, 0.0f, w.Q, p, 0, w.Y, p, 0, w.T, p, 0, 1, 0, CMASK_FULL, KR_FULL, 1, PT_OTHER};
-        if ((rc = gemm_f32(t, st))) return rc;
-    }
+    if ((rc = gram(w.Q, w.Y, n, p, w.T, w, CMASK_FULL, st))) return rc;
     int info = 0;
     IC_CHECK_HIP(hipMemcpyAsync(&info, w.info, sizeof(int), hipMemcpyDeviceToHost, st));
     IC_CHECK_HIP(hipStreamSynchronize(st));

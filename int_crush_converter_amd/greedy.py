@@ -104,8 +104,11 @@ def lowrank_decompose(H, rank_threshold: float = 0.01, max_rank_frac: float = LO
     evecs = torch.empty(N, p, dtype=torch.float32, device=Hg.device)
     ws = nat.workspace(_lib().ic_lowrank_workspace_bytes(N, p), Hg.device)
     sweeps = nat._c.c_int(0)
-    rc = _lib().ic_lowrank_eigs(Hg.data_ptr(), N, p, iters, LOWRANK_SEED, evals.data_ptr(), evecs.data_ptr(),
-                                nat._c.byref(sweeps), ws.data_ptr(), nat.stream())
+    # p > k_cap: a certificate that p eigenvalues exceed the cut settles the refusal early
+    rc = _lib().ic_lowrank_eigs(Hg.data_ptr(), N, p, iters, LOWRANK_SEED, float(rank_threshold), evals.data_ptr(),
+                                evecs.data_ptr(), nat._c.byref(sweeps), ws.data_ptr(), nat.stream())
+    if rc == 1:    # IC_LOWRANK_REFUSED: at least p > k_cap eigenvalues above the cut
+        return None, None, p, False
     if rc == -3:   # orthonormalisation failed: no low-rank basis (the reference's eigh failure path)
         logger.warning("Greedy: low-rank decomposition failed (%s); full-rank search",
                        _lib().ic_last_error().decode(errors="replace"))

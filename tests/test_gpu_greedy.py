@@ -44,8 +44,8 @@ def _eigs(H, p, iters, gpu_dev, seed=7):
     U = torch.empty(n, p, device=gpu_dev)
     ws = nat.workspace(lib.ic_lowrank_workspace_bytes(n, p), gpu_dev)
     sw = nat._c.c_int(0)
-    nat.check(lib.ic_lowrank_eigs(Hg.data_ptr(), n, p, iters, seed, ev.data_ptr(), U.data_ptr(), nat._c.byref(sw),
-                                  ws.data_ptr(), nat.stream()), "ic_lowrank_eigs")
+    nat.check(lib.ic_lowrank_eigs(Hg.data_ptr(), n, p, iters, seed, 0.0, ev.data_ptr(), U.data_ptr(),
+                                  nat._c.byref(sw), ws.data_ptr(), nat.stream()), "ic_lowrank_eigs")
     return ev.cpu(), U.cpu(), sw.value
 
 
