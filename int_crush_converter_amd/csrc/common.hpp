@@ -77,6 +77,33 @@ __device__ __forceinline__ float div_rn(float a, float b, float y, bool b_ok, bo
     return __builtin_fmaf(r, y, q0);
 }
 
+// div_rn for code where the domain test must not branch per lane: the fast
+// path runs for every lane, and only if some lane of the wave is outside
+// its domain (a wave-uniform test) do those lanes take the IEEE division.
+// Same result as div_rn.
+__device__ __forceinline__ float div_rn_wave(float a, float b, float y, bool b_ok) {
+    const float q0 = a * y;
+    const float r = __builtin_fmaf(-q0, b, a);
+    float q = __builtin_fmaf(r, y, q0);
+    const float aa = fabsf(a);
+    const bool ok = b_ok && ((aa >= 0x1p-60f && aa < 0x1p61f) || aa == 0.0f);
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!ok) != 0, 0)) q = ok ? q : a / b;
+    return q;
+}
+
+// rhaz with fewer operations: trunc(x + copysign(0.5, x)).  For x >= 0
+// this is floor(x + 0.5) (x + 0.5 > 0); for x < 0 ceil(x - 0.5).  The one
+// difference is x = -0.0, which gives -0.0 instead of +0.0: an equal code
+// (same int8, same products and sums), so no result can tell them apart.
+__device__ __forceinline__ float rhaz_trunc(float x) {
+    return truncf(x + __builtin_copysignf(0.5f, x));
+}
+
+// clampf as a median of three (NaN still propagates).
+__device__ __forceinline__ float clampf_med3(float x, float lo, float hi) {
+    return x != x ? x : __builtin_amdgcn_fmed3f(x, lo, hi);
+}
+
 // Round half to even (torch.round).
 __device__ __forceinline__ float rhte(float x) { return rintf(x); }
 

@@ -7,15 +7,17 @@
 // update all later columns at once, W[:, end:] -= E @ Hinv[blk, end:].
 //
 // Sweep kernel: the nb x nb Hinv block is staged in LDS once per work-group
-// of 16 rows, one row per wave (16 waves: 4 per SIMD, which hide each
-// other's latency).  Lane l holds columns l and l + 64 of its row.  At step
-// j the owner's value is read into a scalar register (readlane) and every
-// lane quantises it, so the error is already uniform and the division's
-// domain test is a scalar branch; every lane then applies its updates in
-// column order, so every w_k sees exactly the reference's sequence of fp32
-// roundings (bit-exact given the same Hinv).  The next Hinv row and the next
-// pivot data are fetched while the current column is processed.  A lane
-// owns the codes and errors of its two columns and stores them at the end.
+// of 16 rows; a wave holds two rows, 32 lanes each (8 waves: 2 per SIMD,
+// which hide each other's latency).  Lane p of a row slot holds columns
+// p + 32 r (r < 4) of its row.  At step j both owners' values are read into
+// scalar registers (readlane) and each row slot takes its own, so the 32
+// lanes of a row quantise the same value and the error is uniform per row;
+// every
+// lane then applies its updates in column order, so every w_k sees exactly
+// the reference's sequence of fp32 roundings (bit-exact given the same
+// Hinv).  The next Hinv row and the next pivot data are fetched while the
+// current column is processed.  A lane owns the codes and errors of its
+// four columns and stores them at the end.
 //
 // The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
 // order differs from MKL's sgemm, which is the only non-bit-exact step.
@@ -24,9 +26,12 @@
 namespace icq {
 
 constexpr int SW_NB = 128;     // max columns per sweep block
-constexpr int SW_R = SW_NB / 64;   // columns (registers) per lane
-constexpr int SW_ROWS = 16;    // rows (waves) per work-group
-constexpr int SW_THREADS = SW_ROWS * 64;
+constexpr int SW_HALF = 32;    // lanes per row (two rows per wave)
+constexpr int SW_RPW = 64 / SW_HALF;    // rows per wave
+constexpr int SW_R = SW_NB / SW_HALF;   // columns (registers) per lane
+constexpr int SW_WAVES = 8;
+constexpr int SW_ROWS = SW_RPW * SW_WAVES;   // rows per work-group
+constexpr int SW_THREADS = SW_WAVES * 64;
 
 enum SweepMode : int {
     SWEEP_GPTQ = 0,   // per-row scale (+zp), err / Hinv_jj, clamp +-100, NaN -> 0
@@ -90,27 +95,31 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         dok[j] = div_b_ok(d) ? 1 : 0;
     }
     __syncthreads();
-    const int64_t row = (int64_t)blockIdx.x * SW_ROWS + wave;
-    if (row >= a.rows) return;
+    const int half = lane / SW_HALF, p = lane & (SW_HALF - 1);   // half: the wave's row slot
+    const int64_t row0 = (int64_t)blockIdx.x * SW_ROWS + SW_RPW * wave;
+    if (row0 >= a.rows) return;                          // all rows of the wave past the end
+    const int64_t row = row0 + half;
+    const bool rv = row < a.rows;
+    const int64_t rrow = rv ? row : row0;                // a row that exists (results not stored)
 
     float w[R];
-    const float* wrow = a.W + row * a.ldw + col0;
+    const float* wrow = a.W + rrow * a.ldw + col0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int c = r * 64 + lane;
+        const int c = r * SW_HALF + p;
         w[r] = c < nb ? wrow[c] : 0.0f;
     }
     float s_row = 1.0f, z_row = 0.0f;
     float sc[MODE == SWEEP_LDLQ ? R : 1];
     float scr[MODE == SWEEP_LDLQ ? R : 1];
     if (MODE == SWEEP_GPTQ) {
-        s_row = a.s[row];
-        if (a.zp) z_row = a.zp[row];
+        s_row = a.s[rrow];
+        if (a.zp) z_row = a.zp[rrow];
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int c = r * 64 + lane;
-            float v = c < nb ? a.s[row * a.lds + col0 + c] : 1.0f;
+            const int c = r * SW_HALF + p;
+            float v = c < nb ? a.s[rrow * a.lds + col0 + c] : 1.0f;
             v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
             sc[r] = v;
             scr[r] = 1.0f / v;
@@ -120,44 +129,45 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const bool has_zp = a.zp != nullptr;
     const bool srow_ok = div_b_ok(s_row);
 
-    // Column j = 64 r0 + o lives in register r0 of lane o.  Updates are
-    // unconditional on registers r >= r0: the register of column j on lanes
-    // <= o is already quantised and never read again, so those updates are
-    // dead values.
+    // Column j = 32 r0 + o lives in register r0 of lane o of each row slot.
+    // Updates are unconditional on registers r >= r0: the register of
+    // column j on lanes <= o is already quantised and never read again, so
+    // those updates are dead values.
     float qv[R], ev[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) qv[r] = ev[r] = 0.0f;
     float h[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) h[r] = Hs[r * 64 + lane];
+    for (int r = 0; r < R; ++r) h[r] = Hs[r * SW_HALF + p];
     float hd = hjj[0], dvj = dinv[0];
     bool dkj = dok[0] != 0;
 #pragma unroll
     for (int r0 = 0; r0 < R; ++r0) {
-        if (r0 * 64 >= nb) break;
+        if (r0 * SW_HALF >= nb) break;
 #pragma nounroll
-        for (int o = 0; o < 64; ++o) {
-            const int j = r0 * 64 + o;
+        for (int o = 0; o < SW_HALF; ++o) {
+            const int j = r0 * SW_HALF + o;
             if (j >= nb) break;
             const int jn = j + 1 < SW_NB ? j + 1 : j;
             float hn[R];
 #pragma unroll
-            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * 64 + lane];
+            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * SW_HALF + p];
             const float hdn = hjj[jn], dvn = dinv[jn];
             const bool dkn = dok[jn] != 0;
-            const float x = rdlanef(w[r0], o);   // the owner's value, in every lane
+            // the owner's value of this lane's row
+            const float x = half ? rdlanef(w[r0], SW_HALF + o) : rdlanef(w[r0], o);
             float q, e;
             if (MODE == SWEEP_GPTQ) {
-                float y = div_rn(x, s_row, s_rrow, srow_ok);
+                float y = div_rn_wave(x, s_row, s_rrow, srow_ok);
                 if (has_zp) y = y + z_row;
-                q = clampf(rhaz(y), a.qmin, a.qmax);
+                q = clampf_med3(rhaz_trunc(y), a.qmin, a.qmax);
                 const float deq = has_zp ? (q - z_row) * s_row : q * s_row;
-                e = div_rn(x - deq, hd, dvj, dkj);
-                e = clampf(e, -100.0f, 100.0f);
-                if (e != e) e = 0.0f;
+                e = div_rn_wave(x - deq, hd, dvj, dkj);
+                e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
             } else {
-                const float s_el = rdlanef(sc[r0], o), s_rc = rdlanef(scr[r0], o);
-                q = clampf(rhaz(div_rn(x, s_el, s_rc, div_b_ok(s_el))), a.qmin, a.qmax);
+                const float s_el = half ? rdlanef(sc[r0], SW_HALF + o) : rdlanef(sc[r0], o);
+                const float s_rc = half ? rdlanef(scr[r0], SW_HALF + o) : rdlanef(scr[r0], o);
+                q = clampf_med3(rhaz_trunc(div_rn_wave(x, s_el, s_rc, div_b_ok(s_el))), a.qmin, a.qmax);
                 // sign-flip correction (inert for positive scales)
                 const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
                                                   : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
@@ -169,7 +179,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 q = clampf(q, a.qmin, a.qmax);
                 e = (x - q * s_el) * dvj;
             }
-            const bool own = lane == o;
+            const bool own = p == o;
             qv[r0] = own ? q : qv[r0];
             ev[r0] = own ? e : ev[r0];
 #pragma unroll
@@ -182,12 +192,14 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         }
     }
     // codes and errors of the lane's own columns (coalesced per row)
+    if (rv) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int c = r * 64 + lane;
-        if (c < nb) {
-            a.Q[row * a.ldq + col0 + c] = (int8_t)(int)qv[r];
-            a.E[(int64_t)g * a.eg + row * a.lde + c] = ev[r];
+        for (int r = 0; r < R; ++r) {
+            const int c = r * SW_HALF + p;
+            if (c < nb) {
+                a.Q[row * a.ldq + col0 + c] = (int8_t)(int)qv[r];
+                a.E[(int64_t)g * a.eg + row * a.lde + c] = ev[r];
+            }
         }
     }
 }
