@@ -40,6 +40,10 @@ WORKLOADS = {
     "rtn_int8_asym_clip5_rot64_4096x4096": ("rtn8", 4096, 4096, {}),
     "rtn_int4_rot256_64x256": ("rtn4", 64, 256, {}),
     "ldlq_int4_it2_greedy5_rot256_4096x4096": ("ldlq", 4096, 4096, {}),
+    # one block of configs[4]'s 40-block DiT sweep: four layers, block-diagonal Hessians
+    "gptq_int4_rot256_dit_block": ("dit", 0, 0, {"layers": [("qkv", 12288, 4096), ("proj", 4096, 4096),
+                                                            ("mlp_up", 16384, 4096), ("mlp_down", 4096, 16384)],
+                                                 "samples": 4096}),
 }
 DEFAULT = "gptq_int4_rot256_4096x12288"
 
@@ -48,10 +52,28 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def block_hessian(X):
+    """[in/256, 256, 256] block-diagonal Hessian X_b^T X_b / n of X [n, in]."""
+    import torch
+    n, d = X.shape
+    Xb = X.reshape(n, d // 256, 256).permute(1, 0, 2).contiguous()       # [g, n, 256]
+    return torch.bmm(Xb.transpose(1, 2).contiguous(), Xb) / n
+
+
 def make_inputs(kind, M, N, extra, seed=0):
     import torch
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(seed)
+    if kind == "dit":
+        Ws, Hs = [], []
+        for _, out_f, in_f in extra["layers"]:
+            Ws.append((torch.randn(out_f, in_f, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+            s = torch.exp(torch.randn(in_f, generator=g, device=dev))
+            X = torch.randn(extra["samples"], in_f, generator=g, device=dev) * s
+            Hs.append(block_hessian(X))
+            del X
+        torch.cuda.synchronize()
+        return Ws, Hs
     W = (torch.randn(M, N, generator=g, device=dev) * 0.02)
     H = None
     if kind == "rtn8":
@@ -78,6 +100,9 @@ def make_inputs(kind, M, N, extra, seed=0):
 
 def gpu_step(kind, W, H):
     from int_crush_converter_amd import layer as L
+    if kind == "dit":
+        outs = [gpu_step("gptq", Wl, Hl) for Wl, Hl in zip(W, H)]
+        return outs[-1]
     if kind == "gptq":
         W_work, _ = L.prepare_weights(W, 256)
         codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=256, block_size=128, damping=0.01, int_bits=4,
@@ -106,6 +131,8 @@ def cpu_step(kind, W, H):
     """The reference's CPU algorithm (oracle restatement) on the same layer."""
     import torch
     from oracle import torch_ref as ref
+    if kind == "dit":   # bounded sample: the block's first layer (qkv)
+        return cpu_step("gptq", W[0], H[0])
     Wf = W.float()
     Wf = Wf.masked_fill(Wf.abs() > 1000.0, 0.0)
     if kind == "gptq":
@@ -224,7 +251,7 @@ def main():
         torch.cuda.synchronize()
         prof = nat.profile_read()
         nat.profile_enable(False)
-    weights = M * N
+    weights = M * N if kind != "dit" else sum(o * i for _, o, i in extra["layers"])
     value = weights / (ms * 1e-3) / 1e6
     log(f"[bench] {ms:.3f} ms/step, {value:.1f} Mweights/s, mse {out.mse:.3e}")
 
@@ -243,6 +270,8 @@ def main():
         "data": "synthetic (seeded N(0,0.02^2) bf16 weights; H = X^T X / n, X rows N(0, diag(s^2)), "
                 "s ~ LogNormal(0,1)); random-init, no checkpoint",
         "config": {"workload": args.workload, "out_features": M, "in_features": N,
+                   **({"layers": [f"{n} {o}x{i}" for n, o, i in extra["layers"]], "hessian": "block-diagonal 256"}
+                      if kind == "dit" else {}),
                    "layers_per_s": round(1e3 / ms, 4), "rot_size": 256 if kind != "rtn8" else 64,
                    "block": 128, "damping": 0.01},
     }
@@ -258,14 +287,18 @@ def main():
     if not args.no_cpu_baseline:
         threads = torch.get_num_threads()
         log(f"[bench] CPU baseline (oracle, {threads} threads): 1 layer")
-        Wc = W.cpu()
-        Hc = H.cpu() if H is not None else None
+        if kind == "dit":
+            Wc, Hc = [w.cpu() for w in W], [h.cpu() for h in H]
+            sample_w, sample = extra["layers"][0][1] * extra["layers"][0][2], "the qkv layer of one DiT block"
+        else:
+            Wc, Hc = W.cpu(), (H.cpu() if H is not None else None)
+            sample_w, sample = weights, f"1 layer of {args.workload}"
         c0 = time.perf_counter()
         cpu_step(kind, Wc, Hc)
         c1 = time.perf_counter()
-        result["cpu_baseline"] = {"value": round(weights / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
+        result["cpu_baseline"] = {"value": round(sample_w / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
                                   "cores": threads, "kind": "port",
-                                  "sample": f"1 layer of {args.workload} ({c1 - c0:.1f} s), torch CPU oracle "
+                                  "sample": f"{sample} ({c1 - c0:.1f} s), torch CPU oracle "
                                             "restating the reference's CPU path"}
         log(f"[bench] CPU {c1 - c0:.2f} s")
     print(json.dumps(result), flush=True)

@@ -7,17 +7,17 @@
 // update all later columns at once, W[:, end:] -= E @ Hinv[blk, end:].
 //
 // Sweep kernel: the nb x nb Hinv block is staged in LDS once per work-group
-// of 16 rows; a wave holds two rows, 32 lanes each (8 waves: 2 per SIMD,
-// which hide each other's latency).  Lane p of a row slot holds columns
-// p + 32 r (r < 4) of its row.  At step j both owners' values are read into
-// scalar registers (readlane) and each row slot takes its own, so the 32
+// of 8 waves; a wave holds 64 / LPR rows of LPR lanes each (LPR = 32 for
+// a single matrix, 8 for batched groups).  Lane p of a row slot holds
+// columns p + LPR r of its row.  At step j the owners' values are read into
+// scalar registers (readlane) and each row slot takes its own, so the LPR
 // lanes of a row quantise the same value and the error is uniform per row;
 // every
 // lane then applies its updates in column order, so every w_k sees exactly
 // the reference's sequence of fp32 roundings (bit-exact given the same
 // Hinv).  The next Hinv row and the next pivot data are fetched while the
 // current column is processed.  A lane owns the codes and errors of its
-// four columns and stores them at the end.
+// columns and stores them at the end.
 //
 // The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
 // order differs from MKL's sgemm, which is the only non-bit-exact step.
@@ -26,12 +26,18 @@
 namespace icq {
 
 constexpr int SW_NB = 128;     // max columns per sweep block
-constexpr int SW_HALF = 32;    // lanes per row (two rows per wave)
-constexpr int SW_RPW = 64 / SW_HALF;    // rows per wave
-constexpr int SW_R = SW_NB / SW_HALF;   // columns (registers) per lane
 constexpr int SW_WAVES = 8;
-constexpr int SW_ROWS = SW_RPW * SW_WAVES;   // rows per work-group
 constexpr int SW_THREADS = SW_WAVES * 64;
+// Lanes per row: 32 (two rows per wave) when there are few rows, so that
+// enough waves share each SIMD to hide the column chain's latency; 8 (eight
+// rows per wave) when the launch has many waves per SIMD anyway (batched
+// block-diagonal groups), so that the chain's instructions serve more rows.
+constexpr int SW_LPR_LATENCY = 32, SW_LPR_THROUGHPUT = 8;
+// rows x groups from which the throughput variant still gives each SIMD
+// about 4 waves
+constexpr int64_t SW_THROUGHPUT_ROWS = 32768;
+
+template <int LPR> constexpr int sw_rows() { return (64 / LPR) * SW_WAVES; }   // rows per work-group
 
 enum SweepMode : int {
     SWEEP_GPTQ = 0,   // per-row scale (+zp), err / Hinv_jj, clamp +-100, NaN -> 0
@@ -58,9 +64,24 @@ __device__ __forceinline__ float rdlanef(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-template <int MODE>
+// The value v of lane (k LPR + o) of the wave, for the lane's row slot k.
+template <int LPR>
+__device__ __forceinline__ float row_owner(float v, int o, int slot) {
+    float x = rdlanef(v, o);
+#pragma unroll
+    for (int k = 1; k < 64 / LPR; ++k) {
+        const float y = rdlanef(v, k * LPR + o);
+        x = slot == k ? y : x;
+    }
+    return x;
+}
+
+template <int MODE, int LPR>
 __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
-    constexpr int R = SW_R;
+    constexpr int SW_HALF = LPR;
+    constexpr int SW_RPW = 64 / LPR;
+    constexpr int SW_ROWS = SW_RPW * SW_WAVES;
+    constexpr int R = SW_NB / LPR;
     __shared__ float Hs[SW_NB * SW_NB];
     __shared__ float hjj[SW_NB];              // Hinv_jj
     __shared__ float dinv[SW_NB];             // GPTQ: RN(1 / Hinv_jj); LDLQ: 1 / max(Hinv_jj, 1e-8)
@@ -129,7 +150,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const bool has_zp = a.zp != nullptr;
     const bool srow_ok = div_b_ok(s_row);
 
-    // Column j = 32 r0 + o lives in register r0 of lane o of each row slot.
+    // Column j = LPR r0 + o lives in register r0 of lane o of each row slot.
     // Updates are unconditional on registers r >= r0: the register of
     // column j on lanes <= o is already quantised and never read again, so
     // those updates are dead values.
@@ -155,7 +176,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
             const float hdn = hjj[jn], dvn = dinv[jn];
             const bool dkn = dok[jn] != 0;
             // the owner's value of this lane's row
-            const float x = half ? rdlanef(w[r0], SW_HALF + o) : rdlanef(w[r0], o);
+            const float x = row_owner<LPR>(w[r0], o, half);
             float q, e;
             if (MODE == SWEEP_GPTQ) {
                 float y = div_rn_wave(x, s_row, s_rrow, srow_ok);
@@ -165,8 +186,8 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
                 e = div_rn_wave(x - deq, hd, dvj, dkj);
                 e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
             } else {
-                const float s_el = half ? rdlanef(sc[r0], SW_HALF + o) : rdlanef(sc[r0], o);
-                const float s_rc = half ? rdlanef(scr[r0], SW_HALF + o) : rdlanef(scr[r0], o);
+                const float s_el = row_owner<LPR>(sc[r0], o, half);
+                const float s_rc = row_owner<LPR>(scr[r0], o, half);
                 q = clampf_med3(rhaz_trunc(div_rn_wave(x, s_el, s_rc, div_b_ok(s_el))), a.qmin, a.qmax);
                 // sign-flip correction (inert for positive scales)
                 const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
@@ -206,15 +227,20 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 
 static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
-    const int64_t wgs = cdiv(a.rows, SW_ROWS);
+    const bool wide = a.rows * groups >= SW_THROUGHPUT_ROWS;
+    const int64_t wgs = cdiv(a.rows, wide ? sw_rows<SW_LPR_THROUGHPUT>() : sw_rows<SW_LPR_LATENCY>());
     ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
                  (double)groups * (a.rows * a.nb * 9.0 + 4.0 * a.nb * a.nb));
-    if (a.mode == SWEEP_GPTQ)
-        hipLaunchKernelGGL((sweep_kernel<SWEEP_GPTQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
-                           st, a);
-    else
-        hipLaunchKernelGGL((sweep_kernel<SWEEP_LDLQ>), dim3((unsigned)wgs, (unsigned)groups), dim3(SW_THREADS), 0,
-                           st, a);
+    const dim3 grid((unsigned)wgs, (unsigned)groups);
+#define ICQ_SWEEP(M, L) hipLaunchKernelGGL((sweep_kernel<M, L>), grid, dim3(SW_THREADS), 0, st, a)
+    if (a.mode == SWEEP_GPTQ) {
+        if (wide) ICQ_SWEEP(SWEEP_GPTQ, SW_LPR_THROUGHPUT);
+        else ICQ_SWEEP(SWEEP_GPTQ, SW_LPR_LATENCY);
+    } else {
+        if (wide) ICQ_SWEEP(SWEEP_LDLQ, SW_LPR_THROUGHPUT);
+        else ICQ_SWEEP(SWEEP_LDLQ, SW_LPR_LATENCY);
+    }
+#undef ICQ_SWEEP
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

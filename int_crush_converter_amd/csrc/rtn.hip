@@ -281,24 +281,49 @@ __global__ void unpack_int4_kernel(const uint8_t* __restrict__ src, int64_t rows
 
 constexpr int QERR_BLOCKS = 1024;
 
+// Work-group b takes rows b, b + gridDim.x, ...; per row the scale and
+// zero-point are read once and the thread walks the row 4 elements at a
+// time (16-byte W loads, 4-byte code loads) when the row is 16-byte aligned,
+// else one element at a time.  Each thread's partial sums run in a fixed
+// order, so the result does not depend on timing.
 __global__ __launch_bounds__(256) void quant_error_partial(const float* __restrict__ W, int64_t rows, int64_t cols,
                                                            int64_t ld, const int8_t* __restrict__ codes, int64_t ld_q,
                                                            const void* __restrict__ scale, int scale_kind,
                                                            const int8_t* __restrict__ zp, double* part_sum,
                                                            float* part_max) {
-    const int64_t total = rows * cols;
     double acc = 0.0;
     float mx = 0.0f;
-    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
-         g += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = g / cols, c = g - r * cols;
-        float s = scale_kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[r])
-                                  : reinterpret_cast<const float*>(scale)[r];
-        float q = (float)codes[r * ld_q + c];
-        float d = zp ? (q - (float)zp[r]) * s : q * s;
-        float e = W[r * ld + c] - d;
-        acc += (double)e * (double)e;
-        mx = nmax(mx, fabsf(e));
+    const bool vec = (cols % 4 == 0) && (ld % 4 == 0) && (ld_q % 4 == 0) && ((uintptr_t)W % 16 == 0) &&
+                     ((uintptr_t)codes % 4 == 0);
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float s = scale_kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[r])
+                                        : reinterpret_cast<const float*>(scale)[r];
+        const float z = zp ? (float)zp[r] : 0.0f;
+        const float* wr = W + r * ld;
+        const int8_t* qr = codes + r * ld_q;
+        if (vec) {
+            for (int64_t c = 4 * (int64_t)threadIdx.x; c < cols; c += 4 * (int64_t)blockDim.x) {
+                const float4 wv = *reinterpret_cast<const float4*>(wr + c);
+                const char4 qv = *reinterpret_cast<const char4*>(qr + c);
+                const float q[4] = {(float)qv.x, (float)qv.y, (float)qv.z, (float)qv.w};
+                const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float d = zp ? (q[u] - z) * s : q[u] * s;
+                    const float e = w[u] - d;
+                    acc += (double)e * (double)e;
+                    mx = nmax(mx, fabsf(e));
+                }
+            }
+        } else {
+            for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+                const float q = (float)qr[c];
+                const float d = zp ? (q - z) * s : q * s;
+                const float e = wr[c] - d;
+                acc += (double)e * (double)e;
+                mx = nmax(mx, fabsf(e));
+            }
+        }
     }
     __shared__ double ss[4];
     __shared__ float sm[4];

@@ -181,6 +181,44 @@ def test_sweep_single_block_bit_exact(gpu_dev, bits, asym, B, N):
     assert torch.equal(Qg, Q)
 
 
+@pytest.mark.parametrize("bits,asym", [(4, False), (8, True)])
+def test_sweep_batched_groups_bit_exact(gpu_dev, bits, asym):
+    """16 block-diagonal groups of one 128-column block over 2048 rows
+    (rows x groups = 32768: the kernel variant with 8 lanes per row): every
+    group's codes equal the CPU sweep's given the same per-group Hinv."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(40 + bits)
+    M, G, bs = 2048, 16, 128
+    W = torch.randn(M, G * bs, generator=g) * 0.02
+    W[5] = 0.0
+    Hinv = torch.stack([ref.prepare_hinv(lognormal_hessian(bs, 3 * bs, 50 + k), 0.01) for k in range(G)])
+    s, z = ref.gptq_row_params(W, bits, asym)
+    qlim = (-8, 7) if bits == 4 else (-128, 127)
+    Q = torch.zeros(M, G * bs, dtype=torch.int8)
+    for k in range(G):
+        Qk = torch.zeros(M, bs, dtype=torch.int8)
+        ref.gptq_block(W[:, k * bs:(k + 1) * bs].clone(), Qk, s, Hinv[k], 0, bs, bs, *qlim, z)
+        Q[:, k * bs:(k + 1) * bs] = Qk
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, bits, asym)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev).contiguous(), s32, z32, bits, bs, G).cpu()
+    assert torch.equal(Qg, Q)
+
+
+def test_ldlq_sweep_many_rows_bit_exact(gpu_dev):
+    """LDLQ sweep with per-element scales over 32768 rows (8 lanes per row)."""
+    from int_crush_converter_amd.ldlq import _single_pass
+    g = torch.Generator().manual_seed(77)
+    M, N = 32768, 128
+    W = torch.randn(M, N, generator=g) * 0.02
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 3 * N, 13), 0.01)
+    S = (W.abs().amax(dim=1, keepdim=True) / 7.0).clamp(min=1e-5).expand(M, N)
+    S = S * (1 + 0.1 * torch.rand(M, N, generator=g))
+    want = ref.ldlq_single_pass(W, Hinv, S.reshape(-1).clone(), N, -8, 7)
+    got = _single_pass(W.to(gpu_dev), Hinv.to(gpu_dev), S.contiguous().to(gpu_dev), N, 4).cpu()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("B", [16, 64, 128])
 def test_sweep_multi_block_close(gpu_dev, B):
     from int_crush_converter_amd.gptq import row_params, sweep

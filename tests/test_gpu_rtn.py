@@ -183,10 +183,11 @@ def test_pack_validation_vector_path(gpu_dev, bad, err):
     assert torch.equal(pack_int4(v.to(gpu_dev)).cpu(), ref.pack_int4(v))
 
 
-def test_quant_error_matches_oracle(gpu_dev):
-    import ctypes
+@pytest.mark.parametrize("M,N", [(64, 512), (37, 201)])
+def test_quant_error_matches_oracle(gpu_dev, M, N):
+    """16-byte row path (N % 4 == 0) and the element path (ragged N)."""
     from int_crush_converter_amd import _native as nat
-    W = ref.rotate_weights(_w(64, 512, 2), 256)
+    W = _w(M, N, 2)
     s, z = ref.scales_int4_asym(W, W.shape[1])
     q = ref.quant_int4_asym(W, s, z, W.shape[1])
     d = (q.float() - z.float()) * s.float()
@@ -196,7 +197,7 @@ def test_quant_error_matches_oracle(gpu_dev):
     out_s = torch.zeros(1, dtype=torch.float64, device=gpu_dev)
     out_m = torch.zeros(1, dtype=torch.float32, device=gpu_dev)
     ws = torch.empty(nat.lib().ic_quant_error_workspace_bytes(), dtype=torch.uint8, device=gpu_dev)
-    nat.check(nat.lib().ic_quant_error(Wg.data_ptr(), 64, 512, 512, qg.data_ptr(), 512, sg.data_ptr(), 0,
+    nat.check(nat.lib().ic_quant_error(Wg.data_ptr(), M, N, N, qg.data_ptr(), N, sg.data_ptr(), 0,
                                        zg.data_ptr(), out_s.data_ptr(), out_m.data_ptr(), ws.data_ptr(),
                                        nat.stream()), "ic_quant_error")
     assert out_s.item() / W.numel() == pytest.approx(want_mse, rel=1e-9)
