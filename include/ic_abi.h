@@ -283,11 +283,12 @@ int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float*
  * enabled, library launches are bracketed by HIP events on their stream and
  * tagged with a phase: 0 trailing-update GEMM, 1 Cholesky GEMMs, 2 inverse
  * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
- * rotation, 7 RTN / pack / verify, 8 greedy block kernel, 9 other, 10 greedy
- * cross-term GEMMs, 11 Cholesky panel solve.  Enabling resets the record.  ic_profile_read
+ * rotation, 7 RTN quantise / INT4 pack, 8 greedy block kernel, 9 other, 10 greedy
+ * cross-term GEMMs, 11 Cholesky panel solve, 12 RTN scales / clip search,
+ * 13 fp64 verification.  Enabling resets the record.  ic_profile_read
  * synchronises the events and returns, per phase, the summed kernel time
  * (ms), algorithmic flops and bytes, and the launch count (arrays of at least
- * 12 entries). */
+ * 14 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

@@ -69,7 +69,8 @@ _SIGS = {
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
-                "rotate_h", "rtn_pack_verify", "greedy", "other", "gemm_greedy", "chol_panel"]
+                "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
+                "verify"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {
@@ -78,6 +79,10 @@ PROFILE_KERNELS = {
     "panel64_kernel": ["chol_panel"],
     "sweep_kernel": ["sweep"],
     "greedy_block_kernel": ["greedy"],
+    "rotate_rows_reg": ["rotate_w"],
+    "rtn_scales_kernel": ["rtn_scales"],
+    "rtn_quant_kernel": ["rtn_quant_pack"],
+    "quant_error_partial": ["verify"],
 }
 
 

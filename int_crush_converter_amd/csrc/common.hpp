@@ -91,6 +91,20 @@ __device__ __forceinline__ float div_rn_wave(float a, float b, float y, bool b_o
     return q;
 }
 
+// The fast quotient alone, for callers that established the domain of
+// div_rn beforehand (b_ok, and every a in [2^-60, 2^61) or 0).
+__device__ __forceinline__ float div_rn_fast(float a, float b, float y) {
+    const float q0 = a * y;
+    const float r = __builtin_fmaf(-q0, b, a);
+    return __builtin_fmaf(r, y, q0);
+}
+
+// |a| in the numerator domain of div_rn: [2^-60, 2^61) or 0.
+__device__ __forceinline__ bool div_a_ok(float a) {
+    const float aa = fabsf(a);
+    return (aa >= 0x1p-60f && aa < 0x1p61f) || aa == 0.0f;
+}
+
 // rhaz with fewer operations: trunc(x + copysign(0.5, x)).  For x >= 0
 // this is floor(x + 0.5) (x + 0.5 > 0); for x < 0 ceil(x - 0.5).  The one
 // difference is x = -0.0, which gives -0.0 instead of +0.0: an equal code

@@ -17,12 +17,14 @@ enum ProfTag : int {
     PT_SWEEP = 4,        // GPTQ / LDLQ column sweep
     PT_ROTATE = 5,       // weight rotation
     PT_ROTATE_H = 6,     // two-sided Hessian rotation
-    PT_RTN = 7,          // scales / quantise / pack / verify
+    PT_RTN = 7,          // quantise / pack
     PT_GREEDY = 8,       // greedy block kernel + its cross-term GEMMs
     PT_OTHER = 9,
     PT_GEMM_GREEDY = 10, // greedy cross-term GEMMs
     PT_PANEL = 11,       // Cholesky panel solve (fp64 accumulation)
-    PT_COUNT = 12,
+    PT_RTN_SCALES = 12,  // RTN scales / clipping-ratio search
+    PT_VERIFY = 13,      // fp64 quantisation error
+    PT_COUNT = 14,
 };
 
 bool prof_enabled();

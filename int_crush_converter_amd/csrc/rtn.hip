@@ -93,7 +93,24 @@ __device__ __forceinline__ Cand rtn_candidate(const RowStats& st, int bits, int 
     return c;
 }
 
+// Squared error of one clip candidate for one value (fp64).  q =
+// clamp(round_half_even(w / s [+ z])) with w / s correctly rounded: the
+// fast quotient from RN(1/s) when the caller established div_rn's domain
+// (FAST), else the IEEE division, as in the reference.
+template <bool FAST>
+__device__ __forceinline__ double cand_sq_err(float w, const Cand& c, float rs, int asym, float qmin, float qmax) {
+    float y = FAST ? div_rn_fast(w, c.s, rs) : w / c.s;
+    if (asym) y = y + c.z;
+    const float q = clampf_med3(rhte(y), qmin, qmax);
+    const float d = asym ? (q - c.z) * c.s : q * c.s;
+    const float e = w - d;
+    return (double)e * (double)e;
+}
+
 // One wave per row: stats, then either the closed form or the clip search.
+// CR > 0: the row (cols <= 64 CR) is held in registers for all candidates;
+// CR == 0: each candidate re-reads the row (from the caches).
+template <int CR>
 __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
                                                          int64_t ld, int bits, int asym, int n_ratios,
                                                          Ratios rt, uint16_t* __restrict__ scale16, int8_t* __restrict__ zp) {
@@ -102,7 +119,24 @@ __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
     for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * wpb) {
         const float* x = W + r * ld;
-        RowStats st = row_stats_wave(x, cols);
+        float v[CR > 0 ? CR : 1];
+        RowStats st;
+        bool row_ok = false;   // every value of the row in div_rn's numerator domain
+        if (CR > 0) {
+            float mn = INFINITY, mx = -INFINITY, am = 0.0f;
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < CR; ++i) {
+                const int64_t j = lane + 64 * i;
+                v[i] = j < cols ? x[j] : 0.0f;
+                if (j < cols) { mn = nmin(mn, v[i]); mx = nmax(mx, v[i]); am = nmax(am, fabsf(v[i])); }
+                ok = ok && div_a_ok(v[i]);
+            }
+            st = {wave_nmin(mn), wave_nmax(mx), wave_nmax(am)};
+            row_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+        } else {
+            st = row_stats_wave(x, cols);
+        }
         Cand best;
         if (n_ratios == 0) {
             best = rtn_candidate(st, bits, asym, false, 1.0f);
@@ -111,21 +145,19 @@ __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict
         } else {
             double best_m = 0.0;
             for (int k = 0; k < n_ratios; ++k) {
-                float ratio = rt.v[k];
-                Cand c = rtn_candidate(st, bits, asym, true, ratio);
+                const Cand c = rtn_candidate(st, bits, asym, true, rt.v[k]);
+                const float rs = 1.0f / c.s;
                 double acc = 0.0;
-                for (int64_t j = lane; j < cols; j += 64) {
-                    float w = x[j];
-                    float d;
-                    if (asym) {
-                        float q = clampf(rhte(w / c.s + c.z), qmin, qmax);
-                        d = (q - c.z) * c.s;
-                    } else {
-                        float q = clampf(rhte(w / c.s), qmin, qmax);
-                        d = q * c.s;
-                    }
-                    float e = w - d;
-                    acc += (double)e * (double)e;
+                if (CR > 0 && row_ok && div_b_ok(c.s)) {
+#pragma unroll
+                    for (int i = 0; i < CR; ++i)
+                        if (lane + 64 * i < cols) acc += cand_sq_err<true>(v[i], c, rs, asym, qmin, qmax);
+                } else if (CR > 0) {
+#pragma unroll
+                    for (int i = 0; i < CR; ++i)
+                        if (lane + 64 * i < cols) acc += cand_sq_err<false>(v[i], c, rs, asym, qmin, qmax);
+                } else {
+                    for (int64_t j = lane; j < cols; j += 64) acc += cand_sq_err<false>(x[j], c, rs, asym, qmin, qmax);
                 }
                 acc = wave_sum(acc);
                 // strict '<' keeps the first ratio on ties; NaN never wins
@@ -141,45 +173,68 @@ __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict
 
 __device__ __forceinline__ uint8_t nib(float q) { return (uint8_t)(((int)q) & 0xF); }
 
-// 16 columns per lane.  codes: int8 [rows, ld_q]; packed: uint8 [rows, ld_p].
+// One wave per row, 4 consecutive columns per lane and step: 16-byte W
+// loads, 4-byte code stores, 2-byte packed stores (VEC: row pointers and
+// pitches aligned for them; else element by element).  The quotient is the
+// fast correctly rounded one unless some value of the wave's step lies
+// outside div_rn's domain, which takes the IEEE division.
+// codes: int8 [rows, ld_q]; packed: uint8 [rows, ld_p] (low nibble = even column).
+template <bool VEC>
 __global__ __launch_bounds__(256) void rtn_quant_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
                                                         int64_t ld, int bits, const void* __restrict__ scale,
                                                         int scale_kind, const float* __restrict__ zp,
                                                         int8_t* __restrict__ codes, int64_t ld_q,
                                                         uint8_t* __restrict__ packed, int64_t ld_p) {
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
-    const int64_t cpr = cdiv(cols, 16);
-    const int64_t total = rows * cpr;
-    for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
-         g += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = g / cpr;
-        const int64_t c0 = (g - r * cpr) * 16;
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+    for (int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); r < rows; r += nw) {
         const float s = scale_kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[r])
                                         : reinterpret_cast<const float*>(scale)[r];
         const float z = zp ? zp[r] : 0.0f;
-        const float* x = W + r * ld + c0;
-        float q[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (c0 + i < cols) {
-                float y = x[i] / s;
-                if (zp) y = y + z;
-                q[i] = clampf(rhaz(y), qmin, qmax);
+        const float rs = 1.0f / s;
+        const bool s_ok = div_b_ok(s);
+        const float* x = W + r * ld;
+        for (int64_t c0 = 4 * (int64_t)lane; c0 < cols; c0 += 256) {
+            const bool full = c0 + 4 <= cols;
+            float w[4];
+            if (VEC && full) {
+                const float4 t = *reinterpret_cast<const float4*>(x + c0);
+                w[0] = t.x; w[1] = t.y; w[2] = t.z; w[3] = t.w;
             } else {
-                q[i] = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) w[u] = c0 + u < cols ? x[c0 + u] : 0.0f;
             }
-        }
-        if (codes) {
-            int8_t* o = codes + r * ld_q + c0;
+            const bool ok = s_ok && div_a_ok(w[0]) && div_a_ok(w[1]) && div_a_ok(w[2]) && div_a_ok(w[3]);
+            const bool all_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+            float q[4];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (c0 + i < cols) o[i] = (int8_t)(int)q[i];
-        }
-        if (packed) {
-            uint8_t* o = packed + r * ld_p + c0 / 2;
+            for (int u = 0; u < 4; ++u) {
+                float y = all_ok ? div_rn_fast(w[u], s, rs) : (ok ? div_rn_fast(w[u], s, rs) : w[u] / s);
+                if (zp) y = y + z;
+                q[u] = c0 + u < cols ? clampf_med3(rhaz_trunc(y), qmin, qmax) : 0.0f;
+            }
+            if (codes) {
+                int8_t* o = codes + r * ld_q + c0;
+                if (VEC && full) {
+                    *reinterpret_cast<char4*>(o) = make_char4((signed char)(int)q[0], (signed char)(int)q[1],
+                                                              (signed char)(int)q[2], (signed char)(int)q[3]);
+                } else {
 #pragma unroll
-            for (int i = 0; i < 16; i += 2)
-                if (c0 + i < cols) o[i / 2] = (uint8_t)(nib(q[i]) | (nib(q[i + 1]) << 4));
+                    for (int u = 0; u < 4; ++u)
+                        if (c0 + u < cols) o[u] = (int8_t)(int)q[u];
+                }
+            }
+            if (packed) {
+                uint8_t* o = packed + r * ld_p + c0 / 2;
+                const uint8_t b0 = (uint8_t)(nib(q[0]) | (nib(q[1]) << 4)), b1 = (uint8_t)(nib(q[2]) | (nib(q[3]) << 4));
+                if (VEC && full) {
+                    *reinterpret_cast<uint16_t*>(o) = (uint16_t)(b0 | (b1 << 8));
+                } else {
+                    o[0] = b0;
+                    if (c0 + 2 < cols) o[1] = b1;
+                }
+            }
         }
     }
 }
@@ -389,8 +444,13 @@ extern "C" int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t
     if (rows == 0) return IC_OK;
     Ratios rt;
     for (int i = 0; i < MAX_RATIOS; ++i) rt.v[i] = i < n_ratios ? ratios[i] : 1.0f;
-    hipLaunchKernelGGL(rtn_scales_kernel, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows, cols,
-                       ld, bits, asym, n_ratios, rt, scale16, zp);
+    ProfScope prof_scope(as_stream(stream), PT_RTN_SCALES, 0.0, (double)rows * cols * 4.0 + rows * 3.0);
+    if (n_ratios > 0 && cols <= 64 * 64)
+        hipLaunchKernelGGL(rtn_scales_kernel<64>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
+                           cols, ld, bits, asym, n_ratios, rt, scale16, zp);
+    else
+        hipLaunchKernelGGL(rtn_scales_kernel<0>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
+                           cols, ld, bits, asym, n_ratios, rt, scale16, zp);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }
@@ -406,8 +466,14 @@ extern "C" int ic_rtn_quantize(const float* W, int64_t rows, int64_t cols, int64
     IC_REQUIRE(!packed || ld_p >= cdiv(cols, 2), "ic_rtn_quantize: bad ld_p");
     if (rows == 0 || cols == 0) return IC_OK;
     ProfScope prof_scope(as_stream(stream), PT_RTN, 0.0, (double)rows * cols * (4 + (codes ? 1 : 0) + (packed ? 0.5 : 0)));
-    hipLaunchKernelGGL(rtn_quant_kernel, dim3(elem_grid(rows * cdiv(cols, 16))), dim3(256), 0, as_stream(stream), W,
-                       rows, cols, ld, bits, scale, scale_kind, zp, codes, ld_q, packed, ld_p);
+    const bool vec = ((uintptr_t)W % 16 == 0) && ld % 4 == 0 && (!codes || ((uintptr_t)codes % 4 == 0 && ld_q % 4 == 0)) &&
+                     (!packed || ((uintptr_t)packed % 2 == 0 && ld_p % 2 == 0));
+    if (vec)
+        hipLaunchKernelGGL(rtn_quant_kernel<true>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
+                           cols, ld, bits, scale, scale_kind, zp, codes, ld_q, packed, ld_p);
+    else
+        hipLaunchKernelGGL(rtn_quant_kernel<false>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
+                           cols, ld, bits, scale, scale_kind, zp, codes, ld_q, packed, ld_p);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }
@@ -458,7 +524,7 @@ extern "C" int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_
     hipStream_t st = as_stream(stream);
     double* ps = reinterpret_cast<double*>(workspace);
     float* pm = reinterpret_cast<float*>(ps + QERR_BLOCKS);
-    ProfScope prof_scope(st, PT_RTN, 0.0, (double)rows * cols * 5.0);
+    ProfScope prof_scope(st, PT_VERIFY, 0.0, (double)rows * cols * 5.0);
     hipLaunchKernelGGL(quant_error_partial, dim3(QERR_BLOCKS), dim3(256), 0, st, W, rows, cols, ld, codes, ld_q,
                        scale, scale_kind, zp, ps, pm);
     IC_CHECK_LAUNCH();
