@@ -23,10 +23,21 @@ constexpr int NB = 128;
 
 static double dtri(double n) { return n * (n + 1) / 2; }
 
-__global__ void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
+// One work-group of 256 per matrix: the diagonal's loads are issued eight at
+// a time (each touches its own cache line), then summed in fp64.
+__global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
     float* A = H + (int64_t)blockIdx.x * stride;
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) acc += (double)A[i * ld + i];
+    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * (int64_t)blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = i0 + u * (int64_t)blockDim.x;
+            v[u] = i < n ? A[i * ld + i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += (double)v[u];
+    }
     __shared__ double part[4];
     acc = wave_sum(acc);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
@@ -518,6 +529,14 @@ __global__ void put_diag_all_kernel(float* X, int64_t n, int64_t ld, int64_t str
     const float* D = dinv + (int64_t)b * dstride + (int64_t)blockIdx.x * NB * NB;
     float* P = X + (int64_t)b * stride + k0 * ld + k0;
     const int nb = (int)std::min<int64_t>(NB, n - k0);
+    if (nb == NB && ld % 4 == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0) {
+        // whole block, 16-byte rows: 32 float4 per row
+        for (int idx = threadIdx.x; idx < NB * NB / 4; idx += blockDim.x) {
+            const int i = idx >> 5, j4 = (idx & 31) * 4;
+            *reinterpret_cast<float4*>(&P[(int64_t)i * ld + j4]) = *reinterpret_cast<const float4*>(&D[i * NB + j4]);
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < nb * nb; idx += blockDim.x) {
         const int i = idx / nb, j = idx - i * nb;
         P[(int64_t)i * ld + j] = D[i * NB + j];

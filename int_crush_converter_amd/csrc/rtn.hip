@@ -30,10 +30,22 @@ __device__ __forceinline__ float wave_nmin(float v) {
 
 struct RowStats { float mn, mx, amax; };
 
+// One wave per row; 16-byte loads when the row start is 16-byte aligned.
 __device__ RowStats row_stats_wave(const float* __restrict__ x, int64_t cols) {
     const int lane = threadIdx.x & 63;
     float mn = INFINITY, mx = -INFINITY, am = 0.0f;
-    for (int64_t c = lane; c < cols; c += 64) {
+    int64_t c = lane;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        const int64_t c4 = cols & ~(int64_t)3;
+        for (int64_t j = 4 * (int64_t)lane; j < c4; j += 256) {
+            const float4 t = *reinterpret_cast<const float4*>(x + j);
+            const float v[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) { mn = nmin(mn, v[u]); mx = nmax(mx, v[u]); am = nmax(am, fabsf(v[u])); }
+        }
+        c = c4 + lane;
+    }
+    for (; c < cols; c += 64) {
         float v = x[c];
         mn = nmin(mn, v); mx = nmax(mx, v); am = nmax(am, fabsf(v));
     }
