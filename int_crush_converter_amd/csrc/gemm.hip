@@ -1,18 +1,21 @@
 // fp32 GEMM on the CDNA4 matrix cores (v_mfma_f32_16x16x4_f32).
 //
-// Workgroup tile 128x128, K staged 32 at a time through LDS; 4 waves in a
-// 2x2 arrangement, each owning a 64x64 sub-tile held as 4x4 MFMA 16x16
-// accumulators.  Per stage a wave issues 128 MFMAs (4096 cycles of
-// matrix-core time) against 64 LDS reads; the next stage's global loads are
-// issued before the current stage's MFMAs so their latency hides behind
-// them.  Work-group ids are remapped so that each XCD (ids congruent mod 8)
+// Workgroup tile T x T (T = 128, or 64 for launches with fewer 128-tiles
+// than CUs), K staged 32 at a time through LDS; 4 waves in a 2x2
+// arrangement, each owning a T/2 x T/2 sub-tile held as F x F MFMA 16x16
+// accumulators (F = T / 32).  For T = 128 a wave issues 128 MFMAs per stage
+// (4096 cycles of matrix-core time) against 64 LDS reads; the next stage's
+// global loads are issued before the current stage's MFMAs so their latency
+// hides behind them.  The 64 tile has a quarter of the matrix work per
+// stage, so a small launch (e.g. a rank-128 update of a few column blocks)
+// spreads over four times as many CUs and its latency falls accordingly.  Work-group ids are remapped so that each XCD (ids congruent mod 8)
 // owns a balanced set of tile rows and runs 8x8 blocks of tiles at a time,
 // which share A rows / B columns in its L2.
 //
 // Each operand is staged in LDS in its memory order, so every global load
 // and LDS store is a 16-byte vector: a row-major operand tile (A, or B^T)
-// as 128 rows x 32 k at pitch 36 floats, a k-major one (A^T, or B) as 32 k
-// rows x 128 at pitch 144.  Both pitches make the MFMA operand reads (16
+// as T rows x 32 k at pitch 36 floats, a k-major one (A^T, or B) as 32 k
+// rows x T at pitch T + 16.  Both pitches make the MFMA operand reads (16
 // consecutive rows or columns per k) free of bank conflicts.  The transposes
 // are template parameters, and problems made of whole tiles and whole K
 // stages run a kernel instance without bounds checks.
@@ -26,11 +29,20 @@ namespace icq {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
-constexpr int PR = BK + 4;        // pitch of a row-major operand tile [128][32]
-constexpr int PKM = BM + 16;      // pitch of a k-major operand tile [32][128]
-constexpr int TILE_F = BM * PR > BK * PKM ? BM * PR : BK * PKM;   // floats per operand tile
+constexpr int BK = 32;
+constexpr int PR = BK + 4;        // pitch of a row-major operand tile [T][32]
 constexpr int NXCD = 8;
+
+// Tile geometry for tile size T (the output tile is T x T).
+template <int T>
+struct Geo {
+    static constexpr int F = T / 32;            // MFMA fragments per wave and dimension
+    static constexpr int WS = T / 2;             // wave sub-tile
+    static constexpr int PKM = T + 16;           // pitch of a k-major operand tile [32][T]
+    static constexpr int SLOTS = T / 32;         // float4 per thread and operand per stage
+    static constexpr int KROWS = 1024 / T;       // k rows one slot of a k-major tile covers
+    static constexpr int TILE_F = T * PR > BK * PKM ? T * PR : BK * PKM;   // floats per operand tile
+};
 
 struct TileRange { int64_t i0, j0, klo, khi; bool skip; };
 
@@ -42,16 +54,17 @@ __device__ __forceinline__ int64_t isqrt_floor(int64_t x) {
 }
 
 // The tile (ti, tj) with its K range.
+template <int T>
 __device__ __forceinline__ TileRange tile_range(const GemmArgs& g, int64_t ti, int64_t tj) {
     TileRange t;
-    t.i0 = ti * BM; t.j0 = tj * BN;
+    t.i0 = ti * T; t.j0 = tj * T;
     t.skip = false;
-    if (g.cmask == CMASK_LOWER && t.i0 + BM - 1 < t.j0) t.skip = true;
-    if (g.cmask == CMASK_UPPER && t.j0 + BN - 1 < t.i0) t.skip = true;
+    if (g.cmask == CMASK_LOWER && t.i0 + T - 1 < t.j0) t.skip = true;
+    if (g.cmask == CMASK_UPPER && t.j0 + T - 1 < t.i0) t.skip = true;
     t.klo = 0; t.khi = g.K;
     if (g.krange == KR_FROM_MAXIJ) t.klo = t.i0 > t.j0 ? t.i0 : t.j0;
     else if (g.krange == KR_FROM_J) t.klo = t.j0;
-    else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + BM);
+    else if (g.krange == KR_TO_I) t.khi = min(g.K, t.i0 + T);
     else if (g.krange == KR_FROM_I) t.klo = t.i0;
     t.klo = (t.klo / 4) * 4;
     if (t.klo > g.K) t.klo = g.K;
@@ -61,8 +74,9 @@ __device__ __forceinline__ TileRange tile_range(const GemmArgs& g, int64_t ti, i
 // Linear tile id -> tile.  Triangular masks enumerate only tiles that touch
 // the kept triangle (square grids); for KR_FROM_MAXIJ the upper tiles are
 // enumerated by increasing column block so that long-K tiles start first.
+template <int T>
 __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
-    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    const int64_t tm = (g.M + T - 1) / T, tn = (g.N + T - 1) / T;
     int64_t ti, tj;
     if (g.cmask == CMASK_LOWER && tm == tn) {
         int64_t r = (isqrt_floor(8 * id + 1) - 1) / 2;   // id -> (r, c), c <= r
@@ -75,7 +89,7 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
         // K range grows with the tile row: start the long tiles first
         if (g.krange == KR_TO_I) ti = tm - 1 - ti;
     }
-    return tile_range(g, ti, tj);
+    return tile_range<T>(g, ti, tj);
 }
 
 // Work-group b -> tile for rectangular grids with at least NXCD tile rows.
@@ -90,8 +104,9 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
 // panels in its L2); row-dependent work (KR_TO_I, KR_FROM_I) walks rows
 // one after another, longest first, so that every engine gets every 4th
 // tile of every row.  False: no tile.
+template <int T>
 __device__ __forceinline__ bool xcd_tile(const GemmArgs& g, int64_t b, TileRange& t) {
-    const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    const int64_t tm = (g.M + T - 1) / T, tn = (g.N + T - 1) / T;
     const int x = (int)(b % NXCD);
     const int64_t l = b / NXCD;
     const int64_t full = tm / NXCD, rem = tm - full * NXCD;
@@ -111,19 +126,37 @@ __device__ __forceinline__ bool xcd_tile(const GemmArgs& g, int64_t b, TileRange
         q = g0 + (w - tj * G);
     }
     const int64_t ti = q * NXCD + ((q & 1) ? (NXCD - 1 - x) : x);
-    t = tile_range(g, ti, tj);
+    t = tile_range<T>(g, ti, tj);
     return true;
 }
 
-// One operand's share of a stage: 4 float4 per thread (kept in named
-// registers so that no unrolled index can push them to scratch).
+// One operand's share of a stage: SLOTS float4 per thread (kept in named
+// registers so that no unrolled index can push them to scratch; T = 64
+// uses the first two).
 struct Quad { floatx4 v0, v1, v2, v3; };
 
-// A row-major tile (ROWMAJ: element (r, k) at p[r * ld + k]) is read as 128
+template <int S>
+__device__ __forceinline__ floatx4& qslot(Quad& q) {
+    static_assert(S >= 0 && S < 4, "slot");
+    if constexpr (S == 0) return q.v0;
+    else if constexpr (S == 1) return q.v1;
+    else if constexpr (S == 2) return q.v2;
+    else return q.v3;
+}
+template <int S>
+__device__ __forceinline__ const floatx4& qslot(const Quad& q) {
+    if constexpr (S == 0) return q.v0;
+    else if constexpr (S == 1) return q.v1;
+    else if constexpr (S == 2) return q.v2;
+    else return q.v3;
+}
+
+// A row-major tile (ROWMAJ: element (r, k) at p[r * ld + k]) is read as T
 // rows x 8 float4 of k; a k-major one (element (k, c) at p[k * ld + c]) as 32
-// k-rows x 32 float4.  Thread t, slot s: idx = t + 256 s.
-template <bool ROWMAJ>
+// k-rows x T/4 float4.  Thread t, slot s: idx = t + 256 s.
+template <bool ROWMAJ, int T>
 struct OperandLoader {
+    using G = Geo<T>;
     const float* p;     // this thread's slot-0 element at the current stage
     int64_t step;       // pointer advance per stage
     int64_t slot;       // pointer distance between slots
@@ -136,16 +169,18 @@ struct OperandLoader {
             p = base + (m0 + r) * ld + k0 + c;
             step = BK; slot = 32 * ld;
         } else {
-            r = t >> 5; c = (t & 31) * 4;
+            r = t / (T / 4); c = (t % (T / 4)) * 4;
             p = base + (k0 + r) * ld + m0 + c;
-            step = (int64_t)BK * ld; slot = 8 * ld;
+            step = (int64_t)BK * ld; slot = G::KROWS * ld;
         }
     }
     __device__ __forceinline__ void load_fast(Quad& q) const {
         q.v0 = *reinterpret_cast<const floatx4*>(p);
         q.v1 = *reinterpret_cast<const floatx4*>(p + slot);
-        q.v2 = *reinterpret_cast<const floatx4*>(p + 2 * slot);
-        q.v3 = *reinterpret_cast<const floatx4*>(p + 3 * slot);
+        if constexpr (G::SLOTS == 4) {
+            q.v2 = *reinterpret_cast<const floatx4*>(p + 2 * slot);
+            q.v3 = *reinterpret_cast<const floatx4*>(p + 3 * slot);
+        }
     }
     // Element (m, k) exists when m < mlim and k < klim; m0 / k0 are the
     // tile's / stage's origins.
@@ -156,7 +191,7 @@ struct OperandLoader {
         for (int u = 0; u < 4; ++u) {
             int64_t m, k;
             if (ROWMAJ) { m = m0 + r + 32 * s; k = k0 + c + u; }
-            else { k = k0 + r + 8 * s; m = m0 + c + u; }
+            else { k = k0 + r + G::KROWS * s; m = m0 + c + u; }
             e[u] = (m < mlim && k < klim) ? base[ROWMAJ ? m * ld + k : k * ld + m] : 0.0f;
         }
         return floatx4{e[0], e[1], e[2], e[3]};
@@ -165,86 +200,97 @@ struct OperandLoader {
                                                  int64_t ld, const float* base) const {
         q.v0 = get_checked(0, m0, k0, mlim, klim, ld, base);
         q.v1 = get_checked(1, m0, k0, mlim, klim, ld, base);
-        q.v2 = get_checked(2, m0, k0, mlim, klim, ld, base);
-        q.v3 = get_checked(3, m0, k0, mlim, klim, ld, base);
+        if constexpr (G::SLOTS == 4) {
+            q.v2 = get_checked(2, m0, k0, mlim, klim, ld, base);
+            q.v3 = get_checked(3, m0, k0, mlim, klim, ld, base);
+        }
     }
     __device__ __forceinline__ floatx4* at(float* tile, int s) const {
         return ROWMAJ ? reinterpret_cast<floatx4*>(&tile[(r + 32 * s) * PR + c])
-                      : reinterpret_cast<floatx4*>(&tile[(r + 8 * s) * PKM + c]);
+                      : reinterpret_cast<floatx4*>(&tile[(r + G::KROWS * s) * G::PKM + c]);
     }
     __device__ __forceinline__ void store_lds(const Quad& q, float* tile) const {
         *at(tile, 0) = q.v0;
         *at(tile, 1) = q.v1;
-        *at(tile, 2) = q.v2;
-        *at(tile, 3) = q.v3;
+        if constexpr (G::SLOTS == 4) {
+            *at(tile, 2) = q.v2;
+            *at(tile, 3) = q.v3;
+        }
     }
 };
 
 // LDS offset of operand element (m, k) of a tile: row-major tiles are
 // m-major at pitch PR, k-major tiles k-major at pitch PKM.
-template <bool ROWMAJ>
-__device__ __forceinline__ int lds_at(int m, int k) { return ROWMAJ ? m * PR + k : k * PKM + m; }
+template <bool ROWMAJ, int T>
+__device__ __forceinline__ int lds_at(int m, int k) { return ROWMAJ ? m * PR + k : k * Geo<T>::PKM + m; }
 
-// One BK stage of a wave's 64x64 sub-tile; MFMA step s of a group of 16 k
+// F-wide vector of floats (F = 4: 16 bytes, F = 2: 8 bytes).
+template <int F> struct VecF;
+template <> struct VecF<4> { typedef float type __attribute__((ext_vector_type(4))); };
+template <> struct VecF<2> { typedef float type __attribute__((ext_vector_type(2))); };
+
+// One BK stage of a wave's WS x WS sub-tile; MFMA step s of a group of 16 k
 // feeds k = 4 s + l / 16 from lane l.  When both operands are staged k-major
 // (A^T B: the LAUUM), each permutes its rows (A) or columns (B) inside the
-// wave's 64 - fragment a / b at MFMA row / column m is row 4 m + a / column
-// 4 m + b - so one 16-byte LDS read gives a lane all four fragments of one
-// step (WIDE).  Otherwise each fragment value is one 4-byte read, which
+// wave's sub-tile - fragment a / b at MFMA row / column m is row F m + a /
+// column F m + b - so one F-wide LDS read gives a lane all F fragments of
+// one step (WIDE).  Otherwise each fragment value is one 4-byte read, which
 // measured faster there.
-//   row of accumulator (a, v) at lane l:  wi + 16 a + 4 (l/16) + v,  WIDE: wi + 4 (4 (l/16) + v) + a
-//   column of (b) at lane l:              wj + 16 b + l%16,          WIDE: wj + 4 (l%16) + b
-template <int TA, int TB>
+//   row of accumulator (a, v) at lane l:  wi + 16 a + 4 (l/16) + v,  WIDE: wi + F (4 (l/16) + v) + a
+//   column of (b) at lane l:              wj + 16 b + l%16,          WIDE: wj + F (l%16) + b
+template <int TA, int TB, int T>
 __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int wi, int wj, int lane,
-                                          floatx4 (&acc)[4][4]) {
+                                          floatx4 (&acc)[Geo<T>::F][Geo<T>::F]) {
+    constexpr int F = Geo<T>::F, PKM = Geo<T>::PKM;
     constexpr bool AR = TA == 0, BR = TB == 1;   // row-major staging
     constexpr bool WIDE = !AR && !BR;
+    typedef typename VecF<F>::type vecf;
     const int m = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int kq = 0; kq < BK; kq += 16) {
-        floatx4 af[4], bf[4];   // af[a][s], bf[b][s]
+        floatx4 af[F], bf[F];   // af[a][s], bf[b][s]
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int k = kq + 4 * s + g;
             if (WIDE) {
-                const floatx4 ta = *reinterpret_cast<const floatx4*>(&As[k * PKM + wi + 4 * m]);
-                const floatx4 tb = *reinterpret_cast<const floatx4*>(&Bs[k * PKM + wj + 4 * m]);
+                const vecf ta = *reinterpret_cast<const vecf*>(&As[k * PKM + wi + F * m]);
+                const vecf tb = *reinterpret_cast<const vecf*>(&Bs[k * PKM + wj + F * m]);
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
+                for (int x = 0; x < F; ++x) {
                     af[x][s] = ta[x];
                     bf[x][s] = tb[x];
                 }
             } else {
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    af[x][s] = As[lds_at<AR>(wi + 16 * x + m, k)];
-                    bf[x][s] = Bs[lds_at<BR>(wj + 16 * x + m, k)];
+                for (int x = 0; x < F; ++x) {
+                    af[x][s] = As[lds_at<AR, T>(wi + 16 * x + m, k)];
+                    bf[x][s] = Bs[lds_at<BR, T>(wj + 16 * x + m, k)];
                 }
             }
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+            for (int a = 0; a < F; ++a)
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
+                for (int b = 0; b < F; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
     }
 }
 
-template <int TA, int TB, bool CHECK>
+template <int TA, int TB, bool CHECK, int T>
 __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, const float* B, const TileRange& tr,
-                                          float* lds, floatx4 (&acc)[4][4]) {
+                                          float* lds, floatx4 (&acc)[Geo<T>::F][Geo<T>::F]) {
     constexpr bool AR = TA == 0, BR = TB == 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
-    OperandLoader<AR> la;
-    OperandLoader<BR> lb;
+    const int wi = (wave >> 1) * Geo<T>::WS, wj = (wave & 1) * Geo<T>::WS;
+    OperandLoader<AR, T> la;
+    OperandLoader<BR, T> lb;
     la.init(A, g.lda, tr.i0, tr.klo);
     lb.init(B, g.ldb, tr.j0, tr.klo);
     Quad va, vb;
     float* As = lds;
-    float* Bs = lds + TILE_F;
+    float* Bs = lds + Geo<T>::TILE_F;
 #define ICQ_LOAD_STAGE(K0)                                                 \
     do {                                                                   \
         if (CHECK) {                                                       \
@@ -266,20 +312,21 @@ __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, con
         lb.store_lds(vb, Bs);
         __syncthreads();
         if (k0 + BK < tr.khi) ICQ_LOAD_STAGE(k0 + BK);
-        mma_stage<TA, TB>(As, Bs, wi, wj, lane, acc);
+        mma_stage<TA, TB, T>(As, Bs, wi, wj, lane, acc);
     }
 #undef ICQ_LOAD_STAGE
 }
 
-template <int TA, int TB, bool CHECK>
+template <int TA, int TB, bool CHECK, int T>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap) {
-    __shared__ __attribute__((aligned(16))) float lds[2 * TILE_F];
+    constexpr int F = Geo<T>::F;
+    __shared__ __attribute__((aligned(16))) float lds[2 * Geo<T>::TILE_F];
     TileRange tr;
     if (remap) {
-        if (!xcd_tile(g, blockIdx.x, tr)) return;
+        if (!xcd_tile<T>(g, blockIdx.x, tr)) return;
     } else {
         if ((int64_t)blockIdx.x >= ntiles) return;
-        tr = tile_of(g, blockIdx.x);
+        tr = tile_of<T>(g, blockIdx.x);
     }
     if (tr.skip) return;
     const int64_t z = blockIdx.z;
@@ -287,55 +334,56 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
     const float* B = g.B + z * g.sB;
     float* C = g.C + z * g.sC;
 
-    floatx4 acc[4][4];
+    floatx4 acc[F][F];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < F; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < F; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    main_loop<TA, TB, CHECK>(g, A, B, tr, lds, acc);
+    main_loop<TA, TB, CHECK, T>(g, A, B, tr, lds, acc);
 
     constexpr bool WIDE = TA == 1 && TB == 0;
+    typedef typename VecF<F>::type vecf;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;
+    const int wi = (wave >> 1) * Geo<T>::WS, wj = (wave & 1) * Geo<T>::WS;
     const int g4 = 4 * (lane >> 4), m = lane & 15;
     // element (a, b, v) of the accumulators is C[row(a, v)][col(b)] (see mma_stage)
-    auto row_of = [&](int a, int v) -> int64_t { return tr.i0 + (WIDE ? wi + 4 * (g4 + v) + a : wi + 16 * a + g4 + v); };
-    auto col_of = [&](int b) -> int64_t { return tr.j0 + (WIDE ? wj + 4 * m + b : wj + 16 * b + m); };
+    auto row_of = [&](int a, int v) -> int64_t { return tr.i0 + (WIDE ? wi + F * (g4 + v) + a : wi + 16 * a + g4 + v); };
+    auto col_of = [&](int b) -> int64_t { return tr.j0 + (WIDE ? wj + F * m + b : wj + 16 * b + m); };
     const bool full = !CHECK && g.cmask == CMASK_FULL;
-    const bool c16 = (((uintptr_t)C) % 16 == 0) && (g.ldc % 4 == 0);
-    if (WIDE && full && c16) {
-        // the lane's four columns 4 m .. 4 m + 3 are adjacent: 16-byte loads and stores
+    const bool cvec = (((uintptr_t)C) % (4 * F) == 0) && (g.ldc % F == 0);
+    if (WIDE && full && cvec) {
+        // the lane's F columns F m .. F m + F - 1 are adjacent: F-wide loads and stores
         const int64_t j0 = col_of(0);
-        floatx4 cold[4][4];
+        vecf cold[F][4];
         if (g.beta != 0.0f) {
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+            for (int a = 0; a < F; ++a)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    cold[a][v] = *reinterpret_cast<const floatx4*>(&C[row_of(a, v) * g.ldc + j0]);
+                    cold[a][v] = *reinterpret_cast<const vecf*>(&C[row_of(a, v) * g.ldc + j0]);
         }
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < F; ++a)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                floatx4 r;
+                vecf r;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
+                for (int b = 0; b < F; ++b) {
                     r[b] = g.alpha * acc[a][b][v];
                     if (g.beta != 0.0f) r[b] = r[b] + g.beta * cold[a][v][b];
                 }
-                *reinterpret_cast<floatx4*>(&C[row_of(a, v) * g.ldc + j0]) = r;
+                *reinterpret_cast<vecf*>(&C[row_of(a, v) * g.ldc + j0]) = r;
             }
         return;
     }
     // general epilogue: all C loads are issued before any store so their latency overlaps
-    float cold[4][4][4];
+    float cold[F][F][4];
     if (g.beta != 0.0f) {
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < F; ++a)
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
+            for (int b = 0; b < F; ++b)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int64_t i = row_of(a, v), j = col_of(b);
@@ -343,9 +391,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
                 }
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < F; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < F; ++b)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int64_t i = row_of(a, v), j = col_of(b);
@@ -360,31 +408,32 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
             }
 }
 
-int gemm_f32(const GemmArgs& g, hipStream_t st) {
-    if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return IC_OK;
-    const int64_t tm = cdiv(g.M, BM), tn = cdiv(g.N, BN);
-    int64_t tiles = tm * tn;
-    const bool tri = (g.cmask == CMASK_LOWER || g.cmask == CMASK_UPPER) && tm == tn;
-    if (tri) tiles = tm * (tm + 1) / 2;
+// Tiles of size T for a launch (triangular grids count only the kept triangle).
+template <int T>
+static int64_t tile_count(const GemmArgs& g, bool& tri) {
+    const int64_t tm = cdiv(g.M, T), tn = cdiv(g.N, T);
+    tri = (g.cmask == CMASK_LOWER || g.cmask == CMASK_UPPER) && tm == tn;
+    return tri ? tm * (tm + 1) / 2 : tm * tn;
+}
+
+template <int T>
+static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
+    bool tri;
+    const int64_t tiles = tile_count<T>(g, tri);
+    const int64_t tm = cdiv(g.M, T), tn = cdiv(g.N, T);
     IC_REQUIRE(tiles < (1LL << 30) && g.batch <= 65535, "gemm_f32: problem too large");
-    // 16-byte loads need 16-byte aligned bases and leading dimensions
-    const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
-                         g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;
     // triangular enumerations keep their own (long-K-first) order; other
     // grids with at least NXCD tile rows use the XCD row assignment
     const int remap = (!tri && tm >= NXCD) ? 1 : 0;
     const int64_t grid = remap ? cdiv(tm, NXCD) * tn * NXCD : tiles;
     IC_REQUIRE(grid < (1LL << 23), "gemm_f32: problem too large");
-    const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
-    const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
-    ProfScope prof_scope(st, g.tag, fl, by);
     const dim3 gd((unsigned)grid, 1, (unsigned)g.batch);
     // whole tiles and whole K stages everywhere: the kernel without bounds checks
-    const bool exact = aligned && g.M % BM == 0 && g.N % BN == 0 && g.K % BK == 0;
-#define ICQ_GEMM_LAUNCH(TA, TB)                                                                                  \
-    do {                                                                                                        \
-        if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false>), gd, dim3(256), 0, st, g, tiles, remap);  \
-        else hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, true>), gd, dim3(256), 0, st, g, tiles, remap);         \
+    const bool exact = aligned && g.M % T == 0 && g.N % T == 0 && g.K % BK == 0;
+#define ICQ_GEMM_LAUNCH(TA, TB)                                                                                     \
+    do {                                                                                                           \
+        if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false, T>), gd, dim3(256), 0, st, g, tiles, remap);  \
+        else hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, true, T>), gd, dim3(256), 0, st, g, tiles, remap);         \
     } while (0)
     if (!g.transA && !g.transB) ICQ_GEMM_LAUNCH(0, 0);
     else if (!g.transA) ICQ_GEMM_LAUNCH(0, 1);
@@ -393,6 +442,27 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
 #undef ICQ_GEMM_LAUNCH
     IC_CHECK_LAUNCH();
     return IC_OK;
+}
+
+// Launches with fewer 128-tiles than the chip has CUs run 64-tiles, and so
+// do short-K launches (rank-128 updates) with up to two 128-tiles per CU:
+// there the 128-tile's few long stages leave the tail of the launch on a
+// fraction of the chip.
+constexpr int64_t SMALL_TILE_LIMIT = 256;
+constexpr int64_t SHORT_K = 256, SHORT_K_TILE_LIMIT = 1024;
+
+int gemm_f32(const GemmArgs& g, hipStream_t st) {
+    if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return IC_OK;
+    // 16-byte loads need 16-byte aligned bases and leading dimensions
+    const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
+                         g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;
+    const double fl = g.algo_flops > 0 ? g.algo_flops : 2.0 * g.M * g.N * g.K * g.batch;
+    const double by = 4.0 * g.batch * (g.M * g.K + g.K * g.N + g.M * g.N * (g.beta != 0.0f ? 2 : 1));
+    ProfScope prof_scope(st, g.tag, fl, by);
+    bool tri;
+    const int64_t t128 = tile_count<128>(g, tri) * g.batch;
+    if (t128 < SMALL_TILE_LIMIT || (g.K <= SHORT_K && t128 < SHORT_K_TILE_LIMIT)) return launch_gemm<64>(g, aligned, st);
+    return launch_gemm<128>(g, aligned, st);
 }
 
 }  // namespace icq

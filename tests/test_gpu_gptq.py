@@ -50,6 +50,42 @@ def test_sgemm_matches_fp64(gpu_dev, M, N, K, ta, tb):
     assert (got.double() - want).abs().max().item() <= 2e-6 * scale * max(1, K ** 0.5)
 
 
+@pytest.mark.parametrize("M,N,K", [(2304, 2304, 64), (2100, 2200, 70)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_large_tiles_match_fp64(gpu_dev, M, N, K, ta, tb):
+    # >= 256 tiles of 128: the 128-tile kernel (the cases above take the 64-tile one)
+    g = torch.Generator().manual_seed(M + N * 3 + K + 10 * ta + tb)
+    A = torch.randn(K, M, generator=g) if ta else torch.randn(M, K, generator=g)
+    B = torch.randn(N, K, generator=g) if tb else torch.randn(K, N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    want = 0.5 * ((A.T if ta else A).double() @ (B.T if tb else B).double()) - 2.0 * C0.double()
+    got = _sgemm(A.to(gpu_dev), B.to(gpu_dev), C0.clone().to(gpu_dev), ta, tb, 0.5, -2.0).cpu()
+    scale = ((A.T if ta else A).abs().double() @ (B.T if tb else B).abs().double()).max().item() + 1
+    assert (got.double() - want).abs().max().item() <= 2e-6 * scale * max(1, K ** 0.5)
+
+
+@pytest.mark.parametrize("n", [300, 2900])
+def test_sgemm_masks_both_tiles(gpu_dev, n):
+    # n = 2900: 276 lower tiles of 128 (128-tile kernel); n = 300: 64-tile kernel
+    g = torch.Generator().manual_seed(n)
+    X = torch.tril(torch.randn(n, n, generator=g)) / n ** 0.5
+    C = torch.full((n, n), float("nan"))
+    got = _sgemm(X.to(gpu_dev), X.to(gpu_dev), C.to(gpu_dev), 1, 0, 1.0, 0.0, cmask=2, krange=1).cpu()
+    want = X.double().T @ X.double()
+    iu = torch.triu_indices(n, n)
+    assert torch.allclose(got[iu[0], iu[1]].double(), want[iu[0], iu[1]], atol=3e-5)
+    il = torch.tril_indices(n, n, -1)
+    assert torch.isnan(got[il[0], il[1]]).all()
+    A = torch.randn(n, 160, generator=g)
+    C = torch.randn(n, n, generator=g)
+    got = _sgemm(A.to(gpu_dev), A.to(gpu_dev), C.clone().to(gpu_dev), 0, 1, -1.0, 1.0, cmask=1).cpu()
+    want = C.double() - A.double() @ A.double().T
+    il = torch.tril_indices(n, n)
+    assert torch.allclose(got[il[0], il[1]].double(), want[il[0], il[1]], atol=1e-4)
+    iu = torch.triu_indices(n, n, 1)
+    assert torch.equal(got[iu[0], iu[1]], C[iu[0], iu[1]])
+
+
 def test_sgemm_masks(gpu_dev):
     g = torch.Generator().manual_seed(1)
     n = 300
