@@ -277,6 +277,50 @@ int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float*
                       const float* s, int64_t k, int64_t rows, int64_t cols, int passes, int bits,
                       int* passes_run, void* workspace, void* stream);
 
+/* ---------------------------------------------------------------- PermuQuant */
+
+/* Channel second moments mu2[j] = mean(W[:, j]^2) (converter/permuquant.py:
+ * 13-23, channel_second_moments), fp32 [rows, cols] at pitch ld, summed in
+ * the order torch's CPU reduction uses, so the result is bit-exact with the
+ * reference's CPU path.  cpu_vec (16 for AVX-512 torch builds, 8 for AVX2)
+ * is the vector width of that reduction: the last cols % cpu_vec columns take
+ * its scalar loop.  Workspace: ic_col_moments_workspace_bytes. */
+int64_t ic_col_moments_workspace_bytes(int64_t rows, int64_t cols);
+int ic_col_moments(const float* W, int64_t rows, int64_t cols, int64_t ld, int cpu_vec, float* mu2,
+                   void* workspace, void* stream);
+
+/* perm = argsort(v, descending=True) (permuquant.py:38-40, 61-64): a stable
+ * sort, ties in increasing index, NaN first, -0 equal to +0.  torch's CPU
+ * argsort is not stable from 100 elements on, so on exact ties its order
+ * may differ.  perm: int64 [n].  Workspace: ic_argsort_workspace_bytes. */
+int64_t ic_argsort_workspace_bytes(int64_t n);
+int ic_argsort_desc(const float* v, int64_t n, int64_t* perm, void* workspace, void* stream);
+
+/* compute_group_quant_error (permuquant.py:67-111) of W[:, perm] (perm may
+ * be null: W itself): symmetric RTN with fp16 scales per row (bits 8) or per
+ * group of `group` columns (bits 4, the last group zero-padded), then
+ * sum((W - q s)^2) in the order torch's CPU sum uses with `threads` threads,
+ * bit-exact with the reference run with that many threads.  out: one fp32 on
+ * the device.  perm entries must lie in [0, cols).  Workspace:
+ * ic_group_quant_error_workspace_bytes. */
+int64_t ic_group_quant_error_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int bits, int threads);
+int ic_group_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld, const int64_t* perm, int64_t group,
+                         int bits, int threads, float* out, void* workspace, void* stream);
+
+/* torch.sum(x) of n contiguous fp32 values as torch's CPU kernel computes it
+ * with `threads` threads (the reduction inside ic_group_quant_error). */
+int64_t ic_torch_sum_workspace_bytes(int64_t n, int threads);
+int ic_torch_sum(const float* x, int64_t n, int threads, float* out, void* workspace, void* stream);
+
+/* Gathers that apply a permutation (pipeline.py:588-590, 609, 737;
+ * permuquant.py:208-244): dst[r][j] = src[r][perm[j]] for j < n_perm, and
+ * out[i][j] = H[perm[i]][perm[j]] (H[perm][:, perm]).  Indices outside the
+ * source are not read; their outputs are 0. */
+int ic_permute_cols(const float* src, int64_t rows, int64_t src_cols, int64_t ld_src, const int64_t* perm,
+                    int64_t n_perm, float* dst, int64_t ld_dst, void* stream);
+int ic_permute_sym(const float* H, int64_t n, int64_t ld, const int64_t* perm, int64_t n_perm, float* out,
+                   int64_t ld_out, void* stream);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Launch profiler (no reference counterpart; measurement support).  While
@@ -285,10 +329,10 @@ int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float*
  * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
  * rotation, 7 RTN quantise / INT4 pack, 8 greedy block kernel, 9 other, 10 greedy
  * cross-term GEMMs, 11 Cholesky panel solve, 12 RTN scales / clip search,
- * 13 fp64 verification.  Enabling resets the record.  ic_profile_read
- * synchronises the events and returns, per phase, the summed kernel time
- * (ms), algorithmic flops and bytes, and the launch count (arrays of at least
- * 14 entries). */
+ * 13 fp64 verification, 14 PermuQuant (moments, sort, acceptance error,
+ * gathers).  Enabling resets the record.  ic_profile_read synchronises the
+ * events and returns, per phase, the summed kernel time (ms), algorithmic
+ * flops and bytes, and the launch count (arrays of at least 15 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

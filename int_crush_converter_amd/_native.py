@@ -66,11 +66,21 @@ _SIGS = {
                                  _c.POINTER(_i32), _vp, _vp]),
     "ic_profile_enable": (_i32, [_i32]),
     "ic_profile_read": (_i32, [_vp, _vp, _vp, _vp, _i32]),
+    "ic_col_moments_workspace_bytes": (_i64, [_i64, _i64]),
+    "ic_col_moments": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "ic_argsort_workspace_bytes": (_i64, [_i64]),
+    "ic_argsort_desc": (_i32, [_vp, _i64, _vp, _vp, _vp]),
+    "ic_group_quant_error_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32]),
+    "ic_group_quant_error": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "ic_torch_sum_workspace_bytes": (_i64, [_i64, _i32]),
+    "ic_torch_sum": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp]),
+    "ic_permute_cols": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "ic_permute_sym": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
                 "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
-                "verify"]
+                "verify", "permute"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {

@@ -24,7 +24,8 @@ enum ProfTag : int {
     PT_PANEL = 11,       // Cholesky panel solve (fp64 accumulation)
     PT_RTN_SCALES = 12,  // RTN scales / clipping-ratio search
     PT_VERIFY = 13,      // fp64 quantisation error
-    PT_COUNT = 14,
+    PT_PERMUTE = 14,     // PermuQuant moments, sort, acceptance error, gathers
+    PT_COUNT = 15,
 };
 
 bool prof_enabled();

@@ -34,6 +34,7 @@ class LayerOutput:
     fallbacks: list[str] = field(default_factory=list)
     outliers: int = 0
     bad_scales: bool = False
+    perm: torch.Tensor | None = None     # PermuQuant column permutation (int64), if applied
 
 
 def prepare_weights(tensor: torch.Tensor, rot_size: int) -> tuple[torch.Tensor, torch.Tensor]:

@@ -21,10 +21,11 @@ import warnings
 import torch
 from safetensors.torch import load_file, save_file
 
-from .calibration_io import build_name_map, get_hessian, is_dlr, load_calibration
+from .calibration_io import build_name_map, get_hessian, get_permutation, is_dlr, load_calibration
 from .config import DEFAULT_SKIP_PATTERNS
 from .log import logger
 from .types import ProgressCallback, ProgressInfo, ProgressSummary, QuantizeConfig
+from . import _native as nat
 from . import layer as _layer
 
 
@@ -70,8 +71,7 @@ def _validate(config: QuantizeConfig) -> QuantizeConfig:
         raise ValueError(f"svd_rank must be >= 0, got {config.svd_rank}")
     if config.rot_size > 4096:
         raise ValueError(f"rot_size {config.rot_size} exceeds the supported maximum 4096")
-    for flag, what in [(config.use_permuquant, "PermuQuant (--permuquant)"),
-                       (config.smoothquant, "SmoothQuant / SmoothRot (--smoothquant, --smoothrot)"),
+    for flag, what in [(config.smoothquant, "SmoothQuant / SmoothRot (--smoothquant, --smoothrot)"),
                        (config.svd_rank > 0, "SVD-absorbed (--svd-rank)"),
                        (config.piso_scales, "PiSO (--piso)")]:
         if flag:
@@ -82,7 +82,7 @@ def _validate(config: QuantizeConfig) -> QuantizeConfig:
 def _metadata(config: QuantizeConfig, state_dict, skip_patterns) -> dict[str, str]:
     """int_crush.* metadata (converter/pipeline.py:417-487)."""
     is_int8 = config.int_bits == 8
-    method_base = "int_crush"
+    method_base = "int_crush_permuq" if config.use_permuquant else "int_crush"
     method = f"{method_base}_{config.quant_method}" if config.quant_method in ("gptq", "ldlq") else method_base
     asym = config.asymmetric or (config.quant_method == "gptq" and not is_int8)
     md = {
@@ -102,6 +102,9 @@ def _metadata(config: QuantizeConfig, state_dict, skip_patterns) -> dict[str, st
                 padded[name] = str(t.shape[1])
         if padded:
             md["int_crush.padded_layers"] = ";".join(f"{k}={v}" for k, v in padded.items())
+    if config.use_permuquant:
+        md["int_crush.permuquant"] = "true"
+        md["int_crush.permuquant_tau"] = str(config.tau)
     if config.quant_method == "gptq":
         md["int_crush.gptq_block_size"] = str(config.gptq_block_size)
         md["int_crush.damping_ratio"] = str(config.damping)
@@ -125,6 +128,38 @@ def _comfy_tensor(name: str, config: QuantizeConfig, fmt: bool) -> tuple[str, to
     return f"{prefix}.comfy_quant", torch.tensor(list(blob.encode("utf-8")), dtype=torch.uint8)
 
 
+def _permuquant(name: str, W_work: torch.Tensor, orig_in: int, config: QuantizeConfig, calibration, name_map,
+                state: dict):
+    """PermuQuant step (converter/pipeline.py:572-615): permutes the first
+    orig_in columns of W_work in place; returns (perm or None, whether it
+    came from the calibration file)."""
+    from . import permuquant as _pq
+    layer_name = name_map.get(name) if name_map else None
+    cal_perm = None
+    if layer_name is not None and calibration is not None:
+        cal_perm = get_permutation(calibration, layer_name)
+    if cal_perm is not None:
+        of = min(orig_in, cal_perm.shape[0])
+        ps = cal_perm[:of]
+        if ps.numel() and ps.max() < of and ps.min() >= 0 and ps.unique().numel() == ps.numel():
+            W_work[:, :of] = _pq.permute_columns(W_work[:, :of], ps)
+            state["permuted"] += 1
+            logger.debug("PermuQuant applied (from calibration)")
+            return ps.to(W_work.device), True
+        logger.warning("Calibration permutation out of bounds, falling back to weight-only")
+    W_orig = W_work[:, :orig_in]
+    # per-row INT4 for every method: the acceptance check uses the same granularity
+    gs = W_orig.shape[1] if config.int_bits == 4 else config.perm_group_size
+    perm, alpha, accepted = _pq.sweep_alpha(W_orig, None, gs, config.tau, int_bits=config.int_bits)
+    if not accepted:
+        logger.debug("PermuQuant skipped (no improvement)")
+        return None, False
+    W_work[:, :orig_in] = _pq.permute_columns(W_orig, perm)
+    state["permuted"] += 1
+    logger.debug("PermuQuant applied (alpha=%.2f)", alpha)
+    return perm, False
+
+
 def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, calibration, name_map,
                    state: dict) -> _layer.LayerOutput:
     """One layer of the pipeline loop on the GPU; ``state`` carries counters and
@@ -136,6 +171,9 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
         logger.warning("Zeroed %d outlier weight values in %s (|W| > %.0f)", outliers, name, 1000.0)
     fallbacks: list[str] = []
     packed = None
+    perm, perm_from_cal = None, False
+    if config.use_permuquant:
+        perm, perm_from_cal = _permuquant(name, W_work, tensor.shape[1], config, calibration, name_map, state)
     if config.quant_method in ("gptq", "ldlq"):
         layer_name = name_map.get(name) if name_map else None
         hessian = None
@@ -154,6 +192,25 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
                 raise NotImplementedError("DLR Hessians are not supported by this build")
             if not already and config.rot_size > 0:
                 rot_h = config.rot_size
+            if perm is not None and not perm_from_cal:
+                # re-permute the Hessian for a self-computed permutation (pipeline.py:728-756)
+                from . import permuquant as _pq
+                from .rotation import rotate_hessian_gpu
+                if hessian.dim() == 2:
+                    Hg = nat.to_gpu(hessian).float()
+                    if rot_h:
+                        Hg = rotate_hessian_gpu(Hg, rot_h)
+                        rot_h = 0
+                    hessian = _pq.permute_hessian(Hg, perm)
+                else:
+                    # a block-diagonal Hessian cannot be permuted: undo W_work's permutation
+                    of = min(tensor.shape[1], perm.numel())
+                    inv = torch.empty_like(perm)
+                    inv[perm] = torch.arange(perm.numel(), device=perm.device)
+                    W_work[:, :of] = _pq.permute_columns(W_work[:, :of], inv[:of])
+                    perm = None   # no <name>_perm; the layer stays counted as permuted, like the reference
+                    logger.debug("PermuQuant: un-permuted W_work for block-diagonal Hessian for %s (%dD, shape %s)",
+                                 name, hessian.dim(), tuple(hessian.shape))
     if config.quant_method == "gptq":
         if hessian is not None:
             codes, s16, z8 = _layer.gptq_codes(
@@ -173,7 +230,6 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
         H = None
         if hessian is not None:
             from .rotation import rotate_hessian_gpu
-            from . import _native as nat
             H = nat.to_gpu(hessian).float()
             if rot_h:
                 H = rotate_hessian_gpu(H, rot_h)
@@ -190,6 +246,7 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
         method = "rtn"
     out = _layer.finish(W_work, codes, s16, z8, config.int_bits, packed=packed, method=method,
                         fallbacks=fallbacks, outliers=outliers)
+    out.perm = perm
     if out.bad_scales:
         logger.warning("Replaced bad scale values in %s (Inf/NaN/zero); quality may be degraded", name)
     return out
@@ -224,7 +281,7 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
 
     metadata = _metadata(config, state_dict, skip_patterns)
     output: dict[str, torch.Tensor] = {}
-    state = {"gptq": 0, "rtn_fallback": 0}
+    state = {"gptq": 0, "rtn_fallback": 0, "permuted": 0}
     skipped = quantized = 0
     reports: list[dict] = []
     total = sum(1 for n, t in state_dict.items() if not should_skip(n, skip_patterns) and t.dim() == 2)
@@ -256,6 +313,8 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
         if is_int8 and config.comfy_compat:
             k, v = _comfy_tensor(name, config, fmt=True)
             output[k] = v
+        if out.perm is not None:
+            output[f"{name}_perm"] = out.perm.to(torch.int32).cpu()
         quantized += 1
         if progress_callback is not None:
             elapsed = time.monotonic() - t0
@@ -286,7 +345,7 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
     logger.info("Compression ratio: %.2fx", ratio)
     if progress_callback is not None:
         progress_callback(ProgressSummary(
-            total_layers=quantized, skipped_layers=skipped, permuted_layers=0, gptq_layers=state["gptq"],
+            total_layers=quantized, skipped_layers=skipped, permuted_layers=state["permuted"], gptq_layers=state["gptq"],
             rtn_fallback_layers=state["rtn_fallback"], smoothquant_layers=0, svd_layers=0,
             elapsed_seconds=time.monotonic() - t0, input_size_gb=round(in_gb, 2), output_size_gb=round(out_gb, 2),
             compression_ratio=round(ratio, 2)))

@@ -31,6 +31,14 @@ itself; see tests/test_oracle.py):
     exact greedy_pytorch; golden vectors of the reference's own low-rank
     kernel and its full-rank v2 path (Triton interpreter, tests/golden/).
   * iterative LDLQ / final least-squares scales: golden vectors.
+  * PermuQuant (channel_second_moments .. permuquant_layer): the same torch
+    CPU calls as permuquant.py, so torch's own reductions fix the results;
+    pinned by the reference's KATs (tests/unit/test_permuquant_channel.py:
+    formula [[2,-1],[0,3]] -> [2, 5], descending moments, a scaled channel
+    first, alpha 0 = weight-only, alpha 1 = activation order, zero matrix
+    rejected), by brute force (sorted order, valid permutation), and by the
+    identity that per-row errors of W and W[:, perm] are the same multiset
+    (equal in exact arithmetic, so fp64 sums agree).
 """
 
 from __future__ import annotations
@@ -718,3 +726,87 @@ def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=
                            mse=(W - d).double().pow(2).mean().item(),
                            max_err=(W - d).abs().max().item(),
                            method_used="ldlq_cpu", fallbacks=[])
+
+
+# ---------------------------------------------------------------- PermuQuant
+
+def channel_second_moments(W):
+    """permuquant.py:13-23: per-column mean of squares (torch CPU order)."""
+    return (W ** 2).mean(dim=0)
+
+
+def permutation_weight(W):
+    """permuquant.py:26-41: torch's argsort(descending=True) of the moments
+    (not stable on exact ties from 100 elements on)."""
+    return channel_second_moments(W).argsort(descending=True)
+
+
+def permutation_joint(W, act_mu2, alpha):
+    """permuquant.py:44-69."""
+    v = (act_mu2.clamp(min=1e-12) ** alpha) * (channel_second_moments(W).clamp(min=1e-12) ** (1.0 - alpha))
+    return v.argsort(descending=True)
+
+
+def group_quant_error(W, group_size=128, int_bits=4):
+    """permuquant.py:72-111: sum of squared symmetric-RTN errors, as torch's
+    CPU sum computes it with the current torch.get_num_threads()."""
+    M, N = W.shape
+    if int_bits == 8:
+        s = scales_int8_sym(W)
+        dq = (quant_int8_sym(W, s).float() * s.float())[:, :N]
+    else:
+        s = scales_int4_sym(W, group_size)
+        q = quant_int4_sym(W, s, group_size)
+        G = q.shape[1] // group_size
+        dq = (q.reshape(M, G, group_size).float() * s.unsqueeze(2).float()).reshape(M, G * group_size)[:, :N]
+    return ((W - dq) ** 2).sum().item()
+
+
+def permutation_with_acceptance(W, act_mu2=None, alpha=0.5, group_size=128, tau=0.0, int_bits=4):
+    """permuquant.py:114-156: (perm, accepted)."""
+    perm = permutation_joint(W, act_mu2, alpha) if act_mu2 is not None else permutation_weight(W)
+    e0 = group_quant_error(W, group_size, int_bits)
+    e1 = group_quant_error(W[:, perm], group_size, int_bits)
+    rel = (e0 - e1) / e0 if e0 > 0 else 0.0
+    return perm, rel > tau
+
+
+def sweep_alpha(W, act_mu2=None, group_size=128, tau=0.0, num_alpha=11, int_bits=4):
+    """permuquant.py:159-213: (perm, alpha, accepted)."""
+    if num_alpha < 1:
+        raise ValueError(f"num_alpha must be >= 1, got {num_alpha}")
+    if act_mu2 is None or num_alpha == 1:
+        perm, acc = permutation_with_acceptance(W, act_mu2, 0.0, group_size, tau, int_bits)
+        return perm, 0.0, acc
+    best = (None, 0.0, float("inf"))
+    for i in range(num_alpha):
+        a = i / (num_alpha - 1)
+        perm, acc = permutation_with_acceptance(W, act_mu2, a, group_size, tau, int_bits)
+        if acc:
+            err = group_quant_error(W[:, perm], group_size, int_bits)
+            if err < best[2]:
+                best = (perm, a, err)
+    if best[0] is None:
+        return torch.arange(W.shape[1]), 0.0, False
+    return best[0], best[1], True
+
+
+def permuquant_layer(W_work, orig_in, int_bits, tau, perm_group_size=128, cal_perm=None):
+    """The PermuQuant step of the per-layer pipeline (pipeline.py:572-615):
+    returns (W_work permuted in its first orig_in columns, perm or None,
+    came_from_calibration)."""
+    W_work = W_work.clone()
+    if cal_perm is not None:
+        of = min(orig_in, cal_perm.shape[0])
+        ps = cal_perm[:of]
+        if ps.max() < of and ps.min() >= 0 and ps.unique().numel() == ps.numel():
+            W_orig = W_work[:, :of]
+            W_work[:, :of] = W_orig[:, ps]
+            return W_work, ps, True
+    W_orig = W_work[:, :orig_in]
+    gs = W_orig.shape[1] if int_bits == 4 else perm_group_size
+    perm, _, acc = sweep_alpha(W_orig, None, gs, tau, int_bits=int_bits)
+    if acc:
+        W_work[:, :orig_in] = W_orig[:, perm]
+        return W_work, perm, False
+    return W_work, None, False

@@ -161,3 +161,77 @@ def test_cli_end_to_end(gpu_dev, tmp_path):
     assert set(res) == {"b.0.q.weight", "b.0.q.weight_scale", "b.0.q.weight_zp", "b.0.q.bias", "b.0.q.comfy_quant"}
     assert json.loads(bytes(res["b.0.q.comfy_quant"].tolist()).decode()) == {
         "format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 64}
+
+
+@pytest.mark.parametrize("tau", [0.0, -1.0])
+def test_pipeline_permuquant_rtn_vs_oracle(gpu_dev, tmp_path, tau):
+    # tau = -1 accepts every permutation; tau = 0 follows the reference's
+    # (rounding-decided) decision for per-row INT4
+    g = torch.Generator().manual_seed(12)
+    state = {"blk.0.fc.weight": torch.randn(96, 512, generator=g) * 0.02,
+             "blk.0.fc2.weight": torch.randn(40, 256, generator=g) * 0.05}
+    res, md, ev = _run(tmp_path, state, rot_size=256, int_bits=4, use_permuquant=True, tau=tau)
+    assert md["int_crush.method"] == "int_crush_permuq" and md["int_crush.permuquant"] == "true"
+    assert md["int_crush.permuquant_tau"] == str(tau)
+    permuted = 0
+    from int_crush_converter_amd.rotation import rotate_weights
+    for name, W in state.items():
+        # the reference rotates with an MKL sgemm (fp32 order not reproducible):
+        # the permutation and the decision are bit-exact given the rotated weights
+        Wr = rotate_weights(W.float().to(gpu_dev), 256).cpu()
+        assert torch.allclose(Wr, ref.rotate_weights(W.float(), 256), atol=1e-6)
+        Wp, perm, _ = ref.permuquant_layer(Wr, W.shape[1], 4, tau)
+        if tau < 0:
+            assert perm is not None
+        if perm is None:
+            assert f"{name}_perm" not in res
+        else:
+            permuted += 1
+            assert res[f"{name}_perm"].dtype == torch.int32 and torch.equal(res[f"{name}_perm"].long(), perm)
+        s = ref.scales_int4_sym(Wp, Wp.shape[1])
+        assert torch.equal(res[f"{name}_scale"], s)
+        assert torch.equal(res[name], ref.pack_int4(ref.quant_int4_sym(Wp, s, Wp.shape[1])))
+    assert ev[-1].permuted_layers == permuted
+
+
+def test_pipeline_permuquant_gptq_hessians(gpu_dev, tmp_path):
+    # 2-D H: rotated then re-permuted with the weights; 3-D H: the weights
+    # are un-permuted and no permutation is stored; a calibration
+    # permutation is applied as given
+    g = torch.Generator().manual_seed(13)
+    state = {"layers.0.a.weight": torch.randn(64, 512, generator=g) * 0.02,
+             "layers.0.b.weight": torch.randn(48, 256, generator=g) * 0.02,
+             "layers.0.c.weight": torch.randn(32, 256, generator=g) * 0.02}
+    hs = {"layers.0.a": lognormal_hessian(512, 700, 3),
+          "layers.0.b": torch.stack([lognormal_hessian(256, 400, 4)]),
+          "layers.0.c": lognormal_hessian(256, 400, 5)}
+    cal_perm = torch.randperm(256, generator=g)
+    path = str(tmp_path / "cal.pt")
+    torch.save({"hessians": hs, "shapes": {k: list(v.shape) for k, v in hs.items()},
+                "layer_types": {k: "linear" for k in hs}, "permuquant": {"layers.0.c": cal_perm},
+                "metadata": {"num_samples": 256, "hessian_rotated": False, "rot_size": 0}}, path)
+    res, md, ev = _run(tmp_path, state, rot_size=256, quant_method="gptq", calibration_path=path,
+                       use_permuquant=True, tau=-1.0)
+    assert md["int_crush.method"] == "int_crush_permuq_gptq"
+    from int_crush_converter_amd.rotation import rotate_weights
+    # 2-D (the permutation from the GPU-rotated weights, see above)
+    Wr = rotate_weights(state["layers.0.a.weight"].to(gpu_dev), 256).cpu()
+    Wp, perm, _ = ref.permuquant_layer(Wr, 512, 4, -1.0)
+    assert torch.equal(res["layers.0.a.weight_perm"].long(), perm)
+    Hr = ref.rotate_hessian(hs["layers.0.a"], 256)[perm][:, perm]
+    r = ref.gptq_quantize_layer(Wp, Hr, 128, 0.01, 4)
+    assert torch.equal(res["layers.0.a.weight_scale"], r.scales)
+    assert (ref.unpack_int4(res["layers.0.a.weight"], 512) == r.quantized_W).float().mean().item() >= 0.999
+    # 3-D: back to the unpermuted weights, no <name>_perm
+    assert "layers.0.b.weight_perm" not in res
+    Wb = ref.rotate_weights(state["layers.0.b.weight"], 256)
+    rb = ref.gptq_quantize_layer(Wb, ref.rotate_hessian(hs["layers.0.b"], 256), 128, 0.01, 4)
+    assert torch.equal(res["layers.0.b.weight_scale"], rb.scales)
+    assert (ref.unpack_int4(res["layers.0.b.weight"], 256) == rb.quantized_W).float().mean().item() >= 0.999
+    # calibration permutation: weights permuted, the Hessian taken as it is
+    assert torch.equal(res["layers.0.c.weight_perm"].long(), cal_perm)
+    Wc = ref.rotate_weights(state["layers.0.c.weight"], 256)[:, cal_perm]
+    rc = ref.gptq_quantize_layer(Wc, ref.rotate_hessian(hs["layers.0.c"], 256), 128, 0.01, 4)
+    assert torch.equal(res["layers.0.c.weight_scale"], rc.scales)
+    assert (ref.unpack_int4(res["layers.0.c.weight"], 256) == rc.quantized_W).float().mean().item() >= 0.999
+    assert ev[-1].permuted_layers == 3

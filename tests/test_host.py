@@ -39,11 +39,18 @@ def test_validation_errors(kw, msg):
         _validate(cfg(**kw))
 
 
-@pytest.mark.parametrize("kw", [dict(use_permuquant=True), dict(smoothquant=True, int_bits=8),
-                                dict(svd_rank=16), dict(piso_scales=True)])
+@pytest.mark.parametrize("kw", [dict(smoothquant=True, int_bits=8), dict(svd_rank=16), dict(piso_scales=True)])
 def test_unsupported_features_raise(kw):
     with pytest.raises(NotImplementedError):
         _validate(cfg(**kw))
+
+
+def test_permuquant_config_accepted_and_in_metadata():
+    from int_crush_converter_amd.pipeline import _metadata
+    c = _validate(cfg(use_permuquant=True, tau=0.05, quant_method="rtn"))
+    md = _metadata(c, {}, [])
+    assert md["int_crush.method"] == "int_crush_permuq"
+    assert md["int_crush.permuquant"] == "true" and md["int_crush.permuquant_tau"] == "0.05"
 
 
 def test_should_skip_default_patterns():

@@ -433,3 +433,77 @@ def test_greedy_gpu_golden(golden_greedy_gpu, case):
         Hk = (U_k * s_k) @ U_k.T
         Hg = (t[f"{case}.U_k"] * t[f"{case}.s_k"]) @ t[f"{case}.U_k"].T
         assert ((Hk - Hg).norm() / Hg.norm()).item() < 1e-5
+
+
+# ---------------------------------------------------------------- PermuQuant
+
+def test_permuquant_moments_kat():
+    # reference tests/unit/test_permuquant_channel.py: formula, ones, zeros
+    W = torch.tensor([[2.0, -1.0], [0.0, 3.0]])
+    assert torch.equal(ref.channel_second_moments(W), torch.tensor([2.0, 5.0]))
+    assert torch.equal(ref.channel_second_moments(torch.ones(8, 16)), torch.ones(16))
+    assert torch.equal(ref.channel_second_moments(torch.zeros(8, 16)), torch.zeros(16))
+
+
+def test_permuquant_permutation_properties():
+    g = torch.Generator().manual_seed(42)
+    W = torch.randn(16, 64, generator=g)
+    W[:, 0] *= 100.0
+    p = ref.permutation_weight(W)
+    assert sorted(p.tolist()) == list(range(64)) and p[0].item() == 0
+    mu = ref.channel_second_moments(W)[p]
+    assert (mu[:-1] >= mu[1:]).all()
+    # brute force: the order of the moments, no ties in random data
+    mu2 = ref.channel_second_moments(W)
+    assert p.tolist() == sorted(range(64), key=lambda i: -mu2[i].item())
+    act = torch.rand(64, generator=g)
+    assert torch.equal(ref.permutation_joint(W, act, 0.0), p)
+    assert torch.equal(ref.permutation_joint(W, act, 1.0), act.argsort(descending=True))
+
+
+def test_permuquant_per_row_error_is_permutation_invariant():
+    # per-row scales: the squared errors of W[:, perm] are those of W permuted,
+    # so exact sums agree and only fp32 rounding separates the two totals
+    g = torch.Generator().manual_seed(7)
+    W = torch.randn(32, 256, generator=g) * 0.02
+    perm = torch.randperm(256, generator=g)
+    for bits in (4, 8):
+        def errs(X):
+            if bits == 8:
+                s = ref.scales_int8_sym(X)
+                d = ref.quant_int8_sym(X, s).float() * s.float()
+            else:
+                s = ref.scales_int4_sym(X, X.shape[1])
+                d = ref.quant_int4_sym(X, s, X.shape[1]).float() * s.float()
+            return ((X - d) ** 2)
+        e0, e1 = errs(W), errs(W[:, perm])
+        assert torch.equal(e0[:, perm], e1)
+        assert e0.double().sum().item() == pytest.approx(e1.double().sum().item(), rel=1e-12)
+        a = ref.group_quant_error(W, 256, bits)
+        assert a == pytest.approx(e0.double().sum().item(), rel=1e-5)
+
+
+def test_permuquant_acceptance_rules():
+    # zero matrix: error 0 -> never accepted (reference test_zero_weight_matrix)
+    _, acc = ref.permutation_with_acceptance(torch.zeros(8, 64), tau=0.0, group_size=64, int_bits=4)
+    assert acc is False
+    # group scales (group 16 < row): accepted exactly when the reordered
+    # error is smaller (tau = 0), and a high tau rejects (reference
+    # test_tau_high_rejects_most); channel magnitudes log-normal
+    seen = set()
+    for seed in range(6):
+        g = torch.Generator().manual_seed(seed)
+        W = torch.randn(16, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 1.5) * 0.01
+        perm, acc = ref.permutation_with_acceptance(W, tau=0.0, group_size=16, int_bits=4)
+        e0, e1 = ref.group_quant_error(W, 16, 4), ref.group_quant_error(W[:, perm], 16, 4)
+        assert acc == (e1 < e0)
+        seen.add(acc)
+        assert ref.permutation_with_acceptance(W, tau=0.99, group_size=16, int_bits=4)[1] is False
+    assert seen == {True, False}
+    g = torch.Generator().manual_seed(4)
+    W = torch.randn(16, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 1.5) * 0.01
+    perm, acc = ref.permutation_with_acceptance(W, tau=0.0, group_size=16, int_bits=4)
+    with pytest.raises(ValueError):
+        ref.sweep_alpha(torch.randn(8, 64), num_alpha=0)
+    p, a, acc = ref.sweep_alpha(W, None, 16, 0.0, 11, 4)
+    assert a == 0.0 and acc is True and torch.equal(p, perm)
