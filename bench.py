@@ -40,6 +40,8 @@ WORKLOADS = {
     "rtn_int8_asym_clip5_rot64_4096x4096": ("rtn8", 4096, 4096, {}),
     "rtn_int4_rot256_64x256": ("rtn4", 64, 256, {}),
     "ldlq_int4_it2_greedy5_rot256_4096x4096": ("ldlq", 4096, 4096, {}),
+    # PermuQuant (weight-only, tau 0) + RTN INT4 on the headline layer shape
+    "rtn_int4_permuquant_rot256_4096x12288": ("pq4", 4096, 12288, {}),
     # one block of configs[4]'s 40-block DiT sweep: four layers, block-diagonal Hessians
     "gptq_int4_rot256_dit_block": ("dit", 0, 0, {"layers": [("qkv", 12288, 4096), ("proj", 4096, 4096),
                                                             ("mlp_up", 16384, 4096), ("mlp_down", 4096, 16384)],
@@ -84,7 +86,7 @@ def make_inputs(kind, M, N, extra, seed=0):
         z = torch.randn(M, N, generator=g, device=dev)
         chi = (torch.randn(M, N, 4, generator=g, device=dev) ** 2).sum(-1)
         W = z / torch.sqrt(chi / 4) * (0.02 / math.sqrt(2))
-    W = W.to(torch.bfloat16 if kind != "rtn4" else torch.float32)
+    W = W.to(torch.bfloat16 if kind not in ("rtn4",) else torch.float32)
     if kind == "gptq":
         S = extra["samples"]
         s = torch.exp(torch.randn(N, generator=g, device=dev))
@@ -116,6 +118,14 @@ def gpu_step(kind, W, H):
         W_work, _ = L.prepare_weights(W, 256)
         codes, s16, z8, packed = L.rtn_codes(W_work, 4, False, None)
         return L.finish(W_work, codes, s16, z8, 4, packed=packed)
+    if kind == "pq4":
+        from int_crush_converter_amd import permuquant as pq
+        W_work, _ = L.prepare_weights(W, 256)
+        perm, accepted, Wp = pq.weight_only_permutation(W_work, W_work.shape[1], 0.0, 4)
+        if accepted:
+            W_work = Wp
+        codes, s16, z8, packed = L.rtn_codes(W_work, 4, False, None)
+        return L.finish(W_work, codes, s16, z8, 4, packed=packed)
     if kind == "ldlq":
         import warnings
         from int_crush_converter_amd.ldlq import ldlq_quantize_layer
@@ -145,6 +155,10 @@ def cpu_step(kind, W, H):
         q, s, z = ref.rtn_layer(Wr, 8, True, [0.8, 0.85, 0.9, 0.95, 1.0])
     elif kind == "rtn4":
         Wr = ref.rotate_weights(Wf, 256)
+        q, s, z = ref.rtn_layer(Wr, 4, False, None)
+    elif kind == "pq4":
+        Wr = ref.rotate_weights(Wf, 256)
+        Wr, _, _ = ref.permuquant_layer(Wr, Wr.shape[1], 4, 0.0)
         q, s, z = ref.rtn_layer(Wr, 4, False, None)
     else:
         import warnings

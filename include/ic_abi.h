@@ -329,10 +329,11 @@ int ic_permute_sym(const float* H, int64_t n, int64_t ld, const int64_t* perm, i
  * GEMMs, 3 diagonal-block factor, 4 sweep, 5 weight rotation, 6 Hessian
  * rotation, 7 RTN quantise / INT4 pack, 8 greedy block kernel, 9 other, 10 greedy
  * cross-term GEMMs, 11 Cholesky panel solve, 12 RTN scales / clip search,
- * 13 fp64 verification, 14 PermuQuant (moments, sort, acceptance error,
- * gathers).  Enabling resets the record.  ic_profile_read synchronises the
- * events and returns, per phase, the summed kernel time (ms), algorithmic
- * flops and bytes, and the launch count (arrays of at least 15 entries). */
+ * 13 fp64 verification, 14 PermuQuant (moments, sort, error scales,
+ * gathers), 15 PermuQuant ordered error sums.  Enabling resets the record.
+ * ic_profile_read synchronises the events and returns, per phase, the summed
+ * kernel time (ms), algorithmic flops and bytes, and the launch count
+ * (arrays of at least 16 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

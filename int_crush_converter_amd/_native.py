@@ -80,7 +80,7 @@ _SIGS = {
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
                 "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
-                "verify", "permute"]
+                "verify", "permute", "permute_sum"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {
@@ -93,6 +93,7 @@ PROFILE_KERNELS = {
     "rtn_scales_kernel": ["rtn_scales"],
     "rtn_quant_kernel": ["rtn_quant_pack"],
     "quant_error_partial": ["verify"],
+    "fsum_block_kernel": ["permute_sum"],
 }
 
 

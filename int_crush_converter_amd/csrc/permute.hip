@@ -84,12 +84,26 @@ __device__ __forceinline__ float cascade_block(Get get, int64_t b, int lp) {
     const int64_t S = int64_t(1) << lp;
     const int64_t i0 = b << (2 * lp);
     float a1 = 0.0f;
-    for (int64_t g = 0; g < S; ++g) {
-        float a0 = 0.0f;
-        for (int64_t j = 0; j < S; ++j) a0 = a0 + get(i0 + g * S + j);
-        a1 = a1 + a0;
-    }
+    for (int64_t g = 0; g < S; ++g) a1 = a1 + seq_sum(get, i0 + g * S, S);
     return a1;
+}
+
+// Sequential sum (from 0) of get(i0) .. get(i0 + n - 1): the values are
+// loaded GB at a time before they are added, so their latencies overlap.
+constexpr int GB = 16;
+template <typename Get>
+__device__ __forceinline__ float seq_sum(Get get, int64_t i0, int64_t n) {
+    float a = 0.0f;
+    int64_t i = 0;
+    for (; i + GB <= n; i += GB) {
+        float v[GB];
+#pragma unroll
+        for (int u = 0; u < GB; ++u) v[u] = get(i0 + i + u);
+#pragma unroll
+        for (int u = 0; u < GB; ++u) a = a + v[u];
+    }
+    for (; i < n; ++i) a = a + get(i0 + i);
+    return a;
 }
 
 // The cascade of a sequence of L values from its whole-block values
@@ -99,7 +113,21 @@ __device__ float cascade_finish(Blk blk, Get get, int64_t L, int lp) {
     const int64_t S = int64_t(1) << lp;
     const int64_t nb = L >> (2 * lp);
     float a2 = 0.0f, a3 = 0.0f;
-    for (int64_t b = 0; b < nb; ++b) {
+    int64_t b = 0;
+    for (; b + GB <= nb; b += GB) {
+        float v[GB];
+#pragma unroll
+        for (int u = 0; u < GB; ++u) v[u] = blk(b + u);
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+            a2 = a2 + v[u];
+            if (((b + u + 1) & (S - 1)) == 0) {
+                a3 = a3 + a2;
+                a2 = 0.0f;
+            }
+        }
+    }
+    for (; b < nb; ++b) {
         a2 = a2 + blk(b);
         if (((b + 1) & (S - 1)) == 0) {
             a3 = a3 + a2;
@@ -107,13 +135,9 @@ __device__ float cascade_finish(Blk blk, Get get, int64_t L, int lp) {
         }
     }
     int64_t i = nb << (2 * lp);
-    float a1 = 0.0f, a0 = 0.0f;
-    while (i + S <= L) {
-        float g = 0.0f;
-        for (int64_t j = 0; j < S; ++j, ++i) g = g + get(i);
-        a1 = a1 + g;
-    }
-    for (; i < L; ++i) a0 = a0 + get(i);
+    float a1 = 0.0f;
+    for (; i + S <= L; i += S) a1 = a1 + seq_sum(get, i, S);
+    float a0 = seq_sum(get, i, L - i);
     a0 = a0 + a1;
     a0 = a0 + a2;
     a0 = a0 + a3;
@@ -163,32 +187,65 @@ __global__ void colmom_finish_kernel(const float* W, int64_t rows, int64_t cols,
 
 // ------------------------------------------------------------ full sums
 
+// Element access of the summed tensor: a plain fp32 array, or the squared
+// RTN errors of a (column-permuted) matrix computed on the fly.  Both give
+// element k of the logical row-major tensor; at(row, col) is the same for
+// matrices, and the block kernel walks (row, col) incrementally.
+struct ArraySrc {
+    const float* x;
+    int64_t cols;      // row length of the logical tensor (a vector: its length)
+    __device__ __forceinline__ float at(int64_t r, int64_t c) const { return x[r * cols + c]; }
+    __device__ __forceinline__ float operator()(int64_t k) const { return x[k]; }
+};
+
+// e = (w - q s)^2, w = W[r][perm[c]] (or W[r][c]), s the scale of its group,
+// q = clamp(rhaz(w / s), qmin, qmax): the reference's dequantised error.
+struct ErrSrc {
+    const float* W;
+    int64_t ld, cols, group;
+    const int64_t* perm;
+    const float* S;      // [rows, ngroups] scales
+    int64_t ngroups;
+    float qmin, qmax;
+    __device__ __forceinline__ float at(int64_t r, int64_t c) const {
+        const float w = W[r * ld + (perm ? perm[c] : c)];
+        // 32-bit group index (cols < 2^31); one group per row needs none
+        const int64_t gi = ngroups == 1 ? 0 : (int64_t)((uint32_t)c / (uint32_t)group);
+        const float sc = S[r * ngroups + gi];
+        const float q = clampf(rhaz(w / sc), qmin, qmax);
+        const float d = w - q * sc;
+        return d * d;
+    }
+    __device__ __forceinline__ float operator()(int64_t k) const { return at(k / cols, k % cols); }
+};
+
 // torch's contiguous inner sum of x[0 .. L), sequentially (small L).
-__device__ float inner_sum_seq(const float* x, int64_t L) {
+template <typename Src>
+__device__ float inner_sum_seq(const Src& x, int64_t L) {
     const int64_t vs = L / SUM_VEC;
     if (vs == 0) {
         // scalar loop: four interleaved accumulators
         const int64_t n4 = L / 4;
         const int lp = cascade_lp(n4);
         float p[4];
-        for (int k = 0; k < 4; ++k) p[k] = cascade_seq([&](int64_t m) { return x[4 * m + k]; }, n4, lp);
-        for (int64_t i = 4 * n4; i < L; ++i) p[0] = p[0] + x[i];
+        for (int k = 0; k < 4; ++k) p[k] = cascade_seq([&](int64_t m) { return x(4 * m + k); }, n4, lp);
+        for (int64_t i = 4 * n4; i < L; ++i) p[0] = p[0] + x(i);
         return ((p[0] + p[1]) + p[2]) + p[3];
     }
     const int64_t n4 = vs / 4;
     const int lp = cascade_lp(n4);
     float p[SUM_SEQ];
-    for (int s = 0; s < SUM_SEQ; ++s) p[s] = cascade_seq([&](int64_t m) { return x[SUM_SEQ * m + s]; }, n4, lp);
+    for (int s = 0; s < SUM_SEQ; ++s) p[s] = cascade_seq([&](int64_t m) { return x(SUM_SEQ * m + s); }, n4, lp);
     float f = 0.0f;
     for (int l = 0; l < SUM_VEC; ++l) {
         float a = p[l];
-        for (int64_t v = 4 * n4; v < vs; ++v) a = a + x[v * SUM_VEC + l];
+        for (int64_t v = 4 * n4; v < vs; ++v) a = a + x(v * SUM_VEC + l);
         a = a + p[SUM_VEC + l];
         a = a + p[2 * SUM_VEC + l];
         a = a + p[3 * SUM_VEC + l];
         p[l] = a;
     }
-    for (int64_t e = vs * SUM_VEC; e < L; ++e) f = f + x[e];
+    for (int64_t e = vs * SUM_VEC; e < L; ++e) f = f + x(e);
     for (int l = 0; l < SUM_VEC; ++l) f = f + p[l];
     return f;
 }
@@ -216,8 +273,10 @@ static SumPlan sum_plan(int64_t n, int threads) {
 
 // Block values of the 32 interleaved sequences of every chunk: thread
 // (chunk t, block b, sequence s).  The sequence s of a chunk starting at
-// c0 is x[c0 + 32 m + s], m < n4.
-__global__ void fsum_block_kernel(const float* x, SumPlan p, int64_t nbmax, float* B) {
+// c0 is x[c0 + 32 m + s], m < n4; its elements are visited with a running
+// (row, column) of the logical tensor.
+template <typename Src>
+__global__ void fsum_block_kernel(Src x, SumPlan p, int64_t nbmax, float* B) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int t = blockIdx.y;
     const int s = (int)(gid % SUM_SEQ);
@@ -228,8 +287,19 @@ __global__ void fsum_block_kernel(const float* x, SumPlan p, int64_t nbmax, floa
     const int64_t n4 = (L / SUM_VEC) / 4;
     const int lp = cascade_lp(n4);
     if (b >= (n4 >> (2 * lp))) return;
-    const float* xs = x + c0 + s;
-    B[((int64_t)t * nbmax + b) * SUM_SEQ + s] = cascade_block([&](int64_t m) { return xs[SUM_SEQ * m]; }, b, lp);
+    // element m of the sequence is k = k0 + 32 m: its (row, column) from the
+    // block's first (r0, c0) with a division only when a row ends
+    const int64_t k0 = c0 + (b << (2 * lp)) * SUM_SEQ + s;
+    const int64_t r0 = k0 / x.cols, cc0 = k0 - r0 * x.cols;
+    auto get = [&](int64_t m) {
+        int64_t c = cc0 + (m - (b << (2 * lp))) * SUM_SEQ, r = r0;
+        if (c >= x.cols) {
+            r += c / x.cols;
+            c -= (c / x.cols) * x.cols;
+        }
+        return x.at(r, c);
+    };
+    B[((int64_t)t * nbmax + b) * SUM_SEQ + s] = cascade_block(get, b, lp);
 }
 
 // One work-group per chunk: the 32 sequence cascades from the block values,
@@ -237,15 +307,15 @@ __global__ void fsum_block_kernel(const float* x, SumPlan p, int64_t nbmax, floa
 // the leftover scalars and the lanes (thread 0).  Chunk results go to buf
 // (0 + result, like torch's per-thread buffer) or, for a single chunk,
 // straight to out.
-__global__ void fsum_finish_kernel(const float* x, SumPlan p, int64_t nbmax, const float* B, float* buf,
-                                   float* out) {
+template <typename Src>
+__global__ void fsum_finish_kernel(Src x, SumPlan p, int64_t nbmax, const float* B, float* buf, float* out) {
     __shared__ float ps[SUM_SEQ];
     const int t = blockIdx.x;
     const int s = threadIdx.x;
     const int64_t c0 = (int64_t)t * p.chunk;
     const int64_t L = std::min(p.n, c0 + p.chunk) - c0;
     if (L <= 0) return;                                  // uniform in the work-group
-    const float* xc = x + c0;
+    auto xc = [&](int64_t i) { return x(c0 + i); };
     const int64_t vs = L / SUM_VEC;
     if (vs < 64) {
         // a short chunk: the whole inner sum on one thread
@@ -259,9 +329,8 @@ __global__ void fsum_finish_kernel(const float* x, SumPlan p, int64_t nbmax, con
     const int64_t n4 = vs / 4;
     const int lp = cascade_lp(n4);
     if (s < SUM_SEQ) {
-        const float* xs = xc + s;
         auto blk = [&](int64_t b) { return B[((int64_t)t * nbmax + b) * SUM_SEQ + s]; };
-        ps[s] = cascade_finish(blk, [&](int64_t m) { return xs[SUM_SEQ * m]; }, n4, lp);
+        ps[s] = cascade_finish(blk, [&](int64_t m) { return xc(SUM_SEQ * m + s); }, n4, lp);
     }
     __syncthreads();
     if (s == 0) {
@@ -269,13 +338,13 @@ __global__ void fsum_finish_kernel(const float* x, SumPlan p, int64_t nbmax, con
         float lanes[SUM_VEC];
         for (int l = 0; l < SUM_VEC; ++l) {
             float a = ps[l];
-            for (int64_t v = 4 * n4; v < vs; ++v) a = a + xc[v * SUM_VEC + l];
+            for (int64_t v = 4 * n4; v < vs; ++v) a = a + xc(v * SUM_VEC + l);
             a = a + ps[SUM_VEC + l];
             a = a + ps[2 * SUM_VEC + l];
             a = a + ps[3 * SUM_VEC + l];
             lanes[l] = a;
         }
-        for (int64_t e = vs * SUM_VEC; e < L; ++e) f = f + xc[e];
+        for (int64_t e = vs * SUM_VEC; e < L; ++e) f = f + xc(e);
         for (int l = 0; l < SUM_VEC; ++l) f = f + lanes[l];
         if (p.single) out[0] = 0.0f + f;
         else buf[t] = 0.0f + f;
@@ -284,7 +353,7 @@ __global__ void fsum_finish_kernel(const float* x, SumPlan p, int64_t nbmax, con
 
 // The per-thread buffer (T slots, unused ones 0) summed like any tensor.
 __global__ void fsum_buffer_kernel(const float* buf, int T, float* out) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) out[0] = 0.0f + inner_sum_seq(buf, T);
+    if (threadIdx.x == 0 && blockIdx.x == 0) out[0] = 0.0f + inner_sum_seq(ArraySrc{buf, 1}, T);
 }
 
 // Most whole blocks of any chunk (a shorter last chunk can have a smaller
@@ -308,7 +377,8 @@ static int64_t fsum_ws_floats(int64_t n, int threads) {
     return (int64_t)p.nt * std::max<int64_t>(fsum_nbmax(p), 1) * SUM_SEQ + std::max(threads, 1) + 64;
 }
 
-static int torch_sum(const float* x, int64_t n, int threads, float* out, float* ws, hipStream_t st) {
+template <typename Src>
+static int torch_sum(const Src& x, int64_t n, int threads, float* out, float* ws, hipStream_t st) {
     const SumPlan p = sum_plan(n, threads);
     const int64_t nbmax = fsum_nbmax(p);
     float* B = ws;
@@ -316,12 +386,13 @@ static int torch_sum(const float* x, int64_t n, int threads, float* out, float* 
     if (!p.single) IC_CHECK_HIP(hipMemsetAsync(buf, 0, (size_t)p.T * sizeof(float), st));
     if (nbmax > 0) {
         const int64_t per = nbmax * SUM_SEQ;
-        hipLaunchKernelGGL(fsum_block_kernel, dim3((unsigned)cdiv(per, 256), (unsigned)p.nt), dim3(256), 0, st, x, p,
-                           nbmax, B);
+        ProfScope prof_scope(st, PT_PERM_SUM, (double)n, 4.0 * n);
+        hipLaunchKernelGGL(fsum_block_kernel<Src>, dim3((unsigned)cdiv(per, 256), (unsigned)p.nt), dim3(256), 0, st, x,
+                           p, nbmax, B);
         IC_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(fsum_finish_kernel, dim3((unsigned)p.nt), dim3(64), 0, st, x, p, std::max<int64_t>(nbmax, 1),
-                       B, buf, out);
+    hipLaunchKernelGGL(fsum_finish_kernel<Src>, dim3((unsigned)p.nt), dim3(64), 0, st, x, p,
+                       std::max<int64_t>(nbmax, 1), B, buf, out);
     IC_CHECK_LAUNCH();
     if (!p.single) {
         hipLaunchKernelGGL(fsum_buffer_kernel, dim3(1), dim3(64), 0, st, buf, p.T, out);
@@ -351,28 +422,13 @@ __global__ void perm_scales_kernel(const float* W, int64_t cols, int64_t ld, con
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, part[w]);
-        const float s = clampf(m / div, 1e-5f, 65500.0f);
-        S[r * ngroups + g] = f16_bits_to_f32(f32_to_f16_bits(s));
+        S[r * ngroups + g] = f16_bits_to_f32(f32_to_f16_bits(clampf(m / div, 1e-5f, 65500.0f)));
     }
-}
-
-// e[r][j] = (w - q s)^2 with w = W[r][perm[j]] (or W[r][j]), s the scale of
-// its group, q = clamp(rhaz(w / s), qmin, qmax).
-__global__ void perm_sqerr_kernel(const float* W, int64_t rows, int64_t cols, int64_t ld, const int64_t* perm,
-                                  int64_t group, const float* S, int64_t ngroups, float qmin, float qmax, float* e) {
-    const int64_t r = blockIdx.x;
-    const int64_t j = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
-    if (j >= cols) return;
-    const float w = W[r * ld + (perm ? perm[j] : j)];
-    const float s = S[r * ngroups + j / group];
-    const float q = clampf(rhaz(w / s), qmin, qmax);
-    const float d = w - q * s;
-    e[r * cols + j] = d * d;
 }
 
 // ------------------------------------------------------------ sort
 
-constexpr int SORT_TILE = 16384;          // keys sorted in LDS by one work-group
+constexpr int SORT_TILE = 2048;           // keys sorted in LDS by one work-group (one pair per thread)
 constexpr int SORT_THREADS = 1024;
 
 __device__ __forceinline__ uint64_t desc_key(float v, int64_t i) {
@@ -468,6 +524,23 @@ static int argsort_desc(const float* v, int64_t n, int64_t* perm, uint64_t* keys
 
 // ------------------------------------------------------------ gathers
 
+constexpr int ROW_LDS = 16384;     // floats of a row staged in LDS by permute_cols_lds_kernel
+
+// dst[r][j] = src[r][perm[j]] with the row staged in LDS (src_cols <=
+// ROW_LDS): coalesced reads and writes, the gather inside LDS.
+__global__ __launch_bounds__(1024) void permute_cols_lds_kernel(const float* src, int64_t src_cols, int64_t lds,
+                                                                const int64_t* perm, int64_t np, float* dst,
+                                                                int64_t ldd) {
+    __shared__ float row[ROW_LDS];
+    const int64_t r = blockIdx.x;
+    for (int64_t j = threadIdx.x; j < src_cols; j += blockDim.x) row[j] = src[r * lds + j];
+    __syncthreads();
+    for (int64_t j = threadIdx.x; j < np; j += blockDim.x) {
+        const int64_t c = perm[j];
+        dst[r * ldd + j] = (c >= 0 && c < src_cols) ? row[c] : 0.0f;
+    }
+}
+
 // dst[r][j] = src[r][perm[j]] for j < np; indices outside [0, src_cols)
 // are not read (their outputs are 0).
 __global__ void permute_cols_kernel(const float* src, int64_t rows, int64_t src_cols, int64_t lds, const int64_t* perm,
@@ -541,7 +614,7 @@ extern "C" int64_t ic_group_quant_error_workspace_bytes(int64_t rows, int64_t co
     const int64_t g = bits == 8 ? cols : std::max<int64_t>(group, 1);
     const int64_t ngroups = std::max<int64_t>(cdiv(cols, g), 1);
     const int64_t n = rows * cols;
-    return (n + rows * ngroups + fsum_ws_floats(n, std::max(threads, 1))) * (int64_t)sizeof(float) + 512;
+    return (rows * ngroups + fsum_ws_floats(n, std::max(threads, 1))) * (int64_t)sizeof(float) + 512;
 }
 
 extern "C" int ic_group_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld, const int64_t* perm,
@@ -557,23 +630,23 @@ extern "C" int ic_group_quant_error(const float* W, int64_t rows, int64_t cols, 
         return IC_OK;
     }
     const int64_t n = rows * cols;
-    ProfScope prof_scope(st, PT_PERMUTE, 6.0 * n, 4.0 * n * 4);
     const int64_t g = bits == 8 ? cols : group;
     const int64_t ngroups = cdiv(cols, g);
-    float* e = reinterpret_cast<float*>(workspace);
-    float* S = e + n;
+    float* S = reinterpret_cast<float*>(workspace);
     float* sws = S + rows * ngroups;
     const float div = bits == 8 ? 127.0f : 7.0f;
     const float qmin = bits == 8 ? -128.0f : -8.0f, qmax = bits == 8 ? 127.0f : 7.0f;
-    IC_REQUIRE(rows <= 0x7fffffff && ngroups <= 65535, "ic_group_quant_error: too many rows or groups");
-    hipLaunchKernelGGL(perm_scales_kernel, dim3((unsigned)rows, (unsigned)ngroups), dim3(256), 0, st, W, cols, ld,
-                       perm, g, div, S, ngroups);
-    IC_CHECK_LAUNCH();
-    IC_REQUIRE(cdiv(cols, 256) <= 65535, "ic_group_quant_error: too many columns");
-    hipLaunchKernelGGL(perm_sqerr_kernel, dim3((unsigned)rows, (unsigned)cdiv(cols, 256)), dim3(256), 0, st, W, rows,
-                       cols, ld, perm, g, S, ngroups, qmin, qmax, e);
-    IC_CHECK_LAUNCH();
-    return torch_sum(e, n, threads, out, sws, st);
+    IC_REQUIRE(rows <= 0x7fffffff && cols <= 0x7fffffff && ngroups <= 65535,
+               "ic_group_quant_error: too many rows, columns or groups");
+    {
+        // one group per row: its amax does not depend on the column order
+        ProfScope prof_scope(st, PT_PERMUTE, 0.0, 4.0 * n);
+        hipLaunchKernelGGL(perm_scales_kernel, dim3((unsigned)rows, (unsigned)ngroups), dim3(256), 0, st, W, cols,
+                           ld, ngroups == 1 ? nullptr : perm, g, div, S, ngroups);
+        IC_CHECK_LAUNCH();
+    }
+    const ErrSrc src{W, ld, cols, g, perm, S, ngroups, qmin, qmax};
+    return torch_sum(src, n, threads, out, sws, st);
 }
 
 extern "C" int ic_torch_sum(const float* x, int64_t n, int threads, float* out, void* workspace, void* stream) {
@@ -584,7 +657,8 @@ extern "C" int ic_torch_sum(const float* x, int64_t n, int threads, float* out, 
         IC_CHECK_HIP(hipMemsetAsync(out, 0, sizeof(float), st));
         return IC_OK;
     }
-    return torch_sum(x, n, threads, out, reinterpret_cast<float*>(workspace), st);
+    // one logical row: the block kernel's running column rarely wraps
+    return torch_sum(ArraySrc{x, n}, n, threads, out, reinterpret_cast<float*>(workspace), st);
 }
 
 extern "C" int64_t ic_torch_sum_workspace_bytes(int64_t n, int threads) {
@@ -599,9 +673,14 @@ extern "C" int ic_permute_cols(const float* src, int64_t rows, int64_t src_cols,
     if (rows == 0 || n_perm == 0) return IC_OK;
     hipStream_t st = as_stream(stream);
     ProfScope prof_scope(st, PT_PERMUTE, 0.0, 8.0 * rows * n_perm);
-    const unsigned gy = (unsigned)std::min<int64_t>(cdiv(n_perm, 256), 64);
-    hipLaunchKernelGGL(permute_cols_kernel, dim3((unsigned)rows, gy), dim3(256), 0, st, src, rows, src_cols, ld_src,
-                       perm, n_perm, dst, ld_dst);
+    if (src_cols <= ROW_LDS) {
+        hipLaunchKernelGGL(permute_cols_lds_kernel, dim3((unsigned)rows), dim3(1024), 0, st, src, src_cols, ld_src, perm,
+                           n_perm, dst, ld_dst);
+    } else {
+        const unsigned gy = (unsigned)std::min<int64_t>(cdiv(n_perm, 256), 64);
+        hipLaunchKernelGGL(permute_cols_kernel, dim3((unsigned)rows, gy), dim3(256), 0, st, src, rows, src_cols,
+                           ld_src, perm, n_perm, dst, ld_dst);
+    }
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

@@ -24,8 +24,9 @@ enum ProfTag : int {
     PT_PANEL = 11,       // Cholesky panel solve (fp64 accumulation)
     PT_RTN_SCALES = 12,  // RTN scales / clipping-ratio search
     PT_VERIFY = 13,      // fp64 quantisation error
-    PT_PERMUTE = 14,     // PermuQuant moments, sort, acceptance error, gathers
-    PT_COUNT = 15,
+    PT_PERMUTE = 14,     // PermuQuant moments, sort, error scales, gathers
+    PT_PERM_SUM = 15,    // PermuQuant acceptance error: ordered-sum block kernel
+    PT_COUNT = 16,
 };
 
 bool prof_enabled();

@@ -121,6 +121,17 @@ def compute_group_quant_error(W: torch.Tensor, group_size: int = 128, int_bits: 
     return _quant_error(_as_matrix(W), None, group_size, int_bits, threads)
 
 
+def _acceptance(Wg: torch.Tensor, perm: torch.Tensor, group_size: int, tau: float, int_bits: int,
+                threads: int | None):
+    """(accepted, W[:, perm], error of W[:, perm]): the reordered matrix is
+    gathered once (coalesced) and reused by callers that keep it."""
+    error_orig = _quant_error(Wg, None, group_size, int_bits, threads)
+    Wp = permute_columns(Wg, perm)
+    error_reorder = _quant_error(Wp, None, group_size, int_bits, threads)
+    relative_improvement = (error_orig - error_reorder) / error_orig if error_orig > 0 else 0.0
+    return bool(relative_improvement > tau), Wp, error_reorder
+
+
 def find_permutation_with_acceptance(W: torch.Tensor, act_mu2: torch.Tensor | None = None, alpha: float = 0.5,
                                      group_size: int = 128, tau: float = 0.0, int_bits: int = 4, *,
                                      threads: int | None = None) -> tuple[torch.Tensor, bool]:
@@ -129,10 +140,18 @@ def find_permutation_with_acceptance(W: torch.Tensor, act_mu2: torch.Tensor | No
     Wg = _as_matrix(W)
     perm = find_permutation_joint(Wg, act_mu2, alpha, group_size) if act_mu2 is not None \
         else find_permutation_weight(Wg, group_size)
-    error_orig = _quant_error(Wg, None, group_size, int_bits, threads)
-    error_reorder = _quant_error(Wg, perm, group_size, int_bits, threads)
-    relative_improvement = (error_orig - error_reorder) / error_orig if error_orig > 0 else 0.0
-    return perm, bool(relative_improvement > tau)
+    accepted, _, _ = _acceptance(Wg, perm, group_size, tau, int_bits, threads)
+    return perm, accepted
+
+
+def weight_only_permutation(W: torch.Tensor, group_size: int, tau: float, int_bits: int, *,
+                            threads: int | None = None):
+    """sweep_alpha(W, act_mu2=None, ...) as the pipeline calls it, plus the
+    reordered matrix: (perm, accepted, W[:, perm])."""
+    Wg = _as_matrix(W)
+    perm = find_permutation_weight(Wg, group_size)
+    accepted, Wp, _ = _acceptance(Wg, perm, group_size, tau, int_bits, threads)
+    return perm, accepted, Wp
 
 
 def sweep_alpha(W: torch.Tensor, act_mu2: torch.Tensor | None = None, group_size: int = 128, tau: float = 0.0,
@@ -149,10 +168,10 @@ def sweep_alpha(W: torch.Tensor, act_mu2: torch.Tensor | None = None, group_size
     best_perm, best_alpha, best_error, best_accepted = None, 0.0, float("inf"), False
     for i in range(num_alpha):
         alpha = i / (num_alpha - 1)
-        perm, accepted = find_permutation_with_acceptance(Wg, act_mu2, alpha, group_size, tau, int_bits,
-                                                          threads=threads)
+        perm = find_permutation_joint(Wg, act_mu2, alpha, group_size)
+        accepted, _, error = _acceptance(Wg, perm, group_size, tau, int_bits, threads)
         if accepted:
-            error = _quant_error(Wg, perm, group_size, int_bits, threads)
+            # the reference recomputes this error of W[:, perm]: the same value
             if error < best_error:
                 best_error, best_perm, best_alpha, best_accepted = error, perm, alpha, True
     if best_perm is None:

@@ -149,14 +149,15 @@ def _permuquant(name: str, W_work: torch.Tensor, orig_in: int, config: QuantizeC
         logger.warning("Calibration permutation out of bounds, falling back to weight-only")
     W_orig = W_work[:, :orig_in]
     # per-row INT4 for every method: the acceptance check uses the same granularity
+    # (sweep_alpha without activation statistics: one alpha, 0.0)
     gs = W_orig.shape[1] if config.int_bits == 4 else config.perm_group_size
-    perm, alpha, accepted = _pq.sweep_alpha(W_orig, None, gs, config.tau, int_bits=config.int_bits)
+    perm, accepted, Wp = _pq.weight_only_permutation(W_orig, gs, config.tau, config.int_bits)
     if not accepted:
         logger.debug("PermuQuant skipped (no improvement)")
         return None, False
-    W_work[:, :orig_in] = _pq.permute_columns(W_orig, perm)
+    W_work[:, :orig_in] = Wp
     state["permuted"] += 1
-    logger.debug("PermuQuant applied (alpha=%.2f)", alpha)
+    logger.debug("PermuQuant applied (alpha=%.2f)", 0.0)
     return perm, False
 
 
