@@ -79,8 +79,9 @@ def _validate(config: QuantizeConfig) -> QuantizeConfig:
     return config
 
 
-def _metadata(config: QuantizeConfig, state_dict, skip_patterns) -> dict[str, str]:
-    """int_crush.* metadata (converter/pipeline.py:417-487)."""
+def _metadata(config: QuantizeConfig, shapes, skip_patterns) -> dict[str, str]:
+    """int_crush.* metadata (converter/pipeline.py:417-487); ``shapes`` maps
+    tensor names to shapes, in the input's order."""
     is_int8 = config.int_bits == 8
     method_base = "int_crush_permuq" if config.use_permuquant else "int_crush"
     method = f"{method_base}_{config.quant_method}" if config.quant_method in ("gptq", "ldlq") else method_base
@@ -97,9 +98,9 @@ def _metadata(config: QuantizeConfig, state_dict, skip_patterns) -> dict[str, st
         md["int_crush.exclude_patterns"] = ",".join(config.exclude_patterns)
     if config.rot_size > 0:
         padded = {}
-        for name, t in state_dict.items():
-            if t.dim() == 2 and not should_skip(name, skip_patterns) and t.shape[1] % config.rot_size:
-                padded[name] = str(t.shape[1])
+        for name, shape in shapes.items():
+            if len(shape) == 2 and not should_skip(name, skip_patterns) and shape[1] % config.rot_size:
+                padded[name] = str(shape[1])
         if padded:
             md["int_crush.padded_layers"] = ";".join(f"{k}={v}" for k, v in padded.items())
     if config.use_permuquant:
@@ -253,9 +254,96 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
     return out
 
 
-def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallback | None = None) -> None:
+class _MemoryIO:
+    """The reference's own I/O: the whole state dict in host memory, every
+    output gathered and written by one save_file at the end."""
+
+    def __init__(self, path: str):
+        self.state_dict = load_file(path)
+        self.output: dict[str, torch.Tensor] = {}
+
+    def shapes(self):
+        return {n: tuple(t.shape) for n, t in self.state_dict.items()}
+
+    def nbytes(self, name):
+        t = self.state_dict[name]
+        return t.numel() * t.element_size()
+
+    def tensor(self, name):
+        return self.state_dict[name]
+
+    def passthrough(self, name):
+        self.output[name] = self.state_dict[name]
+
+    def emit(self, name, t):
+        self.output[name] = t.cpu()
+
+    def finish(self, path, metadata):
+        output = {k: v.contiguous() for k, v in self.output.items()}
+        save_file(output, path, metadata=metadata)
+        return sum(t.numel() * t.element_size() for t in output.values())
+
+    def abort(self):
+        pass
+
+
+class _StreamIO:
+    """Streaming I/O: layers read from the file on a host thread and copied to
+    the GPU one layer ahead; results copied back and appended to the output
+    file as they are produced; other tensors copied file to file."""
+
+    def __init__(self, path: str, quantized: list[str], device):
+        from .streaming import Prefetcher, SafetensorsIndex
+        self.index = SafetensorsIndex(path)
+        self.device = device
+        self.quantized = quantized
+        self.prefetch = None
+        self.writer = None
+
+    def start(self, out_path: str, metadata: dict):
+        from .streaming import Prefetcher, StreamWriter, header_reserve
+        self.writer = StreamWriter(out_path, header_reserve(self.index, metadata), self.device)
+        self.prefetch = Prefetcher(self.index, self.quantized, self.device)
+
+    def shapes(self):
+        return {n: e[1] for n, e in self.index.entries.items()}
+
+    def nbytes(self, name):
+        return self.index.nbytes(name)
+
+    def tensor(self, name):
+        return self.prefetch.get(name)
+
+    def passthrough(self, name):
+        self.writer.add_file_copy(name, self.index)
+
+    def emit(self, name, t):
+        if t.is_cuda:
+            self.writer.add_device(name, t)
+        else:
+            self.writer.add_host(name, t)
+
+    def finish(self, path, metadata):
+        self.prefetch.close()
+        self.writer.close(metadata)
+        return self.writer.offset
+
+    def abort(self):
+        if self.prefetch is not None:
+            self.prefetch.close()
+        if self.writer is not None:
+            self.writer.abort()
+
+
+def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallback | None = None,
+                   streaming: bool = True) -> None:
     """Quantise every 2-D, non-skipped tensor of ``config.input_path`` and write
-    ``<output_dir>/model.safetensors`` (reference pipeline.py:150-1179)."""
+    ``<output_dir>/model.safetensors`` (reference pipeline.py:150-1179).
+
+    ``streaming`` (default) reads and writes the file layer by layer with the
+    host<->device copies overlapped with the GPU work; False keeps the
+    reference's load-everything / save-once I/O (same output tensors and
+    metadata)."""
     skip_patterns = config.skip_patterns if config.skip_patterns is not None else DEFAULT_SKIP_PATTERNS
     if config.exclude_patterns:
         skip_patterns = list(skip_patterns) + config.exclude_patterns
@@ -269,73 +357,90 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
     os.makedirs(config.output_dir, exist_ok=True)
 
     logger.info("Loading %s...", config.input_path)
-    state_dict = load_file(config.input_path)
-    logger.info("Loaded %d tensors", len(state_dict))
+    if streaming:
+        from .streaming import SafetensorsIndex
+        idx = SafetensorsIndex(config.input_path)
+        shapes = {n: e[1] for n, e in idx.entries.items()}
+        todo = [n for n, sh in shapes.items() if not should_skip(n, skip_patterns) and len(sh) == 2]
+        io = _StreamIO(config.input_path, todo, nat.device())
+    else:
+        io = _MemoryIO(config.input_path)
+        shapes = io.shapes()
+    names = list(shapes)
+    logger.info("Loaded %d tensors", len(names))
 
     calibration, name_map = None, {}
     if config.quant_method in ("gptq", "ldlq") and config.calibration_path:
         logger.info("Loading calibration from %s...", config.calibration_path)
         calibration = load_calibration(config.calibration_path)
         cal_keys = list(calibration["hessians"].keys())
-        name_map = build_name_map(list(state_dict.keys()), cal_keys)
+        name_map = build_name_map(names, cal_keys)
         logger.info("Matched %d/%d calibration layers to model layers", len(name_map), len(cal_keys))
 
-    metadata = _metadata(config, state_dict, skip_patterns)
-    output: dict[str, torch.Tensor] = {}
+    metadata = _metadata(config, shapes, skip_patterns)
+    path = os.path.join(config.output_dir, "model.safetensors")
+    if streaming:
+        io.start(path, metadata)
     state = {"gptq": 0, "rtn_fallback": 0, "permuted": 0}
     skipped = quantized = 0
     reports: list[dict] = []
-    total = sum(1 for n, t in state_dict.items() if not should_skip(n, skip_patterns) and t.dim() == 2)
+    total = sum(1 for n, sh in shapes.items() if not should_skip(n, skip_patterns) and len(sh) == 2)
     t0 = time.monotonic() if progress_callback is not None else None
+    written: set[str] = set()
 
-    for name, tensor in state_dict.items():
-        if should_skip(name, skip_patterns) or tensor.dim() != 2:
-            output[name] = tensor
-            skipped += 1
-            continue
-        logger.info("Quantizing %s (%s)...", name, tensor.shape)
-        out = quantize_layer(name, tensor, config, calibration, name_map, state)
-        logger.debug("MSE=%.6f  max_err=%.4f", out.mse, out.max_err)
-        if config.quality_report_path is not None:
-            fb = list(out.fallbacks) + (["scale_repair"] if out.bad_scales else [])
-            reports.append({
-                "name": name, "method": out.method, "mse": out.mse, "max_err": out.max_err,
-                "scale_range": [out.scales.min().item(), out.scales.max().item()],
-                "fallbacks": fb, "shape": list(tensor.shape), "smoothquant": False, "smoothrot": False,
-                "smooth_source": None, "svd_rank": 0,
-            })
-        output[name] = out.stored.cpu()
-        output[f"{name}_scale"] = out.scales.cpu()
-        if out.zero_points is not None:
-            output[f"{name}_zp"] = out.zero_points.cpu()
-        if is_int8 and config.comfy_int8_fast:
-            k, v = _comfy_tensor(name, config, fmt=False)
-            output[k] = v
-        if is_int8 and config.comfy_compat:
-            k, v = _comfy_tensor(name, config, fmt=True)
-            output[k] = v
-        if out.perm is not None:
-            output[f"{name}_perm"] = out.perm.to(torch.int32).cpu()
-        quantized += 1
-        if progress_callback is not None:
-            elapsed = time.monotonic() - t0
-            remaining = elapsed / quantized * (total - quantized) if quantized > 1 else 0.0
-            progress_callback(ProgressInfo(
-                current_layer=quantized, total_layers=total, layer_name=name, layer_shape=tuple(tensor.shape),
-                elapsed_seconds=elapsed, estimated_remaining_seconds=max(remaining, 0.0), method=out.method,
-                mse=out.mse))
-        if name.endswith(".weight"):
-            bias = name[: -len(".weight")] + ".bias"
-            if bias in state_dict:
-                output[bias] = state_dict[bias]
+    try:
+        for name in names:
+            if should_skip(name, skip_patterns) or len(shapes[name]) != 2:
+                if name not in written:      # a bias may have gone out with its weight already
+                    io.passthrough(name)
+                    written.add(name)
+                skipped += 1
+                continue
+            logger.info("Quantizing %s (%s)...", name, tuple(shapes[name]))
+            out = quantize_layer(name, io.tensor(name), config, calibration, name_map, state)
+            logger.debug("MSE=%.6f  max_err=%.4f", out.mse, out.max_err)
+            if config.quality_report_path is not None:
+                fb = list(out.fallbacks) + (["scale_repair"] if out.bad_scales else [])
+                reports.append({
+                    "name": name, "method": out.method, "mse": out.mse, "max_err": out.max_err,
+                    "scale_range": [out.scales.min().item(), out.scales.max().item()],
+                    "fallbacks": fb, "shape": list(shapes[name]), "smoothquant": False, "smoothrot": False,
+                    "smooth_source": None, "svd_rank": 0,
+                })
+            io.emit(name, out.stored)
+            io.emit(f"{name}_scale", out.scales)
+            if out.zero_points is not None:
+                io.emit(f"{name}_zp", out.zero_points)
+            if is_int8 and config.comfy_int8_fast:
+                k, v = _comfy_tensor(name, config, fmt=False)
+                io.emit(k, v)
+            if is_int8 and config.comfy_compat:
+                k, v = _comfy_tensor(name, config, fmt=True)
+                io.emit(k, v)
+            if out.perm is not None:
+                io.emit(f"{name}_perm", out.perm.to(torch.int32))
+            written.add(name)
+            quantized += 1
+            if progress_callback is not None:
+                elapsed = time.monotonic() - t0
+                remaining = elapsed / quantized * (total - quantized) if quantized > 1 else 0.0
+                progress_callback(ProgressInfo(
+                    current_layer=quantized, total_layers=total, layer_name=name, layer_shape=tuple(shapes[name]),
+                    elapsed_seconds=elapsed, estimated_remaining_seconds=max(remaining, 0.0), method=out.method,
+                    mse=out.mse))
+            if name.endswith(".weight"):
+                bias = name[: -len(".weight")] + ".bias"
+                if bias in shapes and bias not in written:
+                    io.passthrough(bias)
+                    written.add(bias)
+        logger.info("Saving to %s...", path)
+        out_bytes = io.finish(path, metadata)
+    except BaseException:
+        io.abort()
+        raise
 
-    output = {k: v.contiguous() for k, v in output.items()}
-    path = os.path.join(config.output_dir, "model.safetensors")
-    logger.info("Saving to %s...", path)
-    save_file(output, path, metadata=metadata)
-
-    in_gb = sum(t.numel() * t.element_size() for t in state_dict.values()) / (1024 ** 3)
-    out_gb = sum(t.numel() * t.element_size() for t in output.values()) / (1024 ** 3)
+    in_gb = sum(io.nbytes(n) for n in names) / (1024 ** 3)
+    out_gb = out_bytes / (1024 ** 3)
     ratio = in_gb / out_gb if out_gb else 0.0
     logger.info("Done! Quantized %d layers, skipped %d layers", quantized, skipped)
     if config.quant_method in ("gptq", "ldlq"):

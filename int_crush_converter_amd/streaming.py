@@ -1,0 +1,293 @@
+"""Streaming safetensors I/O for the model loop (the reference loads the
+whole model with ``load_file`` and writes it with one ``save_file``,
+converter/pipeline.py:268, 1116-1121).
+
+* ``SafetensorsIndex`` parses a file's header: tensors in data order, which
+  is the order ``load_file`` returns them in (the reference's loop order).
+* ``Prefetcher`` reads the next layers' bytes on a host thread into pinned
+  buffers and copies them to the GPU on a copy stream while the current
+  layer computes.
+* ``StreamWriter`` writes outputs as they are produced: device results are
+  copied to pinned buffers on a D2H stream, a host thread appends them to the
+  file, and tensors passed through unchanged are copied file to file.  The
+  header goes into a region reserved at the start and padded with spaces
+  (the safetensors format allows a space-padded header), so no tensor is
+  held until the end.  The file is written under a temporary name and
+  renamed when complete: an aborted run leaves no output.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import queue
+import struct
+import threading
+
+import torch
+
+ST_TO_TORCH = {
+    "F64": torch.float64, "F32": torch.float32, "F16": torch.float16, "BF16": torch.bfloat16,
+    "I64": torch.int64, "I32": torch.int32, "I16": torch.int16, "I8": torch.int8, "U8": torch.uint8,
+    "BOOL": torch.bool,
+}
+TORCH_TO_ST = {v: k for k, v in ST_TO_TORCH.items()}
+
+
+class SafetensorsIndex:
+    """Header of a safetensors file: name -> (dtype, shape, begin, end) in
+    data order; absolute byte offsets."""
+
+    def __init__(self, path: str):
+        self.path = path
+        with open(path, "rb") as f:
+            n = struct.unpack("<Q", f.read(8))[0]
+            header = json.loads(f.read(n))
+        self.metadata = header.pop("__metadata__", None)
+        base = 8 + n
+        items = sorted(header.items(), key=lambda kv: kv[1]["data_offsets"][0])
+        self.entries = {}
+        for name, e in items:
+            b, end = e["data_offsets"]
+            if e["dtype"] not in ST_TO_TORCH:
+                raise ValueError(f"{path}: unsupported dtype {e['dtype']} for {name}")
+            self.entries[name] = (ST_TO_TORCH[e["dtype"]], tuple(e["shape"]), base + b, base + end)
+
+    def names(self) -> list[str]:
+        return list(self.entries)
+
+    def nbytes(self, name: str) -> int:
+        _, _, b, e = self.entries[name]
+        return e - b
+
+    def read(self, name: str, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The tensor as a CPU tensor (into `out`'s storage when given: a
+        uint8 buffer of at least nbytes, e.g. pinned)."""
+        dtype, shape, b, e = self.entries[name]
+        n = e - b
+        buf = out[:n] if out is not None else torch.empty(n, dtype=torch.uint8)
+        with open(self.path, "rb", buffering=0) as f:
+            f.seek(b)
+            mv = memoryview(buf.numpy())
+            got = 0
+            while got < n:
+                r = f.readinto(mv[got:])
+                if not r:
+                    raise IOError(f"{self.path}: short read of {name}")
+                got += r
+        t = buf.view(dtype) if n else torch.empty(0, dtype=dtype)
+        return t.reshape(shape)
+
+
+class Prefetcher:
+    """Reads `names` in order on a host thread into pinned buffers (`depth`
+    of them) and copies each to the GPU on a copy stream one layer ahead:
+    get(name) returns layer k and starts layer k + 1's copy, which then
+    overlaps the caller's work on layer k.  Names must be requested in
+    order."""
+
+    def __init__(self, index: SafetensorsIndex, names: list[str], device, depth: int = 2):
+        self.index = index
+        self.names = list(names)
+        self.device = device
+        cap = max([index.nbytes(n) for n in self.names] + [1])
+        self.free: queue.Queue = queue.Queue()
+        for _ in range(depth):
+            self.free.put(torch.empty(cap, dtype=torch.uint8, pin_memory=True))
+        self.ready: queue.Queue = queue.Queue()
+        self.stream = torch.cuda.Stream(device=device)
+        self.inflight: dict[str, tuple] = {}
+        self.started = 0
+        self.error: BaseException | None = None
+        self.thread = threading.Thread(target=self._run, daemon=True)
+        self.thread.start()
+
+    def _run(self):
+        try:
+            for name in self.names:
+                buf = self.free.get()
+                if buf is None:
+                    return
+                t = self.index.read(name, buf)
+                self.ready.put((name, buf, t))
+        except BaseException as e:  # surfaced to the consumer
+            self.error = e
+            self.ready.put(None)
+
+    def _start_next(self):
+        if self.started >= len(self.names):
+            return
+        item = self.ready.get()
+        if item is None:
+            raise RuntimeError(f"reading {self.index.path} failed: {self.error}") from self.error
+        name, buf, t = item
+        self.started += 1
+        with torch.cuda.stream(self.stream):
+            g = torch.empty(t.shape, dtype=t.dtype, device=self.device)
+            g.copy_(t, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+        self.inflight[name] = (g, buf, ev)
+
+    def get(self, name: str) -> torch.Tensor:
+        if name not in self.inflight:
+            self._start_next()
+        if name not in self.inflight:
+            raise KeyError(f"{name} requested out of order")
+        g, buf, ev = self.inflight.pop(name)
+        cur = torch.cuda.current_stream(self.device)
+        cur.wait_event(ev)
+        g.record_stream(cur)
+        ev.synchronize()          # its pinned buffer can be refilled
+        self.free.put(buf)
+        self._start_next()
+        return g
+
+    def close(self):
+        for _ in range(4):
+            self.free.put(None)
+
+
+class StreamWriter:
+    """Appends tensors to a safetensors file as they come; header at close."""
+
+    def __init__(self, path: str, reserve: int, device=None):
+        self.path = path
+        self.tmp = path + ".partial"
+        self.reserve = max(int(reserve), 64)
+        self.f = open(self.tmp, "wb")
+        self.f.write(b"\0" * (8 + self.reserve))
+        self.offset = 0
+        self.header: dict[str, dict] = {}
+        self.jobs: queue.Queue = queue.Queue(maxsize=8)
+        self.error: BaseException | None = None
+        self.device = device
+        self.stream = torch.cuda.Stream(device=device) if device is not None else None
+        self.thread = threading.Thread(target=self._run, daemon=True)
+        self.thread.start()
+
+    def _record(self, name, dtype, shape, n):
+        if name in self.header:
+            raise ValueError(f"tensor {name} written twice")
+        self.header[name] = {"dtype": TORCH_TO_ST[dtype], "shape": list(shape),
+                             "data_offsets": [self.offset, self.offset + n]}
+        self.offset += n
+
+    def _run(self):
+        try:
+            while True:
+                job = self.jobs.get()
+                if job is None:
+                    return
+                kind = job[0]
+                if kind == "host":
+                    _, data = job
+                    self.f.write(memoryview(data.numpy()))
+                elif kind == "dev":
+                    _, ev, data = job
+                    ev.synchronize()
+                    self.f.write(memoryview(data.numpy()))
+                elif kind == "copy":
+                    _, src_path, b, n = job
+                    with open(src_path, "rb", buffering=0) as s:
+                        s.seek(b)
+                        left = n
+                        while left:
+                            chunk = s.read(min(left, 64 << 20))
+                            if not chunk:
+                                raise IOError(f"{src_path}: short read")
+                            self.f.write(chunk)
+                            left -= len(chunk)
+        except BaseException as e:
+            self.error = e
+
+    def _put(self, job):
+        if self.error is not None:
+            raise RuntimeError(f"stream writer failed: {self.error}") from self.error
+        self.jobs.put(job)
+
+    def add_host(self, name: str, t: torch.Tensor):
+        t = t.contiguous()
+        data = t.reshape(-1).view(torch.uint8) if t.numel() else torch.empty(0, dtype=torch.uint8)
+        self._record(name, t.dtype, t.shape, data.numel())
+        self._put(("host", data))
+
+    def add_file_copy(self, name: str, index: SafetensorsIndex):
+        dtype, shape, b, e = index.entries[name]
+        self._record(name, dtype, shape, e - b)
+        self._put(("copy", index.path, b, e - b))
+
+    def add_device(self, name: str, t: torch.Tensor):
+        """Copy a GPU tensor to a pinned buffer on the D2H stream (after the
+        current stream's work on it) and append it when the copy is done."""
+        t = t.contiguous()
+        n = t.numel() * t.element_size()
+        self._record(name, t.dtype, t.shape, n)
+        if n == 0:
+            self._put(("host", torch.empty(0, dtype=torch.uint8)))
+            return
+        host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        cur = torch.cuda.current_stream(t.device)
+        self.stream.wait_stream(cur)
+        with torch.cuda.stream(self.stream):
+            host.copy_(t.reshape(-1).view(torch.uint8), non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+        t.record_stream(self.stream)
+        self._put(("dev", ev, host))
+
+    def close(self, metadata: dict | None):
+        self._put(None)
+        self.thread.join()
+        if self.error is not None:
+            self.abort()
+            raise RuntimeError(f"stream writer failed: {self.error}") from self.error
+        hdr = dict(self.header)
+        if metadata:
+            hdr = {"__metadata__": metadata, **hdr}
+        blob = json.dumps(hdr, separators=(",", ":")).encode("utf-8")
+        if len(blob) > self.reserve:
+            # header larger than reserved: rewrite with the data shifted
+            self.f.close()
+            self._rewrite(blob)
+        else:
+            blob = blob + b" " * (self.reserve - len(blob))
+            self.f.seek(0)
+            self.f.write(struct.pack("<Q", len(blob)))
+            self.f.write(blob)
+            self.f.close()
+        os.replace(self.tmp, self.path)
+
+    def _rewrite(self, blob: bytes):
+        pad = (-len(blob)) % 8
+        blob = blob + b" " * pad
+        fixed = self.tmp + ".2"
+        with open(self.tmp, "rb") as src, open(fixed, "wb") as dst:
+            dst.write(struct.pack("<Q", len(blob)))
+            dst.write(blob)
+            src.seek(8 + self.reserve)
+            while True:
+                chunk = src.read(64 << 20)
+                if not chunk:
+                    break
+                dst.write(chunk)
+        os.replace(fixed, self.tmp)
+
+    def abort(self):
+        try:
+            self.jobs.put_nowait(None)
+        except queue.Full:
+            pass
+        try:
+            self.f.close()
+        except Exception:
+            pass
+        if os.path.exists(self.tmp):
+            os.remove(self.tmp)
+
+
+def header_reserve(index: SafetensorsIndex, metadata: dict) -> int:
+    """Bytes to reserve for the output header: up to six entries per input
+    tensor (weights, scale, zero-point, permutation, two ComfyUI blobs)."""
+    per = sum(6 * (len(n) + 160) for n in index.names())
+    return 4096 + per + 2 * len(json.dumps(metadata))

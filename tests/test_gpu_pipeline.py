@@ -235,3 +235,40 @@ def test_pipeline_permuquant_gptq_hessians(gpu_dev, tmp_path):
     assert torch.equal(res["layers.0.c.weight_scale"], rc.scales)
     assert (ref.unpack_int4(res["layers.0.c.weight"], 256) == rc.quantized_W).float().mean().item() >= 0.999
     assert ev[-1].permuted_layers == 3
+
+
+def test_streaming_matches_in_memory_io(gpu_dev, tmp_path):
+    # the streaming loop (prefetch, D2H stream, incremental file) writes the
+    # same tensors and metadata as the reference's load-all / save-once I/O
+    from int_crush_converter_amd.pipeline import quantize_model
+    from int_crush_converter_amd.types import QuantizeConfig
+    g = torch.Generator().manual_seed(21)
+    state = {"blocks.0.attn.qkv.weight": (torch.randn(64, 512, generator=g) * 0.02).to(torch.bfloat16),
+             "blocks.0.attn.qkv.bias": torch.randn(64, generator=g),
+             "blocks.0.norm.weight": torch.ones(512),
+             "blocks.0.mlp.up.weight": torch.randn(96, 300, generator=g) * 0.02,
+             "blocks.0.embed.weight": torch.randn(10, 20, generator=g),
+             "blocks.1.attn.qkv.weight": torch.randn(32, 256, generator=g) * 0.02,
+             "blocks.1.attn.qkv.bias": torch.zeros(32)}
+    hs = {"blocks.0.attn.qkv": lognormal_hessian(512, 600, 7), "blocks.1.attn.qkv": lognormal_hessian(256, 400, 8)}
+    cal = _calib(tmp_path, hs)
+    src = str(tmp_path / "in.safetensors")
+    save_file(state, src)
+    outs = []
+    for streaming in (True, False):
+        d = str(tmp_path / f"o{int(streaming)}")
+        ev = []
+        quantize_model(QuantizeConfig(input_path=src, output_dir=d, rot_size=256, quant_method="gptq",
+                                      calibration_path=cal), progress_callback=ev.append, streaming=streaming)
+        with safe_open(os.path.join(d, "model.safetensors"), framework="pt") as f:
+            md = f.metadata()
+        outs.append((load_file(os.path.join(d, "model.safetensors")), md, ev[-1]))
+    (a, ma, sa), (b, mb, sb) = outs
+    assert ma == mb and set(a) == set(b)
+    for k in a:
+        assert a[k].dtype == b[k].dtype and torch.equal(a[k], b[k]), k
+    assert (sa.total_layers, sa.skipped_layers, sa.gptq_layers, sa.rtn_fallback_layers) == \
+        (sb.total_layers, sb.skipped_layers, sb.gptq_layers, sb.rtn_fallback_layers)
+    assert sa.input_size_gb == sb.input_size_gb and sa.output_size_gb == sb.output_size_gb
+    assert torch.equal(a["blocks.0.attn.qkv.bias"], state["blocks.0.attn.qkv.bias"])
+    assert torch.equal(a["blocks.0.embed.weight"], state["blocks.0.embed.weight"])

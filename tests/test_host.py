@@ -60,14 +60,13 @@ def test_should_skip_default_patterns():
     assert not should_skip("blocks.3.attn.qkv.weight", DEFAULT_SKIP_PATTERNS)
 
 
-def _sd():
-    return {"blocks.0.attn.qkv.weight": torch.zeros(4, 300), "blocks.0.norm.weight": torch.zeros(300),
-            "blocks.0.mlp.up.weight": torch.zeros(4, 512)}
+def _sd():   # name -> shape
+    return {"blocks.0.attn.qkv.weight": (4, 300), "blocks.0.norm.weight": (300,), "blocks.0.mlp.up.weight": (4, 512)}
 
 
 def test_metadata_configs():
     """The output contract of the five benchmark configurations."""
-    sd = {"a.weight": torch.zeros(2, 256)}
+    sd = {"a.weight": (2, 256)}   # name -> shape
     assert _metadata(cfg(rot_size=256, int_bits=4), sd, DEFAULT_SKIP_PATTERNS) == {
         "int_crush.format_version": "3", "int_crush.method": "int_crush", "int_crush.rot_size": "256",
         "int_crush.scale_type": "per_row", "int_crush.hadamard_type": "regular", "int_crush.packing_order": "little"}
