@@ -42,6 +42,12 @@ WORKLOADS = {
     "ldlq_int4_it2_greedy5_rot256_4096x4096": ("ldlq", 4096, 4096, {}),
     # PermuQuant (weight-only, tau 0) + RTN INT4 on the headline layer shape
     "rtn_int4_permuquant_rot256_4096x12288": ("pq4", 4096, 12288, {}),
+    # configs[4] end to end, file to file (quantize_model with streaming I/O):
+    # the first 4 of its 40 DiT blocks, bf16 safetensors + 3-D calibration
+    "e2e_dit_gptq_int4_rot256_4blocks": ("e2e", 0, 0, {"blocks": 4, "samples": 4096,
+                                                       "layers": [("attn.qkv", 12288, 4096), ("attn.proj", 4096, 4096),
+                                                                  ("mlp.up", 16384, 4096),
+                                                                  ("mlp.down", 4096, 16384)]}),
     # one block of configs[4]'s 40-block DiT sweep: four layers, block-diagonal Hessians
     "gptq_int4_rot256_dit_block": ("dit", 0, 0, {"layers": [("qkv", 12288, 4096), ("proj", 4096, 4096),
                                                             ("mlp_up", 16384, 4096), ("mlp_down", 4096, 16384)],
@@ -60,6 +66,41 @@ def block_hessian(X):
     n, d = X.shape
     Xb = X.reshape(n, d // 256, 256).permute(1, 0, 2).contiguous()       # [g, n, 256]
     return torch.bmm(Xb.transpose(1, 2).contiguous(), Xb) / n
+
+
+def make_e2e_files(extra, seed=0):
+    """A model file with configs[4]'s layer shapes (bf16, N(0, 0.02^2)) and a
+    calibration file of 3-D block-diagonal Hessians, in a temporary folder."""
+    import tempfile
+    import torch
+    from safetensors.torch import save_file
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    d = tempfile.mkdtemp(prefix="icq_e2e_")
+    state, hess = {}, {}
+    for b in range(extra["blocks"]):
+        for name, out_f, in_f in extra["layers"]:
+            key = f"blocks.{b}.{name}"
+            state[f"{key}.weight"] = (torch.randn(out_f, in_f, generator=g, device=dev) * 0.02).to(torch.bfloat16).cpu()
+            s = torch.exp(torch.randn(in_f, generator=g, device=dev))
+            X = torch.randn(extra["samples"], in_f, generator=g, device=dev) * s
+            hess[key] = block_hessian(X).cpu()
+            del X
+    src = os.path.join(d, "model.safetensors")
+    save_file(state, src)
+    cal = os.path.join(d, "calibration.pt")
+    torch.save({"hessians": hess, "shapes": {k: list(v.shape) for k, v in hess.items()},
+                "layer_types": {k: "linear" for k in hess},
+                "metadata": {"num_samples": extra["samples"], "hessian_rotated": False}}, cal)
+    weights = sum(t.numel() for t in state.values())
+    return d, src, cal, weights
+
+
+def e2e_run(d, src, cal, streaming):
+    from int_crush_converter_amd.pipeline import quantize_model
+    from int_crush_converter_amd.types import QuantizeConfig
+    quantize_model(QuantizeConfig(input_path=src, output_dir=os.path.join(d, "out"), rot_size=256,
+                                  quant_method="gptq", calibration_path=cal), streaming=streaming)
 
 
 def make_inputs(kind, M, N, extra, seed=0):
@@ -237,6 +278,8 @@ def main():
                           "launches": 3}), flush=True)
         return
     kind, M, N, extra = WORKLOADS[args.workload]
+    if kind == "e2e":
+        return main_e2e(args, extra)
     log(f"[bench] workload {args.workload}: generating inputs")
     W, H = make_inputs(kind, M, N, extra)
     nat.lib()
@@ -316,6 +359,80 @@ def main():
                                             "restating the reference's CPU path"}
         log(f"[bench] CPU {c1 - c0:.2f} s")
     print(json.dumps(result), flush=True)
+
+
+def main_e2e(args, extra):
+    """File to file: quantize_model on a synthetic slice of configs[4]; a step
+    is one whole conversion.  Also times the reference's load-all /
+    save-once I/O on the same files (in_memory_ms)."""
+    import shutil
+    import torch
+    from int_crush_converter_amd import _native as nat
+    log(f"[bench] workload {args.workload}: writing the model and calibration files")
+    d, src, cal, weights = make_e2e_files(extra)
+    try:
+        nat.lib()
+        for _ in range(args.warmup):
+            e2e_run(d, src, cal, True)
+        torch.cuda.synchronize()
+        times = {}
+        for streaming in (True, False):
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                e2e_run(d, src, cal, streaming)
+            torch.cuda.synchronize()
+            times[streaming] = (time.perf_counter() - t0) * 1e3 / args.steps
+        ms = times[True]
+        prof = None
+        if not args.no_profile:
+            nat.profile_enable(True)
+            e2e_run(d, src, cal, True)
+            torch.cuda.synchronize()
+            prof = nat.profile_read()
+            nat.profile_enable(False)
+        in_bytes = os.path.getsize(src)
+        out_bytes = os.path.getsize(os.path.join(d, "out", "model.safetensors"))
+        value = weights / (ms * 1e-3) / 1e6
+        log(f"[bench] {ms:.1f} ms per conversion ({value:.0f} Mweights/s); in-memory I/O {times[False]:.1f} ms")
+        result = {
+            "metric": f"{args.workload} Mweights/s (file to file)",
+            "value": round(value, 3), "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32",
+            "data": "synthetic safetensors file (seeded N(0,0.02^2) bf16 weights) + 3-D calibration Hessians "
+                    "X_b^T X_b / 4096 with LogNormal channel scales; random-init, no checkpoint",
+            "config": {"workload": args.workload, "blocks": extra["blocks"],
+                       "layers": [f"{n} {o}x{i}" for n, o, i in extra["layers"]], "weights": weights,
+                       "input_bytes": in_bytes, "output_bytes": out_bytes, "rot_size": 256, "block": 128,
+                       "damping": 0.01, "in_memory_ms": round(times[False], 3),
+                       "in_memory_mweights_per_s": round(weights / (times[False] * 1e-3) / 1e6, 3),
+                       "streaming_speedup": round(times[False] / ms, 3)},
+        }
+        if prof is not None:
+            dom, roof = roofline_from(prof, args.workload)
+            result["roofline"] = roof
+            result["roofline"]["kernel"] = dom
+            result["phases"] = {k: {"ms_per_step": round(v["ms"], 4), "launches_per_step": v["launches"],
+                                    "TFLOP/s": round(v["flops"] / max(v["ms"], 1e-9) / 1e9, 3),
+                                    "GB/s": round(v["bytes"] / max(v["ms"], 1e-9) / 1e6, 1)}
+                                for k, v in prof.items() if v["launches"]}
+        if not args.no_cpu_baseline:
+            from safetensors import safe_open
+            threads = torch.get_num_threads()
+            name0 = f"blocks.0.{extra['layers'][0][0]}"
+            with safe_open(src, framework="pt") as f:
+                W0 = f.get_tensor(name0 + ".weight")
+            H0 = torch.load(cal, weights_only=True)["hessians"][name0]
+            c0 = time.perf_counter()
+            cpu_step("gptq", W0, H0)
+            c1 = time.perf_counter()
+            result["cpu_baseline"] = {"value": round(W0.numel() / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
+                                      "cores": threads, "kind": "port",
+                                      "sample": f"layer {name0} ({c1 - c0:.1f} s), torch CPU oracle restating "
+                                                "the reference's CPU path (compute only, no file I/O)"}
+        print(json.dumps(result), flush=True)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
 
 
 if __name__ == "__main__":

@@ -45,9 +45,12 @@ def build_name_map(state_dict_keys: list[str], calibration_keys: list[str]) -> d
     return out
 
 
-def get_hessian(calibration: dict, layer_name: str, weight_shape) -> torch.Tensor | dict | None:
+def get_hessian(calibration: dict, layer_name: str, weight_shape, *,
+                device: torch.device | None = None) -> torch.Tensor | dict | None:
     """2-D, 3-D or DLR Hessian of a layer, or None when missing / mismatched /
-    non-finite (reference calibration_io.py:65-123)."""
+    non-finite (reference calibration_io.py:65-123).  With ``device`` a dense
+    Hessian is moved there first and checked and returned there (the host's
+    cores stay free for the file I/O threads)."""
     hessians = calibration["hessians"]
     if layer_name not in hessians:
         return None
@@ -88,6 +91,8 @@ def get_hessian(calibration: dict, layer_name: str, weight_shape) -> torch.Tenso
             return None
     else:
         return None
+    if device is not None:
+        H = H.to(device, non_blocking=False)
     if not torch.isfinite(H).all():
         logger.warning("Hessian for %s contains non-finite values; skipping (RTN fallback)", layer_name)
         return None

@@ -180,7 +180,7 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
         layer_name = name_map.get(name) if name_map else None
         hessian = None
         if layer_name is not None and calibration is not None:
-            hessian = get_hessian(calibration, layer_name, tensor.shape)
+            hessian = get_hessian(calibration, layer_name, tensor.shape, device=nat.device())
         rot_h = 0
         if hessian is not None:
             md = calibration.get("metadata", {}) or {}

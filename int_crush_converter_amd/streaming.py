@@ -8,8 +8,9 @@ converter/pipeline.py:268, 1116-1121).
   buffers and copies them to the GPU on a copy stream while the current
   layer computes.
 * ``StreamWriter`` writes outputs as they are produced: device results are
-  copied to pinned buffers on a D2H stream, a host thread appends them to the
-  file, and tensors passed through unchanged are copied file to file.  The
+  copied to pooled pinned chunks on a D2H stream, host threads write them at
+  the offsets assigned on arrival (positional writes, in parallel), and
+  tensors passed through unchanged are copied file to file.  The
   header goes into a region reserved at the start and padded with spaces
   (the safetensors format allows a space-padded header), so no tensor is
   held until the end.  The file is written under a temporary name and
@@ -79,6 +80,31 @@ class SafetensorsIndex:
         return t.reshape(shape)
 
 
+class PinnedPool:
+    """Process-wide pinned host buffers, allocated once and reused: pinned
+    allocation costs far more than the copies it serves."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._free: dict[int, list[torch.Tensor]] = {}
+
+    def take(self, nbytes: int) -> torch.Tensor:
+        size = 1 << max(20, (max(nbytes, 1) - 1).bit_length())      # power-of-2 size classes from 1 MiB
+        with self._lock:
+            lst = self._free.get(size)
+            if lst:
+                return lst.pop()
+        return torch.empty(size, dtype=torch.uint8, pin_memory=True)
+
+    def give(self, buf: torch.Tensor):
+        with self._lock:
+            self._free.setdefault(buf.numel(), []).append(buf)
+
+
+POOL = PinnedPool()
+CHUNK = 32 << 20          # D2H staging chunk (bytes)
+
+
 class Prefetcher:
     """Reads `names` in order on a host thread into pinned buffers (`depth`
     of them) and copies each to the GPU on a copy stream one layer ahead:
@@ -91,9 +117,10 @@ class Prefetcher:
         self.names = list(names)
         self.device = device
         cap = max([index.nbytes(n) for n in self.names] + [1])
+        self.bufs = [POOL.take(cap) for _ in range(depth)]
         self.free: queue.Queue = queue.Queue()
-        for _ in range(depth):
-            self.free.put(torch.empty(cap, dtype=torch.uint8, pin_memory=True))
+        for b in self.bufs:
+            self.free.put(b)
         self.ready: queue.Queue = queue.Queue()
         self.stream = torch.cuda.Stream(device=device)
         self.inflight: dict[str, tuple] = {}
@@ -144,62 +171,81 @@ class Prefetcher:
         return g
 
     def close(self):
-        for _ in range(4):
+        for _ in range(len(self.bufs) + 2):
             self.free.put(None)
+        self.thread.join()
+        for g, buf, ev in self.inflight.values():
+            ev.synchronize()
+        self.inflight.clear()
+        for b in self.bufs:
+            POOL.give(b)
+        self.bufs = []
 
 
 class StreamWriter:
-    """Appends tensors to a safetensors file as they come; header at close."""
+    """Writes tensors into a safetensors file as they come, with `workers`
+    host threads issuing positional writes at the offsets assigned on
+    arrival; the header goes into the reserved region at close."""
 
-    def __init__(self, path: str, reserve: int, device=None):
+    def __init__(self, path: str, reserve: int, device=None, workers: int = 4):
         self.path = path
         self.tmp = path + ".partial"
         self.reserve = max(int(reserve), 64)
-        self.f = open(self.tmp, "wb")
-        self.f.write(b"\0" * (8 + self.reserve))
+        self.fd = os.open(self.tmp, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+        self.base = 8 + self.reserve
         self.offset = 0
         self.header: dict[str, dict] = {}
-        self.jobs: queue.Queue = queue.Queue(maxsize=8)
+        self.jobs: queue.Queue = queue.Queue(maxsize=16)
         self.error: BaseException | None = None
         self.device = device
         self.stream = torch.cuda.Stream(device=device) if device is not None else None
-        self.thread = threading.Thread(target=self._run, daemon=True)
-        self.thread.start()
+        self.threads = [threading.Thread(target=self._run, daemon=True) for _ in range(workers)]
+        for t in self.threads:
+            t.start()
+        self.closed = False
 
     def _record(self, name, dtype, shape, n):
         if name in self.header:
             raise ValueError(f"tensor {name} written twice")
-        self.header[name] = {"dtype": TORCH_TO_ST[dtype], "shape": list(shape),
-                             "data_offsets": [self.offset, self.offset + n]}
+        off = self.offset
+        self.header[name] = {"dtype": TORCH_TO_ST[dtype], "shape": list(shape), "data_offsets": [off, off + n]}
         self.offset += n
+        return self.base + off
+
+    def _pwrite(self, data, pos):
+        mv = memoryview(data)
+        while len(mv):
+            k = os.pwrite(self.fd, mv, pos)
+            mv = mv[k:]
+            pos += k
 
     def _run(self):
-        try:
-            while True:
-                job = self.jobs.get()
-                if job is None:
-                    return
+        while True:
+            job = self.jobs.get()
+            if job is None:
+                return
+            try:
                 kind = job[0]
                 if kind == "host":
-                    _, data = job
-                    self.f.write(memoryview(data.numpy()))
+                    _, data, pos = job
+                    self._pwrite(data.numpy(), pos)
                 elif kind == "dev":
-                    _, ev, data = job
+                    _, ev, buf, n, pos = job
                     ev.synchronize()
-                    self.f.write(memoryview(data.numpy()))
+                    self._pwrite(buf[:n].numpy(), pos)
+                    POOL.give(buf)
                 elif kind == "copy":
-                    _, src_path, b, n = job
-                    with open(src_path, "rb", buffering=0) as s:
-                        s.seek(b)
-                        left = n
-                        while left:
-                            chunk = s.read(min(left, 64 << 20))
+                    _, src_path, b, n, pos = job
+                    with open(src_path, "rb", buffering=0) as src:
+                        done = 0
+                        while done < n:
+                            chunk = os.pread(src.fileno(), min(n - done, CHUNK), b + done)
                             if not chunk:
                                 raise IOError(f"{src_path}: short read")
-                            self.f.write(chunk)
-                            left -= len(chunk)
-        except BaseException as e:
-            self.error = e
+                            self._pwrite(chunk, pos + done)
+                            done += len(chunk)
+            except BaseException as e:
+                self.error = e
 
     def _put(self, job):
         if self.error is not None:
@@ -209,36 +255,46 @@ class StreamWriter:
     def add_host(self, name: str, t: torch.Tensor):
         t = t.contiguous()
         data = t.reshape(-1).view(torch.uint8) if t.numel() else torch.empty(0, dtype=torch.uint8)
-        self._record(name, t.dtype, t.shape, data.numel())
-        self._put(("host", data))
+        pos = self._record(name, t.dtype, t.shape, data.numel())
+        if data.numel():
+            self._put(("host", data, pos))
 
     def add_file_copy(self, name: str, index: SafetensorsIndex):
         dtype, shape, b, e = index.entries[name]
-        self._record(name, dtype, shape, e - b)
-        self._put(("copy", index.path, b, e - b))
+        pos = self._record(name, dtype, shape, e - b)
+        if e > b:
+            self._put(("copy", index.path, b, e - b, pos))
 
     def add_device(self, name: str, t: torch.Tensor):
-        """Copy a GPU tensor to a pinned buffer on the D2H stream (after the
-        current stream's work on it) and append it when the copy is done."""
+        """Copy a GPU tensor to pooled pinned chunks on the D2H stream (after
+        the current stream's work on it); the writers append each chunk
+        when its copy is done."""
         t = t.contiguous()
         n = t.numel() * t.element_size()
-        self._record(name, t.dtype, t.shape, n)
+        pos = self._record(name, t.dtype, t.shape, n)
         if n == 0:
-            self._put(("host", torch.empty(0, dtype=torch.uint8)))
             return
-        host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
-        cur = torch.cuda.current_stream(t.device)
-        self.stream.wait_stream(cur)
-        with torch.cuda.stream(self.stream):
-            host.copy_(t.reshape(-1).view(torch.uint8), non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record(self.stream)
+        flat = t.reshape(-1).view(torch.uint8)
+        self.stream.wait_stream(torch.cuda.current_stream(t.device))
+        for c0 in range(0, n, CHUNK):
+            k = min(CHUNK, n - c0)
+            buf = POOL.take(k)
+            with torch.cuda.stream(self.stream):
+                buf[:k].copy_(flat[c0:c0 + k], non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(self.stream)
+            self._put(("dev", ev, buf, k, pos + c0))
         t.record_stream(self.stream)
-        self._put(("dev", ev, host))
+
+    def _stop(self):
+        for _ in self.threads:
+            self.jobs.put(None)
+        for t in self.threads:
+            t.join()
 
     def close(self, metadata: dict | None):
-        self._put(None)
-        self.thread.join()
+        self._stop()
+        self.closed = True
         if self.error is not None:
             self.abort()
             raise RuntimeError(f"stream writer failed: {self.error}") from self.error
@@ -248,14 +304,16 @@ class StreamWriter:
         blob = json.dumps(hdr, separators=(",", ":")).encode("utf-8")
         if len(blob) > self.reserve:
             # header larger than reserved: rewrite with the data shifted
-            self.f.close()
+            os.close(self.fd)
             self._rewrite(blob)
         else:
             blob = blob + b" " * (self.reserve - len(blob))
-            self.f.seek(0)
-            self.f.write(struct.pack("<Q", len(blob)))
-            self.f.write(blob)
-            self.f.close()
+            self._pwrite(struct.pack("<Q", len(blob)) + blob, 0)
+            os.close(self.fd)
+        # renaming over an existing file makes some file systems flush the new
+        # one first; the old output is removed only now that the new is whole
+        if os.path.exists(self.path):
+            os.remove(self.path)
         os.replace(self.tmp, self.path)
 
     def _rewrite(self, blob: bytes):
@@ -265,7 +323,7 @@ class StreamWriter:
         with open(self.tmp, "rb") as src, open(fixed, "wb") as dst:
             dst.write(struct.pack("<Q", len(blob)))
             dst.write(blob)
-            src.seek(8 + self.reserve)
+            src.seek(self.base)
             while True:
                 chunk = src.read(64 << 20)
                 if not chunk:
@@ -274,14 +332,18 @@ class StreamWriter:
         os.replace(fixed, self.tmp)
 
     def abort(self):
-        try:
-            self.jobs.put_nowait(None)
-        except queue.Full:
-            pass
-        try:
-            self.f.close()
-        except Exception:
-            pass
+        if not self.closed:
+            self.closed = True
+            try:
+                while True:
+                    self.jobs.get_nowait()
+            except queue.Empty:
+                pass
+            self._stop()
+            try:
+                os.close(self.fd)
+            except OSError:
+                pass
         if os.path.exists(self.tmp):
             os.remove(self.tmp)
 
