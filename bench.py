@@ -42,6 +42,9 @@ WORKLOADS = {
     "ldlq_int4_it2_greedy5_rot256_4096x4096": ("ldlq", 4096, 4096, {}),
     # PermuQuant (weight-only, tau 0) + RTN INT4 on the headline layer shape
     "rtn_int4_permuquant_rot256_4096x12288": ("pq4", 4096, 12288, {}),
+    # GPTQ INT4 on the headline layer shape with a rank-128 DLR Hessian
+    # collected in the rotated space (Woodbury inverse, no densification)
+    "gptq_int4_dlr128_rot256_4096x12288": ("dlr", 4096, 12288, {"rank": 128}),
     # configs[4] end to end, file to file (quantize_model with streaming I/O):
     # the first 4 of its 40 DiT blocks, bf16 safetensors + 3-D calibration
     "e2e_dit_gptq_int4_rot256_4blocks": ("e2e", 0, 0, {"blocks": 4, "samples": 4096,
@@ -128,6 +131,13 @@ def make_inputs(kind, M, N, extra, seed=0):
         chi = (torch.randn(M, N, 4, generator=g, device=dev) ** 2).sum(-1)
         W = z / torch.sqrt(chi / 4) * (0.02 / math.sqrt(2))
     W = W.to(torch.bfloat16 if kind not in ("rtn4",) else torch.float32)
+    if kind == "dlr":
+        # U: r orthogonal-ish directions with decaying energy; D: positive residual diagonal
+        r = extra["rank"]
+        lam = torch.exp(-torch.arange(r, device=dev, dtype=torch.float32) / 32.0) * 4.0
+        U = torch.randn(N, r, generator=g, device=dev) / math.sqrt(N) * lam.sqrt() * math.sqrt(N / 64)
+        D = torch.exp(torch.randn(N, generator=g, device=dev)) ** 2 * 0.25
+        H = {"format": "dlr", "D": D, "U": U.contiguous(), "rank": r, "n": N}
     if kind == "gptq":
         S = extra["samples"]
         s = torch.exp(torch.randn(N, generator=g, device=dev))
@@ -149,6 +159,11 @@ def gpu_step(kind, W, H):
     if kind == "gptq":
         W_work, _ = L.prepare_weights(W, 256)
         codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=256, block_size=128, damping=0.01, int_bits=4,
+                                      asymmetric=False, hessian_method="hinv", fallbacks=[])
+        return L.finish(W_work, codes, s16, z8, 4)
+    if kind == "dlr":
+        W_work, _ = L.prepare_weights(W, 256)
+        codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=0, block_size=128, damping=0.01, int_bits=4,
                                       asymmetric=False, hessian_method="hinv", fallbacks=[])
         return L.finish(W_work, codes, s16, z8, 4)
     if kind == "rtn8":
@@ -190,6 +205,10 @@ def cpu_step(kind, W, H):
         Wr = ref.rotate_weights(Wf, 256)
         Hr = ref.rotate_hessian(H, 256)
         r = ref.gptq_quantize_layer(Wr, Hr, 128, 0.01, 4)
+        q, s, z = r.quantized_W, r.scales, r.zero_points
+    elif kind == "dlr":
+        Wr = ref.rotate_weights(Wf, 256)
+        r = ref.gptq_quantize_layer(Wr, H, 128, 0.01, 4)
         q, s, z = r.quantized_W, r.scales, r.zero_points
     elif kind == "rtn8":
         Wr = ref.rotate_weights(Wf, 64)
@@ -329,6 +348,8 @@ def main():
         "config": {"workload": args.workload, "out_features": M, "in_features": N,
                    **({"layers": [f"{n} {o}x{i}" for n, o, i in extra["layers"]], "hessian": "block-diagonal 256"}
                       if kind == "dit" else {}),
+                   **({"hessian": f"DLR rank {extra['rank']}, collected rotated (Woodbury inverse)"}
+                      if kind == "dlr" else {}),
                    "layers_per_s": round(1e3 / ms, 4), "rot_size": 256 if kind != "rtn8" else 64,
                    "block": 128, "damping": 0.01},
     }
@@ -348,7 +369,9 @@ def main():
             Wc, Hc = [w.cpu() for w in W], [h.cpu() for h in H]
             sample_w, sample = extra["layers"][0][1] * extra["layers"][0][2], "the qkv layer of one DiT block"
         else:
-            Wc, Hc = W.cpu(), (H.cpu() if H is not None else None)
+            Wc = W.cpu()
+            Hc = ({k: (v.cpu() if torch.is_tensor(v) else v) for k, v in H.items()} if isinstance(H, dict)
+                  else H.cpu() if H is not None else None)
             sample_w, sample = weights, f"1 layer of {args.workload}"
         c0 = time.perf_counter()
         cpu_step(kind, Wc, Hc)

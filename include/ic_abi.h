@@ -321,6 +321,34 @@ int ic_permute_cols(const float* src, int64_t rows, int64_t src_cols, int64_t ld
 int ic_permute_sym(const float* H, int64_t n, int64_t ld, const int64_t* perm, int64_t n_perm, float* out,
                    int64_t ld_out, void* stream);
 
+/* ---------------------------------------------------------------- DLR Hessians */
+
+/* Damped inverse of a diagonal + low-rank Hessian H = diag(D) + U U^T by the
+ * Woodbury identity (converter/dlr.py:70-119, woodbury_inverse):
+ * D' = D + damping * max(mean(D + rowsum(U^2)), 1e-6) (damping > 0, else D),
+ * Dinv = 1 / max(D', 1e-12), Z = Dinv U, M = I + U^T Z,
+ * Hinv = diag(Dinv) - (Z M^-1) Z^T.  D fp32 [n], U fp32 [n, r] at pitch ldu
+ * (r may be 0), Hinv fp32 [n, n] at pitch ldh.  M^-1 is the Cholesky inverse
+ * of M; when that factorisation meets a non-positive pivot info[0] is set to
+ * its 1-based column and Hinv is not meaningful: the caller then inverts M
+ * (written to M_out [r, r] when M_out is not null) another way and calls
+ * again with Minv_in (then U^T Z and the factorisation are skipped).
+ * upper_only: only entries on and above the diagonal are computed; entries
+ * less than 128 below the diagonal are set to 0, the rest of the lower
+ * triangle is left as it was (for the GPTQ / LDLQ sweeps, which read rows j
+ * from column j on).  info: 2 ints on the device.  Workspace:
+ * ic_woodbury_workspace_bytes(n, r). */
+int64_t ic_woodbury_workspace_bytes(int64_t n, int64_t r);
+int ic_woodbury_inverse(const float* D, const float* U, int64_t n, int64_t r, int64_t ldu, float damping,
+                        const float* Minv_in, int upper_only, float* Hinv, int64_t ldh, float* M_out, int* info,
+                        void* workspace, void* stream);
+
+/* H = diag(D) + U U^T as a dense fp32 [n, n] matrix at pitch ldh
+ * (converter/dlr.py:122-127, dlr_to_dense; rotation.py:181-184 densifies a
+ * DLR Hessian this way before rotating it). */
+int ic_dlr_to_dense(const float* D, const float* U, int64_t n, int64_t r, int64_t ldu, float* H, int64_t ldh,
+                    void* stream);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Launch profiler (no reference counterpart; measurement support).  While
@@ -330,10 +358,11 @@ int ic_permute_sym(const float* H, int64_t n, int64_t ld, const int64_t* perm, i
  * rotation, 7 RTN quantise / INT4 pack, 8 greedy block kernel, 9 other, 10 greedy
  * cross-term GEMMs, 11 Cholesky panel solve, 12 RTN scales / clip search,
  * 13 fp64 verification, 14 PermuQuant (moments, sort, error scales,
- * gathers), 15 PermuQuant ordered error sums.  Enabling resets the record.
- * ic_profile_read synchronises the events and returns, per phase, the summed
- * kernel time (ms), algorithmic flops and bytes, and the launch count
- * (arrays of at least 16 entries). */
+ * gathers), 15 PermuQuant ordered error sums, 16 DLR r x r products,
+ * 17 DLR n x n product.  Enabling resets the record.  ic_profile_read
+ * synchronises the events and returns, per phase, the summed kernel time
+ * (ms), algorithmic flops and bytes, and the launch count (arrays of at
+ * least 18 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

@@ -76,15 +76,18 @@ _SIGS = {
     "ic_torch_sum": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp]),
     "ic_permute_cols": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "ic_permute_sym": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "ic_woodbury_workspace_bytes": (_i64, [_i64, _i64]),
+    "ic_woodbury_inverse": (_i32, [_vp, _vp, _i64, _i64, _i64, _f32, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "ic_dlr_to_dense": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
                 "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
-                "verify", "permute", "permute_sum"]
+                "verify", "permute", "permute_sum", "dlr", "dlr_gemm"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {
-    "gemm_f32_kernel": ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy"],
+    "gemm_f32_kernel": ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy", "dlr", "dlr_gemm"],
     "potrf_diag_kernel": ["diag_factor"],
     "panel64_kernel": ["chol_panel"],
     "sweep_kernel": ["sweep"],

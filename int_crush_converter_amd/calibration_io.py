@@ -2,20 +2,16 @@
 
 Host-side only: reading the ``.pt`` file (``torch.load(weights_only=True)``),
 matching layer names, and normalising the Hessian formats (full 2-D,
-stacked 3-D blocks, or a list of blocks zero-padded to the largest block).
-Diagonal + low-rank (DLR) Hessians are recognised but not supported by this
-build's quantisers.
+stacked 3-D blocks, a list of blocks zero-padded to the largest block, or a
+diagonal + low-rank dict ``{"format": "dlr", "D": [n], "U": [n, r]}``).
 """
 
 from __future__ import annotations
 
 import torch
 
+from .dlr import is_dlr, validate_dlr
 from .log import logger
-
-
-def is_dlr(h) -> bool:
-    return isinstance(h, dict) and h.get("format") == "dlr"
 
 
 def load_calibration(path: str) -> dict:
@@ -57,14 +53,10 @@ def get_hessian(calibration: dict, layer_name: str, weight_shape, *,
     raw = hessians[layer_name]
     in_features = weight_shape[1]
     if is_dlr(raw):
-        D, U = raw.get("D"), raw.get("U")
-        ok = (isinstance(D, torch.Tensor) and isinstance(U, torch.Tensor) and D.dim() == 1 and U.dim() == 2
-              and D.shape[0] == in_features and U.shape[0] == in_features
-              and bool(torch.isfinite(D).all()) and bool(torch.isfinite(U).all()))
-        if not ok:
+        if not validate_dlr(raw, in_features=in_features):
             logger.warning("DLR Hessian for %s is invalid; skipping (RTN fallback)", layer_name)
             return None
-        return dict(raw)
+        return dict(raw)   # a shallow copy: callers may replace D and U
     if isinstance(raw, list):
         if not raw or not isinstance(raw[0], torch.Tensor):
             return None
@@ -97,6 +89,36 @@ def get_hessian(calibration: dict, layer_name: str, weight_shape, *,
         logger.warning("Hessian for %s contains non-finite values; skipping (RTN fallback)", layer_name)
         return None
     return H
+
+
+def get_hessian_diag(calibration: dict, layer_name: str, in_features: int) -> torch.Tensor | None:
+    """fp32 Hessian diagonal [in_features] of a layer (calibration_io.py:
+    158-240): the ``hessian_diag`` store when present (returned whole when it
+    is shorter), else the diagonal of the 2-D / 3-D / list Hessian (None when
+    shorter than in_features), or D + rowsum(U^2) of a DLR Hessian."""
+    store = calibration.get("hessian_diag")
+    if store and layer_name in store:
+        d = store[layer_name].float()
+        return d[:in_features] if d.shape[0] >= in_features else d
+    hessians = calibration.get("hessians", {})
+    if layer_name not in hessians:
+        return None
+    raw = hessians[layer_name]
+    if is_dlr(raw):
+        d = raw["D"].float() + (raw["U"].float() * raw["U"].float()).sum(dim=1)
+        return d[:in_features] if d.shape[0] >= in_features else d
+    if isinstance(raw, list):
+        parts = [b.diagonal() for b in raw if isinstance(b, torch.Tensor) and b.dim() == 2]
+        if not parts:
+            return None
+        d = torch.cat(parts).float()
+    elif isinstance(raw, torch.Tensor) and raw.dim() == 2:
+        d = raw.diagonal().float()
+    elif isinstance(raw, torch.Tensor) and raw.dim() == 3:
+        d = torch.cat([raw[i].diagonal() for i in range(raw.shape[0])]).float()
+    else:
+        return None
+    return d[:in_features] if d.shape[0] >= in_features else None
 
 
 def get_permutation(calibration: dict, layer_name: str) -> torch.Tensor | None:

@@ -26,7 +26,9 @@ enum ProfTag : int {
     PT_VERIFY = 13,      // fp64 quantisation error
     PT_PERMUTE = 14,     // PermuQuant moments, sort, error scales, gathers
     PT_PERM_SUM = 15,    // PermuQuant acceptance error: ordered-sum block kernel
-    PT_COUNT = 16,
+    PT_DLR = 16,         // Woodbury inverse: r x r products
+    PT_DLR_GEMM = 17,    // Woodbury / dense DLR: the n x n product
+    PT_COUNT = 18,
 };
 
 bool prof_enabled();

@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
+from .dlr import is_dlr, woodbury_inverse
 from .hessian import inverse_batch
 from .log import logger
 from .types import QuantizationResult
@@ -88,8 +89,8 @@ def gptq_quantize_layer(
     piso_scales: torch.Tensor | None = None,
     piso_zero_points: torch.Tensor | None = None,
 ) -> QuantizationResult:
-    """GPTQ with per-row scales (INT4 always asymmetric), 2-D or 3-D Hessian
-    (reference gptq.py:137-417).  ``block_size`` above 128 is run as 128-column
+    """GPTQ with per-row scales (INT4 always asymmetric), 2-D, 3-D or DLR
+    Hessian (reference gptq.py:137-417).  ``block_size`` above 128 is run as 128-column
     sweeps, which is the same update in exact arithmetic."""
     if int_bits not in (4, 8):
         raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
@@ -99,18 +100,26 @@ def gptq_quantize_layer(
         raise ValueError(f"hessian_method must be one of {list(_HESSIAN_METHODS)}, got '{hessian_method}'")
     if piso_scales is not None or piso_zero_points is not None:
         raise NotImplementedError("PiSO scales are not supported by this build")
-    if isinstance(hessian, dict):
-        raise NotImplementedError("DLR Hessians are not supported by this build")
-
     out_dev = W.device
     Wg = nat.to_gpu(W).float().contiguous()
     M, N = Wg.shape
-    Hg = nat.to_gpu(hessian)
     fallbacks: list[str] = []
     s32, z32, s16, z8 = row_params(Wg, int_bits, asymmetric)
     W_work = Wg.clone()
+    Hg = hessian if isinstance(hessian, dict) else nat.to_gpu(hessian)
 
-    if Hg.dim() == 3:
+    if is_dlr(Hg):
+        # Woodbury H^-1, then the 2-D sweep on it directly (gptq.py:322-342:
+        # the DLR branch hands the inverse itself to the column loop, without
+        # the Cholesky step of hessian_method "cholesky")
+        D, U = Hg["D"], Hg["U"]
+        if D.shape[0] != N:
+            raise ValueError(f"DLR Hessian dim {D.shape[0]} != in_features {N}")
+        Hinv = woodbury_inverse(D, U, damping, Wg.device, upper_only=True)
+        Q = sweep(W_work, Hinv, s32, z32, int_bits, block_size)
+    elif isinstance(Hg, dict):
+        raise ValueError(f"Expected 2D tensor, 3D tensor, or DLR dict Hessian, got {type(hessian).__name__}")
+    elif Hg.dim() == 3:
         nblk, bs, _ = Hg.shape
         full = N // bs
         Q = torch.empty(M, N, dtype=torch.int8, device=Wg.device)

@@ -14,6 +14,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native as nat
+from .dlr import dlr_to_dense, is_dlr, woodbury_inverse
 from .config import INT4_SCALE_DIVISOR, INT8_SCALE_DIVISOR, SCALE_MAX, SCALE_MIN, WEIGHT_OUTLIER_CLAMP
 from .gptq import quant_error, row_params, sweep
 from .hessian import inverse_batch
@@ -65,8 +66,20 @@ def rtn_codes(W_work: torch.Tensor, int_bits: int, asymmetric: bool, clipping_ra
 
 def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_size: int, damping: float,
                int_bits: int, asymmetric: bool, hessian_method: str, fallbacks: list[str]):
-    """GPTQ on a rotated W_work with a (raw or rotated) 2-D / 3-D Hessian."""
+    """GPTQ on a rotated W_work with a (raw or rotated) 2-D / 3-D Hessian, or
+    a DLR Hessian (densified when it is to be rotated, as rotation.py:181-184
+    does; else inverted by the Woodbury identity, gptq.py:322-342)."""
     M, N = W_work.shape
+    if is_dlr(H):
+        if rotate_h <= 0:
+            D, U = H["D"], H["U"]
+            if D.shape[0] != N:
+                raise ValueError(f"DLR Hessian dim {D.shape[0]} != in_features {N}")
+            s32, z32, s16, z8 = row_params(W_work, int_bits, asymmetric)
+            Hinv = woodbury_inverse(D, U, damping, W_work.device, upper_only=True)
+            Q = sweep(W_work.clone(), Hinv, s32, z32, int_bits, block_size)
+            return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
+        H = dlr_to_dense(H["D"], H["U"])
     Hsrc = nat.to_gpu(H).float()
     Hg = rotate_hessian_gpu(Hsrc, rotate_h) if rotate_h > 0 else Hsrc
     # a Hessian this function created (rotated, or copied to the GPU / fp32)

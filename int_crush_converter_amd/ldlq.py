@@ -20,6 +20,7 @@ import torch
 from . import _native as nat
 from . import greedy as _greedy
 from .config import LDLQ_MSE_DIVERGENCE, LDLQ_SCALE_MOMENTUM, CONVERGENCE_EPS, CONVERGENCE_IMPROVEMENT_THRESHOLD
+from .dlr import is_dlr, woodbury_inverse
 from .gptq import quant_error, SWEEP_MAX_BLOCK
 from .hessian import inverse_batch
 from .log import logger
@@ -161,8 +162,6 @@ def ldlq_quantize_layer(
         raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
     if W.dim() != 2:
         raise ValueError(f"Expected 2D weight tensor, got {W.dim()}D")
-    if isinstance(hessian, dict):
-        raise NotImplementedError("DLR Hessians are not supported by this build")
     out_dev = W.device
     Wg = nat.to_gpu(W).float().contiguous()
     M, N = Wg.shape
@@ -170,7 +169,19 @@ def ldlq_quantize_layer(
     fallbacks: list[str] = []
 
     H_greedy = None
-    if hessian is not None:
+    if is_dlr(hessian):
+        # Woodbury H^-1 (ldlq.py:149-158).  The reference keeps no dense H for
+        # the greedy search on this branch (it fails there), so greedy passes
+        # with a DLR Hessian are refused up front.
+        D, U = hessian["D"], hessian["U"]
+        if D.shape[0] != N:
+            raise ValueError(f"DLR Hessian dim {D.shape[0]} != in_features {N}")
+        if greedy_passes > 0:
+            raise ValueError("greedy search needs a dense Hessian (DLR given)")
+        Hinv = woodbury_inverse(D, U, damping, Wg.device, upper_only=True)
+    elif isinstance(hessian, dict):
+        raise ValueError("Expected 2D tensor, 3D tensor, or DLR dict Hessian, got dict")
+    elif hessian is not None:
         Hg = nat.to_gpu(hessian).float().contiguous()
         if Hg.dim() == 3:
             nblk, bs, _ = Hg.shape

@@ -3,11 +3,11 @@
 
 Same validation, output tensor names, dtypes and ``int_crush.*`` metadata as
 the reference for the methods this build implements (RTN, GPTQ, LDLQ with
-greedy search, ConvRot rotation).  Each layer goes to the GPU once: the
-per-layer step (``layer.py``) rotates, quantises, verifies and packs there;
-only the stored tensors come back to host memory.  Options that belong to
-other subsystems of the reference (PermuQuant, SmoothQuant / SmoothRot,
-SVD-absorbed, PiSO, DLR Hessians) raise ``NotImplementedError``.
+greedy search, ConvRot rotation, PermuQuant, 2-D / 3-D / DLR Hessians).
+Each layer goes to the GPU once: the per-layer step (``layer.py``) rotates,
+quantises, verifies and packs there; only the stored tensors come back to
+host memory.  Options that belong to other subsystems of the reference
+(SmoothQuant / SmoothRot, SVD-absorbed, PiSO) raise ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -190,15 +190,22 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
                 logger.warning("Calibration rot_size=%s != converter rot_size=%d. Hessian is in the wrong "
                                "rotation space.", cal_rot, config.rot_size)
                 state["rot_warned"] = True
-            if is_dlr(hessian):
-                raise NotImplementedError("DLR Hessians are not supported by this build")
             if not already and config.rot_size > 0:
                 rot_h = config.rot_size
+            if is_dlr(hessian) and rot_h:
+                # rotation densifies a DLR Hessian (rotation.py:181-184)
+                from .dlr import dlr_to_dense
+                from .rotation import rotate_hessian_gpu
+                hessian = rotate_hessian_gpu(dlr_to_dense(hessian["D"], hessian["U"]), rot_h)
+                rot_h = 0
             if perm is not None and not perm_from_cal:
                 # re-permute the Hessian for a self-computed permutation (pipeline.py:728-756)
                 from . import permuquant as _pq
                 from .rotation import rotate_hessian_gpu
-                if hessian.dim() == 2:
+                if is_dlr(hessian):
+                    from .dlr import make_dlr_dict, permute_dlr
+                    hessian = make_dlr_dict(*permute_dlr(hessian["D"], hessian["U"], perm))
+                elif hessian.dim() == 2:
                     Hg = nat.to_gpu(hessian).float()
                     if rot_h:
                         Hg = rotate_hessian_gpu(Hg, rot_h)
@@ -230,7 +237,9 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
     elif config.quant_method == "ldlq":
         from .ldlq import ldlq_quantize_layer
         H = None
-        if hessian is not None:
+        if is_dlr(hessian):
+            H = hessian
+        elif hessian is not None:
             from .rotation import rotate_hessian_gpu
             H = nat.to_gpu(hessian).float()
             if rot_h:

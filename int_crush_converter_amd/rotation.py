@@ -131,11 +131,16 @@ def rotate_hessian_gpu(H: torch.Tensor, rot_size: int) -> torch.Tensor:
 def rotate_hessian(H, rot_size: int):
     """Hessian in the rotated weight space: H_rot = R^T H R (reference
     rotation.py:156-248).  2-D input is zero-padded to a multiple of
-    ``rot_size``; 3-D [blocks, bs, bs] input needs bs % rot_size == 0."""
+    ``rot_size``; 3-D [blocks, bs, bs] input needs bs % rot_size == 0; a DLR
+    dict becomes the rotated dense 2-D Hessian (on the GPU)."""
     if not _is_power_of_two(rot_size):
         raise ValueError(f"rot_size must be a power of 2, got {rot_size}")
     if isinstance(H, dict):
-        raise NotImplementedError("DLR Hessians are not supported by this build")
+        # a DLR Hessian is densified first: rotation does not keep its structure
+        from .dlr import dlr_to_dense, is_dlr
+        if not is_dlr(H):
+            raise ValueError("Expected a 2-D / 3-D tensor or a DLR dict Hessian")
+        H = dlr_to_dense(H["D"], H["U"])
     if H.dim() == 2:
         if H.shape[0] != H.shape[1]:
             raise ValueError(f"Expected square Hessian, got {H.shape}")

@@ -39,6 +39,12 @@ itself; see tests/test_oracle.py):
     rejected), by brute force (sorted order, valid permutation), and by the
     identity that per-row errors of W and W[:, perm] are the same multiset
     (equal in exact arithmetic, so fp64 sums agree).
+  * woodbury_inverse / dlr_to_dense: the fp64 dense inverse of the damped
+    diag(D) + U U^T and the reference's KATs (tests/unit/
+    test_dlr_hessian.py:142-235: damping definition, H H^-1 = I, U = 0 gives
+    diag(1/D), rank one equals Sherman-Morrison's closed form, zero diagonal
+    entries stay finite, symmetry); a factor permutation equals
+    H[perm][:, perm] of the dense form.
 """
 
 from __future__ import annotations
@@ -427,7 +433,8 @@ def gptq_row_params(W, int_bits, asymmetric):
 
 def gptq_quantize_layer(W, H, block_size=128, damping=0.01, int_bits=4,
                         asymmetric=False, hessian_method="hinv"):
-    """gptq.py:137-417 without the PiSO and DLR branches."""
+    """gptq.py:137-417 without the PiSO branch.  A DLR dict H takes the
+    Woodbury inverse straight into the column loop (gptq.py:322-342)."""
     W = W.float()
     M, N = W.shape
     qmin, qmax = (-128, 127) if int_bits == 8 else (-8, 7)
@@ -435,7 +442,11 @@ def gptq_quantize_layer(W, H, block_size=128, damping=0.01, int_bits=4,
     s, z = gptq_row_params(W, int_bits, asymmetric)
     Q = torch.zeros_like(W, dtype=torch.int8)
     Ww = W.clone()
-    if H.dim() == 3:
+    if isinstance(H, dict):
+        if H["D"].shape[0] != N:
+            raise ValueError(f"DLR Hessian dim {H['D'].shape[0]} != in_features {N}")
+        gptq_block(Ww, Q, s, woodbury_inverse(H["D"], H["U"], damping), 0, N, block_size, qmin, qmax, z)
+    elif H.dim() == 3:
         nb, bs, _ = H.shape
         for bi in range(nb):
             c0 = bi * bs
@@ -684,7 +695,15 @@ def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=
     M, N = W.shape
     div = 127.0 if int_bits == 8 else 7.0
     qmin, qmax = (-128, 127) if int_bits == 8 else (-8, 7)
-    if hessian is not None:
+    if isinstance(hessian, dict):
+        # ldlq.py:149-158; the greedy search needs the dense H this branch
+        # never builds (the reference fails there)
+        if hessian["D"].shape[0] != N:
+            raise ValueError(f"DLR Hessian dim {hessian['D'].shape[0]} != in_features {N}")
+        if greedy_passes > 0:
+            raise ValueError("greedy search needs a dense Hessian (DLR given)")
+        Hinv = woodbury_inverse(hessian["D"], hessian["U"], damping)
+    elif hessian is not None:
         H = hessian.float()
         if H.dim() == 3:
             nb, bs, _ = H.shape
@@ -726,6 +745,41 @@ def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=
                            mse=(W - d).double().pow(2).mean().item(),
                            max_err=(W - d).abs().max().item(),
                            method_used="ldlq_cpu", fallbacks=[])
+
+
+# ---------------------------------------------------------------- DLR Hessians
+
+DLR_DIAG_FLOOR = 1e-12        # dlr.py:22
+
+
+def woodbury_inverse(D, U, damping=0.0):
+    """(diag(D) + U U^T + damping * mean(diag H) I)^-1 by the Woodbury
+    identity, dlr.py:76-119: D' = D + damping * max(mean(D + rowsum(U^2)),
+    1e-6), Dinv = 1 / max(D', 1e-12), Z = Dinv U, M = I + U^T Z,
+    H^-1 = diag(Dinv) - (Z M^-1) Z^T, M^-1 by Cholesky (inv, then pinv, when
+    that fails)."""
+    D = D.float()
+    U = U.float()
+    r = U.shape[1]
+    if damping > 0.0:
+        dm = (D + (U * U).sum(dim=1)).mean().clamp(min=DIAG_MEAN_FLOOR)
+        D = D + damping * dm
+    Dinv = 1.0 / D.clamp(min=DLR_DIAG_FLOOR)
+    Z = Dinv.unsqueeze(1) * U
+    M = torch.eye(r, dtype=torch.float32) + U.T @ Z
+    try:
+        Minv = torch.cholesky_inverse(torch.linalg.cholesky(M))
+    except torch.linalg.LinAlgError:
+        try:
+            Minv = torch.linalg.inv(M)
+        except torch.linalg.LinAlgError:
+            Minv = torch.linalg.pinv(M)
+    return torch.diag(Dinv) - Z @ Minv @ Z.T
+
+
+def dlr_to_dense(D, U):
+    """diag(D) + U U^T (dlr.py:122-127)."""
+    return torch.diag(D.float()) + U.float() @ U.float().T
 
 
 # ---------------------------------------------------------------- PermuQuant

@@ -140,3 +140,64 @@ def test_cli_rejects_bad_rot(capsys):
     from int_crush_converter_amd.cli import main
     with pytest.raises(SystemExit):
         main(["-i", "a", "-o", "b", "--rot-size", "12", "-q"])
+
+
+def test_dlr_detection_and_validation():
+    from int_crush_converter_amd import dlr
+    d = dlr.make_dlr_dict(torch.rand(8) + 0.1, torch.randn(8, 4))
+    assert d["rank"] == 4 and d["n"] == 8 and dlr.is_dlr(d)
+    assert not dlr.is_dlr(torch.eye(3)) and not dlr.is_dlr({"D": d["D"], "U": d["U"]})
+    assert not dlr.is_dlr({"format": "block", "D": d["D"], "U": d["U"]})
+    assert dlr.validate_dlr(d, in_features=8) and not dlr.validate_dlr(d, in_features=16)
+    bad = dict(d, D=d["D"].clone())
+    bad["D"][0] = -1.0
+    assert not dlr.validate_dlr(bad)
+    bad["D"][0] = float("nan")
+    assert not dlr.validate_dlr(bad)
+    assert not dlr.validate_dlr(dlr.make_dlr_dict(torch.rand(8), torch.randn(16, 4)))
+    assert not dlr.validate_dlr({"format": "dlr", "D": [1, 2, 3], "U": torch.randn(3, 2)})
+
+
+def test_dlr_factor_transforms():
+    from int_crush_converter_amd import dlr
+    g = torch.Generator().manual_seed(3)
+    D, U, s = torch.rand(16, generator=g) + 0.1, torch.randn(16, 4, generator=g) * 0.3, torch.rand(16, generator=g) + .5
+    Dn, Un = dlr.transform_dlr_for_smoothquant(D, U, s)
+    H = torch.diag(D) + U @ U.T
+    assert torch.allclose(torch.diag(Dn) + Un @ Un.T, H / (s[:, None] * s[None, :]), atol=1e-5)
+    s0 = s.clone()
+    s0[0] = 0.0
+    assert all(torch.isfinite(t).all() for t in dlr.transform_dlr_for_smoothquant(D, U, s0))
+    perm = torch.randperm(16, generator=g)
+    Dp, Up = dlr.permute_dlr(D, U, perm)
+    assert torch.equal(Dp, D[perm]) and torch.equal(Up, U[perm])
+    Dp, Up = dlr.permute_dlr(D, U, perm[:8])
+    assert Dp.shape == (8,) and Up.shape == (8, 4)
+    assert abs(dlr.damped_diag_mean(D, U).item() - H.diagonal().mean().item()) <= 1e-5 * H.diagonal().mean().item()
+    assert dlr.damped_diag_mean(torch.zeros(8), torch.zeros(8, 4)).item() == pytest.approx(1e-6)
+
+
+def test_calibration_dlr(tmp_path):
+    from int_crush_converter_amd import dlr
+    g = torch.Generator().manual_seed(5)
+    D, U = torch.rand(64, generator=g) + 0.1, torch.randn(64, 8, generator=g)
+    cal = {"hessians": {"layer.0": dlr.make_dlr_dict(D, U), "full": torch.eye(64)},
+           "shapes": {}, "layer_types": {}}
+    h = cio.get_hessian(cal, "layer.0", (32, 64))
+    assert dlr.is_dlr(h) and h["D"].shape == (64,) and h["U"].shape == (64, 8)
+    assert cio.get_hessian(cal, "layer.0", (32, 128)) is None
+    neg = dict(cal["hessians"]["layer.0"], D=D.clone())
+    neg["D"][3] = -0.5
+    assert cio.get_hessian({"hessians": {"x": neg}}, "x", (32, 64)) is None
+    diag = cio.get_hessian_diag(cal, "layer.0", 64)
+    assert torch.allclose(diag, D + (U ** 2).sum(dim=1), atol=1e-5)
+    assert cio.get_hessian_diag(cal, "layer.0", 32).shape == (32,)
+    assert cio.get_hessian_diag(cal, "missing", 64) is None
+    assert torch.equal(cio.get_hessian_diag(cal, "full", 64), torch.ones(64))
+    assert cio.get_hessian_diag(cal, "full", 65) is None
+    cal["hessian_diag"] = {"full": torch.arange(10.0)}
+    assert torch.equal(cio.get_hessian_diag(cal, "full", 64), torch.arange(10.0))
+    path = tmp_path / "dlr.pt"
+    torch.save(cal, path)
+    h = cio.get_hessian(cio.load_calibration(str(path)), "layer.0", (32, 64))
+    assert torch.equal(h["D"], D) and torch.equal(h["U"], U)

@@ -507,3 +507,63 @@ def test_permuquant_acceptance_rules():
         ref.sweep_alpha(torch.randn(8, 64), num_alpha=0)
     p, a, acc = ref.sweep_alpha(W, None, 16, 0.0, 11, 4)
     assert a == 0.0 and acc is True and torch.equal(p, perm)
+
+
+# ---------------------------------------------------------------- DLR Hessians
+
+def _dlr(n, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(n, generator=g) + 0.1, torch.randn(n, r, generator=g) * 0.3
+
+
+@pytest.mark.parametrize("damping", [0.0, 0.01, 0.3])
+def test_woodbury_matches_fp64_inverse(damping):
+    # the definition of the damped inverse (tests/unit/test_dlr_hessian.py:142-168)
+    D, U = _dlr(48, 6, 1)
+    H = torch.diag(D.double()) + U.double() @ U.double().T
+    dm = (D.double() + (U.double() ** 2).sum(dim=1)).mean()
+    want = torch.linalg.inv(H + damping * dm * torch.eye(48, dtype=torch.float64))
+    got = ref.woodbury_inverse(D, U, damping).double()
+    assert (got - want).abs().max().item() <= 1e-5 * want.abs().max().item()
+    assert (H @ ref.woodbury_inverse(D, U).double() - torch.eye(48, dtype=torch.float64)).abs().max() < 1e-4
+    assert torch.allclose(got, got.T, atol=1e-6)
+
+
+def test_woodbury_special_cases():
+    D, U = _dlr(16, 1, 2)
+    # U = 0: diag(1/D)
+    assert torch.allclose(ref.woodbury_inverse(D, torch.zeros(16, 1)), torch.diag(1.0 / D), atol=1e-6)
+    # rank one: Sherman-Morrison's closed form
+    Du = U.squeeze(1) / D
+    sm = torch.diag(1.0 / D) - torch.outer(Du, Du) / (1 + (U.squeeze(1) * Du).sum())
+    assert torch.allclose(ref.woodbury_inverse(D, U), sm, atol=1e-6)
+    # a zero diagonal entry is floored, not a division by zero
+    D2 = D.clone()
+    D2[0] = 0.0
+    assert torch.isfinite(ref.woodbury_inverse(D2, torch.randn(16, 4) * 0.3, 0.01)).all()
+    # the damping base is floored at 1e-6 (all-zero factors)
+    got = ref.woodbury_inverse(torch.zeros(8), torch.zeros(8, 2), 0.5)
+    assert torch.allclose(torch.diag(got), torch.full((8,), 1.0 / (0.5 * 1e-6)), rtol=1e-6)
+
+
+def test_dlr_dense_and_permutation():
+    D, U = _dlr(20, 3, 3)
+    H = ref.dlr_to_dense(D, U)
+    assert torch.allclose(H.double(), torch.diag(D.double()) + U.double() @ U.double().T, atol=1e-6)
+    perm = torch.randperm(20, generator=torch.Generator().manual_seed(4))
+    assert torch.allclose(ref.dlr_to_dense(D[perm], U[perm]), H[perm][:, perm], atol=1e-6)
+
+
+def test_gptq_dlr_uses_woodbury_inverse(one_thread):
+    # the DLR branch is the 2-D column loop on the Woodbury inverse itself
+    D, U = _dlr(64, 8, 5)
+    W = torch.randn(16, 64, generator=torch.Generator().manual_seed(6))
+    r = ref.gptq_quantize_layer(W, {"format": "dlr", "D": D, "U": U}, damping=0.01)
+    s, z = ref.gptq_row_params(W, 4, False)
+    Q = torch.zeros(16, 64, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, ref.woodbury_inverse(D, U, 0.01), 0, 64, 128, -8, 7, z)
+    assert torch.equal(r.quantized_W, Q)
+    with pytest.raises(ValueError, match="dim.*in_features"):
+        ref.gptq_quantize_layer(W[:, :32], {"format": "dlr", "D": D, "U": U})
+    with pytest.raises(ValueError):
+        ref.ldlq_quantize_layer(W, {"format": "dlr", "D": D, "U": U}, greedy_passes=1)
