@@ -45,6 +45,8 @@ WORKLOADS = {
     # GPTQ INT4 on the headline layer shape with a rank-128 DLR Hessian
     # collected in the rotated space (Woodbury inverse, no densification)
     "gptq_int4_dlr128_rot256_4096x12288": ("dlr", 4096, 12288, {"rank": 128}),
+    # GPTQ INT4 with PiSO scales (128 coarse + 16 fine candidates per row) on the headline layer
+    "gptq_int4_piso_rot256_4096x12288": ("piso", 4096, 12288, {"samples": 8192, "cpu_rows": 512}),
     # configs[4] end to end, file to file (quantize_model with streaming I/O):
     # the first 4 of its 40 DiT blocks, bf16 safetensors + 3-D calibration
     "e2e_dit_gptq_int4_rot256_4blocks": ("e2e", 0, 0, {"blocks": 4, "samples": 4096,
@@ -138,7 +140,7 @@ def make_inputs(kind, M, N, extra, seed=0):
         U = torch.randn(N, r, generator=g, device=dev) / math.sqrt(N) * lam.sqrt() * math.sqrt(N / 64)
         D = torch.exp(torch.randn(N, generator=g, device=dev)) ** 2 * 0.25
         H = {"format": "dlr", "D": D, "U": U.contiguous(), "rank": r, "n": N}
-    if kind == "gptq":
+    if kind in ("gptq", "piso"):
         S = extra["samples"]
         s = torch.exp(torch.randn(N, generator=g, device=dev))
         H = torch.zeros(N, N, dtype=torch.float32, device=dev)
@@ -160,6 +162,13 @@ def gpu_step(kind, W, H):
         W_work, _ = L.prepare_weights(W, 256)
         codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=256, block_size=128, damping=0.01, int_bits=4,
                                       asymmetric=False, hessian_method="hinv", fallbacks=[])
+        return L.finish(W_work, codes, s16, z8, 4)
+    if kind == "piso":
+        from int_crush_converter_amd import piso
+        W_work, _ = L.prepare_weights(W, 256)
+        ps = piso.compute_piso_scales_int4_asymmetric(W_work, H.diagonal())
+        codes, s16, z8 = L.gptq_codes(W_work, H, rotate_h=256, block_size=128, damping=0.01, int_bits=4,
+                                      asymmetric=False, hessian_method="hinv", fallbacks=[], piso=ps)
         return L.finish(W_work, codes, s16, z8, 4)
     if kind == "dlr":
         W_work, _ = L.prepare_weights(W, 256)
@@ -193,6 +202,9 @@ def gpu_step(kind, W, H):
     raise ValueError(kind)
 
 
+WORKLOADS_CPU_ROWS = 512
+
+
 def cpu_step(kind, W, H):
     """The reference's CPU algorithm (oracle restatement) on the same layer."""
     import torch
@@ -206,6 +218,14 @@ def cpu_step(kind, W, H):
         Hr = ref.rotate_hessian(H, 256)
         r = ref.gptq_quantize_layer(Wr, Hr, 128, 0.01, 4)
         q, s, z = r.quantized_W, r.scales, r.zero_points
+    elif kind == "piso":   # bounded sample: the first rows of the layer
+        Wr = ref.rotate_weights(Wf[:WORKLOADS_CPU_ROWS], 256)
+        s, z = ref.piso_scales_asym(Wr, H.diagonal().contiguous(), 128, 16, -8, 7, 0.5, 2.0)
+        s = s.clamp(min=1e-5, max=65500.0)
+        Q = torch.zeros(Wr.shape, dtype=torch.int8)
+        ref.gptq_block(Wr.clone(), Q, s, ref.prepare_hinv(ref.rotate_hessian(H, 256), 0.01), 0, Wr.shape[1], 128,
+                       -8, 7, z)
+        q, s, z = Q, s.to(torch.float16), z
     elif kind == "dlr":
         Wr = ref.rotate_weights(Wf, 256)
         r = ref.gptq_quantize_layer(Wr, H, 128, 0.01, 4)
@@ -368,6 +388,10 @@ def main():
         if kind == "dit":
             Wc, Hc = [w.cpu() for w in W], [h.cpu() for h in H]
             sample_w, sample = extra["layers"][0][1] * extra["layers"][0][2], "the qkv layer of one DiT block"
+        elif kind == "piso":
+            Wc, Hc = W.cpu(), H.cpu()
+            sample_w = extra["cpu_rows"] * N
+            sample = f"the first {extra['cpu_rows']} rows of 1 layer of {args.workload}"
         else:
             Wc = W.cpu()
             Hc = ({k: (v.cpu() if torch.is_tensor(v) else v) for k, v in H.items()} if isinstance(H, dict)

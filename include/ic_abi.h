@@ -349,6 +349,26 @@ int ic_woodbury_inverse(const float* D, const float* U, int64_t n, int64_t r, in
 int ic_dlr_to_dense(const float* D, const float* U, int64_t n, int64_t r, int64_t ldu, float* H, int64_t ldh,
                     void* stream);
 
+/* ---------------------------------------------------------------- PiSO */
+
+/* PiSO per-row scales (converter/piso.py:28-183, the PyTorch path of
+ * compute_piso_scales_int8 / _int8_asymmetric / _int4 / _int4_asymmetric):
+ * for each row of W (fp32 [rows, cols], pitch ld) the error
+ * sum_d (w_d - dq(w_d; s))^2 h_d (h fp32 [cols]) is evaluated for
+ * s = s_ref * coarse[c], c < num_coarse, the first minimum picks s_best, then
+ * for s_best * fine[f], f < num_fine, whose first minimum is the result.
+ * Symmetric (asym 0): s_ref = max(absmax / qmax, 1e-10), dq = clamp(rhaz(
+ * w / s)) s.  Asymmetric: s_ref = max((max - min) / (qmax - qmin), 1e-10),
+ * s clamped at 1e-10, zp = clamp(rhaz(qmin - min / s)), dq = (clamp(rhaz(
+ * w / s + zp)) - zp) s.  Grid [qmin, qmax] = [-8, 7] (bits 4) or
+ * [-128, 127] (bits 8).  The sums follow torch's CPU order, so scales (fp32
+ * [rows]) and zero-points (int8 [rows], asym only) equal the reference's CPU
+ * path bit for bit.  coarse / fine: the factor tables on the device (the
+ * reference's torch.linspace values), 1 to 1024 entries each. */
+int ic_piso_scales(const float* W, int64_t rows, int64_t cols, int64_t ld, const float* h, int bits, int asym,
+                   const float* coarse, int num_coarse, const float* fine, int num_fine, float* scales,
+                   int8_t* zp, void* stream);
+
 /* ---------------------------------------------------------------- profiling */
 
 /* Launch profiler (no reference counterpart; measurement support).  While
@@ -359,10 +379,10 @@ int ic_dlr_to_dense(const float* D, const float* U, int64_t n, int64_t r, int64_
  * cross-term GEMMs, 11 Cholesky panel solve, 12 RTN scales / clip search,
  * 13 fp64 verification, 14 PermuQuant (moments, sort, error scales,
  * gathers), 15 PermuQuant ordered error sums, 16 DLR r x r products,
- * 17 DLR n x n product.  Enabling resets the record.  ic_profile_read
- * synchronises the events and returns, per phase, the summed kernel time
- * (ms), algorithmic flops and bytes, and the launch count (arrays of at
- * least 18 entries). */
+ * 17 DLR n x n product, 18 PiSO scale search.  Enabling resets the record.
+ * ic_profile_read synchronises the events and returns, per phase, the summed
+ * kernel time (ms), algorithmic flops and bytes, and the launch count (arrays
+ * of at least 19 entries). */
 int ic_profile_enable(int on);
 int ic_profile_read(double* ms, double* flops, double* bytes, int64_t* launches, int ntags);
 

@@ -79,11 +79,12 @@ _SIGS = {
     "ic_woodbury_workspace_bytes": (_i64, [_i64, _i64]),
     "ic_woodbury_inverse": (_i32, [_vp, _vp, _i64, _i64, _i64, _f32, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _vp]),
     "ic_dlr_to_dense": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "ic_piso_scales": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp, _vp]),
 }
 
 PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor", "sweep", "rotate_w",
                 "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
-                "verify", "permute", "permute_sum", "dlr", "dlr_gemm"]
+                "verify", "permute", "permute_sum", "dlr", "dlr_gemm", "piso"]
 
 # kernel -> the profiler phases its launches are tagged with
 PROFILE_KERNELS = {
@@ -97,6 +98,7 @@ PROFILE_KERNELS = {
     "rtn_quant_kernel": ["rtn_quant_pack"],
     "quant_error_partial": ["verify"],
     "fsum_block_kernel": ["permute_sum"],
+    "piso_kernel": ["piso"],
 }
 
 

@@ -75,7 +75,7 @@ def build_parser() -> argparse.ArgumentParser:
     p.add_argument("--rank-threshold", type=float, default=0.01, help="Eigenvalue threshold for low-rank greedy")
     p.add_argument("--comfy-compat", action="store_true", help="Write .comfy_quant (ComfyUI INT8 format)")
     p.add_argument("--comfy-int8-fast", action="store_true", help="Write comfy_quant for ComfyUI-INT8-Fast")
-    p.add_argument("--piso", action="store_true", help="PiSO data-aware scales (not part of this build)")
+    p.add_argument("--piso", action="store_true", help="PiSO data-aware per-row scales (needs --calibration)")
     p.add_argument("--asymmetric", action="store_true", help="Asymmetric quantization (scale + zero-point)")
     p.add_argument("--clipping-ratios", type=str, default=None,
                    help="Comma-separated clipping ratios searched for the lowest-MSE scale per row")

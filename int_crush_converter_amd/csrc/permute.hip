@@ -28,54 +28,9 @@
 
 #include "common.hpp"
 #include "prof.hpp"
+#include "torchsum.hpp"
 
 namespace icq {
-
-constexpr int64_t TORCH_GRAIN = 32768;   // at::internal::GRAIN_SIZE
-constexpr int COL_VEC = 16;              // columns per vector in torch's outer-sum loop
-constexpr int SUM_VEC = 8;               // lanes of the inner-sum vector accumulators
-constexpr int SUM_SEQ = 4 * SUM_VEC;     // interleaved sequences of one chunk
-
-__host__ __device__ inline int ceil_log2(int64_t x) {
-    int r = 0;
-    while ((int64_t(1) << r) < x) ++r;
-    return r;
-}
-// log2 of the cascade's group size for a sequence of L values
-__host__ __device__ inline int cascade_lp(int64_t L) {
-    const int c = ceil_log2(L) / 4;
-    return c > 4 ? c : 4;
-}
-
-// Sequential cascade of torch's multi_row_sum over get(0) .. get(L-1):
-// accumulator 0 takes groups of S values, each group is added to
-// accumulator 1, and every S groups accumulator 1 goes to 2, every S^2
-// groups 2 goes to 3; the rest of the values go to 0; the result is
-// ((a0 + a1) + a2) + a3.
-template <typename Get>
-__device__ float cascade_seq(Get get, int64_t L, int lp) {
-    const int64_t S = int64_t(1) << lp, mask = S - 1;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    int64_t i = 0;
-    while (i + S <= L) {
-        for (int64_t j = 0; j < S; ++j, ++i) a0 = a0 + get(i);
-        a1 = a1 + a0;
-        a0 = 0.0f;
-        if ((i & (mask << lp)) == 0) {
-            a2 = a2 + a1;
-            a1 = 0.0f;
-            if ((i & (mask << (2 * lp))) == 0) {
-                a3 = a3 + a2;
-                a2 = 0.0f;
-            }
-        }
-    }
-    for (; i < L; ++i) a0 = a0 + get(i);
-    a0 = a0 + a1;
-    a0 = a0 + a2;
-    a0 = a0 + a3;
-    return a0;
-}
 
 // The value accumulator 1 holds when block b (S groups of S values) is
 // done: the sequential sum of its S group sums.

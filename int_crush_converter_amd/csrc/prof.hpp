@@ -28,7 +28,8 @@ enum ProfTag : int {
     PT_PERM_SUM = 15,    // PermuQuant acceptance error: ordered-sum block kernel
     PT_DLR = 16,         // Woodbury inverse: r x r products
     PT_DLR_GEMM = 17,    // Woodbury / dense DLR: the n x n product
-    PT_COUNT = 18,
+    PT_PISO = 18,        // PiSO scale search
+    PT_COUNT = 19,
 };
 
 bool prof_enabled();

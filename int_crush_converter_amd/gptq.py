@@ -98,13 +98,15 @@ def gptq_quantize_layer(
         raise ValueError(f"Expected 2D weight tensor, got {W.dim()}D")
     if hessian_method not in _HESSIAN_METHODS:
         raise ValueError(f"hessian_method must be one of {list(_HESSIAN_METHODS)}, got '{hessian_method}'")
-    if piso_scales is not None or piso_zero_points is not None:
-        raise NotImplementedError("PiSO scales are not supported by this build")
     out_dev = W.device
     Wg = nat.to_gpu(W).float().contiguous()
     M, N = Wg.shape
     fallbacks: list[str] = []
-    s32, z32, s16, z8 = row_params(Wg, int_bits, asymmetric)
+    params = None
+    if piso_scales is not None:
+        from .piso import piso_row_params
+        params = piso_row_params(Wg, piso_scales, piso_zero_points, int_bits, asymmetric)
+    s32, z32, s16, z8 = params if params is not None else row_params(Wg, int_bits, asymmetric)
     W_work = Wg.clone()
     Hg = hessian if isinstance(hessian, dict) else nat.to_gpu(hessian)
 
@@ -173,11 +175,18 @@ def gptq_quantize_layer_rtn(
     (reference gptq.py:420-533)."""
     if int_bits not in (4, 8):
         raise ValueError(f"int_bits must be 4 or 8, got {int_bits}")
-    if piso_scales is not None or piso_zero_points is not None:
-        raise NotImplementedError("PiSO scales are not supported by this build")
     out_dev = W.device
     Wg = nat.to_gpu(W).float().contiguous()
     N = Wg.shape[1]
+    if piso_scales is not None:
+        from .piso import rtn_piso_codes
+        r = rtn_piso_codes(Wg, piso_scales, piso_zero_points, int_bits, asymmetric, clipping_ratios)
+        if r is not None:
+            q, s, z, _ = r
+            mse, max_err = quant_error(Wg, q, s, z)
+            return QuantizationResult(
+                quantized_W=q.to(out_dev), scales=s.to(out_dev), zero_points=None if z is None else z.to(out_dev),
+                mse=mse, max_err=max_err, method_used="rtn_piso", fallbacks=[])
     zps = None
     if asymmetric:
         if int_bits == 8:

@@ -64,18 +64,29 @@ def rtn_codes(W_work: torch.Tensor, int_bits: int, asymmetric: bool, clipping_ra
     return codes, s16.reshape(M, 1), None if zp is None else zp.reshape(M, 1), packed
 
 
+def _gptq_params(W_work, int_bits, asymmetric, piso):
+    if piso is not None:
+        from .piso import piso_row_params
+        p = piso_row_params(W_work, piso[0], piso[1], int_bits, asymmetric)
+        if p is not None:
+            return p
+    return row_params(W_work, int_bits, asymmetric)
+
+
 def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_size: int, damping: float,
-               int_bits: int, asymmetric: bool, hessian_method: str, fallbacks: list[str]):
+               int_bits: int, asymmetric: bool, hessian_method: str, fallbacks: list[str], piso=None):
     """GPTQ on a rotated W_work with a (raw or rotated) 2-D / 3-D Hessian, or
     a DLR Hessian (densified when it is to be rotated, as rotation.py:181-184
-    does; else inverted by the Woodbury identity, gptq.py:322-342)."""
+    does; else inverted by the Woodbury identity, gptq.py:322-342).  ``piso``:
+    (scales [M, 1], zero-points [M, 1] or None) from the PiSO search, which
+    replace the row scales (gptq.py:210-252)."""
     M, N = W_work.shape
     if is_dlr(H):
         if rotate_h <= 0:
             D, U = H["D"], H["U"]
             if D.shape[0] != N:
                 raise ValueError(f"DLR Hessian dim {D.shape[0]} != in_features {N}")
-            s32, z32, s16, z8 = row_params(W_work, int_bits, asymmetric)
+            s32, z32, s16, z8 = _gptq_params(W_work, int_bits, asymmetric, piso)
             Hinv = woodbury_inverse(D, U, damping, W_work.device, upper_only=True)
             Q = sweep(W_work.clone(), Hinv, s32, z32, int_bits, block_size)
             return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
@@ -92,7 +103,7 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
         return rotate_hessian_gpu(src, rotate_h) if rotate_h > 0 else src
 
     inv_kw = dict(inplace=True, restore=restore, upper_only=True) if own else dict(upper_only=True)
-    s32, z32, s16, z8 = row_params(W_work, int_bits, asymmetric)
+    s32, z32, s16, z8 = _gptq_params(W_work, int_bits, asymmetric, piso)
     Ww = W_work.clone()
     if Hg.dim() == 3:
         nblk, bs, _ = Hg.shape

@@ -3,11 +3,12 @@
 
 Same validation, output tensor names, dtypes and ``int_crush.*`` metadata as
 the reference for the methods this build implements (RTN, GPTQ, LDLQ with
-greedy search, ConvRot rotation, PermuQuant, 2-D / 3-D / DLR Hessians).
+greedy search, ConvRot rotation, PermuQuant, PiSO scales, 2-D / 3-D / DLR
+Hessians).
 Each layer goes to the GPU once: the per-layer step (``layer.py``) rotates,
 quantises, verifies and packs there; only the stored tensors come back to
 host memory.  Options that belong to other subsystems of the reference
-(SmoothQuant / SmoothRot, SVD-absorbed, PiSO) raise ``NotImplementedError``.
+(SmoothQuant / SmoothRot, SVD-absorbed) raise ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -72,8 +73,7 @@ def _validate(config: QuantizeConfig) -> QuantizeConfig:
     if config.rot_size > 4096:
         raise ValueError(f"rot_size {config.rot_size} exceeds the supported maximum 4096")
     for flag, what in [(config.smoothquant, "SmoothQuant / SmoothRot (--smoothquant, --smoothrot)"),
-                       (config.svd_rank > 0, "SVD-absorbed (--svd-rank)"),
-                       (config.piso_scales, "PiSO (--piso)")]:
+                       (config.svd_rank > 0, "SVD-absorbed (--svd-rank)")]:
         if flag:
             raise NotImplementedError(f"{what} is not part of this build's quantization path")
     return config
@@ -162,6 +162,43 @@ def _permuquant(name: str, W_work: torch.Tensor, orig_in: int, config: QuantizeC
     return perm, False
 
 
+def _piso(name: str, tensor: torch.Tensor, W_work: torch.Tensor, outliers: int, config: QuantizeConfig,
+          calibration, name_map, state: dict):
+    """PiSO scales of one layer (pipeline.py:286-360): on the rotated weights
+    as loaded (no outlier zeroing) with the calibration's Hessian diagonal
+    zero-padded to the rotated width.  INT8: symmetric scales; INT4:
+    asymmetric scales and zero-points.  A failed search leaves the layer
+    without PiSO, as in the reference.  Returns (scales, zero-points or None)."""
+    from .calibration_io import get_hessian_diag
+    from . import piso as _piso_mod
+    layer_name = name_map.get(name)
+    if layer_name is None:
+        return None
+    h = get_hessian_diag(calibration, layer_name, tensor.shape[1])
+    if h is None:
+        return None
+    if outliers:
+        from .rotation import rotate_rows_gpu
+        Wr = rotate_rows_gpu(nat.to_gpu(tensor), config.rot_size if config.rot_size > 0 else 1)
+    else:
+        Wr = W_work          # nothing was zeroed: the same rotated weights
+    h = nat.to_gpu(h).float()
+    if h.shape[0] < Wr.shape[1]:
+        h = torch.nn.functional.pad(h, (0, Wr.shape[1] - h.shape[0]))
+    try:
+        if config.int_bits == 8:
+            res = (_piso_mod.compute_piso_scales_int8(Wr, h), None)
+        else:
+            res = _piso_mod.compute_piso_scales_int4_asymmetric(Wr, h)
+    except (ValueError, torch.cuda.OutOfMemoryError) as exc:
+        logger.warning("PiSO failed for %s: %s", layer_name, exc)
+        return None
+    state["piso"] += 1
+    if res[1] is not None:
+        state["piso_zp"] += 1
+    return res
+
+
 def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, calibration, name_map,
                    state: dict) -> _layer.LayerOutput:
     """One layer of the pipeline loop on the GPU; ``state`` carries counters and
@@ -173,6 +210,9 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
         logger.warning("Zeroed %d outlier weight values in %s (|W| > %.0f)", outliers, name, 1000.0)
     fallbacks: list[str] = []
     packed = None
+    piso = None
+    if config.piso_scales and calibration is not None:
+        piso = _piso(name, tensor, W_work, outliers, config, calibration, name_map, state)
     perm, perm_from_cal = None, False
     if config.use_permuquant:
         perm, perm_from_cal = _permuquant(name, W_work, tensor.shape[1], config, calibration, name_map, state)
@@ -225,13 +265,22 @@ def quantize_layer(name: str, tensor: torch.Tensor, config: QuantizeConfig, cali
             codes, s16, z8 = _layer.gptq_codes(
                 W_work, hessian, rotate_h=rot_h, block_size=config.gptq_block_size, damping=config.damping,
                 int_bits=config.int_bits, asymmetric=config.asymmetric, hessian_method=config.hessian_method,
-                fallbacks=fallbacks)
+                fallbacks=fallbacks, piso=piso)
             method = "gptq_hip"
             state["gptq"] += 1
         else:
-            codes, s16, z8, packed = _layer.rtn_codes(W_work, config.int_bits, config.asymmetric,
-                                                      config.clipping_ratios)
-            method = "rtn"
+            r = None
+            if piso is not None:
+                from .piso import rtn_piso_codes
+                r = rtn_piso_codes(W_work, piso[0], piso[1], config.int_bits, config.asymmetric,
+                                   config.clipping_ratios)
+            if r is not None:
+                codes, s16, z8, packed = r
+                method = "rtn_piso"
+            else:
+                codes, s16, z8, packed = _layer.rtn_codes(W_work, config.int_bits, config.asymmetric,
+                                                          config.clipping_ratios)
+                method = "rtn"
             state["rtn_fallback"] += 1
             logger.debug("No calibration data, using RTN fallback")
     elif config.quant_method == "ldlq":
@@ -387,10 +436,16 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
         logger.info("Matched %d/%d calibration layers to model layers", len(name_map), len(cal_keys))
 
     metadata = _metadata(config, shapes, skip_patterns)
+    piso_on = config.piso_scales and calibration is not None
+    if piso_on:
+        # the counts are known at the end; these placeholders size the
+        # streaming writer's header reservation
+        n2d = str(sum(1 for sh in shapes.values() if len(sh) == 2))
+        metadata.update({"int_crush.piso": "true", "int_crush.piso_layers": n2d, "int_crush.piso_zero_points": n2d})
     path = os.path.join(config.output_dir, "model.safetensors")
     if streaming:
         io.start(path, metadata)
-    state = {"gptq": 0, "rtn_fallback": 0, "permuted": 0}
+    state = {"gptq": 0, "rtn_fallback": 0, "permuted": 0, "piso": 0, "piso_zp": 0}
     skipped = quantized = 0
     reports: list[dict] = []
     total = sum(1 for n, sh in shapes.items() if not should_skip(n, skip_patterns) and len(sh) == 2)
@@ -442,6 +497,15 @@ def quantize_model(config: QuantizeConfig, *, progress_callback: ProgressCallbac
                 if bias in shapes and bias not in written:
                     io.passthrough(bias)
                     written.add(bias)
+        if piso_on:
+            # pipeline.py:462-466
+            for k in ("int_crush.piso", "int_crush.piso_layers", "int_crush.piso_zero_points"):
+                metadata.pop(k)
+            if state["piso"]:
+                metadata["int_crush.piso"] = "true"
+                metadata["int_crush.piso_layers"] = str(state["piso"])
+                if state["piso_zp"]:
+                    metadata["int_crush.piso_zero_points"] = str(state["piso_zp"])
         logger.info("Saving to %s...", path)
         out_bytes = io.finish(path, metadata)
     except BaseException:

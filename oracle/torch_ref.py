@@ -39,6 +39,12 @@ itself; see tests/test_oracle.py):
     rejected), by brute force (sorted order, valid permutation), and by the
     identity that per-row errors of W and W[:, perm] are the same multiset
     (equal in exact arithmetic, so fp64 sums agree).
+  * piso_scales_sym / piso_scales_asym: brute force in fp64 on small rows
+    (every candidate's error; the chosen one is within fp32 rounding of the
+    smallest and is a table entry times the stage's base), the reference's
+    behaviour tests (tests/gpu/test_piso_triton.py:86-170, 470-516: shapes,
+    positive scales, all-zero rows, large weights, zero-point range), and a
+    planted case whose optimum is known in closed form.
   * woodbury_inverse / dlr_to_dense: the fp64 dense inverse of the damped
     diag(D) + U U^T and the reference's KATs (tests/unit/
     test_dlr_hessian.py:142-235: damping definition, H H^-1 = I, U = 0 gives
@@ -780,6 +786,70 @@ def woodbury_inverse(D, U, damping=0.0):
 def dlr_to_dense(D, U):
     """diag(D) + U U^T (dlr.py:122-127)."""
     return torch.diag(D.float()) + U.float() @ U.float().T
+
+
+# ---------------------------------------------------------------- PiSO
+
+def _piso_batch(W, bytes_per_row):
+    return max(1, min(W.shape[0], (512 * 1024 * 1024) // max(1, bytes_per_row)))
+
+
+def piso_scales_sym(W, h_diag, num_coarse, num_fine, qmin, qmax, divisor):
+    """piso.py:28-94 (_compute_piso_scales_pytorch): per-row symmetric scale
+    grid search, the first minimum of each stage."""
+    M, D = W.shape
+    out = torch.empty(M, 1, dtype=torch.float32)
+    cf = torch.linspace(0.5, 2.0, num_coarse, dtype=torch.float32)
+    ff = torch.linspace(0.95, 1.05, num_fine, dtype=torch.float32)
+    bs = _piso_batch(W, (num_coarse + num_fine) * D * 4)
+    for r0 in range(0, M, bs):
+        Wb = W[r0:r0 + bs]
+        B = Wb.shape[0]
+        sa = (Wb.abs().amax(dim=1, keepdim=True) / divisor).clamp(min=1e-10)
+        sc = sa * cf.unsqueeze(0)
+        W3 = Wb.unsqueeze(1)
+        s3 = sc.unsqueeze(2)
+        q = rhaz(W3 / s3).clamp(qmin, qmax)
+        cost = ((W3 - q * s3) ** 2 * h_diag).sum(dim=2)
+        best = sc[torch.arange(B), cost.argmin(dim=1)]
+        sf = best.unsqueeze(1) * ff.unsqueeze(0)
+        s3 = sf.unsqueeze(2)
+        q = rhaz(W3 / s3).clamp(qmin, qmax)
+        cost = ((W3 - q * s3) ** 2 * h_diag).sum(dim=2)
+        out[r0:r0 + B, 0] = sf[torch.arange(B), cost.argmin(dim=1)]
+    return out
+
+
+def piso_scales_asym(W, h_diag, num_coarse, num_fine, qmin, qmax, lo, hi):
+    """piso.py:97-183 (_compute_piso_scales_asymmetric_pytorch): scales and
+    zero-points, every candidate clamped at 1e-10."""
+    M, D = W.shape
+    out = torch.empty(M, 1, dtype=torch.float32)
+    zps = torch.empty(M, 1, dtype=torch.int8)
+    cf = torch.linspace(lo, hi, num_coarse, dtype=torch.float32)
+    ff = torch.linspace(0.95, 1.05, num_fine, dtype=torch.float32)
+    divisor = float(qmax - qmin)
+    bs = _piso_batch(W, (num_coarse + num_fine) * D * 4)
+    for r0 in range(0, M, bs):
+        Wb = W[r0:r0 + bs].float()
+        B = Wb.shape[0]
+        wmin = Wb.amin(dim=1, keepdim=True)
+        wmax = Wb.amax(dim=1, keepdim=True)
+        sref = ((wmax - wmin) / divisor).clamp(min=1e-10)
+        W3 = Wb.unsqueeze(1)
+        best = None
+        for factors, base in ((cf, sref), (ff, None)):
+            s = ((base if best is None else best.unsqueeze(1)) * factors.unsqueeze(0)).clamp(min=1e-10)
+            s3 = s.unsqueeze(2)
+            z3 = rhaz(qmin - wmin.unsqueeze(2) / s3).clamp(qmin, qmax)
+            q = rhaz(W3 / s3 + z3).clamp(qmin, qmax)
+            cost = ((W3 - (q - z3) * s3) ** 2 * h_diag).sum(dim=2)
+            idx = cost.argmin(dim=1)
+            best = s[torch.arange(B), idx]
+            bz = z3.squeeze(2)[torch.arange(B), idx]
+        out[r0:r0 + B, 0] = best
+        zps[r0:r0 + B, 0] = bz.to(torch.int8)
+    return out, zps
 
 
 # ---------------------------------------------------------------- PermuQuant

@@ -39,7 +39,7 @@ def test_validation_errors(kw, msg):
         _validate(cfg(**kw))
 
 
-@pytest.mark.parametrize("kw", [dict(smoothquant=True, int_bits=8), dict(svd_rank=16), dict(piso_scales=True)])
+@pytest.mark.parametrize("kw", [dict(smoothquant=True, int_bits=8), dict(svd_rank=16)])
 def test_unsupported_features_raise(kw):
     with pytest.raises(NotImplementedError):
         _validate(cfg(**kw))
@@ -201,3 +201,18 @@ def test_calibration_dlr(tmp_path):
     torch.save(cal, path)
     h = cio.get_hessian(cio.load_calibration(str(path)), "layer.0", (32, 64))
     assert torch.equal(h["D"], D) and torch.equal(h["U"], U)
+
+
+def test_piso_config_accepted():
+    c = _validate(cfg(piso_scales=True, quant_method="gptq", calibration_path="c"))
+    assert c.piso_scales
+
+
+def test_piso_api_validation():
+    from int_crush_converter_amd import piso
+    with pytest.raises(ValueError, match="2D"):
+        piso.compute_piso_scales_int8(torch.randn(8), torch.ones(64))
+    with pytest.raises(ValueError, match="in_features"):
+        piso.compute_piso_scales_int8(torch.randn(8, 64), torch.ones(32))
+    with pytest.raises(ValueError, match="num_coarse"):
+        piso.compute_piso_scales_int4(torch.randn(8, 64), torch.ones(64), num_coarse=0)

@@ -567,3 +567,75 @@ def test_gptq_dlr_uses_woodbury_inverse(one_thread):
         ref.gptq_quantize_layer(W[:, :32], {"format": "dlr", "D": D, "U": U})
     with pytest.raises(ValueError):
         ref.ldlq_quantize_layer(W, {"format": "dlr", "D": D, "U": U}, greedy_passes=1)
+
+
+# ---------------------------------------------------------------- PiSO
+
+def _piso_cost64(w, h, s, zp, qmin, qmax):
+    """fp64 error of one candidate; q from the fp32 quotient (numpy)."""
+    w32, s32 = w.astype(np.float32), np.float32(s)
+    t = (w32 / s32).astype(np.float32)
+    if zp is not None:
+        t = (t + np.float32(zp)).astype(np.float32)
+    q = np.where(t >= 0, np.floor(t + np.float32(0.5)), np.ceil(t - np.float32(0.5))).clip(qmin, qmax)
+    dq = (q - (zp or 0.0)) * float(s32)
+    return float(((w.astype(np.float64) - dq) ** 2 * h.astype(np.float64)).sum())
+
+
+@pytest.mark.parametrize("asym,bits", [(False, 8), (False, 4), (True, 8), (True, 4)])
+def test_piso_choices_are_fp64_optimal(asym, bits):
+    # brute force: every stage's pick is within fp32 noise of that stage's fp64 minimum
+    g = torch.Generator().manual_seed(bits + 10 * asym)
+    W = torch.randn(12, 200, generator=g) * torch.exp(torch.randn(200, generator=g) * 0.5)
+    h = torch.rand(200, generator=g) + 0.01
+    qmin, qmax = (-128, 127) if bits == 8 else (-8, 7)
+    nc, nf = 24, 6
+    lo, hi = (0.8, 1.2) if (asym and bits == 8) else (0.5, 2.0)
+    if asym:
+        S, Z = ref.piso_scales_asym(W, h, nc, nf, qmin, qmax, lo, hi)
+    else:
+        S, Z = ref.piso_scales_sym(W, h, nc, nf, qmin, qmax, float(qmax)), None
+    # the factor tables are the reference's torch.linspace constants
+    cf = torch.linspace(lo, hi, nc, dtype=torch.float32).numpy()
+    ff = torch.linspace(0.95, 1.05, nf, dtype=torch.float32).numpy()
+    for r in range(W.shape[0]):
+        w, hv = W[r].numpy(), h.numpy()
+        sref = np.float32((w.max() - w.min()) / np.float32(qmax - qmin)) if asym else \
+            np.float32(np.abs(w).max() / np.float32(qmax))
+
+        def zp_of(s):
+            z = np.float32(qmin) - np.float32(np.float32(w.min()) / np.float32(s))
+            return float(np.clip(np.floor(z + 0.5) if z >= 0 else np.ceil(z - 0.5), qmin, qmax)) if asym else None
+
+        cs = [np.float32(max(sref * f, 1e-10) if asym else sref * f) for f in cf]
+        cc = [_piso_cost64(w, hv, s, zp_of(s), qmin, qmax) for s in cs]
+        # the final scale is base * fine factor for a base whose coarse cost is near-minimal
+        fs = None
+        for ci in np.argsort(cc):
+            if cc[ci] > min(cc) * (1 + 1e-5) + 1e-30:
+                break
+            cand = [np.float32(max(cs[ci] * f, 1e-10) if asym else cs[ci] * f) for f in ff]
+            if np.float32(S[r, 0].item()) in cand:
+                fs = cand
+                break
+        assert fs is not None, r
+        fc = [_piso_cost64(w, hv, s, zp_of(s), qmin, qmax) for s in fs]
+        k = fs.index(np.float32(S[r, 0].item()))
+        assert fc[k] <= min(fc) * (1 + 1e-5) + 1e-30
+        if asym:
+            assert Z[r, 0].item() == zp_of(fs[k])
+
+
+def test_piso_closed_forms_and_reference_behaviour():
+    # all-zero rows: every cost is 0, the first candidate of each stage wins
+    s = ref.piso_scales_sym(torch.zeros(2, 64), torch.ones(64), 16, 4, -128, 127, 127.0)
+    assert s[0, 0].item() == np.float32(np.float32(np.float32(1e-10) * np.float32(0.5)) * np.float32(0.95))
+    s, z = ref.piso_scales_asym(torch.zeros(2, 64), torch.ones(64), 16, 4, -8, 7, 0.5, 2.0)
+    assert s[0, 0].item() == np.float32(1e-10) and z[0, 0].item() == -8
+    # tests/gpu/test_piso_triton.py:133-148: scale ~ |w|max / 127 for large weights
+    g = torch.Generator().manual_seed(99)
+    W = torch.randn(16, 256, generator=g) * 100.0
+    s = ref.piso_scales_sym(W, torch.ones(256), 16, 4, -128, 127, 127.0)
+    assert s.shape == (16, 1) and s.min() > 0.1 and s.max() < 10.0
+    s, z = ref.piso_scales_asym(W, torch.rand(256, generator=g) + 1e-6, 16, 4, -128, 127, 0.8, 1.2)
+    assert (s > 0).all() and z.dtype == torch.int8 and z.min() >= -128 and z.max() <= 127
