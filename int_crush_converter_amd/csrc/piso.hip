@@ -24,7 +24,7 @@
 namespace icq {
 namespace {
 
-constexpr int PISO_THREADS = 512;
+constexpr int PISO_THREADS = 1024;
 constexpr int PISO_GROUPS = PISO_THREADS / SUM_SEQ;   // candidate groups of 32 lanes
 constexpr int PISO_MAXK = 4;                           // candidates per lane
 constexpr int PISO_SLOTS = PISO_GROUPS * PISO_MAXK;    // candidates per pass
@@ -54,10 +54,11 @@ struct Cand {
     bool fast;        // w / s by the Markstein sequence (exact in its domain)
 };
 
-template <bool ASYM>
+// FAST: every candidate of the caller takes the Markstein division
+template <bool ASYM, bool FAST = false>
 __device__ __forceinline__ float piso_err(float w, float h, const Cand& c, float qmin, float qmax) {
     float t;
-    if (c.fast) {
+    if (FAST || c.fast) {
         const float q0 = w * c.y;
         const float r = __builtin_fmaf(-q0, c.s, w);
         t = __builtin_fmaf(r, c.y, q0);
@@ -122,14 +123,28 @@ __device__ void eval_costs(const float* wv, const float* hv, int64_t L, float ba
                 cd[k] = make_cand<ASYM>(base, factor[c], wmin, qmin, qmax, row_ok);
             }
             float out[K];
-            cascade_seq_k<K>(
-                [&](int64_t m, float (&e)[K]) {
-                    const int64_t i = m * SUM_SEQ + s;
-                    const float w = wv[i], h = hv[i];
+            bool all_fast = true;
 #pragma unroll
-                    for (int k = 0; k < K; ++k) e[k] = piso_err<ASYM>(w, h, cd[k], qmin, qmax);
-                },
-                n4, lp, out);
+            for (int k = 0; k < K; ++k) all_fast = all_fast && cd[k].fast;
+            if (all_fast) {
+                cascade_seq_k<K>(
+                    [&](int64_t m, float (&e)[K]) {
+                        const int64_t i = m * SUM_SEQ + s;
+                        const float w = wv[i], h = hv[i];
+#pragma unroll
+                        for (int k = 0; k < K; ++k) e[k] = piso_err<ASYM, true>(w, h, cd[k], qmin, qmax);
+                    },
+                    n4, lp, out);
+            } else {
+                cascade_seq_k<K>(
+                    [&](int64_t m, float (&e)[K]) {
+                        const int64_t i = m * SUM_SEQ + s;
+                        const float w = wv[i], h = hv[i];
+#pragma unroll
+                        for (int k = 0; k < K; ++k) e[k] = piso_err<ASYM>(w, h, cd[k], qmin, qmax);
+                    },
+                    n4, lp, out);
+            }
 #pragma unroll
             for (int k = 0; k < K; ++k) part[g * K + k][s] = out[k];
         }
