@@ -97,7 +97,7 @@ PROFILE_KERNELS = {
     "rtn_scales_kernel": ["rtn_scales"],
     "rtn_quant_kernel": ["rtn_quant_pack"],
     "quant_error_partial": ["verify"],
-    "fsum_block_kernel": ["permute_sum"],
+    "fsum_group_kernel": ["permute_sum"],   # (fsum_block_kernel: its fallback for cascade groups above 32)
     "piso_kernel": ["piso"],
 }
 

@@ -257,6 +257,56 @@ __global__ void fsum_block_kernel(Src x, SumPlan p, int64_t nbmax, float* B) {
     B[((int64_t)t * nbmax + b) * SUM_SEQ + s] = cascade_block(get, b, lp);
 }
 
+// The same block values with 2^LP times the parallelism: work-group (block
+// b, chunk t), thread (sequence s, group g) sums the S = 2^LP values of group
+// g in order, and thread (s, 0) adds the S group sums in order, which is
+// the sequence of additions cascade_block makes.
+template <typename Src, int LP>
+__global__ __launch_bounds__(SUM_SEQ << LP) void fsum_group_kernel(Src x, SumPlan p, int64_t nbmax, float* B) {
+    constexpr int S = 1 << LP;
+    __shared__ float G[S][SUM_SEQ + 1];
+    const int s = threadIdx.x % SUM_SEQ, g = threadIdx.x / SUM_SEQ;
+    const int t = blockIdx.y;
+    const int64_t b = blockIdx.x;
+    const int64_t c0 = (int64_t)t * p.chunk;
+    const int64_t L = std::min(p.n, c0 + p.chunk) - c0;
+    if (L <= 0) return;                                  // uniform in the work-group
+    const int64_t n4 = (L / SUM_VEC) / 4;
+    if (b >= (n4 >> (2 * LP))) return;                   // uniform in the work-group
+    const int64_t m0 = (b << (2 * LP)) + (int64_t)g * S;
+    const int64_t k0 = c0 + m0 * SUM_SEQ + s;
+    const int64_t r0 = k0 / x.cols, cc0 = k0 - r0 * x.cols;
+    auto get = [&](int64_t m) {
+        int64_t c = cc0 + (m - m0) * SUM_SEQ, r = r0;
+        if (c >= x.cols) {
+            r += c / x.cols;
+            c -= (c / x.cols) * x.cols;
+        }
+        return x.at(r, c);
+    };
+    G[g][s] = seq_sum(get, m0, S);
+    __syncthreads();
+    if (g == 0) {
+        float a1 = 0.0f;
+        for (int q = 0; q < S; ++q) a1 = a1 + G[q][s];
+        B[((int64_t)t * nbmax + b) * SUM_SEQ + s] = a1;
+    }
+}
+
+// The cascade's log2 group size shared by every chunk of the plan, or -1.
+static int common_lp(const SumPlan& p) {
+    int lp = -1;
+    for (int t = 0; t < p.nt; ++t) {
+        const int64_t c0 = (int64_t)t * p.chunk;
+        const int64_t L = std::min(p.n, c0 + p.chunk) - c0;
+        if (L <= 0) continue;
+        const int l = cascade_lp((L / SUM_VEC) / 4);
+        if (lp >= 0 && l != lp) return -1;
+        lp = l;
+    }
+    return lp;
+}
+
 // One work-group per chunk: the 32 sequence cascades from the block values,
 // then the chunk's leftover vectors, the merge of the four accumulators,
 // the leftover scalars and the lanes (thread 0).  Chunk results go to buf
@@ -342,8 +392,17 @@ static int torch_sum(const Src& x, int64_t n, int threads, float* out, float* ws
     if (nbmax > 0) {
         const int64_t per = nbmax * SUM_SEQ;
         ProfScope prof_scope(st, PT_PERM_SUM, (double)n, 4.0 * n);
-        hipLaunchKernelGGL(fsum_block_kernel<Src>, dim3((unsigned)cdiv(per, 256), (unsigned)p.nt), dim3(256), 0, st, x,
-                           p, nbmax, B);
+        const int lp = common_lp(p);
+        if (lp == 4) {
+            hipLaunchKernelGGL((fsum_group_kernel<Src, 4>), dim3((unsigned)nbmax, (unsigned)p.nt), dim3(SUM_SEQ << 4),
+                               0, st, x, p, nbmax, B);
+        } else if (lp == 5) {
+            hipLaunchKernelGGL((fsum_group_kernel<Src, 5>), dim3((unsigned)nbmax, (unsigned)p.nt), dim3(SUM_SEQ << 5),
+                               0, st, x, p, nbmax, B);
+        } else {
+            hipLaunchKernelGGL(fsum_block_kernel<Src>, dim3((unsigned)cdiv(per, 256), (unsigned)p.nt), dim3(256), 0,
+                               st, x, p, nbmax, B);
+        }
         IC_CHECK_LAUNCH();
     }
     hipLaunchKernelGGL(fsum_finish_kernel<Src>, dim3((unsigned)p.nt), dim3(64), 0, st, x, p,
