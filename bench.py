@@ -206,13 +206,17 @@ WORKLOADS_CPU_ROWS = 512
 
 
 def cpu_step(kind, W, H):
-    """The reference's CPU algorithm (oracle restatement) on the same layer."""
+    """The reference's CPU algorithm (oracle restatement) on the same layer.
+    Returns what the parity check needs: codes, stored scales, zero-points,
+    the oracle-rotated W (rows of the sample) and, for a dense Hessian, the
+    rotated H."""
     import torch
     from oracle import torch_ref as ref
     if kind == "dit":   # bounded sample: the block's first layer (qkv)
         return cpu_step("gptq", W[0], H[0])
     Wf = W.float()
     Wf = Wf.masked_fill(Wf.abs() > 1000.0, 0.0)
+    Hr = None
     if kind == "gptq":
         Wr = ref.rotate_weights(Wf, 256)
         Hr = ref.rotate_hessian(H, 256)
@@ -251,6 +255,98 @@ def cpu_step(kind, W, H):
     (Wr - d).double().pow(2).mean().item()
     if kind != "rtn8":
         ref.pack_int4(q)
+    return {"q": q, "s": s, "z": z, "Wr": Wr, "Hr": Hr}
+
+
+def oracle_self_codes(cpu):
+    """The oracle's GPTQ codes again with half the CPU threads: LAPACK's
+    Cholesky / inverse change their fp32 summation order with the thread
+    count, which measures the reference's own run-to-run noise."""
+    import torch
+    from oracle import torch_ref as ref
+    threads = torch.get_num_threads()
+    torch.set_num_threads(max(1, threads // 2))
+    try:
+        Hinv = ref.prepare_hinv(cpu["Hr"], 0.01)
+    finally:
+        torch.set_num_threads(threads)
+    s32, z = ref.gptq_row_params(cpu["Wr"], 4, False)
+    Q = torch.zeros(cpu["Wr"].shape, dtype=torch.int8)
+    ref.gptq_block(cpu["Wr"].clone(), Q, s32, Hinv, 0, cpu["Wr"].shape[1], 128, -8, 7, z)
+    return Q
+
+
+def oracle_on_gpu_rotation(out, H):
+    """The oracle's GPTQ layer on the GPU-rotated W and H of the timed step
+    (the same quantiser inputs; the rotations round differently)."""
+    from oracle import torch_ref as ref
+    from int_crush_converter_amd.rotation import rotate_hessian_gpu
+    Hg = rotate_hessian_gpu(H, 256).cpu()
+    return ref.gptq_quantize_layer(out.W_work.cpu(), Hg, 128, 0.01, 4).quantized_W
+
+
+def parity(kind, out, cpu, self_codes=None, same_codes=None):
+    """Codes of the timed GPU step against the oracle's: share of equal codes
+    (against the oracle from the same raw inputs, and against the oracle on
+    the GPU-rotated inputs), relative tr(dW H dW^T) difference (dense-Hessian
+    GPTQ), stored-scale equality and the largest fp16-ulp scale difference;
+    for GPTQ also the oracle's own noise (half the CPU threads, and its
+    layer on the GPU's rotation)."""
+    import torch
+    dev = torch.device("cuda:0")
+    rows = cpu["q"].shape[0]
+    q = out.codes[:rows].cpu()
+    s = out.scales.reshape(-1)[:rows].cpu()
+    s_ref = cpu["s"].reshape(-1)
+    res = {"vs": "oracle (the reference's CPU algorithm) on the same inputs", "rows": rows,
+           "agreement": round((q == cpu["q"]).float().mean().item(), 6),
+           "scales_equal": bool(torch.equal(s.to(s_ref.dtype), s_ref))}
+    if s_ref.dtype == torch.float16:
+        ulps = (s.view(torch.int16).int() - s_ref.view(torch.int16).int()).abs().max().item()
+        res["scale_max_fp16_ulps"] = int(ulps)
+    if cpu["Hr"] is not None:
+        Hr = cpu["Hr"] if cpu["Hr"].dim() == 2 else torch.block_diag(*cpu["Hr"])
+        Hd = Hr.to(dev).double()
+        Wd = cpu["Wr"].to(dev).double()
+
+        def proxy(Q, sc, zp):
+            d = (Q.to(dev).double() - (zp.to(dev).double().reshape(-1, 1) if zp is not None else 0)) \
+                * sc.to(dev).double().reshape(-1, 1) - Wd
+            return ((d @ Hd) * d).sum().item()
+
+        p_ref = proxy(cpu["q"], cpu["s"].float(), cpu["z"])
+        zg = None if out.zero_points is None else out.zero_points.reshape(-1)[:rows].cpu()
+        res["proxy_rel"] = round(proxy(q, s.float(), zg) / p_ref - 1, 7)
+        if self_codes is not None:
+            res["oracle_self_agreement"] = round((self_codes == cpu["q"]).float().mean().item(), 6)
+            res["oracle_self_proxy_rel"] = round(proxy(self_codes, cpu["s"].float(), cpu["z"]) / p_ref - 1, 7)
+        if same_codes is not None:
+            res["agreement_same_inputs"] = round((q == same_codes).float().mean().item(), 6)
+            res["oracle_rotation_agreement"] = round((same_codes == cpu["q"]).float().mean().item(), 6)
+        del Hd, Wd
+    return res
+
+
+def host_cpu():
+    """Model name, sockets, cores and SMT of the host (lscpu), and the CPU
+    share this process may use."""
+    import subprocess
+    info = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    out = {"model": info.get("Model name"), "sockets": info.get("Socket(s)"),
+           "cores_per_socket": info.get("Core(s) per socket"), "threads_per_core": info.get("Thread(s) per core"),
+           "logical_cpus": os.cpu_count()}
+    try:
+        out["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    return out
 
 
 def measured_traffic(workload, kernel):
@@ -383,6 +479,8 @@ def main():
                                 "GB/s": round(v["bytes"] / max(v["ms"], 1e-9) / 1e6, 1)}
                             for k, v in prof.items() if v["launches"]}
     if not args.no_cpu_baseline:
+        # torch's intra-op threads: OMP_NUM_THREADS, the CPU share of one GPU
+        # on the box (os.cpu_count() counts the whole host)
         threads = torch.get_num_threads()
         log(f"[bench] CPU baseline (oracle, {threads} threads): 1 layer")
         if kind == "dit":
@@ -398,13 +496,20 @@ def main():
                   else H.cpu() if H is not None else None)
             sample_w, sample = weights, f"1 layer of {args.workload}"
         c0 = time.perf_counter()
-        cpu_step(kind, Wc, Hc)
+        cpu = cpu_step(kind, Wc, Hc)
         c1 = time.perf_counter()
         result["cpu_baseline"] = {"value": round(sample_w / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
                                   "cores": threads, "kind": "port",
                                   "sample": f"{sample} ({c1 - c0:.1f} s), torch CPU oracle "
-                                            "restating the reference's CPU path"}
-        log(f"[bench] CPU {c1 - c0:.2f} s")
+                                            "restating the reference's CPU path",
+                                  "host": host_cpu()}
+        log(f"[bench] CPU {c1 - c0:.2f} s; parity of the timed step's output")
+        # untimed: the codes of the timed step against the oracle's
+        ref_out = gpu_step("gptq", W[0], H[0]) if kind == "dit" else out
+        self_codes = oracle_self_codes(cpu) if kind == "gptq" else None
+        same_codes = oracle_on_gpu_rotation(out, H) if kind == "gptq" else None
+        result["parity"] = parity(kind, ref_out, cpu, self_codes, same_codes)
+        log(f"[bench] parity {result['parity']}")
     print(json.dumps(result), flush=True)
 
 
@@ -476,7 +581,8 @@ def main_e2e(args, extra):
             result["cpu_baseline"] = {"value": round(W0.numel() / (c1 - c0) / 1e6, 3), "unit": "Mweights/s",
                                       "cores": threads, "kind": "port",
                                       "sample": f"layer {name0} ({c1 - c0:.1f} s), torch CPU oracle restating "
-                                                "the reference's CPU path (compute only, no file I/O)"}
+                                                "the reference's CPU path (compute only, no file I/O)",
+                                      "host": host_cpu()}
         print(json.dumps(result), flush=True)
     finally:
         shutil.rmtree(d, ignore_errors=True)

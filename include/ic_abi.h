@@ -162,6 +162,15 @@ int64_t ic_hessian_inverse_workspace_bytes(int64_t batch, int64_t n);
 int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damping, int method,
                        int* info, void* workspace, void* stream);
 
+/* Damping alone, in place on `batch` dense fp32 matrices [n, n] (back to
+ * back): H <- H + fp32(damping) * max(mean(diag H), 1e-6) * I, the mean
+ * summed in torch's CPU order (its scalar reduction of the strided
+ * diagonal; one-thread order from n = 32768 on) and divided by n, as the
+ * reference's H.diagonal().mean() (converter/gptq.py:104, 118;
+ * converter/ldlq.py:83, 169, 207-209, where the damped H also feeds the
+ * greedy search).  ic_hessian_inverse applies the same damping first. */
+int ic_damp_hessian(float* H, int64_t batch, int64_t n, float damping, void* stream);
+
 /* Lower Cholesky factor in place (upper part of the diagonal 128-blocks set
  * to 0, the rest of the upper triangle untouched); info as above; workspace
  * as for ic_hessian_inverse.  Replaces torch.linalg.cholesky. */
@@ -225,7 +234,9 @@ int ic_ldlq_update_scales(const float* W, const int8_t* Q, const float* cur, con
                           int64_t n, float momentum, float lo, float hi, float* out, void* stream);
 
 /* Per-row least-squares scale clamp(sum(q w) / max(sum(q q), 1e-8), min 1e-5)
- * (converter/ldlq.py:227-231, 262-265). */
+ * (converter/ldlq.py:227-231, 262-265), both row sums of fp32 products in
+ * torch's CPU inner-sum order (thread-count independent for rows >= 2, and
+ * for one row below 32768 columns), so the scales equal the reference's. */
 int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64_t cols, float* out, void* stream);
 
 /* Full-rank greedy coordinate descent on the integer grid minimising

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "chol.hpp"
+#include "torchsum.hpp"
 
 namespace icq {
 
@@ -23,28 +24,38 @@ constexpr int NB = 128;
 
 static double dtri(double n) { return n * (n + 1) / 2; }
 
-// One work-group of 256 per matrix: the diagonal's loads are issued eight at
-// a time (each touches its own cache line), then summed in fp64.
+// One work-group of 256 per matrix: H += damping * max(mean(diag H), 1e-6) * I
+// with the mean computed as the reference computes H.diagonal().mean() on
+// the CPU (converter/gptq.py:104, 118; ldlq.py:83, 169, 207): torch's fp32
+// scalar row_sum of the strided diagonal, then one IEEE division by n.  (At
+// n >= 32768 torch splits a full reduction over its CPU threads, so this is
+// its one-thread order there.)  The diagonal is staged in LDS first, so
+// every load is in flight at once.
+constexpr int DAMP_LDS = 16384;
 __global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t ld, int64_t stride, float damping) {
     float* A = H + (int64_t)blockIdx.x * stride;
-    double acc = 0.0;
-    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * (int64_t)blockDim.x) {
-        float v[8];
+    __shared__ float dg[DAMP_LDS];
+    __shared__ float blk[RS_MAX_BLOCKS];
+    __shared__ float part[4];
+    const bool staged = n <= DAMP_LDS;
+    if (staged) {
+        for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * (int64_t)blockDim.x) {
+            float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int64_t i = i0 + u * (int64_t)blockDim.x;
-            v[u] = i < n ? A[i * ld + i] : 0.0f;
+            for (int u = 0; u < 8; ++u) {
+                const int64_t i = i0 + u * (int64_t)blockDim.x;
+                v[u] = i < n ? A[i * ld + i] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t i = i0 + u * (int64_t)blockDim.x;
+                if (i < n) dg[i] = v[u];
+            }
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += (double)v[u];
     }
-    __shared__ double part[4];
-    acc = wave_sum(acc);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
     __syncthreads();
-    double tot = 0.0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += part[w];
-    float mean = (float)(tot / (double)n);
+    const float sum = row_sum_wg([&](int64_t i) { return staged ? dg[i] : A[i * ld + i]; }, n, blk, part);
+    float mean = sum / (float)n;
     mean = mean > 1e-6f ? mean : (mean != mean ? mean : 1e-6f);
     const float delta = damping * mean;
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) A[i * ld + i] = A[i * ld + i] + delta;
@@ -664,6 +675,15 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
         hipLaunchKernelGGL(lower_to_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
         IC_CHECK_LAUNCH();
     }
+    return IC_OK;
+}
+
+extern "C" int ic_damp_hessian(float* H, int64_t batch, int64_t n, float damping, void* stream) {
+    IC_REQUIRE(H || batch == 0 || n == 0, "ic_damp_hessian: null pointer");
+    IC_REQUIRE(n >= 0 && batch >= 0 && batch < (1LL << 31), "ic_damp_hessian: bad size");
+    if (n == 0 || batch == 0) return IC_OK;
+    hipLaunchKernelGGL(damp_kernel, dim3((unsigned)batch), dim3(256), 0, as_stream(stream), H, n, n, n * n, damping);
+    IC_CHECK_LAUNCH();
     return IC_OK;
 }
 

@@ -9,6 +9,7 @@
 // sum_j' d_j' H[j', j] - the same quantity in exact arithmetic as the
 // reference's per-column GEMV (its fp32 rounding differs).
 #include "gemm.hpp"
+#include "torchsum.hpp"
 
 namespace icq {
 
@@ -85,27 +86,44 @@ __global__ void ldlq_update_kernel(const float* W, const int8_t* Q, const float*
 }
 
 // Per-row least squares scale clamp(sum(q w) / max(sum(q q), 1e-8), min=1e-5)
-// (ldlq.py:227-231, 262-265), fp64 accumulation rounded once to fp32.
+// (ldlq.py:227-231, 262-265).  The reference sums the fp32 products
+// (Q_float * W, Q_float * Q_float) over each row with torch's CPU inner
+// sum (one CPU thread per row when there is more than one row), so the
+// sums here follow that order: lane s (< 32) of a row's wave takes
+// sequence s of the numerator, lane 32 + s that of the denominator, and one
+// lane per sum finishes it (the leftover vectors, the merge, the leftover
+// scalars, the lanes).  A wave per row, four rows per work-group.
 __global__ __launch_bounds__(256) void ls_scales_kernel(const int8_t* Q, const float* W, int64_t rows, int64_t cols,
                                                         float* out) {
-    const int64_t r = blockIdx.x;
-    if (r >= rows) return;
-    double num = 0.0, den = 0.0;
-    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float q = (float)Q[r * cols + c];
-        num += (double)(q * W[r * cols + c]);
-        den += (double)(q * q);
+    __shared__ float part[4][2][SUM_SEQ];
+    __shared__ float dens[4];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t r0 = (int64_t)blockIdx.x * 4 + wv;
+    const bool live = r0 < rows;
+    const int64_t r = live ? r0 : rows - 1;
+    const int8_t* q = Q + r * cols;
+    const float* w = W + r * cols;
+    auto xn = [&](int64_t i) { const float qf = (float)q[i]; return qf * w[i]; };
+    auto xd = [&](int64_t i) { const float qf = (float)q[i]; return qf * qf; };
+    const int which = lane >> 5, s = lane & (SUM_SEQ - 1);
+    float sum = 0.0f;
+    if (cols >= SUM_VEC) {
+        const int64_t n4 = cols / SUM_VEC / 4;
+        const int lp = cascade_lp(n4);
+        part[wv][which][s] = which == 0 ? cascade_seq([&](int64_t m) { return xn(m * SUM_SEQ + s); }, n4, lp)
+                                        : cascade_seq([&](int64_t m) { return xd(m * SUM_SEQ + s); }, n4, lp);
+        __syncthreads();
+        if (s == 0) sum = which == 0 ? inner_sum_finish(part[wv][0], xn, cols) : inner_sum_finish(part[wv][1], xd, cols);
+    } else {
+        __syncthreads();
+        if (s == 0) sum = which == 0 ? inner_sum_short(xn, cols) : inner_sum_short(xd, cols);
     }
-    __shared__ double sn[4], sd[4];
-    num = wave_sum(num);
-    den = wave_sum(den);
-    if ((threadIdx.x & 63) == 0) { sn[threadIdx.x >> 6] = num; sd[threadIdx.x >> 6] = den; }
+    if (lane == 32) dens[wv] = sum;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float n32 = (float)(sn[0] + sn[1] + sn[2] + sn[3]);
-        float d32 = (float)(sd[0] + sd[1] + sd[2] + sd[3]);
+    if (lane == 0 && live) {
+        float d32 = dens[wv];
         d32 = d32 < 1e-8f ? 1e-8f : d32;
-        out[r] = nclampmin(n32 / d32, 1e-5f);
+        out[r] = nclampmin(sum / d32, 1e-5f);
     }
 }
 
@@ -402,7 +420,8 @@ extern "C" int ic_ldlq_update_scales(const float* W, const int8_t* Q, const floa
 extern "C" int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64_t cols, float* out, void* stream) {
     IC_REQUIRE(Q && W && out && rows < (1LL << 31), "ic_ls_scales: bad arguments");
     if (rows == 0) return IC_OK;
-    hipLaunchKernelGGL(ls_scales_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), Q, W, rows, cols, out);
+    hipLaunchKernelGGL(ls_scales_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, as_stream(stream), Q, W, rows,
+                       cols, out);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

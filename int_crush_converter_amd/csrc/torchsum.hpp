@@ -136,4 +136,90 @@ __device__ float inner_sum_short(X x, int64_t L) {
     return ((p[0] + p[1]) + p[2]) + p[3];
 }
 
+// ---------------------------------------------------------------- row_sum
+// torch's scalar reduction of L values x(0 .. L - 1) (a strided or short
+// row: the diagonal of a matrix, H.diagonal().sum() below the parallel grain
+// size): four interleaved sequences x(4 m + k), m < L / 4, each a cascade
+// with group size S = 2^cascade_lp(L / 4); the last L mod 4 values go to
+// sequence 0; the result is ((p0 + p1) + p2) + p3.  The whole-block values
+// of the cascades (S groups of S values each) are independent, so a
+// work-group computes them in parallel and then finishes each sequence in
+// the cascade's own order.
+
+// The value the cascade's second accumulator holds after block b of a
+// sequence get(0 ..): the sum from 0 of its S group sums.
+template <typename Get>
+__device__ float rs_block(Get get, int64_t b, int lp) {
+    const int64_t S = int64_t(1) << lp, i0 = b << (2 * lp);
+    float a1 = 0.0f;
+    for (int64_t g = 0; g < S; ++g) {
+        float a0 = 0.0f;
+        for (int64_t j = 0; j < S; ++j) a0 = a0 + get(i0 + g * S + j);
+        a1 = a1 + a0;
+    }
+    return a1;
+}
+
+// The cascade of a sequence of L values given its whole-block values
+// blk(0 .. L / S^2 - 1): the blocks into the third accumulator (flushed to
+// the fourth every S blocks), then the values after the last whole block.
+template <typename Blk, typename Get>
+__device__ float rs_finish(Blk blk, Get get, int64_t L, int lp) {
+    const int64_t S = int64_t(1) << lp;
+    const int64_t nb = L >> (2 * lp);
+    float a2 = 0.0f, a3 = 0.0f;
+    for (int64_t b = 0; b < nb; ++b) {
+        a2 = a2 + blk(b);
+        if (((b + 1) & (S - 1)) == 0) {
+            a3 = a3 + a2;
+            a2 = 0.0f;
+        }
+    }
+    int64_t i = nb << (2 * lp);
+    float a1 = 0.0f;
+    for (; i + S <= L; i += S) {
+        float a0 = 0.0f;
+        for (int64_t j = 0; j < S; ++j) a0 = a0 + get(i + j);
+        a1 = a1 + a0;
+    }
+    float a0 = 0.0f;
+    for (; i < L; ++i) a0 = a0 + get(i);
+    a0 = a0 + a1;
+    a0 = a0 + a2;
+    return a0 + a3;
+}
+
+// row_sum of x(0 .. L - 1) by the threads of a work-group (all of them must
+// call it); blk: LDS scratch of RS_MAX_BLOCKS floats.  Every thread gets the
+// result.
+constexpr int RS_MAX_BLOCKS = 256;
+template <typename X>
+__device__ float row_sum_wg(X x, int64_t L, float* blk, float* part) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int64_t n4 = L / 4;
+    const int lp = cascade_lp(n4);
+    const int64_t nb = n4 >> (2 * lp);
+    const bool blocked = 4 * nb <= RS_MAX_BLOCKS;
+    if (blocked) {
+        for (int64_t u = t; u < 4 * nb; u += nt) {
+            const int k = (int)(u & 3);
+            const int64_t b = u >> 2;
+            blk[u] = rs_block([&](int64_t m) { return x(4 * m + k); }, b, lp);
+        }
+    }
+    __syncthreads();
+    if (t < 4) {
+        const int k = t;
+        auto get = [&](int64_t m) { return x(4 * m + k); };
+        part[k] = blocked ? rs_finish([&](int64_t b) { return blk[4 * b + k]; }, get, n4, lp)
+                          : cascade_seq(get, n4, lp);
+    }
+    __syncthreads();
+    float p0 = part[0];
+    for (int64_t i = 4 * n4; i < L; ++i) p0 = p0 + x(i);
+    const float r = ((p0 + part[1]) + part[2]) + part[3];
+    __syncthreads();   // part[] may be reused by the caller
+    return r;
+}
+
 }  // namespace icq

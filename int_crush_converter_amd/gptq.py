@@ -78,6 +78,39 @@ def sweep(W_work: torch.Tensor, Hinv: torch.Tensor, s32: torch.Tensor, z32: torc
     return Q
 
 
+def block_cover(N: int, nblk: int, bs: int) -> tuple[int, int]:
+    """(whole blocks swept as one batch, width of the partial block after
+    them) for a 3-D Hessian [nblk, bs, bs] over N columns.  Follows the
+    reference's loop over the Hessian's blocks (gptq.py:345-366): block b
+    covers columns [b bs, min((b + 1) bs, N)); blocks past column N do
+    nothing, and columns past the last block are not swept (their codes stay
+    0, as quantized_W = zeros_like(W) leaves them)."""
+    full = min(N // bs, nblk) if bs > 0 else 0
+    rem = min(bs, N - full * bs) if full < nblk else 0
+    return full, rem
+
+
+def sweep_block_diagonal(W_work: torch.Tensor, Hg: torch.Tensor, damping: float, hessian_method: str,
+                         fallbacks: list[str], s32, z32, int_bits: int, block_size: int) -> torch.Tensor:
+    """GPTQ over a block-diagonal 3-D Hessian: the whole blocks inverted as a
+    batch and swept as independent column groups of one launch, the partial
+    last block on its own.  W_work is scratch (its columns may be changed);
+    returns int8 codes."""
+    M, N = W_work.shape
+    nblk, bs, _ = Hg.shape
+    full, rem = block_cover(N, nblk, bs)
+    Q = torch.zeros(M, N, dtype=torch.int8, device=W_work.device)
+    if full > 0:
+        Hinv = inverse_batch(Hg[:full].float(), damping, hessian_method, fallbacks, upper_only=True)
+        Q[:, :full * bs] = sweep(W_work[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits, block_size,
+                                 groups=full)
+    if rem > 0:
+        c0 = full * bs
+        Hinv = inverse_batch(Hg[full, :rem, :rem].float(), damping, hessian_method, fallbacks, upper_only=True)
+        Q[:, c0:c0 + rem] = sweep(W_work[:, c0:c0 + rem].contiguous(), Hinv, s32, z32, int_bits, block_size)
+    return Q
+
+
 def gptq_quantize_layer(
     W: torch.Tensor,
     hessian: torch.Tensor,
@@ -122,19 +155,7 @@ def gptq_quantize_layer(
     elif isinstance(Hg, dict):
         raise ValueError(f"Expected 2D tensor, 3D tensor, or DLR dict Hessian, got {type(hessian).__name__}")
     elif Hg.dim() == 3:
-        nblk, bs, _ = Hg.shape
-        full = N // bs
-        Q = torch.empty(M, N, dtype=torch.int8, device=Wg.device)
-        if full > 0:
-            Hinv = inverse_batch(Hg[:full].float(), damping, hessian_method, fallbacks, upper_only=True)
-            Q[:, :full * bs] = sweep(W_work[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits,
-                                     block_size, groups=full)
-        if full * bs < N:
-            if full >= nblk:
-                raise ValueError(f"3-D Hessian with {nblk} blocks of {bs} does not cover {N} columns")
-            rem = N - full * bs
-            Hinv = inverse_batch(Hg[full, :rem, :rem].float(), damping, hessian_method, fallbacks, upper_only=True)
-            Q[:, full * bs:] = sweep(W_work[:, full * bs:].contiguous(), Hinv, s32, z32, int_bits, block_size)
+        Q = sweep_block_diagonal(W_work, Hg, damping, hessian_method, fallbacks, s32, z32, int_bits, block_size)
     elif Hg.dim() == 2:
         if tuple(Hg.shape) != (N, N):
             raise ValueError(f"Hessian shape {hessian.shape} != ({N}, {N})")

@@ -15,15 +15,18 @@ import warnings
 import torch
 
 from . import _native as nat
-from .config import DIAG_MEAN_FLOOR
 from .log import logger
 
 METHODS = {"hinv": 0, "cholesky": 1}
 
 
 def _damped(H: torch.Tensor, damping: float) -> torch.Tensor:
-    dm = H.diagonal().mean().clamp(min=DIAG_MEAN_FLOOR)
-    return H + damping * dm * torch.eye(H.shape[0], dtype=torch.float32, device=H.device)
+    """H + damping * max(mean(diag H), 1e-6) * I as a new tensor (the
+    library's damping kernel, the reference's CPU summation order)."""
+    out = H.float().contiguous().clone()
+    nat.check(nat.lib().ic_damp_hessian(out.data_ptr(), 1, out.shape[0], float(damping), nat.stream()),
+              "ic_damp_hessian")
+    return out
 
 
 def _fallback_inverse(H_damped: torch.Tensor) -> torch.Tensor:
@@ -89,16 +92,27 @@ def inverse_batch(H: torch.Tensor, damping: float, method: str = "hinv",
             Hi = _fallback_inverse(Hd)
         else:
             Hi = None
-        if code == 0:
-            out[b] = Hi
-            continue
-        if Hi is None:
-            # chol(H) worked but chol(H^-1) did not: return H^-1 itself (gptq.py:106-110)
-            Hi = inverse_batch((orig if inplace else Hb)[b], damping, "hinv")
-            out[b] = Hi
-            continue
-        try:
-            out[b] = torch.linalg.cholesky(Hi).T
-        except torch.linalg.LinAlgError:
-            out[b] = Hi
+        src = (orig if inplace else Hb)[b]
+        out[b] = fallback_output(code, Hi, lambda: inverse_batch(src, damping, "hinv"))
     return out[0] if squeeze else out
+
+
+def fallback_output(code: int, Hi: torch.Tensor | None, hinv_of_input) -> torch.Tensor:
+    """The matrix the reference hands to the column loop when a GPU Cholesky
+    failed.  ``code``: 0 = method "hinv", 2 = "hinv" with only the upper
+    triangle read (both: converter/gptq.py:113-121, the inverse itself),
+    1 = method "cholesky" (converter/gptq.py:91-110: the upper Cholesky factor
+    of the inverse, or the inverse when that factorisation fails).  ``Hi``:
+    the inv / pinv fallback of the damped H when chol(H) failed, None when
+    chol(H) worked and only chol(H^-1) failed (then ``hinv_of_input()`` gives
+    H^-1)."""
+    if code in (0, 2):
+        if Hi is None:
+            raise ValueError("fallback_output: method hinv needs the fallback inverse")
+        return Hi
+    if Hi is None:
+        return hinv_of_input()
+    try:
+        return torch.linalg.cholesky(Hi).T
+    except torch.linalg.LinAlgError:
+        return Hi

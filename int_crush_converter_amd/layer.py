@@ -16,7 +16,7 @@ import torch
 from . import _native as nat
 from .dlr import dlr_to_dense, is_dlr, woodbury_inverse
 from .config import INT4_SCALE_DIVISOR, INT8_SCALE_DIVISOR, SCALE_MAX, SCALE_MIN, WEIGHT_OUTLIER_CLAMP
-from .gptq import quant_error, row_params, sweep
+from .gptq import quant_error, row_params, sweep, sweep_block_diagonal
 from .hessian import inverse_batch
 from .rotation import rotate_rows_gpu, rotate_hessian_gpu
 from . import scales as _scales
@@ -106,16 +106,7 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
     s32, z32, s16, z8 = _gptq_params(W_work, int_bits, asymmetric, piso)
     Ww = W_work.clone()
     if Hg.dim() == 3:
-        nblk, bs, _ = Hg.shape
-        full = N // bs
-        Q = torch.empty(M, N, dtype=torch.int8, device=W_work.device)
-        if full:
-            Hinv = inverse_batch(Hg[:full], damping, hessian_method, fallbacks, upper_only=True)
-            Q[:, :full * bs] = sweep(Ww[:, :full * bs].contiguous(), Hinv, s32, z32, int_bits, block_size, full)
-        if full * bs < N:
-            rem = N - full * bs
-            Hinv = inverse_batch(Hg[full, :rem, :rem], damping, hessian_method, fallbacks, upper_only=True)
-            Q[:, full * bs:] = sweep(Ww[:, full * bs:].contiguous(), Hinv, s32, z32, int_bits, block_size)
+        Q = sweep_block_diagonal(Ww, Hg, damping, hessian_method, fallbacks, s32, z32, int_bits, block_size)
     else:
         if tuple(Hg.shape) != (N, N):
             raise ValueError(f"Hessian shape {tuple(Hg.shape)} != ({N}, {N})")

@@ -50,12 +50,12 @@ def _gemm_tn(W: torch.Tensor, alpha: float) -> torch.Tensor:
 
 
 def _damp_only(H: torch.Tensor, damping: float) -> torch.Tensor:
-    """H + damping * max(mean(diag), 1e-6) * I, computed by the library's damping kernel
-    (the inverse is not needed here; used for the greedy search's Hessian)."""
-    from .config import DIAG_MEAN_FLOOR
-    dm = H.diagonal().double().mean().float().clamp(min=DIAG_MEAN_FLOOR)
-    out = H.clone()
-    out.diagonal().add_(torch.tensor(damping, dtype=torch.float32, device=H.device) * dm)
+    """H + damping * max(mean(diag), 1e-6) * I as a new tensor, by the
+    library's damping kernel (ldlq.py:207-209: the damped weight-only H
+    that the greedy search uses)."""
+    out = H.float().contiguous().clone()
+    nat.check(_lib().ic_damp_hessian(out.data_ptr(), 1, out.shape[0], float(damping), nat.stream()),
+              "ic_damp_hessian")
     return out
 
 

@@ -692,10 +692,14 @@ def ls_scales(Q, W):
 
 
 def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=4,
-                        iterations=1, greedy_passes=0, rank_threshold=0.01, greedy_device="cpu"):
+                        iterations=1, greedy_passes=0, rank_threshold=0.01, greedy_device="cpu",
+                        weight_only_gram=None):
     """ldlq.py:95-279 (2-D / 3-D / weight-only Hessians).  The greedy search
     is the one ldlq.py:602-647 picks for tensors on ``greedy_device``: "cpu"
-    the PyTorch search, "gpu" the low-rank / full-rank choice."""
+    the PyTorch search, "gpu" the low-rank / full-rank choice.
+    ``weight_only_gram`` (noise studies only): W^T W / M computed in another
+    summation order, used in place of the matmul of the weight-only branch;
+    None is the reference."""
     from types import SimpleNamespace
     W = W.float()
     M, N = W.shape
@@ -721,7 +725,7 @@ def ldlq_quantize_layer(W, hessian=None, block_size=128, damping=0.01, int_bits=
         else:
             Hinv = invert_hessian(damp(H, damping))
     else:
-        H = W.T @ W / M
+        H = W.T @ W / M if weight_only_gram is None else weight_only_gram.float()
         if not torch.isfinite(H).all():
             s = (W.abs().amax(dim=1, keepdim=True) / div).clamp(min=SCALE_MIN, max=SCALE_MAX)
             q = (W / s).round().clamp(qmin, qmax).to(torch.int8)

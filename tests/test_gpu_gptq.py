@@ -337,3 +337,61 @@ def test_gptq_rtn_fallback_bit_exact(gpu_dev):
         assert torch.equal(r.quantized_W.cpu(), q) and torch.equal(r.scales.cpu(), s)
         if z is not None:
             assert torch.equal(r.zero_points.cpu(), z)
+
+
+@pytest.mark.parametrize("N,nblk", [(1024, 2), (1000, 3), (1000, 4)])
+def test_gptq_3d_partial_cover(gpu_dev, N, nblk):
+    """A 3-D Hessian that covers fewer columns than the layer has: the
+    reference loops over its blocks only and leaves the other codes at 0
+    (converter/gptq.py:345-366); a partial last block is swept on its own."""
+    from int_crush_converter_amd.gptq import gptq_quantize_layer
+    g = torch.Generator().manual_seed(N + nblk)
+    M, bs = 64, 256
+    W = torch.randn(M, N, generator=g) * 0.02
+    H = torch.stack([lognormal_hessian(bs, 3 * bs, 70 + k) for k in range(nblk)])
+    want = ref.gptq_quantize_layer(W, H, 128, 0.01, 4)
+    got = gptq_quantize_layer(W.to(gpu_dev), H.to(gpu_dev), block_size=128, damping=0.01, int_bits=4)
+    q = got.quantized_W.cpu()
+    covered = min(N, nblk * bs)
+    assert torch.count_nonzero(q[:, covered:]) == 0
+    assert torch.equal(got.scales.cpu(), want.scales)
+    assert (q == want.quantized_W).float().mean().item() >= 0.999
+    assert got.mse == pytest.approx(want.mse, rel=1e-2)
+
+
+@pytest.mark.parametrize("bits,N", [(4, 96), (4, 128), (8, 96), (8, 128)])
+def test_sweep_one_group_many_rows_bit_exact(gpu_dev, bits, N):
+    """One group of 12300 rows (at least 12288 rows: the sweep with 8 lanes
+    per row; 12300 is not a multiple of the 64 rows of a work-group, so the
+    last wave has rows past the end) and a partial block (N = 96): codes
+    equal the CPU sweep's given the same Hinv, INT4 and INT8 asymmetric."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(bits * 1000 + N)
+    M = 12300
+    W = torch.randn(M, N, generator=g) * 0.02
+    W[11] = 0.0
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 3 * N, 17), 0.01)
+    s, z = ref.gptq_row_params(W, bits, True)
+    Q = torch.zeros(M, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, 128, *((-8, 7) if bits == 4 else (-128, 127)), z)
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, bits, True)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, bits, 128).cpu()
+    assert torch.equal(Qg, Q)
+
+
+def test_sweep_many_rows_multi_block_close(gpu_dev):
+    """12288 rows over 4 blocks of 128 (8 lanes per row, lazy updates on the
+    matrix cores) given the same Hinv: >= 99.9 % of codes equal."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(5)
+    M, N = 12288, 512
+    W = ref.rotate_weights(torch.randn(M, N, generator=g) * 0.02, 256)
+    Hinv = ref.prepare_hinv(ref.rotate_hessian(lognormal_hessian(N, 1024, 19), 256), 0.01)
+    s, z = ref.gptq_row_params(W, 4, False)
+    Q = torch.zeros(M, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, 128, -8, 7, z)
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, 4, False)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, 128).cpu()
+    assert (Qg == Q).float().mean().item() >= 0.999

@@ -2,11 +2,12 @@
 scales) and the full-rank greedy search against the CPU oracle and the
 reference's golden vectors.
 
-Bars: single-block LDLQ sweep bit-exact given the same Hinv; layer codes
->= 99 % equal at these small sizes (least-squares scales are fp64 sums here,
-fp32 sums in the reference, so an fp16 scale can differ by 1 ulp and shift a
-later greedy decision); stored fp16 scales within 1 ulp; greedy passes never
-increase tr(dW H dW^T) and end coordinate-wise optimal.
+Bars: single-block LDLQ sweep bit-exact given the same Hinv; least-squares
+scales and the damped diagonal bit-exact (both summed in torch's CPU order);
+the reference's golden layers >= 99.9 % equal codes with the stored fp16
+scales bit-exact (measured: every code and scale equal); greedy passes never
+increase tr(dW H dW^T) and end coordinate-wise optimal; the C4-shaped layer
+against the oracle's own fp32 noise.
 """
 
 from __future__ import annotations
@@ -56,9 +57,11 @@ def test_ldlq_golden(gpu_dev, golden, case):
                                 greedy_passes=m["greedy"], greedy_backend="full")
     q = r.quantized_W.cpu()
     agree = (q == t[f"{case}.q"]).float().mean().item()
-    assert agree >= 0.99, agree
+    print(f"[parity] ldlq_golden {case} agreement={agree:.6f} "
+          f"scales_equal={torch.equal(r.scales.cpu(), t[case + '.scales'])}", flush=True)
+    assert agree >= 0.999, agree
     assert r.zero_points is None and r.scales.dtype == torch.float16
-    assert _fp16_ulps(r.scales.cpu(), t[f"{case}.scales"]) <= 1
+    assert torch.equal(r.scales.cpu(), t[f"{case}.scales"])
     assert r.mse == pytest.approx(m["mse"], rel=0.05)
 
 
@@ -98,7 +101,9 @@ def test_greedy_matches_oracle(gpu_dev):
     Q0 = ref.rhaz(W / s[:, None]).clamp(-8, 7)
     want = ref.greedy_pytorch(W, Q0.clone(), s[:, None].expand(M, N), H, 2, -8, 7)
     got = greedy_local_search(W.to(gpu_dev), Q0.to(torch.int8).to(gpu_dev), s.to(gpu_dev), H.to(gpu_dev), 2, 4).cpu()
-    assert (got == want).float().mean().item() >= 0.98
+    agree = (got == want).float().mean().item()
+    print(f"[parity] greedy_vs_oracle agreement={agree:.6f}", flush=True)
+    assert agree >= 0.999
 
 
 def test_ldlq_layer_vs_oracle_moderate(gpu_dev):
@@ -110,7 +115,10 @@ def test_ldlq_layer_vs_oracle_moderate(gpu_dev):
         warnings.simplefilter("ignore")
         want = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=0)
         got = ldlq_quantize_layer(W.to(gpu_dev), None, 128, 0.01, 4, iterations=2, greedy_passes=0)
-    assert (got.quantized_W.cpu() == want.quantized_W).float().mean().item() >= 0.995
+    agree = (got.quantized_W.cpu() == want.quantized_W).float().mean().item()
+    print(f"[parity] ldlq_moderate agreement={agree:.6f} "
+          f"scales_equal={torch.equal(got.scales.cpu(), want.scales)}", flush=True)
+    assert agree >= 0.999
     assert got.mse == pytest.approx(want.mse, rel=0.02)
 
 
@@ -120,3 +128,120 @@ def test_ldlq_errors(gpu_dev):
         ldlq_quantize_layer(torch.randn(4, 8, device=gpu_dev), int_bits=5)
     with pytest.raises(ValueError):
         ldlq_quantize_layer(torch.randn(8, device=gpu_dev))
+
+
+@pytest.mark.parametrize("rows,cols", [(2, 3), (5, 7), (3, 8), (77, 33), (64, 256), (9, 5000), (1024, 4096),
+                                       (300, 12288)])
+def test_ls_scales_bit_exact(gpu_dev, rows, cols):
+    """Least-squares row scales summed in torch's CPU inner-sum order equal
+    the reference's (Q_float * W).sum(dim=1) / (Q_float**2).sum(dim=1)
+    bit for bit, including all-zero code rows (denominator floor)."""
+    from int_crush_converter_amd.ldlq import _ls_scales
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    W = torch.randn(rows, cols, generator=g) * 0.02
+    Q = torch.randint(-8, 8, (rows, cols), generator=g, dtype=torch.int8)
+    Q[1] = 0
+    want = ref.ls_scales(Q, W).squeeze(1)
+    got = _ls_scales(Q.to(gpu_dev), W.to(gpu_dev)).cpu()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("n", [1, 3, 5, 64, 200, 1024, 4097, 12288, 16385, 20000])
+def test_damping_bit_exact(gpu_dev, n):
+    """The damped diagonal uses the reference's H.diagonal().mean() (torch's
+    CPU scalar reduction of the strided diagonal): bit-exact with the
+    oracle's damp, also beyond the LDS-staged size (16384)."""
+    from int_crush_converter_amd import _native as nat
+    g = torch.Generator().manual_seed(n)
+    d = torch.exp(torch.randn(n, generator=g) * 2)
+    H = torch.diag(d)
+    if n > 1:
+        H[0, 1] = H[1, 0] = 0.5
+    want = ref.damp(H, 0.01)
+    Hg = H.to(gpu_dev).contiguous()
+    nat.check(nat.lib().ic_damp_hessian(Hg.data_ptr(), 1, n, 0.01, nat.stream()), "ic_damp_hessian")
+    assert torch.equal(Hg.cpu(), want)
+
+
+def test_damping_batched_bit_exact(gpu_dev):
+    from int_crush_converter_amd import _native as nat
+    g = torch.Generator().manual_seed(11)
+    Hb = torch.stack([lognormal_hessian(256, 300, k) for k in range(5)])
+    want = torch.stack([ref.damp(Hb[k], 0.05) for k in range(5)])
+    Hg = Hb.to(gpu_dev).contiguous()
+    nat.check(nat.lib().ic_damp_hessian(Hg.data_ptr(), 5, 256, 0.05, nat.stream()), "ic_damp_hessian")
+    assert torch.equal(Hg.cpu(), want)
+
+
+def _student_t(M, N, g):
+    z = torch.randn(M, N, generator=g)
+    chi = (torch.randn(M, N, 4, generator=g) ** 2).sum(-1)
+    return z / torch.sqrt(chi / 4) * (0.02 / 2 ** 0.5)
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_ldlq_c4_shaped_vs_reference_noise(gpu_dev, n):
+    """configs[3]'s recipe at M = N = n: Student-t (nu = 4) weights scaled to
+    std 0.02, rot256, weight-only H = W^T W / M, 2 LDLQ iterations, then 5
+    greedy passes through the default dispatch (eigen-truncation, refused by
+    the rank gate for this full-rank H, then the full-rank search), against
+    the oracle's ldlq_quantize_layer with the reference's GPU backend choice
+    (converter/ldlq.py:602-647, converter/greedy.py:207-285, 487-541).  The
+    bar is the oracle's own noise under the two fp32 summation orders this
+    path depends on, changed together as another machine's BLAS / LAPACK
+    would: W^T W / M summed in two K halves (another K-blocking of the
+    Gram matrix) and the inverse with half the CPU threads (LAPACK's order
+    changes with the thread count); each change alone is reported too.
+    Given the same Hessian inverse the GPU's sweep, and given the same start
+    its greedy search, equal the oracle's codes (tests above); what remains
+    here is GEMM and inverse rounding, which the greedy search amplifies."""
+    from int_crush_converter_amd.ldlq import ldlq_quantize_layer
+    g = torch.Generator().manual_seed(n + 3)
+    W = ref.rotate_weights(_student_t(n, n, g), 256)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        want = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5, greedy_device="gpu")
+        h = n // 2
+        gram = (W[:h].T @ W[:h] + W[h:].T @ W[h:]) / n
+        alt_h = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5, greedy_device="gpu",
+                                        weight_only_gram=gram)
+        threads = torch.get_num_threads()
+        torch.set_num_threads(max(1, threads // 2))
+        try:
+            alt = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5,
+                                          greedy_device="gpu")
+            alt_b = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5,
+                                            greedy_device="gpu", weight_only_gram=gram)
+        finally:
+            torch.set_num_threads(threads)
+        got = ldlq_quantize_layer(W.to(gpu_dev), None, 128, 0.01, 4, iterations=2, greedy_passes=5)
+    H = (W.T.double() @ W.double()) / n
+
+    def proxy(Q, s):
+        d = Q.double() * s.double() - W.double()
+        return ((d @ H) * d).sum().item()
+
+    q = got.quantized_W.cpu()
+    p_ref = proxy(want.quantized_W, want.scales.float())
+    rel = proxy(q, got.scales.cpu().float()) / p_ref - 1
+    alts = (alt, alt_h, alt_b)
+    rel_self = max(abs(proxy(a.quantized_W, a.scales.float()) / p_ref - 1) for a in alts)
+    agree = (q == want.quantized_W).float().mean().item()
+    self_threads, self_gram, self_both = ((a.quantized_W == want.quantized_W).float().mean().item() for a in alts)
+    self_agree = min(self_threads, self_gram, self_both)
+    ulps = _fp16_ulps(got.scales.cpu(), want.scales)
+    ulps_self = max(_fp16_ulps(a.scales, want.scales) for a in alts)
+    rows_ulp = int((got.scales.cpu() != want.scales).sum())
+    print(f"[parity] ldlq_c4 n={n} agreement={agree:.6f} self_threads={self_threads:.6f} self_gram={self_gram:.6f} "
+          f"self_both={self_both:.6f} proxy_rel={rel:.3g} self_proxy_rel={rel_self:.3g} scale_max_ulps={ulps} "
+          f"self_scale_max_ulps={ulps_self} scale_rows_differing={rows_ulp}", flush=True)
+    # measured: 99.86 % / 99.81 % at n = 1024 / 2048 against the oracle's
+    # 99.88-99.97 % / 99.92-99.95 %; the GPU's Hessian inverse is up to 3x
+    # less accurate than LAPACK's on this H (the GEMMs sum long K ranges in
+    # one sequential fp32 accumulator), hence 1.5e-3 here
+    assert agree >= self_agree - 1.5e-3, (agree, self_threads, self_gram, self_both)
+    assert abs(rel) <= max(1e-3, 2 * rel_self), (rel, rel_self)
+    # a row whose codes moved to another local minimum of the greedy search
+    # has another least-squares scale; equal codes give equal scales
+    # (test_ls_scales_bit_exact)
+    assert ulps <= max(1, 2 * ulps_self)

@@ -48,7 +48,15 @@ def test_pipeline_matches_reference_golden(gpu_dev, golden, tmp_path, tag):
             assert torch.equal(res[k], v), k
         else:
             agree = (res[k] == v).float().mean().item()
-            assert agree >= 0.9999, (k, agree)
+            # the stored bytes follow from the rotated weights, and the GPU's
+            # butterfly rotation rounds differently from the reference's
+            # matmul: measured 0 differing bytes in every RTN4 tensor and 1
+            # of 135168 over the RTN8-asymmetric ones (a code at a rounding
+            # boundary); given identical rotated weights the bytes are
+            # bit-exact (test_pipeline_rtn_bytes_vs_oracle)
+            nd = int((res[k] != v).sum())
+            print(f"[parity] pipeline_golden {tag} {k} bytes_differing={nd} of {v.numel()}", flush=True)
+            assert nd <= 2, (k, nd)
 
 
 def test_pipeline_rtn_bytes_vs_oracle(gpu_dev, tmp_path):
@@ -133,7 +141,10 @@ def test_pipeline_ldlq_weight_only(gpu_dev, tmp_path):
         # H = W^T W / 64 has rank 64 <= 0.3 x 256: the reference on a GPU takes the low-rank greedy
         r = ref.ldlq_quantize_layer(Wr, None, 128, 0.01, 4, iterations=2, greedy_passes=2, greedy_device="gpu")
     q = ref.unpack_int4(res["l.0.w.weight"], 256)
-    assert (q == r.quantized_W).float().mean().item() >= 0.98
+    agree = (q == r.quantized_W).float().mean().item()
+    print(f"[parity] pipeline_ldlq_weight_only agreement={agree:.6f} "
+          f"scales_equal={torch.equal(res['l.0.w.weight_scale'], r.scales)}", flush=True)
+    assert agree >= 0.999
 
 
 def test_pipeline_callback_abort_leaves_no_output(gpu_dev, tmp_path):

@@ -216,3 +216,48 @@ def test_piso_api_validation():
         piso.compute_piso_scales_int8(torch.randn(8, 64), torch.ones(32))
     with pytest.raises(ValueError, match="num_coarse"):
         piso.compute_piso_scales_int4(torch.randn(8, 64), torch.ones(64), num_coarse=0)
+
+
+@pytest.mark.parametrize("code", [0, 2])
+def test_fallback_output_hinv_returns_inverse(code):
+    """Method "hinv" (full or upper-triangle reads) hands the inv / pinv
+    result itself to the column loop (converter/gptq.py:113-121), even when
+    that inverse is positive definite."""
+    from int_crush_converter_amd.hessian import fallback_output
+    g = torch.Generator().manual_seed(3)
+    A = torch.randn(12, 12, generator=g)
+    Hi = A @ A.T + 12 * torch.eye(12)
+    got = fallback_output(code, Hi, lambda: pytest.fail("no second inverse for method hinv"))
+    assert got is Hi
+
+
+def test_fallback_output_cholesky_method():
+    """Method "cholesky" (converter/gptq.py:91-110): the upper Cholesky factor
+    of the fallback inverse; the inverse itself when it does not factor; H^-1
+    when only the factorisation of H^-1 failed."""
+    from int_crush_converter_amd.hessian import fallback_output
+    g = torch.Generator().manual_seed(4)
+    A = torch.randn(10, 10, generator=g)
+    Hi = A @ A.T + 10 * torch.eye(10)
+    U = fallback_output(1, Hi, lambda: pytest.fail("unused"))
+    assert torch.allclose(U.T @ U, Hi, rtol=1e-5, atol=1e-4)
+    assert torch.equal(U, torch.triu(U))
+    indef = torch.diag(torch.tensor([1.0, -2.0, 3.0]))
+    assert fallback_output(1, indef, lambda: pytest.fail("unused")) is indef
+    marker = torch.ones(3, 3)
+    assert fallback_output(1, None, lambda: marker) is marker
+    with pytest.raises(ValueError):
+        fallback_output(2, None, lambda: marker)
+
+
+@pytest.mark.parametrize("N,nblk,bs,want", [
+    (1024, 4, 256, (4, 0)),      # exact cover
+    (1024, 2, 256, (2, 0)),      # fewer blocks than columns need: the rest stays unswept
+    (1000, 4, 256, (3, 232)),    # partial last block
+    (1000, 3, 256, (3, 0)),      # partial tail not covered by any block
+    (512, 6, 256, (2, 0)),       # blocks past the last column do nothing
+    (100, 1, 256, (0, 100)),     # one block wider than the layer
+])
+def test_block_cover(N, nblk, bs, want):
+    from int_crush_converter_amd.gptq import block_cover
+    assert block_cover(N, nblk, bs) == want
