@@ -204,6 +204,24 @@ int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const f
                      const float* s32, const float* z32, int bits, int block, int8_t* Q,
                      void* workspace, void* stream);
 
+/* Allocation-free variant of ic_gptq_quantize.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as ic_gptq_quantize without the
+ * workspace: the lazy update's error matrix lives in a static device array
+ * of ic_gptq_noalloc_scratch_bytes() = 128 MiB per GPU (held until the
+ * process ends), which must hold groups x rows x S fp32 errors, S the
+ * super-block width (1024 at block 128 for one matrix, the block for 3-D
+ * groups), else IC_ERR_ARG: rows <= 32768 for one matrix, rows x groups
+ * <= 262144 for 3-D groups at block 128.  The call allocates nothing and
+ * records no profiler events.  Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads)
+ * race. */
+int64_t ic_gptq_noalloc_scratch_bytes(void);
+int ic_gptq_quantize_noalloc(float* W, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
+                             const float* s32, const float* z32, int bits, int block, int8_t* Q,
+                             void* stream);
+
 /* LDLQ sweep (converter/ldlq.py:369-417, converter/ldlq_triton.py:23-162,
  * converter/rounding.py:115-155): per-element scales [rows, N] (floored at
  * 1e-8), error times 1/max(Hinv_jj, 1e-8), no clamp, sign-flip rule.

@@ -21,6 +21,8 @@
 //
 // The lazy trailing update is an fp32-MFMA GEMM (gemm_f32); its summation
 // order differs from MKL's sgemm, which is the only non-bit-exact step.
+#include <mutex>
+
 #include "gemm.hpp"
 
 namespace icq {
@@ -356,6 +358,60 @@ extern "C" int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t grou
     const int64_t N = gw * groups;
     return layer_sweep(W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
                        reinterpret_cast<float*>(workspace), SWEEP_GPTQ, as_stream(stream));
+}
+
+// ------------------------------------------------ allocation-free GPTQ sweep
+// For callers that cannot allocate device memory (HIP graph capture, serving
+// loops): the error matrix E of the lazy update lives in a static device
+// array of NOALLOC_SCRATCH_BYTES per GPU (held until the process ends),
+// whose address is looked up once per device.  In host code `scratch` only
+// names the symbol; its device address is the one hipGetSymbolAddress
+// returns.  Every call on a GPU shares that GPU's array, so calls that
+// overlap on one GPU race.  Nothing in it needs to start at zero: the sweep
+// writes every error column a lazy update reads.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = int64_t(128) << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+static std::mutex g_scratch_mu;
+
+static int scratch_address(void** out) {
+    int dev = -1;
+    IC_CHECK_HIP(hipGetDevice(&dev));
+    IC_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, "ic_gptq_quantize_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        IC_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        IC_REQUIRE(p != nullptr, "ic_gptq_quantize_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return IC_OK;
+}
+
+extern "C" int64_t ic_gptq_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int ic_gptq_quantize_noalloc(float* W, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
+                                        const float* s32, const float* z32, int bits, int block, int8_t* Q,
+                                        void* stream) {
+    IC_REQUIRE(W && Hinv && s32 && Q, "ic_gptq_quantize_noalloc: null pointer");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_gptq_quantize_noalloc: bits must be 4 or 8");
+    IC_REQUIRE(groups >= 1 && gw >= 0 && rows >= 0, "ic_gptq_quantize_noalloc: bad size");
+    if (rows == 0 || gw == 0) return IC_OK;
+    IC_REQUIRE(block >= 1 && block <= SW_NB, "ic_gptq_quantize_noalloc: block size must be in [1, 128]");
+    IC_REQUIRE(rows <= NOALLOC_SCRATCH_BYTES && groups <= NOALLOC_SCRATCH_BYTES &&
+                   groups * rows * super_cols(groups, block) * (int64_t)sizeof(float) <= NOALLOC_SCRATCH_BYTES,
+               "ic_gptq_quantize_noalloc: rows x groups x super-block columns need more than the 128 MiB "
+               "static scratch; use ic_gptq_quantize with a workspace");
+    void* ws = nullptr;
+    int rc = scratch_address(&ws);
+    if (rc) return rc;
+    ProfSuppress no_events;   // a recording profiler scope would create HIP events
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    const int64_t N = gw * groups;
+    return layer_sweep(W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
+                       reinterpret_cast<float*>(ws), SWEEP_GPTQ, as_stream(stream));
 }
 
 extern "C" int ic_ldlq_quantize(float* W, int64_t rows, int64_t N, const float* Hinv, const float* scales,

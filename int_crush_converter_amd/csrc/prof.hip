@@ -17,10 +17,15 @@ static bool g_on = false;
 static std::vector<ProfRec> g_recs;   // events are reused across resets
 static size_t g_used = 0;
 
+static thread_local bool t_suppress = false;
+
 bool prof_enabled() { return g_on; }
 
+ProfSuppress::ProfSuppress() : prev_(t_suppress) { t_suppress = true; }
+ProfSuppress::~ProfSuppress() { t_suppress = prev_; }
+
 ProfScope::ProfScope(hipStream_t st, int tag, double flops, double bytes) : st_(st) {
-    if (!g_on) return;
+    if (!g_on || t_suppress) return;
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_used == g_recs.size()) {
         ProfRec r;

@@ -34,6 +34,16 @@ enum ProfTag : int {
 
 bool prof_enabled();
 
+// While alive, ProfScope records nothing on this thread (the allocation-free
+// entry points: a recording scope creates HIP events).
+class ProfSuppress {
+public:
+    ProfSuppress();
+    ~ProfSuppress();
+private:
+    bool prev_;
+};
+
 class ProfScope {
 public:
     ProfScope(hipStream_t st, int tag, double flops, double bytes);
