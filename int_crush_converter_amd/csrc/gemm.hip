@@ -32,6 +32,17 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int BK = 32;
 constexpr int PR = BK + 4;        // pitch of a row-major operand tile [T][32]
 constexpr int NXCD = 8;
+// Accumulation chunk: every kc values of k (aligned to absolute multiples of
+// kc, GemmArgs::kc) a fresh set of accumulators is summed, then folded into the running
+// result.  A single fp32 accumulator over a long K range gathers rounding
+// error in proportion to K; chunking keeps it near kc + K / kc, like a
+// blocked CPU BLAS.  With alpha = -1, beta = 1 the running result starts
+// as C and each chunk's product is subtracted from it as soon as it is
+// complete: C <- (..((C - P_0) - P_1)..) - P_last, the sequence of roundings of
+// consecutive rank-kc updates (the GPTQ / LDLQ lazy updates of the
+// reference, one per block of kc columns: bit-exact with them when the
+// chunk products are).
+enum ChunkMode : int { CHUNK_SUM = 1, CHUNK_SUB = 2 };
 
 // Tile geometry for tile size T (the output tile is T x T).
 template <int T>
@@ -278,9 +289,11 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, int 
     }
 }
 
-template <int TA, int TB, bool CHECK, int T>
+template <int TA, int TB, bool CHECK, int T, int CHUNK>
 __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, const float* B, const TileRange& tr,
-                                          float* lds, floatx4 (&acc)[Geo<T>::F][Geo<T>::F]) {
+                                          float* lds, floatx4 (&acc)[Geo<T>::F][Geo<T>::F],
+                                          floatx4 (&run)[Geo<T>::F][Geo<T>::F]) {
+    constexpr int F = Geo<T>::F;
     constexpr bool AR = TA == 0, BR = TB == 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = (wave >> 1) * Geo<T>::WS, wj = (wave & 1) * Geo<T>::WS;
@@ -313,12 +326,29 @@ __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, con
         __syncthreads();
         if (k0 + BK < tr.khi) ICQ_LOAD_STAGE(k0 + BK);
         mma_stage<TA, TB, T>(As, Bs, wi, wj, lane, acc);
+        if ((((k0 + BK) & (g.kc - 1)) == 0) || k0 + BK >= tr.khi) {
+            // end of a chunk (or of the K range): fold it into the running result
+#pragma unroll
+            for (int a = 0; a < F; ++a)
+#pragma unroll
+                for (int b = 0; b < F; ++b) {
+                    run[a][b] = CHUNK == CHUNK_SUB ? run[a][b] - acc[a][b] : run[a][b] + acc[a][b];
+                    acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
     }
 #undef ICQ_LOAD_STAGE
 }
 
-template <int TA, int TB, bool CHECK, int T>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntiles, int remap) {
+// CHUNK_SUB is launched only for alpha = -1, beta = 1: C is read before the
+// K loop and every chunk is subtracted from it; CHUNK_SUM keeps the
+// epilogue C <- alpha * sum + beta * C.
+// Two work-groups per CU (one wave of each per SIMD) hide each other's
+// barriers and LDS staging: the register budget is held to 256 per lane.
+template <int TA, int TB, bool CHECK, int T, int CHUNK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f32_kernel(GemmArgs g,
+                                                                                              int64_t ntiles,
+                                                                                              int remap) {
     constexpr int F = Geo<T>::F;
     __shared__ __attribute__((aligned(16))) float lds[2 * Geo<T>::TILE_F];
     TileRange tr;
@@ -334,14 +364,6 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
     const float* B = g.B + z * g.sB;
     float* C = g.C + z * g.sC;
 
-    floatx4 acc[F][F];
-#pragma unroll
-    for (int a = 0; a < F; ++a)
-#pragma unroll
-        for (int b = 0; b < F; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    main_loop<TA, TB, CHECK, T>(g, A, B, tr, lds, acc);
-
     constexpr bool WIDE = TA == 1 && TB == 0;
     typedef typename VecF<F>::type vecf;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -351,12 +373,44 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
     auto row_of = [&](int a, int v) -> int64_t { return tr.i0 + (WIDE ? wi + F * (g4 + v) + a : wi + 16 * a + g4 + v); };
     auto col_of = [&](int b) -> int64_t { return tr.j0 + (WIDE ? wj + F * m + b : wj + 16 * b + m); };
     const bool full = !CHECK && g.cmask == CMASK_FULL;
+
+    floatx4 acc[F][F], run[F][F];
+    // the C tile's addresses for the loads before the K loop come from a copy
+    // of the base pointer the compiler cannot identify with C, so that they are
+    // recomputed for the stores instead of being held through the loop
+    const float* Cl = C;
+    if (CHUNK == CHUNK_SUB) asm volatile("" : "+s"(Cl));
+#pragma unroll
+    for (int a = 0; a < F; ++a)
+#pragma unroll
+        for (int b = 0; b < F; ++b) {
+            acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (CHUNK == CHUNK_SUB) {
+                // the running result starts as C (elements past the matrix: 0, never stored)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int64_t i = row_of(a, v), j = col_of(b);
+                    run[a][b][v] = (full || (i < g.M && j < g.N)) ? Cl[i * g.ldc + j] : 0.0f;
+                }
+            } else {
+                run[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+
+    main_loop<TA, TB, CHECK, T, CHUNK>(g, A, B, tr, lds, acc, run);
+    // the epilogue below stores alpha * acc + beta * C
+    const float alpha = CHUNK == CHUNK_SUB ? 1.0f : g.alpha;
+    const float beta = CHUNK == CHUNK_SUB ? 0.0f : g.beta;
+#pragma unroll
+    for (int a = 0; a < F; ++a)
+#pragma unroll
+        for (int b = 0; b < F; ++b) acc[a][b] = run[a][b];
     const bool cvec = (((uintptr_t)C) % (4 * F) == 0) && (g.ldc % F == 0);
     if (WIDE && full && cvec) {
         // the lane's F columns F m .. F m + F - 1 are adjacent: F-wide loads and stores
         const int64_t j0 = col_of(0);
         vecf cold[F][4];
-        if (g.beta != 0.0f) {
+        if (beta != 0.0f) {
 #pragma unroll
             for (int a = 0; a < F; ++a)
 #pragma unroll
@@ -370,8 +424,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
                 vecf r;
 #pragma unroll
                 for (int b = 0; b < F; ++b) {
-                    r[b] = g.alpha * acc[a][b][v];
-                    if (g.beta != 0.0f) r[b] = r[b] + g.beta * cold[a][v][b];
+                    r[b] = alpha * acc[a][b][v];
+                    if (beta != 0.0f) r[b] = r[b] + beta * cold[a][v][b];
                 }
                 *reinterpret_cast<vecf*>(&C[row_of(a, v) * g.ldc + j0]) = r;
             }
@@ -379,7 +433,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
     }
     // general epilogue: all C loads are issued before any store so their latency overlaps
     float cold[F][F][4];
-    if (g.beta != 0.0f) {
+    if (beta != 0.0f) {
 #pragma unroll
         for (int a = 0; a < F; ++a)
 #pragma unroll
@@ -402,8 +456,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g, int64_t ntile
                     if (g.cmask == CMASK_LOWER && i < j) continue;
                     if (g.cmask == CMASK_UPPER && i > j) continue;
                 }
-                float r = g.alpha * acc[a][b][v];
-                if (g.beta != 0.0f) r = r + g.beta * cold[a][b][v];
+                float r = alpha * acc[a][b][v];
+                if (beta != 0.0f) r = r + beta * cold[a][b][v];
                 C[i * g.ldc + j] = r;
             }
 }
@@ -430,15 +484,25 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
     const dim3 gd((unsigned)grid, 1, (unsigned)g.batch);
     // whole tiles and whole K stages everywhere: the kernel without bounds checks
     const bool exact = aligned && g.M % T == 0 && g.N % T == 0 && g.K % BK == 0;
-#define ICQ_GEMM_LAUNCH(TA, TB)                                                                                     \
-    do {                                                                                                           \
-        if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false, T>), gd, dim3(256), 0, st, g, tiles, remap);  \
-        else hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, true, T>), gd, dim3(256), 0, st, g, tiles, remap);         \
+    // updates C <- C - op(A) op(B) with op(A) = A subtract chunk by chunk;
+    // everything else sums the chunks
+    const bool sub = g.alpha == -1.0f && g.beta == 1.0f && !g.transA;
+#define ICQ_GEMM_LAUNCH(TA, TB, CH)                                                                                    \
+    do {                                                                                                              \
+        if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false, T, CH>), gd, dim3(256), 0, st, g, tiles, remap);  \
+        else hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, true, T, CH>), gd, dim3(256), 0, st, g, tiles, remap);         \
     } while (0)
-    if (!g.transA && !g.transB) ICQ_GEMM_LAUNCH(0, 0);
-    else if (!g.transA) ICQ_GEMM_LAUNCH(0, 1);
-    else if (!g.transB) ICQ_GEMM_LAUNCH(1, 0);
-    else ICQ_GEMM_LAUNCH(1, 1);
+    if (!g.transA && !g.transB) {
+        if (sub) ICQ_GEMM_LAUNCH(0, 0, CHUNK_SUB);
+        else ICQ_GEMM_LAUNCH(0, 0, CHUNK_SUM);
+    } else if (!g.transA) {
+        if (sub) ICQ_GEMM_LAUNCH(0, 1, CHUNK_SUB);
+        else ICQ_GEMM_LAUNCH(0, 1, CHUNK_SUM);
+    } else if (!g.transB) {
+        ICQ_GEMM_LAUNCH(1, 0, CHUNK_SUM);
+    } else {
+        ICQ_GEMM_LAUNCH(1, 1, CHUNK_SUM);
+    }
 #undef ICQ_GEMM_LAUNCH
     IC_CHECK_LAUNCH();
     return IC_OK;
@@ -453,6 +517,7 @@ constexpr int64_t SHORT_K = 256, SHORT_K_TILE_LIMIT = 1024;
 
 int gemm_f32(const GemmArgs& g, hipStream_t st) {
     if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return IC_OK;
+    IC_REQUIRE(g.kc >= BK && g.kc <= 4096 && (g.kc & (g.kc - 1)) == 0, "gemm_f32: kc must be a power of two >= 32");
     // 16-byte loads need 16-byte aligned bases and leading dimensions
     const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
                          g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;

@@ -32,6 +32,7 @@ struct GemmArgs {
     int64_t batch;
     int tag = PT_OTHER;        // profiler phase
     double algo_flops = 0.0;   // algorithmic flops of the launch (0: 2*M*N*K*batch)
+    int kc = 128;              // accumulation chunk along K: a power of two, at least 32
 };
 
 // Launches on `st`; returns IC_OK or an error code.  Safe in place (C aliases

@@ -300,9 +300,14 @@ static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t 
     IC_REQUIRE(B >= 1 && B <= SW_NB, "block size must be in [1, 128]");
     const int64_t SB = super_cols(groups, B);   // error matrix E: [groups][rows][SB]
     // W[:, c0 : c0+nc] -= E[:, e0 : e0+k] @ Hinv[h0 : h0+k, c0 : c0+nc]   (per group)
+    // the GEMM subtracts its K range chunk by chunk; with chunks of one block
+    // every weight receives the per-block updates W -= E_b Hinv[b, :] of the
+    // reference in its order (block sizes 32, 64, 128)
+    const int kc = (B == 32 || B == 64 || B == 128) ? B : 128;
     auto update = [&](int64_t e0, int64_t h0, int64_t k, int64_t c0, int64_t nc) {
         GemmArgs ga{rows, nc, k, -1.0f, 1.0f, E + e0, SB, rows * SB, Hinv + h0 * ldh + c0, ldh, hg,
                     W + c0, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
+        ga.kc = kc;
         return gemm_f32(ga, st);
     };
     for (int64_t sb0 = 0; sb0 < gw; sb0 += SB) {

@@ -255,8 +255,12 @@ def test_ldlq_sweep_many_rows_bit_exact(gpu_dev):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("B", [16, 64, 128])
+@pytest.mark.parametrize("B", [16, 32, 64, 128])
 def test_sweep_multi_block_close(gpu_dev, B):
+    """Whole-layer sweep given the same Hinv.  Block sizes 32 / 64 / 128: the
+    lazy updates subtract one block's product at a time, as the reference
+    does, so every code is equal; other block sizes sum whole 128-chunks of
+    k first (>= 99.9 %)."""
     from int_crush_converter_amd.gptq import row_params, sweep
     g = torch.Generator().manual_seed(B)
     M, N = 256, 1024
@@ -269,7 +273,33 @@ def test_sweep_multi_block_close(gpu_dev, B):
     Wg = W.to(gpu_dev)
     s32, z32, _, _ = row_params(Wg, 4, False)
     Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, B).cpu()
+    if B in (32, 64, 128):
+        assert torch.equal(Qg, Q)
     assert (Qg == Q).float().mean().item() >= 0.999
+
+
+@pytest.mark.parametrize("M,N,K,kblk", [(300, 700, 1024, 128), (4096, 1000, 1024, 128), (129, 700, 384, 128)])
+def test_sgemm_update_equals_blockwise_cpu_updates(gpu_dev, M, N, K, kblk):
+    """C <- C - A B on the GPU with a long K equals the CPU's rank-128 updates
+    applied in order, C - A[:, :128] B[:128] - A[:, 128:256] B[128:256] - ...,
+    bit for bit: the kernel subtracts each 128-chunk of k, summed from zero
+    in k order (the order of MKL's sgemm at K = 128), as soon as it is
+    complete.  (MKL sums a lone last column, N mod 16 = 1, in another
+    order; measured equal for every other shape tried.)"""
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g)
+    C = torch.randn(M, N, generator=g)
+    want = C.clone()
+    for k0 in range(0, K, kblk):
+        want = want - A[:, k0:k0 + kblk] @ B[k0:k0 + kblk]
+    from int_crush_converter_amd import _native as nat
+    Cg = C.to(gpu_dev)
+    Ag, Bg = A.to(gpu_dev), B.to(gpu_dev)
+    nat.check(nat.lib().ic_sgemm(0, 0, M, N, K, -1.0, Ag.data_ptr(), K, Bg.data_ptr(), N, 1.0, Cg.data_ptr(), N,
+                                 0, 0, nat.stream()), "ic_sgemm")
+    got = Cg.cpu()
+    assert torch.equal(got, want)
 
 
 def _proxy(W, Q, s16, z8, H):
