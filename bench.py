@@ -385,6 +385,33 @@ def roofline_from(prof, workload):
                   "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, name)}
 
 
+def hbm_ceiling(nbytes=1 << 30, reps=10):
+    """GB/s of the library's streaming probes (ic_hbm_stream) on 1 GiB: the
+    practical HBM ceiling of the box for each read/write mix.  Bytes counted:
+    copy read + written, read, write, convert 2 read + 4 written per element."""
+    import torch
+    from int_crush_converter_amd import _native as nat
+    L = nat.lib()
+    src = torch.ones(nbytes // 4, device="cuda:0")
+    dst = torch.empty(nbytes // 2, device="cuda:0")     # room for kind 3's 2 x nbytes
+    out = {}
+    for kind, name, moved in ((0, "copy", 2 * nbytes), (1, "read", nbytes), (2, "write", nbytes),
+                              (3, "bf16_to_fp32", 3 * nbytes)):
+        call = lambda: nat.check(L.ic_hbm_stream(kind, src.data_ptr(), dst.data_ptr(), nbytes, nat.stream()),
+                                 "ic_hbm_stream")
+        call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = {"GB/s": round(moved / ms / 1e6, 1), "us": round(ms * 1e3, 1), "bytes": moved}
+    return {"hbm_ceiling": out, "peak_GB/s": PEAK_HBM_GBS}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -395,6 +422,8 @@ def main():
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB fp32 device copy (3 times), the reference for HBM counters")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only time the library's streaming probes (copy, read, write, bf16->fp32 convert)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build runs the per-layer path on a single MI355X "
@@ -411,6 +440,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": True, "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
                           "launches": 3}), flush=True)
+        return
+    if args.hbm_ceiling:
+        print(json.dumps(hbm_ceiling()), flush=True)
         return
     kind, M, N, extra = WORKLOADS[args.workload]
     if kind == "e2e":

@@ -400,6 +400,13 @@ int ic_piso_scales(const float* W, int64_t rows, int64_t cols, int64_t ld, const
 
 /* ---------------------------------------------------------------- profiling */
 
+/* HBM ceiling probes (measurement only; no counterpart in the reference):
+ * kind 0 copies `bytes` from src to dst, 1 reads them (dst: a float the
+ * kernel may write), 2 writes `bytes` to dst, 3 converts bf16 src (`bytes`)
+ * to fp32 dst (2 x bytes); 16-byte coalesced accesses, four loads in flight
+ * per thread.  bench.py --hbm-ceiling times them. */
+int ic_hbm_stream(int kind, const void* src, void* dst, int64_t bytes, void* stream);
+
 /* Launch profiler (no reference counterpart; measurement support).  While
  * enabled, library launches are bracketed by HIP events on their stream and
  * tagged with a phase: 0 trailing-update GEMM, 1 Cholesky GEMMs, 2 inverse

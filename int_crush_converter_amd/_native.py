@@ -67,6 +67,7 @@ _SIGS = {
     "ic_greedy_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "ic_greedy_lowrank": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32,
                                  _c.POINTER(_i32), _vp, _vp]),
+    "ic_hbm_stream": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "ic_profile_enable": (_i32, [_i32]),
     "ic_profile_read": (_i32, [_vp, _vp, _vp, _vp, _i32]),
     "ic_col_moments_workspace_bytes": (_i64, [_i64, _i64]),

@@ -180,6 +180,108 @@ __global__ __launch_bounds__(256) void rotate_rows_reg(
     flush_count(cnt, nz);
 }
 
+// Rotation of 256-column groups with fully coalesced accesses (rows made of
+// whole 16-byte aligned groups).  A wave takes four (row, group) items at
+// a time, one per 16-lane row of the wave: lane p (< 16) of a row holds the
+// in-group columns 64 i + 4 p + e (i, e < 4), so every load and store
+// instruction moves 16 contiguous lanes x 16 bytes (fp32) or 8 bytes
+// (bf16 / fp16) per item.  The base-4 digits of the in-group index are e
+// (digit 0, in registers), p & 3 (digit 1, the quad: DPP quad permutes),
+// p >> 2 (digit 2, the 16-lane row: DPP mirrors composed with quad
+// permutes) and i (digit 3, in registers); the stages run in that order,
+// with the same additions as rotate_rows_reg, whose results they equal.
+template <int CTRL1, int CTRL2>
+__device__ __forceinline__ float dpp2(float v) {
+    return dpp<CTRL2>(dpp<CTRL1>(v));
+}
+constexpr int ROW_MIRROR = 0x140, ROW_HALF_MIRROR = 0x141;
+
+// One radix-4 stage across lanes p ^ 4, p ^ 8, p ^ 12 of a 16-lane row:
+// p ^ 7 (half mirror) then ^ 3 gives p ^ 4; p ^ 15 (mirror) then ^ 7 gives
+// p ^ 8; p ^ 15 then ^ 3 gives p ^ 12.
+__device__ __forceinline__ float bfly4_row(float v) {
+    const float a = v + dpp2<ROW_HALF_MIRROR, QP_XOR3>(v);
+    const float s = a + dpp2<ROW_MIRROR, ROW_HALF_MIRROR>(a);
+    return __builtin_fmaf(s, 0.5f, -dpp2<ROW_MIRROR, QP_XOR3>(v));
+}
+
+template <int DT>
+__device__ __forceinline__ void load4(const void* src, int64_t off, float (&v)[4]) {
+    if (DT == IC_DTYPE_F32) {
+        const floatx4_t t = *reinterpret_cast<const floatx4_t*>(reinterpret_cast<const float*>(src) + off);
+        v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+    } else {
+        typedef unsigned int uintx2_t __attribute__((ext_vector_type(2)));
+        const uintx2_t t = *reinterpret_cast<const uintx2_t*>(reinterpret_cast<const uint16_t*>(src) + off);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (DT == IC_DTYPE_BF16) {
+                v[2 * k] = __uint_as_float(t[k] << 16);
+                v[2 * k + 1] = __uint_as_float(t[k] & 0xffff0000u);
+            } else {
+                v[2 * k] = f16_bits_to_f32((uint16_t)(t[k] & 0xffffu));
+                v[2 * k + 1] = f16_bits_to_f32((uint16_t)(t[k] >> 16));
+            }
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void rotate256_coal(const void* __restrict__ src, int64_t rows, int64_t groups,
+                                                      int64_t ld_src, float* __restrict__ dst, int64_t ld_dst,
+                                                      float zero_above, unsigned long long* nz) {
+    unsigned cnt = 0;
+    const int lane = threadIdx.x & 63, p = lane & 15, u = lane >> 4;
+    const int64_t items = rows * groups;
+    const int64_t nwave = (int64_t)gridDim.x * 4;
+    // every lane of a wave runs the same number of iterations (the DPP
+    // exchanges need the whole row of 16 lanes): items past the end are
+    // clamped to the last one and not stored
+    for (int64_t w0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; w0 < items; w0 += nwave * 4) {
+        const bool live = w0 + u < items;
+        const int64_t it = live ? w0 + u : items - 1;
+        const int64_t r = it / groups, g = it - r * groups;
+        const int64_t so = r * ld_src + g * 256 + 4 * p, doff = r * ld_dst + g * 256 + 4 * p;
+        float v[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) load4<DT>(src, so + 64 * i, v[i]);
+        if (zero_above > 0.0f) {
+            // outliers zeroed; counted once per wave, clamped items excluded
+            unsigned wc = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool out = fabsf(v[i][e]) > zero_above;
+                    wc += (unsigned)__popcll(__ballot(out && live));
+                    v[i][e] = out ? 0.0f : v[i][e];
+                }
+            if (lane == 0) cnt += wc;
+        }
+        // digit 0
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bfly4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        // digit 1 (the quad), digit 2 (the row of 16)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = bfly4_quad(v[i][e]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = bfly4_row(v[i][e]);
+        // digit 3
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bfly4(v[0][e], v[1][e], v[2][e], v[3][e]);
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<floatx4_t*>(dst + doff + 64 * i) = floatx4_t{v[i][0], v[i][1], v[i][2], v[i][3]};
+        }
+    }
+    flush_count(cnt, nz);
+}
+
 // Column pass of R^T H R for groups of 256 rows: in place on fp32 [n, n]
 // matrices.  Work-group: one 256-row group x 64 columns; thread (c, q)
 // (c = t % 64 the column, q = t / 64 the wave) loads rows 64 q .. 64 q + 63 of
@@ -340,6 +442,27 @@ static int rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t col
                "ic_rotate_rows: in-place needs f32 and equal ld");
     if (rows == 0 || cols_pad == 0) return IC_OK;
     hipStream_t st = as_stream(stream);
+    {
+        const size_t esz = src_dtype == IC_DTYPE_F32 ? 4 : 2;
+        const bool coal = rot == 256 && cols == cols_pad && ((uintptr_t)src % 16 == 0) &&
+                          ((ld_src * esz) % 16 == 0) && ((uintptr_t)dst % 16 == 0) && (ld_dst % 4 == 0);
+        if (coal) {
+            const int64_t groups = cols / 256, items = rows * groups;
+            const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(items, 16), 4096));
+            ProfScope prof_scope(st, tag, 8.0 * rows * cols_pad, (double)rows * cols * esz + 4.0 * rows * cols_pad);
+            if (src_dtype == IC_DTYPE_F32)
+                hipLaunchKernelGGL(rotate256_coal<IC_DTYPE_F32>, dim3(grid), dim3(256), 0, st, src, rows, groups,
+                                   ld_src, dst, ld_dst, zero_above, n_zeroed);
+            else if (src_dtype == IC_DTYPE_BF16)
+                hipLaunchKernelGGL(rotate256_coal<IC_DTYPE_BF16>, dim3(grid), dim3(256), 0, st, src, rows, groups,
+                                   ld_src, dst, ld_dst, zero_above, n_zeroed);
+            else
+                hipLaunchKernelGGL(rotate256_coal<IC_DTYPE_F16>, dim3(grid), dim3(256), 0, st, src, rows, groups,
+                                   ld_src, dst, ld_dst, zero_above, n_zeroed);
+            IC_CHECK_LAUNCH();
+            return IC_OK;
+        }
+    }
     if (rot >= 4 && rot <= 256 && is_pow4(rot) && cols_pad % 16 == 0 && rows * (cols_pad / 16) < (1LL << 31)) {
         size_t esz = src_dtype == IC_DTYPE_F32 ? 4 : 2;
         bool vec_ok = ((uintptr_t)src % 16 == 0) && ((ld_src * esz) % 16 == 0) && ((uintptr_t)dst % 16 == 0) &&

@@ -5,11 +5,13 @@
 //
 // Bit-exactness: codes and fp16 scales reproduce the fp32 formulas of
 // converter/scales.py exactly (IEEE division, no contraction, rhaz with the
-// literal +-0.5, round-half-even in the clip search).  The clip-search MSE is
-// accumulated in fp64, so only candidates whose fp32 MSEs tie to within the
-// reference's own fp32 summation noise could be chosen differently.
+// literal +-0.5, round-half-even in the clip search).  The clip search's
+// per-row MSE is the reference's (W - dequant).pow(2).mean(dim=-1): fp32
+// squares summed in torch's CPU inner-sum order, divided by the row length
+// (rows up to 15872 columns; longer rows accumulate in fp64).
 #include "common.hpp"
 #include "prof.hpp"
+#include "torchsum.hpp"
 
 namespace icq {
 
@@ -183,6 +185,103 @@ __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict
     }
 }
 
+// fp32 squared error of one clip candidate for one value (the elementwise
+// steps of the reference's mse before its sum).
+template <bool FAST>
+__device__ __forceinline__ float cand_sq(float w, const Cand& c, float rs, int asym, float qmin, float qmax) {
+    float y = FAST ? div_rn_fast(w, c.s, rs) : w / c.s;
+    if (asym) y = y + c.z;
+    const float q = clampf_med3(rhte(y), qmin, qmax);
+    const float d = asym ? (q - c.z) * c.s : q * c.s;
+    const float e = w - d;
+    return e * e;
+}
+
+// Clip search with the reference's fp32 MSE, one work-group (256 threads)
+// per row: the row is staged in LDS (cols <= CLIP_LDS_COLS), its min / max /
+// absmax reduced, then thread (candidate k, sequence q) runs the cascade of
+// sequence q (values 32 m + q) of candidate k's squared errors, eight
+// candidates per pass, and one thread per candidate finishes torch's inner
+// sum (leftover vectors, merge, leftover scalars, lanes) and divides by the
+// row length.  The first minimum (strict <, a NaN never wins) is kept.
+constexpr int64_t CLIP_LDS_COLS = 15872;   // the row plus the static arrays within 64 KB of LDS
+constexpr int CLIP_PASS = 256 / SUM_SEQ;   // candidates per pass
+
+__global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
+                                                       int64_t ld, int bits, int asym, int n_ratios, Ratios rt,
+                                                       uint16_t* __restrict__ scale16, int8_t* __restrict__ zp) {
+    extern __shared__ float xs[];                   // the row, cols floats
+    __shared__ float part[CLIP_PASS][SUM_SEQ];
+    __shared__ float mses[MAX_RATIOS];
+    __shared__ float red[4][3];
+    __shared__ int red_ok[4];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* x = W + r * ld;
+        float mn = INFINITY, mx = -INFINITY, am = 0.0f;
+        bool ok = true;
+        for (int64_t j = t; j < cols; j += 256) {
+            const float v = x[j];
+            xs[j] = v;
+            mn = nmin(mn, v);
+            mx = nmax(mx, v);
+            am = nmax(am, fabsf(v));
+            ok = ok && div_a_ok(v);
+        }
+        mn = wave_nmin(mn);
+        mx = wave_nmax(mx);
+        am = wave_nmax(am);
+        const bool wok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+        if (lane == 0) {
+            red[wv][0] = mn; red[wv][1] = mx; red[wv][2] = am;
+            red_ok[wv] = wok;
+        }
+        __syncthreads();
+        RowStats st{red[0][0], red[0][1], red[0][2]};
+        bool row_ok = red_ok[0] != 0;
+        for (int w = 1; w < 4; ++w) {
+            st.mn = nmin(st.mn, red[w][0]);
+            st.mx = nmax(st.mx, red[w][1]);
+            st.amax = nmax(st.amax, red[w][2]);
+            row_ok = row_ok && red_ok[w] != 0;
+        }
+        const int64_t n4 = cols / SUM_VEC / 4;
+        const int lp = cascade_lp(n4);
+        for (int k0 = 0; k0 < n_ratios; k0 += CLIP_PASS) {
+            const int kk = t / SUM_SEQ, q = t % SUM_SEQ, k = k0 + kk;
+            if (k < n_ratios && cols >= SUM_VEC) {
+                const Cand c = rtn_candidate(st, bits, asym, true, rt.v[k]);
+                const float rs = 1.0f / c.s;
+                part[kk][q] = row_ok && div_b_ok(c.s)
+                    ? cascade_seq([&](int64_t m) { return cand_sq<true>(xs[m * SUM_SEQ + q], c, rs, asym, qmin, qmax); },
+                                  n4, lp)
+                    : cascade_seq([&](int64_t m) { return cand_sq<false>(xs[m * SUM_SEQ + q], c, rs, asym, qmin, qmax); },
+                                  n4, lp);
+            }
+            __syncthreads();
+            if (t < CLIP_PASS && k0 + t < n_ratios) {
+                const Cand c = rtn_candidate(st, bits, asym, true, rt.v[k0 + t]);
+                const float rs = 1.0f / c.s;
+                auto sq = [&](int64_t i) { return cand_sq<false>(xs[i], c, rs, asym, qmin, qmax); };
+                const float sum = cols >= SUM_VEC ? inner_sum_finish(part[t], sq, cols) : inner_sum_short(sq, cols);
+                mses[k0 + t] = sum / (float)cols;
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            int best = 0;
+            float bm = mses[0];
+            for (int k = 1; k < n_ratios; ++k)
+                if (mses[k] < bm) { bm = mses[k]; best = k; }
+            const Cand c = rtn_candidate(st, bits, asym, true, rt.v[best]);
+            scale16[r] = f32_to_f16_bits(c.s);
+            if (asym && zp) zp[r] = (int8_t)(int)c.z;
+        }
+        __syncthreads();   // xs and part are reused by the next row
+    }
+}
+
 __device__ __forceinline__ uint8_t nib(float q) { return (uint8_t)(((int)q) & 0xF); }
 
 // One wave per row, 4 consecutive columns per lane and step: 16-byte W
@@ -207,16 +306,26 @@ __global__ __launch_bounds__(256) void rtn_quant_kernel(const float* __restrict_
         const float rs = 1.0f / s;
         const bool s_ok = div_b_ok(s);
         const float* x = W + r * ld;
-        for (int64_t c0 = 4 * (int64_t)lane; c0 < cols; c0 += 256) {
-            const bool full = c0 + 4 <= cols;
-            float w[4];
-            if (VEC && full) {
+        // QU column steps of the wave per pass, all their loads in flight first
+        constexpr int QU = 4;
+        for (int64_t cb = 4 * (int64_t)lane; cb < cols; cb += 256 * QU) {
+          float wq[QU][4];
+#pragma unroll
+          for (int k = 0; k < QU; ++k) {
+            const int64_t c0 = cb + 256 * k;
+            if (VEC && c0 + 4 <= cols) {
                 const float4 t = *reinterpret_cast<const float4*>(x + c0);
-                w[0] = t.x; w[1] = t.y; w[2] = t.z; w[3] = t.w;
+                wq[k][0] = t.x; wq[k][1] = t.y; wq[k][2] = t.z; wq[k][3] = t.w;
             } else {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) w[u] = c0 + u < cols ? x[c0 + u] : 0.0f;
+                for (int u = 0; u < 4; ++u) wq[k][u] = c0 + u < cols ? x[c0 + u] : 0.0f;
             }
+          }
+#pragma unroll
+          for (int k = 0; k < QU; ++k) {
+            const int64_t c0 = cb + 256 * k;
+            const bool full = c0 + 4 <= cols;
+            const float* w = wq[k];
             const bool ok = s_ok && div_a_ok(w[0]) && div_a_ok(w[1]) && div_a_ok(w[2]) && div_a_ok(w[3]);
             const bool all_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
             float q[4];
@@ -242,11 +351,12 @@ __global__ __launch_bounds__(256) void rtn_quant_kernel(const float* __restrict_
                 const uint8_t b0 = (uint8_t)(nib(q[0]) | (nib(q[1]) << 4)), b1 = (uint8_t)(nib(q[2]) | (nib(q[3]) << 4));
                 if (VEC && full) {
                     *reinterpret_cast<uint16_t*>(o) = (uint16_t)(b0 | (b1 << 8));
-                } else {
+                } else if (c0 < cols) {
                     o[0] = b0;
                     if (c0 + 2 < cols) o[1] = b1;
                 }
             }
+          }
         }
     }
 }
@@ -369,17 +479,30 @@ __global__ __launch_bounds__(256) void quant_error_partial(const float* __restri
         const float* wr = W + r * ld;
         const int8_t* qr = codes + r * ld_q;
         if (vec) {
-            for (int64_t c = 4 * (int64_t)threadIdx.x; c < cols; c += 4 * (int64_t)blockDim.x) {
-                const float4 wv = *reinterpret_cast<const float4*>(wr + c);
-                const char4 qv = *reinterpret_cast<const char4*>(qr + c);
-                const float q[4] = {(float)qv.x, (float)qv.y, (float)qv.z, (float)qv.w};
-                const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+            // four column steps per pass, their loads in flight together
+            constexpr int EU = 4;
+            const int64_t step = 4 * (int64_t)blockDim.x;
+            for (int64_t cb = 4 * (int64_t)threadIdx.x; cb < cols; cb += EU * step) {
+                float4 wv[EU];
+                char4 qv[EU];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float d = zp ? (q[u] - z) * s : q[u] * s;
-                    const float e = w[u] - d;
-                    acc += (double)e * (double)e;
-                    mx = nmax(mx, fabsf(e));
+                for (int k = 0; k < EU; ++k) {
+                    const int64_t c = cb + k * step;
+                    wv[k] = c < cols ? *reinterpret_cast<const float4*>(wr + c) : float4{0.f, 0.f, 0.f, 0.f};
+                    qv[k] = c < cols ? *reinterpret_cast<const char4*>(qr + c) : char4{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int k = 0; k < EU; ++k) {
+                    if (cb + k * step >= cols) continue;
+                    const float q[4] = {(float)qv[k].x, (float)qv[k].y, (float)qv[k].z, (float)qv[k].w};
+                    const float w[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float d = zp ? (q[u] - z) * s : q[u] * s;
+                        const float e = w[u] - d;
+                        acc += (double)e * (double)e;
+                        mx = nmax(mx, fabsf(e));
+                    }
                 }
             }
         } else {
@@ -457,7 +580,11 @@ extern "C" int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t
     Ratios rt;
     for (int i = 0; i < MAX_RATIOS; ++i) rt.v[i] = i < n_ratios ? ratios[i] : 1.0f;
     ProfScope prof_scope(as_stream(stream), PT_RTN_SCALES, 0.0, (double)rows * cols * 4.0 + rows * 3.0);
-    if (n_ratios > 0 && cols <= 64 * 64)
+    if (n_ratios > 0 && cols <= CLIP_LDS_COLS)
+        hipLaunchKernelGGL(rtn_clip_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(256),
+                           cols * sizeof(float), as_stream(stream), W, rows, cols, ld, bits, asym, n_ratios, rt,
+                           scale16, zp);
+    else if (n_ratios > 0 && cols <= 64 * 64)
         hipLaunchKernelGGL(rtn_scales_kernel<64>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
                            cols, ld, bits, asym, n_ratios, rt, scale16, zp);
     else

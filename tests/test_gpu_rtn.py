@@ -57,6 +57,42 @@ def test_rotate_weights_deterministic(gpu_dev):
     assert torch.equal(a, b)
 
 
+def _rotate_raw(src, dtype_code, rows, cols, ld_src, zero_above=0.0, nz=None):
+    from int_crush_converter_amd import _native as nat
+    out = torch.empty(rows, cols, dtype=torch.float32, device=src.device)
+    nat.check(nat.lib().ic_rotate_rows(src.data_ptr(), dtype_code, rows, cols, ld_src, out.data_ptr(), cols, cols,
+                                       256, float(zero_above), nat.ptr(nz), nat.stream()), "ic_rotate_rows")
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,cols", [(33, 512), (7, 256), (1, 1024), (129, 768)])
+def test_rotate256_coalesced_equals_register_kernel(gpu_dev, dtype, rows, cols):
+    """The coalesced 256-group kernel (aligned whole-group rows) gives the
+    same bits as the per-lane register kernel, which an unaligned source
+    (one element in) forces, with outlier zeroing and its count (item counts
+    not a multiple of the four per wave)."""
+    from int_crush_converter_amd import _native as nat
+    g = torch.Generator().manual_seed(rows * cols)
+    W = torch.randn(rows, cols + 8, generator=g) * 0.02
+    W[0, 5] = 5000.0
+    W[-1, cols - 1] = -2000.0
+    buf = W.to(dtype).to(gpu_dev)
+    code = nat.dtype_code(buf)
+    aligned = buf[:, :cols].contiguous()
+    nz_a = torch.zeros(1, dtype=torch.int64, device=gpu_dev)
+    nz_b = torch.zeros(1, dtype=torch.int64, device=gpu_dev)
+    a = _rotate_raw(aligned, code, rows, cols, cols, 1000.0, nz_a)
+    # the same rows read one element in (pitch cols + 8): no 16-byte alignment
+    shifted = torch.cat([torch.zeros(rows, 1, dtype=dtype), W.to(dtype)[:, :cols + 7]], 1).to(gpu_dev)
+    b = torch.empty(rows, cols, dtype=torch.float32, device=gpu_dev)
+    nat.check(nat.lib().ic_rotate_rows(shifted.data_ptr() + shifted.element_size(), code, rows, cols, cols + 8,
+                                       b.data_ptr(), cols, cols, 256, 1000.0, nz_b.data_ptr(), nat.stream()),
+              "ic_rotate_rows")
+    assert torch.equal(a, b)
+    assert int(nz_a.item()) == int(nz_b.item()) == 2
+
+
 @pytest.mark.parametrize("rot,n", [(16, 64), (64, 192), (256, 512), (256, 300), (128, 256)])
 def test_rotate_hessian_2d(gpu_dev, rot, n):
     from int_crush_converter_amd.rotation import rotate_hessian
@@ -109,6 +145,29 @@ def test_rtn_bit_exact(gpu_dev, bits, asym, ratios):
     if z_want is not None:
         assert torch.equal(z_got.cpu(), z_want)
     assert torch.equal(q_got.cpu(), q_want)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (64, 7), (9, 15872), (5, 16000), (33, 1000)])
+@pytest.mark.parametrize("bits,asym", [(8, True), (4, False)])
+def test_clip_search_bit_exact_widths(gpu_dev, rows, cols, bits, asym):
+    """The clip search at C2's shape (INT8 asymmetric, five ratios, 1 % of
+    the input columns x 20) and at widths around the LDS-staged limit
+    (15872 columns; 16000 takes the fp64-sum kernel): scales and zero-points
+    equal the oracle's, whose MSE is the reference's fp32 mean."""
+    from int_crush_converter_amd import scales as S
+    W = _w(rows, cols, rows + cols + bits, outliers=max(1, cols // 100))
+    Wg = W.to(gpu_dev)
+    if asym:
+        fn_w, fn_g = ((lambda: ref.scales_int8_asym(W, RATIOS)),
+                      (lambda: S.calculate_scales_int8_asymmetric(Wg, clipping_ratios=RATIOS)))
+    else:
+        fn_w, fn_g = ((lambda: (ref.scales_int4_sym(W, cols, RATIOS), None)),
+                      (lambda: (S.calculate_scales(Wg, cols, clipping_ratios=RATIOS), None)))
+    s_want, z_want = fn_w()
+    s_got, z_got = fn_g()
+    assert torch.equal(s_got.cpu(), s_want)
+    if z_want is not None:
+        assert torch.equal(z_got.cpu(), z_want)
 
 
 def test_rtn_group_wise(gpu_dev):
