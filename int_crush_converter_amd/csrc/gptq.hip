@@ -79,6 +79,110 @@ __device__ __forceinline__ float row_owner(float v, int o, int slot) {
     return x;
 }
 
+// The column loop of one sweep block for the lane's row slot.  Column
+// j = LPR r0 + o lives in register r0 of lane o of each row slot; updates are
+// unconditional on registers r >= r0 (the register of column j on lanes <= o
+// is already quantised and never read again, so those updates are dead).
+//
+// EXACT = false: every division takes the fast correctly rounded quotient
+// without a per-column test.  The GPTQ code needs only the rounding of
+// y = x / s (+ zp), which the fast quotient gets right for every x: below
+// 2^-60 the quotient is far below the half-unit of the rounding, and from
+// 2^61 on (or inf / NaN) x * RN(1/s) has the sign, the magnitude beyond the
+// clamp and the NaN of x / s.  The normalised error (x - deq) / Hinv_jj must
+// be exact, so a residual outside [2^-60, 2^61) (other than 0 or NaN), or a
+// pivot or scale outside [2^-30, 2^31), sets `unsafe` and the caller redoes
+// the block with EXACT = true, the wave-uniform test of div_rn_wave.
+template <int MODE, int LPR, bool ZP, bool EXACT>
+__device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[SW_NB / LPR],
+                                           float (&ev)[SW_NB / LPR], const float* sc, const float* scr,
+                                           const float* Hs, const float* hjj, const float* dinv, const int* dok,
+                                           int nb, int p, int half, float s_row, float s_rrow, bool srow_ok,
+                                           float z_row, float qmin, float qmax, bool& unsafe) {
+    constexpr int SW_HALF = LPR;
+    constexpr int R = SW_NB / LPR;
+#pragma unroll
+    for (int r = 0; r < R; ++r) qv[r] = ev[r] = 0.0f;
+    float h[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) h[r] = Hs[r * SW_HALF + p];
+    float hd = hjj[0], dvj = dinv[0];
+    bool dkj = dok[0] != 0;
+    bool bad = false;
+#pragma unroll
+    for (int r0 = 0; r0 < R; ++r0) {
+        if (r0 * SW_HALF >= nb) break;
+#pragma nounroll
+        for (int o = 0; o < SW_HALF; ++o) {
+            const int j = r0 * SW_HALF + o;
+            if (j >= nb) break;
+            const int jn = j + 1 < SW_NB ? j + 1 : j;
+            float hn[R];
+#pragma unroll
+            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * SW_HALF + p];
+            const float hdn = hjj[jn], dvn = dinv[jn];
+            const bool dkn = dok[jn] != 0;
+            // the owner's value of this lane's row
+            const float x = row_owner<LPR>(w[r0], o, half);
+            float q, e;
+            if (MODE == SWEEP_GPTQ) {
+                float y;
+                if (EXACT) {
+                    y = div_rn_wave(x, s_row, s_rrow, srow_ok);
+                } else {
+                    y = div_rn_fast(x, s_row, s_rrow);
+                    y = fabsf(x) < 0x1p61f ? y : x * s_rrow;
+                }
+                if (ZP) y = y + z_row;
+                q = clampf_med3(rhaz_trunc(y), qmin, qmax);
+                const float deq = ZP ? (q - z_row) * s_row : q * s_row;
+                const float num = x - deq;
+                if (EXACT) {
+                    e = div_rn_wave(num, hd, dvj, dkj);
+                } else {
+                    e = div_rn_fast(num, hd, dvj);
+                    const float an = fabsf(num);
+                    bad = bad || !dkj || (an < 0x1p-60f && an != 0.0f) || (an >= 0x1p61f);
+                }
+                e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
+            } else {
+                const float s_el = row_owner<LPR>(sc[r0], o, half);
+                const float s_rc = row_owner<LPR>(scr[r0], o, half);
+                float y;
+                if (EXACT) {
+                    y = div_rn_wave(x, s_el, s_rc, div_b_ok(s_el));
+                } else {
+                    y = div_rn_fast(x, s_el, s_rc);
+                    y = fabsf(x) < 0x1p61f ? y : x * s_rc;
+                    bad = bad || !div_b_ok(s_el);
+                }
+                q = clampf_med3(rhaz_trunc(y), qmin, qmax);
+                // sign-flip correction (inert for positive scales)
+                const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
+                                                  : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
+                const float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
+                const bool flip = ws * qs < 0.0f;
+                const bool can = flip && (q > qmin);
+                if (flip && q == qmin) q = qmax;
+                if (can) q = -q;
+                q = clampf(q, qmin, qmax);
+                e = (x - q * s_el) * dvj;
+            }
+            const bool own = p == o;
+            qv[r0] = own ? q : qv[r0];
+            ev[r0] = own ? e : ev[r0];
+#pragma unroll
+            for (int r = r0; r < R; ++r) w[r] = w[r] - e * h[r];
+#pragma unroll
+            for (int r = r0; r < R; ++r) h[r] = hn[r];
+            hd = hdn;
+            dvj = dvn;
+            dkj = dkn;
+        }
+    }
+    unsafe = unsafe || bad;
+}
+
 template <int MODE, int LPR>
 __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     constexpr int SW_HALF = LPR;
@@ -153,68 +257,27 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     const bool has_zp = a.zp != nullptr;
     const bool srow_ok = div_b_ok(s_row);
 
-    // Column j = LPR r0 + o lives in register r0 of lane o of each row slot.
-    // Updates are unconditional on registers r >= r0: the register of
-    // column j on lanes <= o is already quantised and never read again, so
-    // those updates are dead values.
     float qv[R], ev[R];
+    float w0[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) qv[r] = ev[r] = 0.0f;
-    float h[R];
+    for (int r = 0; r < R; ++r) w0[r] = w[r];
+    bool unsafe = MODE == SWEEP_GPTQ && !srow_ok;
+#define ICQ_COLS(ZP, EXACT) \
+    sweep_cols<MODE, LPR, ZP, EXACT>(w, qv, ev, sc, scr, Hs, hjj, dinv, dok, nb, p, half, s_row, s_rrow, srow_ok, \
+                                     z_row, a.qmin, a.qmax, unsafe)
+    if (has_zp) ICQ_COLS(true, false);
+    else ICQ_COLS(false, false);
+    // A value outside the fast division's exact domain (none in practice:
+    // a residual below 2^-60 or above 2^61, or a pivot / scale outside
+    // [2^-30, 2^31)): the wave runs the block again with the IEEE-exact
+    // division test on every column.
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(unsafe) != 0, 0)) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) h[r] = Hs[r * SW_HALF + p];
-    float hd = hjj[0], dvj = dinv[0];
-    bool dkj = dok[0] != 0;
-#pragma unroll
-    for (int r0 = 0; r0 < R; ++r0) {
-        if (r0 * SW_HALF >= nb) break;
-#pragma nounroll
-        for (int o = 0; o < SW_HALF; ++o) {
-            const int j = r0 * SW_HALF + o;
-            if (j >= nb) break;
-            const int jn = j + 1 < SW_NB ? j + 1 : j;
-            float hn[R];
-#pragma unroll
-            for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * SW_HALF + p];
-            const float hdn = hjj[jn], dvn = dinv[jn];
-            const bool dkn = dok[jn] != 0;
-            // the owner's value of this lane's row
-            const float x = row_owner<LPR>(w[r0], o, half);
-            float q, e;
-            if (MODE == SWEEP_GPTQ) {
-                float y = div_rn_wave(x, s_row, s_rrow, srow_ok);
-                if (has_zp) y = y + z_row;
-                q = clampf_med3(rhaz_trunc(y), a.qmin, a.qmax);
-                const float deq = has_zp ? (q - z_row) * s_row : q * s_row;
-                e = div_rn_wave(x - deq, hd, dvj, dkj);
-                e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
-            } else {
-                const float s_el = row_owner<LPR>(sc[r0], o, half);
-                const float s_rc = row_owner<LPR>(scr[r0], o, half);
-                q = clampf_med3(rhaz_trunc(div_rn_wave(x, s_el, s_rc, div_b_ok(s_el))), a.qmin, a.qmax);
-                // sign-flip correction (inert for positive scales)
-                const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
-                                                  : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
-                const float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
-                const bool flip = ws * qs < 0.0f;
-                const bool can = flip && (q > a.qmin);
-                if (flip && q == a.qmin) q = a.qmax;
-                if (can) q = -q;
-                q = clampf(q, a.qmin, a.qmax);
-                e = (x - q * s_el) * dvj;
-            }
-            const bool own = p == o;
-            qv[r0] = own ? q : qv[r0];
-            ev[r0] = own ? e : ev[r0];
-#pragma unroll
-            for (int r = r0; r < R; ++r) w[r] = w[r] - e * h[r];
-#pragma unroll
-            for (int r = r0; r < R; ++r) h[r] = hn[r];
-            hd = hdn;
-            dvj = dvn;
-            dkj = dkn;
-        }
+        for (int r = 0; r < R; ++r) w[r] = w0[r];
+        if (has_zp) ICQ_COLS(true, true);
+        else ICQ_COLS(false, true);
     }
+#undef ICQ_COLS
     // codes and errors of the lane's own columns (coalesced per row)
     if (rv) {
 #pragma unroll

@@ -217,6 +217,35 @@ def test_sweep_single_block_bit_exact(gpu_dev, bits, asym, B, N):
     assert torch.equal(Qg, Q)
 
 
+@pytest.mark.parametrize("case", ["tiny_rows", "tiny_pivots", "huge_rows"])
+@pytest.mark.parametrize("rows", [77, 12300])
+def test_sweep_exact_fallback_bit_exact(gpu_dev, case, rows):
+    """Inputs outside the fast division's exact domain make the sweep redo
+    the block with the IEEE-exact test: rows of values near 1e-25 (residuals
+    below 2^-60), an inverse Hessian scaled to pivots below 2^-30, and rows
+    near 1e20 (residuals from 2^61 on).  Codes equal the CPU sweep's given
+    the same Hinv, for the 2-rows-per-wave and 8-rows-per-wave kernels."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(rows + len(case))
+    N = 128
+    W = torch.randn(rows, N, generator=g) * 0.02
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 3 * N, 21), 0.01)
+    if case == "tiny_rows":
+        W[1] = W[1] * 1e-23
+        W[rows // 2] = W[rows // 2] * 1e-30
+    elif case == "tiny_pivots":
+        Hinv = Hinv * 1e-12
+    else:
+        W[2] = W[2] * 1e22
+    s, z = ref.gptq_row_params(W, 4, False)
+    Q = torch.zeros(rows, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, 128, -8, 7, z)
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, 4, False)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, 128).cpu()
+    assert torch.equal(Qg, Q)
+
+
 @pytest.mark.parametrize("bits,asym", [(4, False), (8, True)])
 def test_sweep_batched_groups_bit_exact(gpu_dev, bits, asym):
     """16 block-diagonal groups of one 128-column block over 2048 rows
