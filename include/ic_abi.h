@@ -127,6 +127,11 @@ int ic_quant_error(const float* W, int64_t rows, int64_t cols, int64_t ld,
                    const int8_t* zp, double* out_sumsq, float* out_maxabs, void* workspace,
                    void* stream);
 
+/* flag[0] = 1 when any of the n scales (fp16 bits for scale_kind 0, fp32 for
+ * 1) is +-Inf, NaN or 0, else 0 (device).  Replaces the bad-scale test of
+ * converter/pipeline.py:938-940 (scales.isinf() | isnan() | == 0). */
+int ic_scale_status(const void* scale, int scale_kind, int64_t n, int32_t* flag, void* stream);
+
 /* ---------------------------------------------------------------- fp32 GEMM */
 
 /* C = alpha * op(A) op(B) + beta * C on the fp32 matrix cores, row-major.

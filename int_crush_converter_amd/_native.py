@@ -43,6 +43,7 @@ _SIGS = {
     "ic_unpack_int4": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ic_quant_error_workspace_bytes": (_i64, []),
     "ic_quant_error": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ic_scale_status": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "ic_sgemm": (_i32, [_i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64, _f32, _vp, _i64, _i32, _i32, _vp]),
     "ic_hessian_inverse_workspace_bytes": (_i64, [_i64, _i64]),
     "ic_hessian_inverse": (_i32, [_vp, _i64, _i64, _f32, _i32, _vp, _vp, _vp]),

@@ -58,7 +58,24 @@ __global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t 
     float mean = sum / (float)n;
     mean = mean > 1e-6f ? mean : (mean != mean ? mean : 1e-6f);
     const float delta = damping * mean;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) A[i * ld + i] = A[i * ld + i] + delta;
+    if (staged) {
+        // the diagonal is in LDS: stores only, none waits for a load
+        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) A[i * ld + i] = dg[i] + delta;
+        return;
+    }
+    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * (int64_t)blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = i0 + u * (int64_t)blockDim.x;
+            v[u] = i < n ? A[i * ld + i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = i0 + u * (int64_t)blockDim.x;
+            if (i < n) A[i * ld + i] = v[u] + delta;
+        }
+    }
 }
 
 // Factor the diagonal block [k0, k0+nb) of matrix blockIdx.x in place (lower,

@@ -39,7 +39,20 @@ __device__ RowStats row_stats_wave(const float* __restrict__ x, int64_t cols) {
     int64_t c = lane;
     if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
         const int64_t c4 = cols & ~(int64_t)3;
-        for (int64_t j = 4 * (int64_t)lane; j < c4; j += 256) {
+        int64_t j = 4 * (int64_t)lane;
+        // four 16-byte loads in flight per lane (min / max do not depend on order)
+        for (; j + 768 < c4; j += 1024) {
+            float4 t[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[k] = *reinterpret_cast<const float4*>(x + j + 256 * k);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float v[4] = {t[k].x, t[k].y, t[k].z, t[k].w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) { mn = nmin(mn, v[u]); mx = nmax(mx, v[u]); am = nmax(am, fabsf(v[u])); }
+            }
+        }
+        for (; j < c4; j += 256) {
             const float4 t = *reinterpret_cast<const float4*>(x + j);
             const float v[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
@@ -548,6 +561,20 @@ __global__ __launch_bounds__(256) void quant_error_final(const double* part_sum,
     }
 }
 
+// flag = 1 when any of the n scales (fp16 bits or fp32) is +-Inf, NaN or 0,
+// else 0: the reference's bad-scale test (converter/pipeline.py:938-940).
+__global__ __launch_bounds__(1024) void scale_status_kernel(const void* __restrict__ scale, int kind, int64_t n,
+                                                           int32_t* flag) {
+    int bad = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float s = kind == 0 ? f16_bits_to_f32(reinterpret_cast<const uint16_t*>(scale)[i])
+                                  : reinterpret_cast<const float*>(scale)[i];
+        bad |= (!(fabsf(s) <= 3.402823466e38f) || s == 0.0f) ? 1 : 0;   // NaN fails the comparison
+    }
+    bad = __syncthreads_or(bad);
+    if (threadIdx.x == 0) *flag = bad ? 1 : 0;
+}
+
 static int rows_grid(int64_t rows, int waves_per_block) {
     return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(rows, waves_per_block), 65535));
 }
@@ -646,6 +673,15 @@ extern "C" int ic_unpack_int4(const uint8_t* src, int64_t rows, int64_t k, int64
     if (rows == 0 || k == 0) return IC_OK;
     hipLaunchKernelGGL(unpack_int4_kernel, dim3(elem_grid(rows * k)), dim3(256), 0, as_stream(stream), src, rows, k,
                        ld_src, dst, ld_dst);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+extern "C" int ic_scale_status(const void* scale, int scale_kind, int64_t n, int32_t* flag, void* stream) {
+    IC_REQUIRE(scale && flag, "ic_scale_status: null pointer");
+    IC_REQUIRE(scale_kind == 0 || scale_kind == 1, "ic_scale_status: scale_kind must be 0 (f16) or 1 (f32)");
+    IC_REQUIRE(n >= 0, "ic_scale_status: negative size");
+    hipLaunchKernelGGL(scale_status_kernel, dim3(1), dim3(1024), 0, as_stream(stream), scale, scale_kind, n, flag);
     IC_CHECK_LAUNCH();
     return IC_OK;
 }

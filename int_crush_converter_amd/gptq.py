@@ -45,22 +45,35 @@ def row_params(W: torch.Tensor, int_bits: int, asymmetric: bool):
     return s32, z32, s16, z8
 
 
+def scale_operand(scale: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """Scales as the ABI reads them: contiguous fp16 (kind 0) or fp32 (kind 1)."""
+    if scale.dtype == torch.float16:
+        return scale.reshape(-1).contiguous(), 0
+    return scale.reshape(-1).float().contiguous(), 1
+
+
+def launch_quant_error(W: torch.Tensor, Q: torch.Tensor, scale: torch.Tensor, zp8: torch.Tensor | None,
+                       sumsq_ptr: int, max_ptr: int) -> None:
+    """Enqueue ``ic_quant_error``: the fp64 sum of squared errors of
+    (Q - zp) * scale against W goes to ``sumsq_ptr`` and the max |error| (fp32)
+    to ``max_ptr`` (device addresses); nothing is synchronised."""
+    M, N = W.shape
+    ws = nat.workspace(nat.lib().ic_quant_error_workspace_bytes(), W.device)
+    sc, kind = scale_operand(scale)
+    zp = None if zp8 is None else zp8.reshape(-1).to(torch.int8).contiguous()
+    nat.check(nat.lib().ic_quant_error(W.data_ptr(), M, N, N, Q.data_ptr(), N, sc.data_ptr(), kind, nat.ptr(zp),
+                                       sumsq_ptr, max_ptr, ws.data_ptr(), nat.stream()),
+              "ic_quant_error")
+
+
 def quant_error(W: torch.Tensor, Q: torch.Tensor, scale: torch.Tensor, zp8: torch.Tensor | None):
     """(mse, max_err) of (Q - zp) * scale against W, scale fp16 or fp32 [M]."""
-    M, N = W.shape
     if W.numel() == 0:
         return float("nan"), 0.0
     out = torch.zeros(2, dtype=torch.float64, device=W.device)
-    mx = torch.zeros(1, dtype=torch.float32, device=W.device)
-    ws = nat.workspace(nat.lib().ic_quant_error_workspace_bytes(), W.device)
-    kind = 0 if scale.dtype == torch.float16 else 1
-    sc = scale.reshape(-1).contiguous() if kind == 0 else scale.reshape(-1).float().contiguous()
-    zp = None if zp8 is None else zp8.reshape(-1).to(torch.int8).contiguous()
-    nat.check(nat.lib().ic_quant_error(W.data_ptr(), M, N, N, Q.data_ptr(), N, sc.data_ptr(), kind, nat.ptr(zp),
-                                       out.data_ptr(), mx.data_ptr(), ws.data_ptr(), nat.stream()),
-              "ic_quant_error")
-    sumsq = out[0].item()
-    return sumsq / W.numel(), mx.item()
+    launch_quant_error(W, Q, scale, zp8, out.data_ptr(), out.data_ptr() + 8)
+    host = out.cpu()
+    return host[0].item() / W.numel(), host[1:].view(torch.float32)[0].item()
 
 
 def sweep(W_work: torch.Tensor, Hinv: torch.Tensor, s32: torch.Tensor, z32: torch.Tensor | None,

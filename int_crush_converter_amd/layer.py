@@ -16,7 +16,7 @@ import torch
 from . import _native as nat
 from .dlr import dlr_to_dense, is_dlr, woodbury_inverse
 from .config import INT4_SCALE_DIVISOR, INT8_SCALE_DIVISOR, SCALE_MAX, SCALE_MIN, WEIGHT_OUTLIER_CLAMP
-from .gptq import quant_error, row_params, sweep, sweep_block_diagonal
+from .gptq import launch_quant_error, row_params, scale_operand, sweep, sweep_block_diagonal
 from .hessian import inverse_batch
 from .rotation import rotate_rows_gpu, rotate_hessian_gpu
 from . import scales as _scales
@@ -187,15 +187,38 @@ def repair_bad_scales(W_work, codes, scales, zero_points, is_int8):
 
 
 def finish(W_work, codes, s16, z8, int_bits, packed=None, **kw) -> LayerOutput:
-    """Verification, bad-scale repair and packing (pipeline.py:919-1013)."""
-    mse, max_err = quant_error(W_work, codes, s16, z8)
-    bad = bool((s16.isinf() | s16.isnan() | (s16 == 0)).any().item())
+    """Verification, bad-scale repair and packing (pipeline.py:919-1013).
+
+    The verification sums, the bad-scale test and (INT4) the packing with its
+    range check are enqueued together and read back in one transfer; rows
+    with bad scales are repaired and re-packed afterwards (a rare path)."""
+    M, N = codes.shape
+    dev = codes.device
+    # one status block: [0] fp64 sum of squares, bytes 8..11 fp32 max |error|,
+    # int32 [3] bad-scale flag, int32 [4:7] packing flags (non-finite, < -8, > 7)
+    status = torch.zeros(4, dtype=torch.float64, device=dev)
+    base = status.data_ptr()
+    if W_work.numel():
+        launch_quant_error(W_work, codes, s16, z8, base, base + 8)
+    sc, kind = scale_operand(s16)
+    nat.check(nat.lib().ic_scale_status(sc.data_ptr(), kind, sc.numel(), base + 12, nat.stream()), "ic_scale_status")
+    if int_bits == 4 and packed is None:
+        packed = torch.empty(M, (N + 1) // 2, dtype=torch.uint8, device=dev)
+        if codes.numel():
+            nat.check(nat.lib().ic_pack_int4(codes.data_ptr(), 0, M, N, N, packed.data_ptr(), packed.shape[1],
+                                             base + 16, nat.stream()), "ic_pack_int4")
+    host = status.cpu()
+    words = host.view(torch.int32)
+    mse = host[0].item() / W_work.numel() if W_work.numel() else float("nan")
+    max_err = host[1:2].view(torch.float32)[0].item() if W_work.numel() else 0.0
+    bad = bool(words[3].item())
     if bad:
         codes, s16, z8, _ = repair_bad_scales(W_work, codes, s16, z8, int_bits == 8)
-        packed = None
-    if int_bits == 8:
-        stored = codes
-    else:
-        stored = packed if packed is not None else pack_codes(codes)
+        packed = pack_codes(codes) if int_bits == 4 else None
+    elif int_bits == 4:
+        nf, lo, hi = (int(v) for v in words[4:7].tolist())
+        if nf or lo or hi:
+            pack_codes(codes)   # raises the reference's INT4PackingError
+    stored = codes if int_bits == 8 else packed
     return LayerOutput(stored=stored, scales=s16, zero_points=z8, codes=codes, W_work=W_work, mse=mse,
                        max_err=max_err, bad_scales=bad, **kw)
