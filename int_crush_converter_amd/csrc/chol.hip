@@ -13,6 +13,7 @@
 //  4. lauum:  H^-1 (upper triangle) = X^T X, one GEMM whose tile (I, J)
 //             only runs k >= max(I, J) because X is lower triangular.
 // Flops: n^3/3 each for 2-4; all but the nb x nb factorisations are MFMA.
+#include <utility>
 #include <vector>
 
 #include "chol.hpp"
@@ -88,26 +89,30 @@ __global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t 
 // blocks and their inverses feed every later step, and an fp64 factor keeps
 // the whole inverse at the accuracy of the reference's LAPACK fp32 path.
 //
-// The block is processed in 16 panels of 8 columns.  Both the block A and
-// R (X = L^-1 under construction, started as I) live in MFMA accumulators:
-// the 36 lower 16x16 tiles of each are dealt round-robin to the 4 waves (9
-// per wave).  Per panel:
-//   1. the tiles holding the panel columns publish them to LDS, and the
-//      tiles holding rows j0..j0+7 of R publish those rows;
-//   2. wave 0 factors the panel (rows j0..127, 8 columns) in registers, two
-//      rows per lane, broadcasting pivots and the 8x8 diagonal block with
-//      readlane (no barrier per column), and puts the final L columns into
-//      an fp32 image of L in LDS and, in fp64, into the step-4 operands;
-//   3. meanwhile wave 1 finishes the rows of X = L^-1 of the previous panel
-//      by forward substitution with that panel's 8x8 diagonal block (two
-//      columns of X per lane) and stores them to Dinv / Dinv64 (whole rows:
-//      coalesced) - X runs one panel behind A, which never reads it;
-//   4. every wave applies the rank-8 updates A -= L_p L_p^T (this panel) and
-//      R -= L_p X_p (the previous panel) to its live tiles with
-//      v_mfma_f64_16x16x4_f64.
-// Elements that are already final (or above the diagonal) may receive
-// updates in step 4; they are never read again.  At the end the block
-// writes the image of L row by row.
+// The block is processed in 16 panels of 8 columns by 8 waves.  Both the
+// block A and R (X = L^-1 under construction, started as I) live in MFMA
+// accumulators: the 36 lower 16x16 tiles of each are dealt to waves 1..7
+// round-robin in column-major order (so one tile column spreads over
+// several waves).  Wave 0 owns no tile: it runs the serial part, the
+// column-by-column factorisation of each panel and the forward substitution
+// for the rows of X, while the other waves apply the rank-8 updates on the
+// matrix cores (v_mfma_f64_16x16x4_f64).  Look-ahead keeps the factorisation
+// off the MFMA path; iteration it has two phases:
+//   U: wave 0 factors panel it (from the published tile column, two rows
+//      per lane, pivots and the panel's rows broadcast by readlane); the
+//      others apply panel it - 1's update A -= L L^T to every live tile
+//      outside the next tile column (which got it in phase A of it - 1) and
+//      panel it - 2's update R -= L X to R, then publish rows of R of panel
+//      it - 1 (now final up to their own diagonal block);
+//   A: the owners of the tile column holding panel it + 1 apply panel it's
+//      update to it and publish it for wave 0; wave 0 turns the published
+//      rows of R into the rows of X of panel it - 1 (forward substitution
+//      with that panel's 8x8 diagonal block) and stores them to Dinv /
+//      Dinv64 (whole rows: coalesced).
+// Every element receives its updates in panel order with the same fp64
+// operations, so the result does not depend on the schedule.  Elements that
+// are already final (or above the diagonal) may receive updates; they are
+// never read again.  At the end the block writes the image of L row by row.
 //
 // MFMA 16x16x4 f64 operand layout (lane l of 64; D differs from the f32
 // variant's 4*(l/16) + v):
@@ -122,16 +127,42 @@ __device__ __forceinline__ double rdlane(double v, int l) {
     return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
 }
 
-constexpr int DSLOTS = 9;   // 36 lower tiles / 4 waves
+constexpr int DIAG_WAVES = 8;            // wave 0: factorisation; 1..7: tiles
+constexpr int DIAG_TILES = 36;           // lower 16x16 tiles of the 8x8 tile grid
+constexpr int DSLOTS = 6;                // tiles per MFMA wave (at most)
 
-// Lower 16x16 tile `id`, row-major over the lower triangle of the 8x8 tile
-// grid: tile row and tile column.  Wave W owns the tiles id = 4 s + W.
-constexpr int tri_row(int id) {
-    int I = 0;
-    while ((I + 1) * (I + 2) / 2 <= id) ++I;
-    return I;
+// Lower tile `id` in column-major order over the lower triangle: tile column
+// and tile row.  Wave W (1..7) owns the tiles id = W - 1 + 7 s.
+constexpr int cm_col(int id) {
+    int J = 0;
+    while (id >= 8 - J) { id -= 8 - J; ++J; }
+    return J;
 }
-constexpr int tri_col(int id) { return id - tri_row(id) * (tri_row(id) + 1) / 2; }
+constexpr int cm_row(int id) {
+    int J = 0;
+    while (id >= 8 - J) { id -= 8 - J; ++J; }
+    return J + id;
+}
+constexpr int tile_id(int W, int s) { return W - 1 + 7 * s; }
+
+// Slot S of wave W as compile-time constants, and a loop over a wave's
+// slots that hands each one to f as a type (so every tile coordinate is a
+// constant and the accumulators are indexed statically).
+template <int W, int S>
+struct DiagSlot {
+    static constexpr int s = S;
+    static constexpr bool ok = tile_id(W, S) < DIAG_TILES;
+    static constexpr int I = ok ? cm_row(tile_id(W, S)) : 0;
+    static constexpr int J = ok ? cm_col(tile_id(W, S)) : 0;
+};
+template <int W, typename F, int... S>
+__device__ __forceinline__ void each_slot_impl(F&& f, std::integer_sequence<int, S...>) {
+    (f(DiagSlot<W, S>{}), ...);
+}
+template <int W, typename F>
+__device__ __forceinline__ void each_slot(F&& f) {
+    each_slot_impl<W>(f, std::make_integer_sequence<int, DSLOTS>{});
+}
 
 // Panel-local k (0..7) is stored at kperm(k), so that the two k values a
 // lane feeds to the two MFMA steps of a panel, lr and lr + 4, are adjacent.
@@ -142,75 +173,25 @@ __device__ __forceinline__ constexpr int kperm(int k) { return (k & 3) * 2 + (k 
 // Arrays indexed by a row of the block have a spare row NB, where accesses
 // for rows past the block are clamped (so they need no branch).
 constexpr int DP = 9, RP = 17;
+constexpr int PLBUF = 3;   // L panels in use: it (phase A), it - 1 (A update), it - 2 (R update)
 
 struct DiagShared {
-    double pRaw[NB + 1][RP];   // the panel's tile column of A (16 columns; row NB stays 0)
-    double pL[2][NB + 1][DP];  // final L columns of the last two panels, at kperm
-    double dL[2][8][8];        // the 8x8 diagonal blocks of L of the last two panels
-    double rinv[2][8];         // and their pivots' reciprocal square roots
-    double rowR[8][NB];        // rows of R of the panel whose X rows are due
-    double rowXt[NB][DP];      // final rows of X = L^-1 of that panel, transposed, at kperm
-    float Lfin[NB + 1][NB + 1];   // L as it is finalised, zero above the diagonal
+    double pRaw[NB + 1][RP];       // the tile column of A holding the next panel (row NB stays 0)
+    double pL[PLBUF][NB + 1][DP];  // final L columns of the last three panels, at kperm
+    double dL[2][8][8];            // the 8x8 diagonal blocks of L of the last two panels
+    double rinv[2][8];             // and their pivots' reciprocal square roots
+    double rowR[8][NB];            // rows of R of the panel whose X rows are due
+    double rowXt[NB][DP];          // final rows of X = L^-1 of that panel, transposed, at kperm
+    float Lfin[NB + 1][NB + 1];    // L as it is finalised, zero above the diagonal
 };
 
-// The body of potrf_diag_kernel for wave W; every tile coordinate is a
-// compile-time constant, so the accumulators and the per-panel operand
-// registers are indexed statically.  Iteration it factors panel it (wave 0)
-// and finishes the rows of X of panel it - 1 (wave 1) at the same time: the
-// factorisation of A never reads X, so X runs one panel behind.
-template <int W>
-__device__ __forceinline__ void potrf_diag_wave(DiagShared& sh, const float* A, int64_t ld, int nb, float* D,
-                                                double* D64, int lane, int& bad) {
-    const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
-    ddoublex4 accA[DSLOTS], accX[DSLOTS];
-    // All 36 loads in flight at once: addresses are clamped into the block
-    // (every load is in bounds, no branch) and values outside it replaced.
-    float raw[DSLOTS][4];
-#pragma unroll
-    for (int s = 0; s < DSLOTS; ++s)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int i = tri_row(4 * s + W) * 16 + lr + 4 * v, j = tri_col(4 * s + W) * 16 + lj;
-            const int ic = i < nb ? i : nb - 1, jc = j < nb ? j : nb - 1;
-            raw[s][v] = A[(int64_t)ic * ld + jc];
-        }
-#pragma unroll
-    for (int s = 0; s < DSLOTS; ++s)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int i = tri_row(4 * s + W) * 16 + lr + 4 * v, j = tri_col(4 * s + W) * 16 + lj;
-            const double pad = (i == j) ? 1.0 : 0.0;
-            accA[s][v] = j > i ? 0.0 : (i < nb ? (double)raw[s][v] : pad);
-            accX[s][v] = pad;
-        }
-
+// Wave 0: phase U factors panel it, phase A finishes the rows of X of panel
+// it - 1.  Two barriers per iteration, matching diag_tile_wave.
+__device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, float* D, double* D64, int lane, int& bad) {
     for (int it = 0; it <= 16; ++it) {
-        // panel it of A (it < 16) and panel it - 1 of X (it >= 1)
-        const int j0 = it * 8, Jp = it >> 1, co = (it & 1) * 8, pb = it & 1;
-        const int x0 = j0 - 8, Jx = (it - 1) >> 1, cx = ((it - 1) & 1) * 8, xbuf = pb ^ 1;
-        // 1. publish the tile column of A that holds the panel (all 16
-        //    columns) and rows x0..x0+7 of R
-#pragma unroll
-        for (int s = 0; s < DSLOTS; ++s) {
-            const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
-            if (it < 16 && J == Jp) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) sh.pRaw[I * 16 + lr + 4 * v][lj] = accA[s][v];
-            }
-            if (it >= 1 && I == Jx) {
-                if (cx == 0) {
-                    sh.rowR[lr][J * 16 + lj] = accX[s][0];
-                    sh.rowR[lr + 4][J * 16 + lj] = accX[s][1];
-                } else {
-                    sh.rowR[lr][J * 16 + lj] = accX[s][2];
-                    sh.rowR[lr + 4][J * 16 + lj] = accX[s][3];
-                }
-            }
-        }
-        __syncthreads();
-        if (W == 0 && it < 16) {
-            // 2. wave 0 factors panel it (rows j0..127), two rows per lane;
-            //    rows past the block read the zero row NB
+        if (it < 16) {
+            const int j0 = it * 8, co = (it & 1) * 8, pb = it % PLBUF, db = it & 1;
+            // rows j0..127, two per lane; rows past the block read the zero row NB
             const int ra = j0 + lane, rb = j0 + lane + 64;
             const int rac = ra < NB ? ra : NB, rbc = rb < NB ? rb : NB;
             double va[8], vb[8], rinvv[8];
@@ -242,11 +223,11 @@ __device__ __forceinline__ void potrf_diag_wave(DiagShared& sh, const float* A, 
                     vb[c2] = fma(-vb[c], lk, vb[c2]);
                 }
             }
-            // the panel's L columns: fp64 operands for step 3, its 8x8
-            // diagonal block and pivots for the rows of X, and the fp32 image
-            // of L (rows past the block go to the spare row NB).  Rows of pL
-            // above the panel keep older values: they only reach elements
-            // that are final already, which are never read again.
+            // the panel's L columns (fp64 MFMA operands), its 8x8 diagonal
+            // block and pivots for the rows of X, and the fp32 image of L
+            // (rows past the block go to the spare row NB).  Rows of pL above
+            // the panel keep older values: they only reach elements that are
+            // final already, which are never read again.
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 sh.pL[pb][rac][kperm(c)] = va[c];
@@ -256,44 +237,45 @@ __device__ __forceinline__ void potrf_diag_wave(DiagShared& sh, const float* A, 
             }
             if (lane < 8) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) sh.dL[pb][lane][c] = va[c];
+                for (int c = 0; c < 8; ++c) sh.dL[db][lane][c] = va[c];
             }
             if (lane == 0) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) sh.rinv[pb][c] = rinvv[c];
+                for (int c = 0; c < 8; ++c) sh.rinv[db][c] = rinvv[c];
             }
         }
-        if (W == 1 && it >= 1) {
-            // 2'. wave 1: rows x0..x0+7 of X = L^-1 by forward substitution
-            //     with panel it - 1's diagonal block, two columns per lane;
-            //     stored to Dinv / Dinv64 as whole rows (coalesced)
+        __syncthreads();
+        if (it >= 1) {
+            // rows x0..x0+7 of X = L^-1 by forward substitution with panel
+            // it - 1's diagonal block, two columns per lane
+            const int x0 = (it - 1) * 8, xb = (it - 1) & 1;
             const int qa = lane, qb = lane + 64;
-            double xa[8], xb[8], l[8][8], ri[8];
+            double xa[8], xc[8], l[8][8], ri[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 xa[c] = sh.rowR[c][qa];
-                xb[c] = sh.rowR[c][qb];
-                ri[c] = sh.rinv[xbuf][c];
+                xc[c] = sh.rowR[c][qb];
+                ri[c] = sh.rinv[xb][c];
 #pragma unroll
-                for (int c2 = 0; c2 < c; ++c2) l[c][c2] = sh.dL[xbuf][c][c2];
+                for (int c2 = 0; c2 < c; ++c2) l[c][c2] = sh.dL[xb][c][c2];
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
 #pragma unroll
                 for (int c2 = 0; c2 < c; ++c2) {
                     xa[c] = fma(-l[c][c2], xa[c2], xa[c]);
-                    xb[c] = fma(-l[c][c2], xb[c2], xb[c]);
+                    xc[c] = fma(-l[c][c2], xc[c2], xc[c]);
                 }
                 xa[c] = qa <= x0 + 7 ? xa[c] * ri[c] : 0.0;
-                xb[c] = qb <= x0 + 7 ? xb[c] * ri[c] : 0.0;
+                xc[c] = qb <= x0 + 7 ? xc[c] * ri[c] : 0.0;
             }
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 sh.rowXt[qa][kperm(c)] = xa[c];
-                sh.rowXt[qb][kperm(c)] = xb[c];
+                sh.rowXt[qb][kperm(c)] = xc[c];
                 const int row = x0 + c;
                 const double oa = (row < nb && qa < nb) ? xa[c] : 0.0;
-                const double ob = (row < nb && qb < nb) ? xb[c] : 0.0;
+                const double ob = (row < nb && qb < nb) ? xc[c] : 0.0;
                 D[row * NB + qa] = (float)oa;
                 D[row * NB + qb] = (float)ob;
                 D64[row * NB + qa] = oa;
@@ -301,74 +283,175 @@ __device__ __forceinline__ void potrf_diag_wave(DiagShared& sh, const float* A, 
             }
         }
         __syncthreads();
-        // 3. rank-8 updates on the matrix cores, operands from registers:
-        //    A -= L_p L_p^T for panel it (live tiles: J*16+15 >= j0+8) and
-        //    R -= L_x X_x for panel it - 1 (rows below it, columns up to it),
-        //    opL[r][ks] = L[16 r + lj][panel col 4 ks + lr] (0 above the panel),
-        //    opX[r][ks] = X[panel row 4 ks + lr][16 r + lj].
-        //    Elements that are already final receive updates too; they are
-        //    never read again (their final values went to Lfin and Dinv).
-        if (it < 16) {
-            double opL[8][2];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                opL[r][0] = sh.pL[pb][r * 16 + lj][2 * lr];
-                opL[r][1] = sh.pL[pb][r * 16 + lj][2 * lr + 1];
-            }
-#pragma unroll
-            for (int s = 0; s < DSLOTS; ++s) {
-                const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
-                if (J * 16 + 15 >= j0 + 8) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks)
-                        accA[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opL[I][ks], opL[J][ks], accA[s], 0, 0, 0);
-                }
-            }
-        }
-        if (it >= 1 && it < 16) {
-            double opM[8][2], opX[8][2];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                opM[r][0] = sh.pL[xbuf][r * 16 + lj][2 * lr];
-                opM[r][1] = sh.pL[xbuf][r * 16 + lj][2 * lr + 1];
-                opX[r][0] = sh.rowXt[r * 16 + lj][2 * lr];
-                opX[r][1] = sh.rowXt[r * 16 + lj][2 * lr + 1];
-            }
-#pragma unroll
-            for (int s = 0; s < DSLOTS; ++s) {
-                const int I = tri_row(4 * s + W), J = tri_col(4 * s + W);
-                if (I * 16 + 15 >= x0 + 8 && J * 16 <= x0 + 7) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks)
-                        accX[s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opM[I][ks], opX[J][ks], accX[s], 0, 0, 0);
-                }
-            }
-        }
     }
 }
 
-__global__ __launch_bounds__(256) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0, int nb,
-                                                         float* dinv, double* dinv64, int64_t dstride, int* info) {
+// Operands of a rank-8 update from an L panel (or the X rows) in LDS:
+// op[r][ks] = P[16 r + lj][2 lr + ks] (panel columns 4 ks + lr, at kperm).
+__device__ __forceinline__ void load_op(const double (*P)[DP], int r, int lr, int lj, double (&op)[2]) {
+    op[0] = P[r * 16 + lj][2 * lr];
+    op[1] = P[r * 16 + lj][2 * lr + 1];
+}
+
+// Waves 1..7: the tiles of A and R.  Every tile coordinate is a compile-time
+// constant, so accumulators are indexed statically.
+template <int W>
+__device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, int64_t ld, int nb, int lane) {
+    const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
+    ddoublex4 accA[DSLOTS], accX[DSLOTS];
+    // all loads in flight at once: addresses are clamped into the block (no
+    // branch) and values outside it replaced
+    float raw[DSLOTS][4];
+    each_slot<W>([&](auto t) {
+        using T = decltype(t);
+        if constexpr (T::ok) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = T::I * 16 + lr + 4 * v, j = T::J * 16 + lj;
+                const int ic = i < nb ? i : nb - 1, jc = j < nb ? j : nb - 1;
+                raw[T::s][v] = A[(int64_t)ic * ld + jc];
+            }
+        }
+    });
+    each_slot<W>([&](auto t) {
+        using T = decltype(t);
+        if constexpr (T::ok) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = T::I * 16 + lr + 4 * v, j = T::J * 16 + lj;
+                const double pad = (i == j) ? 1.0 : 0.0;
+                accA[T::s][v] = j > i ? 0.0 : (i < nb ? (double)raw[T::s][v] : pad);
+                accX[T::s][v] = pad;
+            }
+        }
+    });
+    // tile column 0 for panel 0
+    each_slot<W>([&](auto t) {
+        using T = decltype(t);
+        if constexpr (T::ok && T::J == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sh.pRaw[T::I * 16 + lr + 4 * v][lj] = accA[T::s][v];
+        }
+    });
+    __syncthreads();
+    for (int it = 0; it <= 16; ++it) {
+        // ---- phase U
+        if (it >= 1) {
+            // panel p = it - 1: A -= L_p L_p^T on live tiles outside tile
+            // column it >> 1 (updated in phase A of iteration p)
+            const int p = it - 1, skipJ = it >> 1, lim = 8 * p + 8;
+            const double (*P)[DP] = sh.pL[p % PLBUF];
+            double op[8][2];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) load_op(P, r, lr, lj, op[r]);
+            each_slot<W>([&](auto t) {
+                using T = decltype(t);
+                if constexpr (T::ok) {
+                    if (T::J != skipJ && T::J * 16 + 15 >= lim) {
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            accA[T::s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-op[T::I][ks], op[T::J][ks], accA[T::s],
+                                                                              0, 0, 0);
+                    }
+                }
+            });
+        }
+        if (it >= 2) {
+            // panel q = it - 2: R -= L_q X_q for rows below the panel and
+            // columns up to its end
+            const int q = it - 2, x0 = 8 * q;
+            const double (*P)[DP] = sh.pL[q % PLBUF];
+            double opM[8][2], opX[8][2];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                load_op(P, r, lr, lj, opM[r]);
+                load_op(sh.rowXt, r, lr, lj, opX[r]);
+            }
+            each_slot<W>([&](auto t) {
+                using T = decltype(t);
+                if constexpr (T::ok) {
+                    if (T::I * 16 + 15 >= x0 + 8 && T::J * 16 <= x0 + 7) {
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            accX[T::s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opM[T::I][ks], opX[T::J][ks],
+                                                                              accX[T::s], 0, 0, 0);
+                    }
+                }
+            });
+        }
+        if (it >= 1) {
+            // rows x0..x0+7 of R (panel it - 1) for wave 0's substitution
+            const int Jx = (it - 1) >> 1, cx = ((it - 1) & 1) * 8;
+            each_slot<W>([&](auto t) {
+                using T = decltype(t);
+                if constexpr (T::ok) {
+                    if (T::I == Jx) {
+                        if (cx == 0) {
+                            sh.rowR[lr][T::J * 16 + lj] = accX[T::s][0];
+                            sh.rowR[lr + 4][T::J * 16 + lj] = accX[T::s][1];
+                        } else {
+                            sh.rowR[lr][T::J * 16 + lj] = accX[T::s][2];
+                            sh.rowR[lr + 4][T::J * 16 + lj] = accX[T::s][3];
+                        }
+                    }
+                }
+            });
+        }
+        __syncthreads();
+        // ---- phase A: panel it's update of the tile column holding panel it + 1, published
+        if (it <= 14) {
+            const int Jn = (it + 1) >> 1;
+            const double (*P)[DP] = sh.pL[it % PLBUF];
+            double opn[2];
+            load_op(P, Jn, lr, lj, opn);
+            each_slot<W>([&](auto t) {
+                using T = decltype(t);
+                if constexpr (T::ok) {
+                    if (T::J == Jn) {
+                        double opi[2];
+                        load_op(P, T::I, lr, lj, opi);
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks)
+                            accA[T::s] = __builtin_amdgcn_mfma_f64_16x16x4f64(-opi[ks], opn[ks], accA[T::s], 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) sh.pRaw[T::I * 16 + lr + 4 * v][lj] = accA[T::s][v];
+                    }
+                }
+            });
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0,
+                                                                    int nb, float* dinv, double* dinv64,
+                                                                    int64_t dstride, int* info) {
     __shared__ __attribute__((aligned(16))) DiagShared sh;
     const int b = blockIdx.x;
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
     float* D = dinv + (int64_t)b * dstride;
     double* D64 = dinv64 + (int64_t)b * dstride;
     const int lane = threadIdx.x & 63;
-    // uniform in the wave; each wave runs the same loop (two barriers per panel)
+    // uniform in the wave; every wave runs 1 + 2 * 17 barriers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Lfin starts at 0 (its upper part is never written) and so does the
-    // spare row of pRaw; the first barrier inside the loop orders this
-    for (int idx = threadIdx.x; idx < (NB + 1) * (NB + 1); idx += 256) (&sh.Lfin[0][0])[idx] = 0.0f;
+    // spare row of pRaw; the first barrier orders this
+    for (int idx = threadIdx.x; idx < (NB + 1) * (NB + 1); idx += DIAG_WAVES * 64) (&sh.Lfin[0][0])[idx] = 0.0f;
     if (threadIdx.x < RP) sh.pRaw[NB][threadIdx.x] = 0.0;
     int bad = 0;
-    if (wave == 0) potrf_diag_wave<0>(sh, A, ld, nb, D, D64, lane, bad);
-    else if (wave == 1) potrf_diag_wave<1>(sh, A, ld, nb, D, D64, lane, bad);
-    else if (wave == 2) potrf_diag_wave<2>(sh, A, ld, nb, D, D64, lane, bad);
-    else potrf_diag_wave<3>(sh, A, ld, nb, D, D64, lane, bad);
+    switch (wave) {
+        case 0: __syncthreads(); diag_factor_wave(sh, nb, D, D64, lane, bad); break;
+        case 1: diag_tile_wave<1>(sh, A, ld, nb, lane); break;
+        case 2: diag_tile_wave<2>(sh, A, ld, nb, lane); break;
+        case 3: diag_tile_wave<3>(sh, A, ld, nb, lane); break;
+        case 4: diag_tile_wave<4>(sh, A, ld, nb, lane); break;
+        case 5: diag_tile_wave<5>(sh, A, ld, nb, lane); break;
+        case 6: diag_tile_wave<6>(sh, A, ld, nb, lane); break;
+        default: diag_tile_wave<7>(sh, A, ld, nb, lane); break;
+    }
     __syncthreads();
     // write L (its upper part is 0 in Lfin), row-coalesced
-    for (int idx = threadIdx.x; idx < NB * NB; idx += 256) {
+    for (int idx = threadIdx.x; idx < NB * NB; idx += DIAG_WAVES * 64) {
         const int i = idx >> 7, j = idx & (NB - 1);
         if (i < nb && j < nb) A[(int64_t)i * ld + j] = sh.Lfin[i][j];
     }
@@ -502,7 +585,7 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* din
             double* Dk64 = dinv64 + kb * NB * NB;
             {
                 ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
-                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, ld, sH, k0, nb, Dk,
+                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(DIAG_WAVES * 64), 0, st, H, ld, sH, k0, nb, Dk,
                                    Dk64, dstride, info);
                 IC_CHECK_LAUNCH();
             }
