@@ -105,10 +105,10 @@ __global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t 
 //      panel it - 2's update R -= L X to R, then publish rows of R of panel
 //      it - 1 (now final up to their own diagonal block);
 //   A: the owners of the tile column holding panel it + 1 apply panel it's
-//      update to it and publish it for wave 0; wave 0 turns the published
-//      rows of R into the rows of X of panel it - 1 (forward substitution
-//      with that panel's 8x8 diagonal block) and stores them to Dinv /
-//      Dinv64 (whole rows: coalesced).
+//      update to it and publish it for wave 0; waves 0 and 1 turn the
+//      published rows of R into the rows of X of panel it - 1 (forward
+//      substitution with that panel's 8x8 diagonal block, a column per
+//      lane) and store them to Dinv / Dinv64 (whole rows: coalesced).
 // Every element receives its updates in panel order with the same fp64
 // operations, so the result does not depend on the schedule.  Elements that
 // are already final (or above the diagonal) may receive updates; they are
@@ -185,8 +185,39 @@ struct DiagShared {
     float Lfin[NB + 1][NB + 1];    // L as it is finalised, zero above the diagonal
 };
 
-// Wave 0: phase U factors panel it, phase A finishes the rows of X of panel
-// it - 1.  Two barriers per iteration, matching diag_tile_wave.
+// Rows 8 p .. 8 p + 7 of X = L^-1, column q: forward substitution with panel
+// p's 8x8 diagonal block of L from the published rows of R; the result goes
+// to rowXt (for the R updates) and to Dinv / Dinv64 (whole rows: coalesced
+// over the lanes).  Phase A splits the columns over waves 0 and 1.
+__device__ __forceinline__ void x_rows(DiagShared& sh, int p, int q, int nb, float* D, double* D64) {
+    const int x0 = p * 8, xb = p & 1;
+    double x[8], l[8][8], ri[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        x[c] = sh.rowR[c][q];
+        ri[c] = sh.rinv[xb][c];
+#pragma unroll
+        for (int c2 = 0; c2 < c; ++c2) l[c][c2] = sh.dL[xb][c][c2];
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int c2 = 0; c2 < c; ++c2) x[c] = fma(-l[c][c2], x[c2], x[c]);
+        x[c] = q <= x0 + 7 ? x[c] * ri[c] : 0.0;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        sh.rowXt[q][kperm(c)] = x[c];
+        const int row = x0 + c;
+        const double o = (row < nb && q < nb) ? x[c] : 0.0;
+        D[row * NB + q] = (float)o;
+        D64[row * NB + q] = o;
+    }
+}
+
+// Wave 0: phase U factors panel it, phase A finishes columns 0..63 of the
+// rows of X of panel it - 1.  Two barriers per iteration, matching
+// diag_tile_wave.
 __device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, float* D, double* D64, int lane, int& bad) {
     for (int it = 0; it <= 16; ++it) {
         if (it < 16) {
@@ -245,43 +276,7 @@ __device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, float* 
             }
         }
         __syncthreads();
-        if (it >= 1) {
-            // rows x0..x0+7 of X = L^-1 by forward substitution with panel
-            // it - 1's diagonal block, two columns per lane
-            const int x0 = (it - 1) * 8, xb = (it - 1) & 1;
-            const int qa = lane, qb = lane + 64;
-            double xa[8], xc[8], l[8][8], ri[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                xa[c] = sh.rowR[c][qa];
-                xc[c] = sh.rowR[c][qb];
-                ri[c] = sh.rinv[xb][c];
-#pragma unroll
-                for (int c2 = 0; c2 < c; ++c2) l[c][c2] = sh.dL[xb][c][c2];
-            }
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-#pragma unroll
-                for (int c2 = 0; c2 < c; ++c2) {
-                    xa[c] = fma(-l[c][c2], xa[c2], xa[c]);
-                    xc[c] = fma(-l[c][c2], xc[c2], xc[c]);
-                }
-                xa[c] = qa <= x0 + 7 ? xa[c] * ri[c] : 0.0;
-                xc[c] = qb <= x0 + 7 ? xc[c] * ri[c] : 0.0;
-            }
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                sh.rowXt[qa][kperm(c)] = xa[c];
-                sh.rowXt[qb][kperm(c)] = xc[c];
-                const int row = x0 + c;
-                const double oa = (row < nb && qa < nb) ? xa[c] : 0.0;
-                const double ob = (row < nb && qb < nb) ? xc[c] : 0.0;
-                D[row * NB + qa] = (float)oa;
-                D[row * NB + qb] = (float)ob;
-                D64[row * NB + qa] = oa;
-                D64[row * NB + qb] = ob;
-            }
-        }
+        if (it >= 1) x_rows(sh, it - 1, lane, nb, D, D64);
         __syncthreads();
     }
 }
@@ -296,7 +291,8 @@ __device__ __forceinline__ void load_op(const double (*P)[DP], int r, int lr, in
 // Waves 1..7: the tiles of A and R.  Every tile coordinate is a compile-time
 // constant, so accumulators are indexed statically.
 template <int W>
-__device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, int64_t ld, int nb, int lane) {
+__device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, int64_t ld, int nb, float* D,
+                                               double* D64, int lane) {
     const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
     ddoublex4 accA[DSLOTS], accX[DSLOTS];
     // all loads in flight at once: addresses are clamped into the block (no
@@ -419,6 +415,8 @@ __device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, i
                 }
             });
         }
+        // columns 64..127 of the rows of X of panel it - 1 (wave 0 does 0..63)
+        if (W == 1 && it >= 1) x_rows(sh, it - 1, 64 + lane, nb, D, D64);
         __syncthreads();
     }
 }
@@ -441,13 +439,13 @@ __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, i
     int bad = 0;
     switch (wave) {
         case 0: __syncthreads(); diag_factor_wave(sh, nb, D, D64, lane, bad); break;
-        case 1: diag_tile_wave<1>(sh, A, ld, nb, lane); break;
-        case 2: diag_tile_wave<2>(sh, A, ld, nb, lane); break;
-        case 3: diag_tile_wave<3>(sh, A, ld, nb, lane); break;
-        case 4: diag_tile_wave<4>(sh, A, ld, nb, lane); break;
-        case 5: diag_tile_wave<5>(sh, A, ld, nb, lane); break;
-        case 6: diag_tile_wave<6>(sh, A, ld, nb, lane); break;
-        default: diag_tile_wave<7>(sh, A, ld, nb, lane); break;
+        case 1: diag_tile_wave<1>(sh, A, ld, nb, D, D64, lane); break;
+        case 2: diag_tile_wave<2>(sh, A, ld, nb, D, D64, lane); break;
+        case 3: diag_tile_wave<3>(sh, A, ld, nb, D, D64, lane); break;
+        case 4: diag_tile_wave<4>(sh, A, ld, nb, D, D64, lane); break;
+        case 5: diag_tile_wave<5>(sh, A, ld, nb, D, D64, lane); break;
+        case 6: diag_tile_wave<6>(sh, A, ld, nb, D, D64, lane); break;
+        default: diag_tile_wave<7>(sh, A, ld, nb, D, D64, lane); break;
     }
     __syncthreads();
     // write L (its upper part is 0 in Lfin), row-coalesced
