@@ -138,7 +138,10 @@ int ic_scale_status(const void* scale, int scale_kind, int64_t n, int32_t* flag,
  * cmask 0 full / 1 lower (i >= j) / 2 upper (i <= j) output; krange 0 full /
  * 1 k >= max(tile i0, j0) / 2 k >= tile j0 / 3 k < tile i0 + 128 /
  * 4 k >= tile i0 (skips the zero half of a triangular operand).  beta == 0 never reads C.
- * Replaces the torch matmuls of converter/rounding.py:103 and
+ * alpha = -1, beta = 1 with op(A) = A subtracts one 128-wide chunk of K at a
+ * time, C <- (..((C - P_0) - P_1)..) - P_last: the roundings of consecutive
+ * rank-128 updates; otherwise the chunk sums are added and alpha, beta
+ * applied once.  * Replaces the torch matmuls of converter/rounding.py:103 and
  * converter/gptq_triton.py:178-180 (lazy trailing update) and the LAPACK
  * level-3 kernels behind torch.linalg.cholesky / cholesky_inverse. */
 int ic_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,

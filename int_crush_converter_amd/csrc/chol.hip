@@ -604,6 +604,7 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* din
                 GemmArgs g{m, w, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, H + k1 * ld + k1, ld, sH, 0, 1,
                            CMASK_LOWER, KR_FULL, batch, PT_GEMM_CHOL,
                            (double)batch * 2.0 * (dtri((double)w) + (double)(m - w) * w) * nb};
+                g.chunk_sub = 1;   // a sequence of rank-128 updates, like LAPACK's blocked potrf
                 int rc = gemm_f32(g, st);
                 if (rc) return rc;
             }
@@ -615,6 +616,7 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* din
             const int64_t k = s1 - s0;
             GemmArgs g{m, m, k, -1.0f, 1.0f, P, ld, sH, P, ld, sH, H + s1 * ld + s1, ld, sH, 0, 1, CMASK_LOWER,
                        KR_FULL, batch, PT_GEMM_CHOL, (double)batch * 2.0 * dtri((double)m) * k};
+            g.chunk_sub = 1;
             int rc = gemm_f32(g, st);
             if (rc) return rc;
         }

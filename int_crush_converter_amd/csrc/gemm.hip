@@ -340,7 +340,7 @@ __device__ __forceinline__ void main_loop(const GemmArgs& g, const float* A, con
 #undef ICQ_LOAD_STAGE
 }
 
-// CHUNK_SUB is launched only for alpha = -1, beta = 1: C is read before the
+// CHUNK_SUB (GemmArgs::chunk_sub; alpha = -1, beta = 1): C is read before the
 // K loop and every chunk is subtracted from it; CHUNK_SUM keeps the
 // epilogue C <- alpha * sum + beta * C.
 // Two work-groups per CU (one wave of each per SIMD) hide each other's
@@ -484,9 +484,11 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
     const dim3 gd((unsigned)grid, 1, (unsigned)g.batch);
     // whole tiles and whole K stages everywhere: the kernel without bounds checks
     const bool exact = aligned && g.M % T == 0 && g.N % T == 0 && g.K % BK == 0;
-    // updates C <- C - op(A) op(B) with op(A) = A subtract chunk by chunk;
-    // everything else sums the chunks
-    const bool sub = g.alpha == -1.0f && g.beta == 1.0f && !g.transA;
+    // exact rank-kc update sequences subtract chunk by chunk; everything else
+    // sums the chunks and applies alpha, beta once.  With one chunk (K <= kc)
+    // the two are the same: fl(-P + C) = fl(C - P), and the sum form keeps C
+    // out of the registers of the K loop.
+    const bool sub = g.chunk_sub != 0 && g.K > g.kc;
 #define ICQ_GEMM_LAUNCH(TA, TB, CH)                                                                                    \
     do {                                                                                                              \
         if (exact) hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, false, T, CH>), gd, dim3(256), 0, st, g, tiles, remap);  \
@@ -518,6 +520,8 @@ constexpr int64_t SHORT_K = 256, SHORT_K_TILE_LIMIT = 1024;
 int gemm_f32(const GemmArgs& g, hipStream_t st) {
     if (g.M <= 0 || g.N <= 0 || g.batch <= 0) return IC_OK;
     IC_REQUIRE(g.kc >= BK && g.kc <= 4096 && (g.kc & (g.kc - 1)) == 0, "gemm_f32: kc must be a power of two >= 32");
+    IC_REQUIRE(!g.chunk_sub || (g.alpha == -1.0f && g.beta == 1.0f && !g.transA),
+               "gemm_f32: chunk-by-chunk subtraction needs alpha = -1, beta = 1 and op(A) = A");
     // 16-byte loads need 16-byte aligned bases and leading dimensions
     const bool aligned = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
                          g.ldb % 4 == 0 && g.sA % 4 == 0 && g.sB % 4 == 0;
@@ -541,5 +545,8 @@ extern "C" int ic_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
     IC_REQUIRE(M >= 0 && N >= 0 && K >= 0, "ic_sgemm: negative size");
     IC_REQUIRE(cmask >= 0 && cmask <= 2 && krange >= 0 && krange <= 4, "ic_sgemm: bad mask");
     GemmArgs g{M, N, K, alpha, beta, A, lda, 0, B, ldb, 0, C, ldc, 0, transA, transB, cmask, krange, 1};
+    // C - A op(B) subtracts one 128-wide chunk of K at a time, the sequence
+    // of the reference's per-block updates
+    g.chunk_sub = (alpha == -1.0f && beta == 1.0f && !transA) ? 1 : 0;
     return gemm_f32(g, as_stream(stream));
 }

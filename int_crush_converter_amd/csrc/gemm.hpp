@@ -33,6 +33,10 @@ struct GemmArgs {
     int tag = PT_OTHER;        // profiler phase
     double algo_flops = 0.0;   // algorithmic flops of the launch (0: 2*M*N*K*batch)
     int kc = 128;              // accumulation chunk along K: a power of two, at least 32
+    // 1: C <- (..((C - P_0) - P_1)..) - P_last, chunk by chunk (alpha = -1,
+    // beta = 1, op(A) = A), the roundings of consecutive rank-kc updates; C
+    // is held in registers through the K loop.  0: C <- alpha * sum + beta * C.
+    int chunk_sub = 0;
 };
 
 // Launches on `st`; returns IC_OK or an error code.  Safe in place (C aliases

@@ -371,6 +371,7 @@ static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t 
         GemmArgs ga{rows, nc, k, -1.0f, 1.0f, E + e0, SB, rows * SB, Hinv + h0 * ldh + c0, ldh, hg,
                     W + c0, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
         ga.kc = kc;
+        ga.chunk_sub = 1;   // the reference's per-block updates, one after the other
         return gemm_f32(ga, st);
     };
     for (int64_t sb0 = 0; sb0 < gw; sb0 += SB) {
