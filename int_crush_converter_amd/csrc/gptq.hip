@@ -85,14 +85,13 @@ __device__ __forceinline__ float row_owner(float v, int o, int slot) {
 // is already quantised and never read again, so those updates are dead).
 //
 // EXACT = false: every division takes the fast correctly rounded quotient
-// without a per-column test.  The GPTQ code needs only the rounding of
-// y = x / s (+ zp), which the fast quotient gets right for every x: below
-// 2^-60 the quotient is far below the half-unit of the rounding, and from
-// 2^61 on (or inf / NaN) x * RN(1/s) has the sign, the magnitude beyond the
-// clamp and the NaN of x / s.  The normalised error (x - deq) / Hinv_jj must
-// be exact, so a residual outside [2^-60, 2^61) (other than 0 or NaN), or a
-// pivot or scale outside [2^-30, 2^31), sets `unsafe` and the caller redoes
-// the block with EXACT = true, the wave-uniform test of div_rn_wave.
+// without a per-column test.  It is exact for dividends in [2^-60, 2^61)
+// (or 0, and NaN passes through as NaN) and divisors in [2^-30, 2^31).  The
+// lane keeps the largest |x| and |x - deq| and the smallest nonzero
+// |x - deq| of its columns; a value outside that domain, or a pivot or scale
+// outside [2^-30, 2^31) (tested once per block / row), sets `unsafe` and the
+// caller redoes the block with EXACT = true, the wave-uniform test of
+// div_rn_wave.
 template <int MODE, int LPR, bool ZP, bool EXACT>
 __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[SW_NB / LPR],
                                            float (&ev)[SW_NB / LPR], const float* sc, const float* scr,
@@ -109,6 +108,10 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
     float hd = hjj[0], dvj = dinv[0];
     bool dkj = dok[0] != 0;
     bool bad = false;
+    // the fast division's domain, checked once after the block: the largest
+    // |dividend| (and |x|, which also covers +-Inf) and the smallest nonzero
+    // |dividend| of the lane's columns; NaN passes both paths alike
+    float amax = 0.0f, amin = INFINITY;
 #pragma unroll
     for (int r0 = 0; r0 < R; ++r0) {
         if (r0 * SW_HALF >= nb) break;
@@ -131,7 +134,6 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
                     y = div_rn_wave(x, s_row, s_rrow, srow_ok);
                 } else {
                     y = div_rn_fast(x, s_row, s_rrow);
-                    y = fabsf(x) < 0x1p61f ? y : x * s_rrow;
                 }
                 if (ZP) y = y + z_row;
                 q = clampf_med3(rhaz_trunc(y), qmin, qmax);
@@ -142,7 +144,8 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
                 } else {
                     e = div_rn_fast(num, hd, dvj);
                     const float an = fabsf(num);
-                    bad = bad || !dkj || (an < 0x1p-60f && an != 0.0f) || (an >= 0x1p61f);
+                    amax = fmaxf(amax, fmaxf(fabsf(x), an));
+                    amin = fminf(amin, an == 0.0f ? INFINITY : an);
                 }
                 e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
             } else {
@@ -180,6 +183,7 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
             dkj = dkn;
         }
     }
+    if (!EXACT && MODE == SWEEP_GPTQ) bad = bad || amax >= 0x1p61f || amin < 0x1p-60f;
     unsafe = unsafe || bad;
 }
 
@@ -213,6 +217,7 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 #pragma unroll
         for (int k = 0; k < PER; ++k) Hs[(i0 + k * STEP) * SW_NB + c] = tmp[k];
     }
+    int piv_ok = 1;
     if (t < SW_NB) {
         const int j = t;
         const float hd = j < nb ? H[(int64_t)j * a.ldh + j] : 1.0f;
@@ -220,9 +225,11 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
         if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
         hjj[j] = hd;
         dinv[j] = 1.0f / d;
-        dok[j] = div_b_ok(d) ? 1 : 0;
+        piv_ok = div_b_ok(d) ? 1 : 0;
+        dok[j] = piv_ok;
     }
-    __syncthreads();
+    // every pivot of the block inside the fast division's domain
+    const bool pivots_ok = __syncthreads_and(piv_ok) != 0;
     const int half = lane / SW_HALF, p = lane & (SW_HALF - 1);   // half: the wave's row slot
     const int64_t row0 = (int64_t)blockIdx.x * SW_ROWS + SW_RPW * wave;
     if (row0 >= a.rows) return;                          // all rows of the wave past the end
@@ -261,16 +268,16 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     float w0[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) w0[r] = w[r];
-    bool unsafe = MODE == SWEEP_GPTQ && !srow_ok;
+    bool unsafe = MODE == SWEEP_GPTQ && !(srow_ok && pivots_ok);
 #define ICQ_COLS(ZP, EXACT) \
     sweep_cols<MODE, LPR, ZP, EXACT>(w, qv, ev, sc, scr, Hs, hjj, dinv, dok, nb, p, half, s_row, s_rrow, srow_ok, \
                                      z_row, a.qmin, a.qmax, unsafe)
     if (has_zp) ICQ_COLS(true, false);
     else ICQ_COLS(false, false);
     // A value outside the fast division's exact domain (none in practice:
-    // a residual below 2^-60 or above 2^61, or a pivot / scale outside
-    // [2^-30, 2^31)): the wave runs the block again with the IEEE-exact
-    // division test on every column.
+    // a weight or residual of magnitude 2^61 or more, a nonzero residual
+    // below 2^-60, or a pivot / scale outside [2^-30, 2^31)): the wave runs
+    // the block again with the IEEE-exact division test on every column.
     if (__builtin_expect(__builtin_amdgcn_ballot_w64(unsafe) != 0, 0)) {
 #pragma unroll
         for (int r = 0; r < R; ++r) w[r] = w0[r];
