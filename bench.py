@@ -53,6 +53,12 @@ WORKLOADS = {
                                                        "layers": [("attn.qkv", 12288, 4096), ("attn.proj", 4096, 4096),
                                                                   ("mlp.up", 16384, 4096),
                                                                   ("mlp.down", 4096, 16384)]}),
+    # configs[4] end to end at its stated size: all 40 DiT blocks (16 GB of bf16
+    # weights in, 4 GB of packed codes out), file to file
+    "e2e_dit_gptq_int4_rot256_40blocks": ("e2e", 0, 0, {"blocks": 40, "samples": 4096,
+                                                        "layers": [("attn.qkv", 12288, 4096), ("attn.proj", 4096, 4096),
+                                                                   ("mlp.up", 16384, 4096),
+                                                                   ("mlp.down", 4096, 16384)]}),
     # one block of configs[4]'s 40-block DiT sweep: four layers, block-diagonal Hessians
     "gptq_int4_rot256_dit_block": ("dit", 0, 0, {"layers": [("qkv", 12288, 4096), ("proj", 4096, 4096),
                                                             ("mlp_up", 16384, 4096), ("mlp_down", 4096, 16384)],
@@ -91,6 +97,8 @@ def make_e2e_files(extra, seed=0):
             X = torch.randn(extra["samples"], in_f, generator=g, device=dev) * s
             hess[key] = block_hessian(X).cpu()
             del X
+        if (b + 1) % 4 == 0:
+            log(f"[bench] generated {b + 1} of {extra['blocks']} blocks")
     src = os.path.join(d, "model.safetensors")
     save_file(state, src)
     cal = os.path.join(d, "calibration.pt")
