@@ -182,8 +182,19 @@ struct DiagShared {
     double rinv[2][8];             // and their pivots' reciprocal square roots
     double rowR[8][NB];            // rows of R of the panel whose X rows are due
     double rowXt[NB][DP];          // final rows of X = L^-1 of that panel, transposed, at kperm
-    float Lfin[NB + 1][NB + 1];    // L as it is finalised, zero above the diagonal
+    float Lfin[NB + 1][NB + 1];    // L as it is finalised (on and below the diagonal)
 };
+
+// Barrier between the phases of the diagonal-block kernel: the waves hand
+// data to each other only through LDS, so each waits for its own LDS
+// operations and no more.  (__syncthreads() would also wait for the global
+// stores of the Dinv rows, which only later kernels read: a store round trip
+// per phase.)
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Rows 8 p .. 8 p + 7 of X = L^-1, column q: forward substitution with panel
 // p's 8x8 diagonal block of L from the published rows of R; the result goes
@@ -215,69 +226,79 @@ __device__ __forceinline__ void x_rows(DiagShared& sh, int p, int q, int nb, flo
     }
 }
 
+// Panel it (columns j0 .. j0 + 7, rows j0 .. 127) on wave 0, two rows per
+// lane: rows j0 + lane and (TWO: it < 8) j0 + 64 + lane.  From it = 8 on
+// the second set lies past the block and is skipped.  Pivots and the
+// panel's rows are broadcast by readlane.
+template <bool TWO>
+__device__ __forceinline__ void factor_panel(DiagShared& sh, int it, int lane, int& bad) {
+    const int j0 = it * 8, co = (it & 1) * 8, pb = it % PLBUF, db = it & 1;
+    // rows past the block read the zero row NB
+    const int ra = j0 + lane, rb = j0 + lane + 64;
+    const int rac = ra < NB ? ra : NB, rbc = rb < NB ? rb : NB;
+    double va[8], vb[8], rinvv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        va[c] = sh.pRaw[rac][co + c];
+        vb[c] = TWO ? sh.pRaw[rbc][co + c] : 0.0;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        double d = rdlane(va[c], c);
+        if (!(d > 0.0)) {
+            if (!bad) bad = j0 + c + 1;
+            d = 1.0;
+        }
+        // 1/sqrt(d) from the hardware estimate and two Newton steps
+        // (relative error far below fp32's), then sqrt(d) = d / sqrt(d)
+        double rinv = __builtin_amdgcn_rsq(d);
+        rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
+        rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
+        const double ljj = d * rinv;
+        va[c] = lane > c ? va[c] * rinv : (lane == c ? ljj : 0.0);
+        if (TWO) vb[c] = vb[c] * rinv;
+        rinvv[c] = rinv;
+#pragma unroll
+        for (int c2 = c + 1; c2 < 8; ++c2) {
+            const double lk = rdlane(va[c], c2);
+            va[c2] = fma(-va[c], lk, va[c2]);
+            if (TWO) vb[c2] = fma(-vb[c], lk, vb[c2]);
+        }
+    }
+    // the panel's L columns (fp64 MFMA operands), its 8x8 diagonal block and
+    // pivots for the rows of X, and the fp32 image of L (rows past the block
+    // go to the spare row NB).  Rows of pL above the panel keep older values:
+    // they only reach elements that are final already, which are never read
+    // again.
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        sh.pL[pb][rac][kperm(c)] = va[c];
+        sh.Lfin[rac][j0 + c] = (float)va[c];
+        if (TWO) {
+            sh.pL[pb][rbc][kperm(c)] = vb[c];
+            sh.Lfin[rbc][j0 + c] = (float)vb[c];
+        }
+    }
+    if (lane < 8) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sh.dL[db][lane][c] = va[c];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sh.rinv[db][c] = rinvv[c];
+    }
+}
+
 // Wave 0: phase U factors panel it, phase A finishes columns 0..63 of the
 // rows of X of panel it - 1.  Two barriers per iteration, matching
 // diag_tile_wave.
 __device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, float* D, double* D64, int lane, int& bad) {
     for (int it = 0; it <= 16; ++it) {
-        if (it < 16) {
-            const int j0 = it * 8, co = (it & 1) * 8, pb = it % PLBUF, db = it & 1;
-            // rows j0..127, two per lane; rows past the block read the zero row NB
-            const int ra = j0 + lane, rb = j0 + lane + 64;
-            const int rac = ra < NB ? ra : NB, rbc = rb < NB ? rb : NB;
-            double va[8], vb[8], rinvv[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                va[c] = sh.pRaw[rac][co + c];
-                vb[c] = sh.pRaw[rbc][co + c];
-            }
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                double d = rdlane(va[c], c);
-                if (!(d > 0.0)) {
-                    if (!bad) bad = j0 + c + 1;
-                    d = 1.0;
-                }
-                // 1/sqrt(d) from the hardware estimate and two Newton steps
-                // (relative error far below fp32's), then sqrt(d) = d / sqrt(d)
-                double rinv = __builtin_amdgcn_rsq(d);
-                rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
-                rinv = rinv * fma(-0.5 * d * rinv, rinv, 1.5);
-                const double ljj = d * rinv;
-                va[c] = lane > c ? va[c] * rinv : (lane == c ? ljj : 0.0);
-                vb[c] = vb[c] * rinv;
-                rinvv[c] = rinv;
-#pragma unroll
-                for (int c2 = c + 1; c2 < 8; ++c2) {
-                    const double lk = rdlane(va[c], c2);
-                    va[c2] = fma(-va[c], lk, va[c2]);
-                    vb[c2] = fma(-vb[c], lk, vb[c2]);
-                }
-            }
-            // the panel's L columns (fp64 MFMA operands), its 8x8 diagonal
-            // block and pivots for the rows of X, and the fp32 image of L
-            // (rows past the block go to the spare row NB).  Rows of pL above
-            // the panel keep older values: they only reach elements that are
-            // final already, which are never read again.
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                sh.pL[pb][rac][kperm(c)] = va[c];
-                sh.pL[pb][rbc][kperm(c)] = vb[c];
-                sh.Lfin[rac][j0 + c] = (float)va[c];
-                sh.Lfin[rbc][j0 + c] = (float)vb[c];
-            }
-            if (lane < 8) {
-#pragma unroll
-                for (int c = 0; c < 8; ++c) sh.dL[db][lane][c] = va[c];
-            }
-            if (lane == 0) {
-#pragma unroll
-                for (int c = 0; c < 8; ++c) sh.rinv[db][c] = rinvv[c];
-            }
-        }
-        __syncthreads();
+        if (it < 8) factor_panel<true>(sh, it, lane, bad);
+        else if (it < 16) factor_panel<false>(sh, it, lane, bad);
+        lds_barrier();
         if (it >= 1) x_rows(sh, it - 1, lane, nb, D, D64);
-        __syncthreads();
+        lds_barrier();
     }
 }
 
@@ -393,7 +414,7 @@ __device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, i
                 }
             });
         }
-        __syncthreads();
+        lds_barrier();
         // ---- phase A: panel it's update of the tile column holding panel it + 1, published
         if (it <= 14) {
             const int Jn = (it + 1) >> 1;
@@ -417,7 +438,7 @@ __device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, i
         }
         // columns 64..127 of the rows of X of panel it - 1 (wave 0 does 0..63)
         if (W == 1 && it >= 1) x_rows(sh, it - 1, 64 + lane, nb, D, D64);
-        __syncthreads();
+        lds_barrier();
     }
 }
 
@@ -432,9 +453,7 @@ __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, i
     const int lane = threadIdx.x & 63;
     // uniform in the wave; every wave runs 1 + 2 * 17 barriers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // Lfin starts at 0 (its upper part is never written) and so does the
-    // spare row of pRaw; the first barrier orders this
-    for (int idx = threadIdx.x; idx < (NB + 1) * (NB + 1); idx += DIAG_WAVES * 64) (&sh.Lfin[0][0])[idx] = 0.0f;
+    // the spare row of pRaw starts at 0; the first barrier orders this
     if (threadIdx.x < RP) sh.pRaw[NB][threadIdx.x] = 0.0;
     int bad = 0;
     switch (wave) {
@@ -448,10 +467,15 @@ __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, i
         default: diag_tile_wave<7>(sh, A, ld, nb, D, D64, lane); break;
     }
     __syncthreads();
-    // write L (its upper part is 0 in Lfin), row-coalesced
-    for (int idx = threadIdx.x; idx < NB * NB; idx += DIAG_WAVES * 64) {
-        const int i = idx >> 7, j = idx & (NB - 1);
-        if (i < nb && j < nb) A[(int64_t)i * ld + j] = sh.Lfin[i][j];
+    // write L, row-coalesced: Lfin holds every element on and below the
+    // diagonal (panel p writes rows 8 p .. 127 of its columns); the upper
+    // triangle is 0.  Eight LDS reads in flight per batch of stores.
+    constexpr int PER_THREAD = NB * NB / (DIAG_WAVES * 64);
+#pragma unroll 8
+    for (int u = 0; u < PER_THREAD; ++u) {
+        const int idx = (int)threadIdx.x + u * DIAG_WAVES * 64, i = idx >> 7, j = idx & (NB - 1);
+        const float v = j <= i ? sh.Lfin[i][j] : 0.0f;
+        if (i < nb && j < nb) A[(int64_t)i * ld + j] = v;
     }
     if (threadIdx.x == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
 }
