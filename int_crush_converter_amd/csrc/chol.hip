@@ -505,11 +505,12 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
     ddoublex4 acc[8];
 #pragma unroll
     for (int J = 0; J < 8; ++J) acc[J] = ddoublex4{0.0, 0.0, 0.0, 0.0};
-    for (int kc = 0; kc < nb; kc += PK) {
-        // all global loads of the chunk in flight before the LDS stores
-        constexpr int NA = PR * PK / 256, ND = NB * PK / 256;
-        float av[NA];
-        double dv[ND];
+    // the next chunk's global loads are issued before the current chunk's
+    // MFMAs, so that only the first chunk waits for memory
+    constexpr int NA = PR * PK / 256, ND = NB * PK / 256;
+    float av[NA];
+    double dv[ND];
+    auto load_chunk = [&](int kc) {
 #pragma unroll
         for (int u = 0; u < NA; ++u) {
             const int idx = t + u * 256, r = idx / PK, k = idx % PK;
@@ -521,6 +522,9 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
             const int idx = t + u * 256, j = idx / PK, k = idx % PK;
             dv[u] = D64[j * NB + kc + k];
         }
+    };
+    load_chunk(0);
+    for (int kc = 0; kc < nb; kc += PK) {
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < NA; ++u) {
@@ -533,6 +537,7 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
             Ds[(idx / PK) * PD + idx % PK] = dv[u];
         }
         __syncthreads();
+        if (kc + PK < nb) load_chunk(kc + PK);
 #pragma unroll
         for (int ks = 0; ks < PK / 4; ++ks) {
             const int k = ks * 4 + lk;
