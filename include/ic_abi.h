@@ -212,6 +212,17 @@ int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t groups, const f
                      const float* s32, const float* z32, int bits, int block, int8_t* Q,
                      void* workspace, void* stream);
 
+/* ic_gptq_quantize with the weights read from W_in, which is left unchanged,
+ * and the working residual kept in W [rows, groups*gw] (same layout), whose
+ * initial contents are never read: the first block is swept from W_in and the
+ * first lazy update of every other column reads W_in and writes W.  W == W_in
+ * is ic_gptq_quantize.  Same codes as ic_gptq_quantize on a copy of W_in.
+ * Replaces the working copy W_work = W.clone() of converter/gptq.py:320
+ * together with the sweep of ic_gptq_quantize, without copying the layer. */
+int ic_gptq_quantize_from(const float* W_in, float* W, int64_t rows, int64_t gw, int64_t groups,
+                          const float* Hinv, const float* s32, const float* z32, int bits, int block,
+                          int8_t* Q, void* workspace, void* stream);
+
 /* Allocation-free variant of ic_gptq_quantize.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

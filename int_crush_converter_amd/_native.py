@@ -52,6 +52,7 @@ _SIGS = {
     "ic_gptq_row_params": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ic_gptq_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "ic_gptq_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
+    "ic_gptq_quantize_from": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "ic_gptq_noalloc_scratch_bytes": (_i64, []),
     "ic_gptq_quantize_noalloc": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ic_ldlq_quantize": (_i32, [_vp, _i64, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),

@@ -378,7 +378,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // the C tile's addresses for the loads before the K loop come from a copy
     // of the base pointer the compiler cannot identify with C, so that they are
     // recomputed for the stores instead of being held through the loop
-    const float* Cl = C;
+    const float* Cl = g.Cin ? g.Cin + z * g.sC : C;
     if (CHUNK == CHUNK_SUB) asm volatile("" : "+s"(Cl));
 #pragma unroll
     for (int a = 0; a < F; ++a)
@@ -405,7 +405,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     for (int a = 0; a < F; ++a)
 #pragma unroll
         for (int b = 0; b < F; ++b) acc[a][b] = run[a][b];
-    const bool cvec = (((uintptr_t)C) % (4 * F) == 0) && (g.ldc % F == 0);
+    const float* Cr = g.Cin ? g.Cin + z * g.sC : C;   // the old C of the epilogue
+    const bool cvec = (((uintptr_t)C) % (4 * F) == 0) && (((uintptr_t)Cr) % (4 * F) == 0) && (g.ldc % F == 0);
     if (WIDE && full && cvec) {
         // the lane's F columns F m .. F m + F - 1 are adjacent: F-wide loads and stores
         const int64_t j0 = col_of(0);
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             for (int a = 0; a < F; ++a)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    cold[a][v] = *reinterpret_cast<const vecf*>(&C[row_of(a, v) * g.ldc + j0]);
+                    cold[a][v] = *reinterpret_cast<const vecf*>(&Cr[row_of(a, v) * g.ldc + j0]);
         }
 #pragma unroll
         for (int a = 0; a < F; ++a)
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int64_t i = row_of(a, v), j = col_of(b);
-                    cold[a][b][v] = (full || (i < g.M && j < g.N)) ? C[i * g.ldc + j] : 0.0f;
+                    cold[a][b][v] = (full || (i < g.M && j < g.N)) ? Cr[i * g.ldc + j] : 0.0f;
                 }
     }
 #pragma unroll

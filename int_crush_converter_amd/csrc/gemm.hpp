@@ -37,6 +37,9 @@ struct GemmArgs {
     // beta = 1, op(A) = A), the roundings of consecutive rank-kc updates; C
     // is held in registers through the K loop.  0: C <- alpha * sum + beta * C.
     int chunk_sub = 0;
+    // Where the old C is read (same pitch and batch stride as C); null: C.
+    // Lets a first update read pristine weights and write a separate buffer.
+    const float* Cin = nullptr;
 };
 
 // Launches on `st`; returns IC_OK or an error code.  Safe in place (C aliases

@@ -364,9 +364,14 @@ static int64_t super_cols(int64_t groups, int block) {
     return groups == 1 ? std::max<int64_t>(b, (SUPER / b) * b) : b;
 }
 
-static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t groups, const float* Hinv,
-                       int64_t ldh, int64_t hg, const float* s, int64_t lds, const float* zp, float qmin,
-                       float qmax, int B, int8_t* Q, int64_t ldq, float* E, int mode, hipStream_t st) {
+// Win: the weights as given; W: the working weights.  With Win != W, W's
+// initial contents are never read: the first block is swept from Win, and
+// the first update of every other column (the one after the first block,
+// and the trailing one after the first super-block) reads Win and writes W,
+// so no copy of the layer is made (W == Win: in place).
+static int layer_sweep(const float* Win, float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t groups,
+                       const float* Hinv, int64_t ldh, int64_t hg, const float* s, int64_t lds, const float* zp,
+                       float qmin, float qmax, int B, int8_t* Q, int64_t ldq, float* E, int mode, hipStream_t st) {
     IC_REQUIRE(B >= 1 && B <= SW_NB, "block size must be in [1, 128]");
     const int64_t SB = super_cols(groups, B);   // error matrix E: [groups][rows][SB]
     // W[:, c0 : c0+nc] -= E[:, e0 : e0+k] @ Hinv[h0 : h0+k, c0 : c0+nc]   (per group)
@@ -374,28 +379,30 @@ static int layer_sweep(float* W, int64_t ldw, int64_t rows, int64_t gw, int64_t 
     // every weight receives the per-block updates W -= E_b Hinv[b, :] of the
     // reference in its order (block sizes 32, 64, 128)
     const int kc = (B == 32 || B == 64 || B == 128) ? B : 128;
-    auto update = [&](int64_t e0, int64_t h0, int64_t k, int64_t c0, int64_t nc) {
+    auto update = [&](int64_t e0, int64_t h0, int64_t k, int64_t c0, int64_t nc, bool first) {
         GemmArgs ga{rows, nc, k, -1.0f, 1.0f, E + e0, SB, rows * SB, Hinv + h0 * ldh + c0, ldh, hg,
                     W + c0, ldw, gw, 0, 0, CMASK_FULL, KR_FULL, groups, PT_GEMM_TRAIL};
         ga.kc = kc;
         ga.chunk_sub = 1;   // the reference's per-block updates, one after the other
+        if (first && Win != W) ga.Cin = Win + c0;
         return gemm_f32(ga, st);
     };
     for (int64_t sb0 = 0; sb0 < gw; sb0 += SB) {
         const int64_t sbe = std::min<int64_t>(gw, sb0 + SB);
         for (int64_t b0 = sb0; b0 < sbe; b0 += B) {
             const int nb = (int)std::min<int64_t>(B, sbe - b0);
-            SweepArgs a{W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh, hg, s, lds, zp, qmin, qmax,
-                        Q, ldq, E + (b0 - sb0), SB, rows * SB, mode};
+            // the sweep reads W (never writes it); the first block is read from Win
+            SweepArgs a{b0 == 0 ? const_cast<float*>(Win) : W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh,
+                        hg, s, lds, zp, qmin, qmax, Q, ldq, E + (b0 - sb0), SB, rows * SB, mode};
             int rc = launch_sweep(a, (int)groups, st);
             if (rc) return rc;
             if (b0 + nb < sbe) {
-                rc = update(b0 - sb0, b0, nb, b0 + nb, sbe - b0 - nb);
+                rc = update(b0 - sb0, b0, nb, b0 + nb, sbe - b0 - nb, b0 == 0);
                 if (rc) return rc;
             }
         }
         if (sbe < gw) {
-            int rc = update(0, sb0, sbe - sb0, sbe, gw - sbe);
+            int rc = update(0, sb0, sbe - sb0, sbe, gw - sbe, sb0 == 0);
             if (rc) return rc;
         }
     }
@@ -432,7 +439,20 @@ extern "C" int ic_gptq_quantize(float* W, int64_t rows, int64_t gw, int64_t grou
     if (rows == 0 || gw == 0) return IC_OK;
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
     const int64_t N = gw * groups;
-    return layer_sweep(W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
+    return layer_sweep(W, W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
+                       reinterpret_cast<float*>(workspace), SWEEP_GPTQ, as_stream(stream));
+}
+
+extern "C" int ic_gptq_quantize_from(const float* W_in, float* W, int64_t rows, int64_t gw, int64_t groups,
+                                     const float* Hinv, const float* s32, const float* z32, int bits, int block,
+                                     int8_t* Q, void* workspace, void* stream) {
+    IC_REQUIRE(W_in && W && Hinv && s32 && Q && workspace, "ic_gptq_quantize_from: null pointer");
+    IC_REQUIRE(bits == 4 || bits == 8, "ic_gptq_quantize_from: bits must be 4 or 8");
+    IC_REQUIRE(groups >= 1 && gw >= 0 && rows >= 0, "ic_gptq_quantize_from: bad size");
+    if (rows == 0 || gw == 0) return IC_OK;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    const int64_t N = gw * groups;
+    return layer_sweep(W_in, W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
                        reinterpret_cast<float*>(workspace), SWEEP_GPTQ, as_stream(stream));
 }
 
@@ -486,7 +506,7 @@ extern "C" int ic_gptq_quantize_noalloc(float* W, int64_t rows, int64_t gw, int6
     ProfSuppress no_events;   // a recording profiler scope would create HIP events
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
     const int64_t N = gw * groups;
-    return layer_sweep(W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
+    return layer_sweep(W, W, N, rows, gw, groups, Hinv, gw, gw * gw, s32, 0, z32, qmin, qmax, block, Q, N,
                        reinterpret_cast<float*>(ws), SWEEP_GPTQ, as_stream(stream));
 }
 
@@ -496,6 +516,6 @@ extern "C" int ic_ldlq_quantize(float* W, int64_t rows, int64_t N, const float* 
     IC_REQUIRE(bits == 4 || bits == 8, "ic_ldlq_quantize: bits must be 4 or 8");
     if (rows == 0 || N == 0) return IC_OK;
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
-    return layer_sweep(W, N, rows, N, 1, Hinv, N, N * N, scales, N, nullptr, qmin, qmax, block, Q, N,
+    return layer_sweep(W, W, N, rows, N, 1, Hinv, N, N * N, scales, N, nullptr, qmin, qmax, block, Q, N,
                        reinterpret_cast<float*>(workspace), SWEEP_LDLQ, as_stream(stream));
 }

@@ -78,16 +78,20 @@ def quant_error(W: torch.Tensor, Q: torch.Tensor, scale: torch.Tensor, zp8: torc
 
 def sweep(W_work: torch.Tensor, Hinv: torch.Tensor, s32: torch.Tensor, z32: torch.Tensor | None,
           int_bits: int, block_size: int, groups: int = 1) -> torch.Tensor:
-    """Run the GPTQ sweep in place on W_work [M, groups*gw]; Hinv [gw, gw] or
+    """Run the GPTQ sweep on W_work [M, groups*gw] (contiguous fp32, left
+    unchanged: the working residual lives in a buffer of the same size that
+    the library fills without copying W_work); Hinv [gw, gw] or
     [groups, gw, gw].  Returns int8 codes [M, groups*gw]."""
     M, N = W_work.shape
     gw = N // groups
     Q = torch.empty(M, N, dtype=torch.int8, device=W_work.device)
+    R = torch.empty_like(W_work)
     blk = min(int(block_size), SWEEP_MAX_BLOCK)
     ws = nat.workspace(nat.lib().ic_gptq_workspace_bytes(M, groups, blk), W_work.device)
-    nat.check(nat.lib().ic_gptq_quantize(W_work.data_ptr(), M, gw, groups, Hinv.data_ptr(), s32.data_ptr(),
-                                         nat.ptr(z32), int_bits, blk, Q.data_ptr(), ws.data_ptr(), nat.stream()),
-              "ic_gptq_quantize")
+    nat.check(nat.lib().ic_gptq_quantize_from(W_work.data_ptr(), R.data_ptr(), M, gw, groups, Hinv.data_ptr(),
+                                              s32.data_ptr(), nat.ptr(z32), int_bits, blk, Q.data_ptr(),
+                                              ws.data_ptr(), nat.stream()),
+              "ic_gptq_quantize_from")
     return Q
 
 
@@ -107,7 +111,7 @@ def sweep_block_diagonal(W_work: torch.Tensor, Hg: torch.Tensor, damping: float,
                          fallbacks: list[str], s32, z32, int_bits: int, block_size: int) -> torch.Tensor:
     """GPTQ over a block-diagonal 3-D Hessian: the whole blocks inverted as a
     batch and swept as independent column groups of one launch, the partial
-    last block on its own.  W_work is scratch (its columns may be changed);
+    last block on its own.  W_work is left unchanged;
     returns int8 codes."""
     M, N = W_work.shape
     nblk, bs, _ = Hg.shape
@@ -153,7 +157,7 @@ def gptq_quantize_layer(
         from .piso import piso_row_params
         params = piso_row_params(Wg, piso_scales, piso_zero_points, int_bits, asymmetric)
     s32, z32, s16, z8 = params if params is not None else row_params(Wg, int_bits, asymmetric)
-    W_work = Wg.clone()
+    W_work = Wg.contiguous()   # the sweep leaves it unchanged
     Hg = hessian if isinstance(hessian, dict) else nat.to_gpu(hessian)
 
     if is_dlr(Hg):

@@ -88,7 +88,7 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
                 raise ValueError(f"DLR Hessian dim {D.shape[0]} != in_features {N}")
             s32, z32, s16, z8 = _gptq_params(W_work, int_bits, asymmetric, piso)
             Hinv = woodbury_inverse(D, U, damping, W_work.device, upper_only=True)
-            Q = sweep(W_work.clone(), Hinv, s32, z32, int_bits, block_size)
+            Q = sweep(W_work, Hinv, s32, z32, int_bits, block_size)
             return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
         H = dlr_to_dense(H["D"], H["U"])
     Hsrc = nat.to_gpu(H).float()
@@ -104,14 +104,14 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
 
     inv_kw = dict(inplace=True, restore=restore, upper_only=True) if own else dict(upper_only=True)
     s32, z32, s16, z8 = _gptq_params(W_work, int_bits, asymmetric, piso)
-    Ww = W_work.clone()
+    # the sweep reads W_work and keeps its working residual elsewhere
     if Hg.dim() == 3:
-        Q = sweep_block_diagonal(Ww, Hg, damping, hessian_method, fallbacks, s32, z32, int_bits, block_size)
+        Q = sweep_block_diagonal(W_work, Hg, damping, hessian_method, fallbacks, s32, z32, int_bits, block_size)
     else:
         if tuple(Hg.shape) != (N, N):
             raise ValueError(f"Hessian shape {tuple(Hg.shape)} != ({N}, {N})")
         Hinv = inverse_batch(Hg, damping, hessian_method, fallbacks, **inv_kw)
-        Q = sweep(Ww, Hinv, s32, z32, int_bits, block_size)
+        Q = sweep(W_work, Hinv, s32, z32, int_bits, block_size)
     return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
 
 

@@ -454,3 +454,42 @@ def test_sweep_many_rows_multi_block_close(gpu_dev):
     s32, z32, _, _ = row_params(Wg, 4, False)
     Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, 128).cpu()
     assert (Qg == Q).float().mean().item() >= 0.999
+
+
+@pytest.mark.parametrize("M,gw,groups,block", [(300, 100, 1, 32), (257, 2500, 1, 128), (130, 256, 3, 128),
+                                               (64, 1100, 1, 64), (70, 128, 1, 128)])
+def test_sweep_from_leaves_input_and_matches_in_place(gpu_dev, M, gw, groups, block):
+    """ic_gptq_quantize_from reads the weights without changing them and never
+    reads the residual buffer's initial contents (filled with NaN here): its
+    codes equal ic_gptq_quantize's on a copy, bit for bit, and so does every
+    residual column it writes (all but each group's first block, which is
+    swept straight from the input).  One block, one super-block, several
+    super-blocks with a partial last one, 3-D groups, block sizes 32 / 64 / 128."""
+    from int_crush_converter_amd import _native as nat
+    L = nat.lib()
+    g = torch.Generator().manual_seed(M + gw + groups + block)
+    N = gw * groups
+    W = (torch.randn(M, N, generator=g) * 0.02).to(gpu_dev)
+    Hs = [ref.prepare_hinv(lognormal_hessian(gw, 2 * gw, 7 + k), 0.01) for k in range(groups)]
+    Hinv = (torch.stack(Hs) if groups > 1 else Hs[0]).to(gpu_dev).contiguous()
+    s = (W.abs().amax(dim=1) / 7.0).clamp(min=1e-5).contiguous()
+    z = torch.zeros(M, device=gpu_dev)
+    ws = nat.workspace(L.ic_gptq_workspace_bytes(M, groups, block), W.device)
+    Wk = W.clone()
+    Q0 = torch.full((M, N), 99, dtype=torch.int8, device=gpu_dev)
+    nat.check(L.ic_gptq_quantize(Wk.data_ptr(), M, gw, groups, Hinv.data_ptr(), s.data_ptr(), z.data_ptr(), 4,
+                                 block, Q0.data_ptr(), ws.data_ptr(), nat.stream()), "ic_gptq_quantize")
+    W_in = W.clone()
+    R = torch.full((M, N), float("nan"), device=gpu_dev)
+    Q1 = torch.full((M, N), 99, dtype=torch.int8, device=gpu_dev)
+    nat.check(L.ic_gptq_quantize_from(W_in.data_ptr(), R.data_ptr(), M, gw, groups, Hinv.data_ptr(), s.data_ptr(),
+                                      z.data_ptr(), 4, block, Q1.data_ptr(), ws.data_ptr(), nat.stream()),
+              "ic_gptq_quantize_from")
+    torch.cuda.synchronize()
+    assert torch.equal(Q1, Q0)
+    assert torch.equal(W_in, W)
+    first = torch.zeros(N, dtype=torch.bool, device=gpu_dev)
+    for k in range(groups):
+        first[k * gw: k * gw + min(block, gw)] = True
+    assert bool(R[:, first].isnan().all())
+    assert torch.equal(R[:, ~first], Wk[:, ~first])
