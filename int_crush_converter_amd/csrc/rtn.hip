@@ -200,28 +200,34 @@ __global__ __launch_bounds__(256) void rtn_scales_kernel(const float* __restrict
 
 // fp32 squared error of one clip candidate for one value (the elementwise
 // steps of the reference's mse before its sum).
-template <bool FAST>
-__device__ __forceinline__ float cand_sq(float w, const Cand& c, float rs, int asym, float qmin, float qmax) {
+// FAST: the caller checked that the row holds no NaN and every value and the
+// scale lie in the fast division's domain, so y is finite and the clamp
+// needs no NaN test.
+template <bool FAST, bool ASYM>
+__device__ __forceinline__ float cand_sq(float w, const Cand& c, float rs, float qmin, float qmax) {
     float y = FAST ? div_rn_fast(w, c.s, rs) : w / c.s;
-    if (asym) y = y + c.z;
-    const float q = clampf_med3(rhte(y), qmin, qmax);
-    const float d = asym ? (q - c.z) * c.s : q * c.s;
+    if (ASYM) y = y + c.z;
+    const float q = FAST ? __builtin_amdgcn_fmed3f(rhte(y), qmin, qmax) : clampf_med3(rhte(y), qmin, qmax);
+    const float d = ASYM ? (q - c.z) * c.s : q * c.s;
     const float e = w - d;
     return e * e;
 }
 
-// Clip search with the reference's fp32 MSE, one work-group (256 threads)
-// per row: the row is staged in LDS (cols <= CLIP_LDS_COLS), its min / max /
-// absmax reduced, then thread (candidate k, sequence q) runs the cascade of
-// sequence q (values 32 m + q) of candidate k's squared errors, eight
+// Clip search with the reference's fp32 MSE, one work-group per row: the row
+// is staged in LDS (cols <= CLIP_LDS_COLS), its min / max / absmax reduced,
+// then thread (candidate k, sequence q) runs the cascade of sequence q
+// (values 32 m + q) of candidate k's squared errors, blockDim / 32
 // candidates per pass, and one thread per candidate finishes torch's inner
 // sum (leftover vectors, merge, leftover scalars, lanes) and divides by the
-// row length.  The first minimum (strict <, a NaN never wins) is kept.
+// row length.  The first minimum (strict <, a NaN never wins) is kept.  The
+// work-group has 32 threads per candidate rounded up to whole waves (at most
+// 256), so that e.g. 5 candidates take 3 waves, not 4 with 3/8 idle.
 constexpr int64_t CLIP_LDS_COLS = 15872;   // the row plus the static arrays within 64 KB of LDS
-constexpr int CLIP_PASS = 256 / SUM_SEQ;   // candidates per pass
+constexpr int CLIP_PASS = 256 / SUM_SEQ;   // candidates per pass at most
 
+template <bool ASYM>
 __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
-                                                       int64_t ld, int bits, int asym, int n_ratios, Ratios rt,
+                                                       int64_t ld, int bits, int n_ratios, Ratios rt,
                                                        uint16_t* __restrict__ scale16, int8_t* __restrict__ zp) {
     extern __shared__ float xs[];                   // the row, cols floats
     __shared__ float part[CLIP_PASS][SUM_SEQ];
@@ -229,12 +235,13 @@ __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__
     __shared__ float red[4][3];
     __shared__ int red_ok[4];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int nt = blockDim.x, nwv = nt >> 6, pass = nt / SUM_SEQ;
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* x = W + r * ld;
         float mn = INFINITY, mx = -INFINITY, am = 0.0f;
         bool ok = true;
-        for (int64_t j = t; j < cols; j += 256) {
+        for (int64_t j = t; j < cols; j += nt) {
             const float v = x[j];
             xs[j] = v;
             mn = nmin(mn, v);
@@ -253,7 +260,7 @@ __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__
         __syncthreads();
         RowStats st{red[0][0], red[0][1], red[0][2]};
         bool row_ok = red_ok[0] != 0;
-        for (int w = 1; w < 4; ++w) {
+        for (int w = 1; w < nwv; ++w) {
             st.mn = nmin(st.mn, red[w][0]);
             st.mx = nmax(st.mx, red[w][1]);
             st.amax = nmax(st.amax, red[w][2]);
@@ -261,22 +268,22 @@ __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__
         }
         const int64_t n4 = cols / SUM_VEC / 4;
         const int lp = cascade_lp(n4);
-        for (int k0 = 0; k0 < n_ratios; k0 += CLIP_PASS) {
+        for (int k0 = 0; k0 < n_ratios; k0 += pass) {
             const int kk = t / SUM_SEQ, q = t % SUM_SEQ, k = k0 + kk;
             if (k < n_ratios && cols >= SUM_VEC) {
-                const Cand c = rtn_candidate(st, bits, asym, true, rt.v[k]);
+                const Cand c = rtn_candidate(st, bits, ASYM, true, rt.v[k]);
                 const float rs = 1.0f / c.s;
                 part[kk][q] = row_ok && div_b_ok(c.s)
-                    ? cascade_seq([&](int64_t m) { return cand_sq<true>(xs[m * SUM_SEQ + q], c, rs, asym, qmin, qmax); },
+                    ? cascade_seq([&](int64_t m) { return cand_sq<true, ASYM>(xs[m * SUM_SEQ + q], c, rs, qmin, qmax); },
                                   n4, lp)
-                    : cascade_seq([&](int64_t m) { return cand_sq<false>(xs[m * SUM_SEQ + q], c, rs, asym, qmin, qmax); },
+                    : cascade_seq([&](int64_t m) { return cand_sq<false, ASYM>(xs[m * SUM_SEQ + q], c, rs, qmin, qmax); },
                                   n4, lp);
             }
             __syncthreads();
-            if (t < CLIP_PASS && k0 + t < n_ratios) {
-                const Cand c = rtn_candidate(st, bits, asym, true, rt.v[k0 + t]);
+            if (t < pass && k0 + t < n_ratios) {
+                const Cand c = rtn_candidate(st, bits, ASYM, true, rt.v[k0 + t]);
                 const float rs = 1.0f / c.s;
-                auto sq = [&](int64_t i) { return cand_sq<false>(xs[i], c, rs, asym, qmin, qmax); };
+                auto sq = [&](int64_t i) { return cand_sq<false, ASYM>(xs[i], c, rs, qmin, qmax); };
                 const float sum = cols >= SUM_VEC ? inner_sum_finish(part[t], sq, cols) : inner_sum_short(sq, cols);
                 mses[k0 + t] = sum / (float)cols;
             }
@@ -287,9 +294,9 @@ __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__
             float bm = mses[0];
             for (int k = 1; k < n_ratios; ++k)
                 if (mses[k] < bm) { bm = mses[k]; best = k; }
-            const Cand c = rtn_candidate(st, bits, asym, true, rt.v[best]);
+            const Cand c = rtn_candidate(st, bits, ASYM, true, rt.v[best]);
             scale16[r] = f32_to_f16_bits(c.s);
-            if (asym && zp) zp[r] = (int8_t)(int)c.z;
+            if (ASYM && zp) zp[r] = (int8_t)(int)c.z;
         }
         __syncthreads();   // xs and part are reused by the next row
     }
@@ -607,10 +614,17 @@ extern "C" int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t
     Ratios rt;
     for (int i = 0; i < MAX_RATIOS; ++i) rt.v[i] = i < n_ratios ? ratios[i] : 1.0f;
     ProfScope prof_scope(as_stream(stream), PT_RTN_SCALES, 0.0, (double)rows * cols * 4.0 + rows * 3.0);
-    if (n_ratios > 0 && cols <= CLIP_LDS_COLS)
-        hipLaunchKernelGGL(rtn_clip_kernel, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(256),
-                           cols * sizeof(float), as_stream(stream), W, rows, cols, ld, bits, asym, n_ratios, rt,
-                           scale16, zp);
+    if (n_ratios > 0 && cols <= CLIP_LDS_COLS) {
+        const int threads = (int)std::min<int64_t>(256, cdiv((int64_t)n_ratios * SUM_SEQ, 64) * 64);
+        if (asym)
+            hipLaunchKernelGGL(rtn_clip_kernel<true>, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(threads),
+                               cols * sizeof(float), as_stream(stream), W, rows, cols, ld, bits, n_ratios, rt,
+                               scale16, zp);
+        else
+            hipLaunchKernelGGL(rtn_clip_kernel<false>, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(threads),
+                               cols * sizeof(float), as_stream(stream), W, rows, cols, ld, bits, n_ratios, rt,
+                               scale16, zp);
+    }
     else if (n_ratios > 0 && cols <= 64 * 64)
         hipLaunchKernelGGL(rtn_scales_kernel<64>, dim3(rows_grid(rows, 4)), dim3(256), 0, as_stream(stream), W, rows,
                            cols, ld, bits, asym, n_ratios, rt, scale16, zp);

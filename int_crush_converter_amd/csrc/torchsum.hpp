@@ -33,6 +33,8 @@ __device__ float cascade_seq(Get get, int64_t L, int lp) {
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     int64_t i = 0;
     while (i + S <= L) {
+        // S >= 16: the values of a group are fetched four at a time
+#pragma unroll 4
         for (int64_t j = 0; j < S; ++j, ++i) a0 = a0 + get(i);
         a1 = a1 + a0;
         a0 = 0.0f;
