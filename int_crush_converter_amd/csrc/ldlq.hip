@@ -338,15 +338,46 @@ constexpr int PROXY_PARTS = 1024;
 // later super-blocks come from the updated err.  Same sums as one GEMM per
 // block over all of err, in another fp32 order.
 constexpr int64_t GSB = 512;
+// The cross-term GEMM of a super-block has few 128-tiles (rows / 128 x 4)
+// and a long K (= cols): it runs as GSPLIT products over K / GSPLIT each
+// (GSPLIT times the tiles, two per CU), summed in order by split_sum_kernel.
+constexpr int GSPLIT = 4;
 
+// C[r][c] = ((P_0 + P_1) + P_2) + P_3 for the GSPLIT partial products
+// (pitch GSB, stride rows * GSB).
+__global__ void split_sum_kernel(const float* __restrict__ P, int64_t rows, int64_t sw, float* __restrict__ C) {
+    const int64_t total = rows * sw, stride = rows * GSB;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / sw, c = i - r * sw, o = r * GSB + c;
+        float v = P[o];
+#pragma unroll
+        for (int k = 1; k < GSPLIT; ++k) v = v + P[k * stride + o];
+        C[o] = v;
+    }
+}
+
+// part: scratch for the split products (GSPLIT * rows * GSB floats), or null.
 static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* C,
-                       float* D, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
+                       float* D, float* part, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
     for (int64_t s0 = 0; s0 < cols; s0 += GSB) {
         const int64_t sw = std::min<int64_t>(GSB, cols - s0);
-        GemmArgs g{rows, sw, cols, 1.0f, 0.0f, err, cols, 0, Hc + s0 * cols, cols, 0, C, GSB, 0, 0, 1, CMASK_FULL,
-                   KR_FULL, 1, PT_GEMM_GREEDY};
-        int rc = gemm_f32(g, st);
-        if (rc) return rc;
+        const int64_t ks = cols / GSPLIT;
+        const bool split = part && cols % (GSPLIT * 128) == 0 && cdiv(rows, 128) * cdiv(sw, 128) < 256 &&
+                           ks >= 1024;
+        int rc;
+        if (split) {
+            GemmArgs g{rows, sw, ks, 1.0f, 0.0f, err, cols, ks, Hc + s0 * cols, cols, ks, part, GSB, rows * GSB,
+                       0, 1, CMASK_FULL, KR_FULL, GSPLIT, PT_GEMM_GREEDY};
+            g.algo_flops = 2.0 * rows * sw * cols;
+            if ((rc = gemm_f32(g, st))) return rc;
+            hipLaunchKernelGGL(split_sum_kernel, dim3(egrid(rows * sw)), dim3(256), 0, st, part, rows, sw, C);
+            IC_CHECK_LAUNCH();
+        } else {
+            GemmArgs g{rows, sw, cols, 1.0f, 0.0f, err, cols, 0, Hc + s0 * cols, cols, 0, C, GSB, 0, 0, 1,
+                       CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
+            if ((rc = gemm_f32(g, st))) return rc;
+        }
         for (int64_t j0 = s0; j0 < s0 + sw; j0 += GB) {
             const int nb = (int)std::min<int64_t>(GB, s0 + sw - j0);
             {
@@ -427,7 +458,7 @@ extern "C" int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64
 }
 
 extern "C" int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols) {
-    return (2 * rows * cols + rows * (GSB + GB)) * (int64_t)sizeof(float) + 256;
+    return (2 * rows * cols + rows * (GSB + GB) + GSPLIT * rows * GSB) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
@@ -442,8 +473,9 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
     float* cross = Qf + rows * cols;
     hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
     IC_CHECK_LAUNCH();
+    float* part = cross + rows * (GSB + GB);
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, cross + rows * GSB, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, cross + rows * GSB, part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
@@ -452,8 +484,8 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
 }
 
 extern "C" int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k) {
-    return (3 * rows * cols + rows * (GSB + GB) + cols * cols + cols * std::max<int64_t>(k, 1) + cols) *
-               (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
+    return (3 * rows * cols + rows * (GSB + GB) + cols * cols + cols * std::max<int64_t>(k, 1) + cols +
+            GSPLIT * rows * GSB) * (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
 }
 
 extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float* H, const float* U,
@@ -474,7 +506,9 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     float* Hk = D + rows * GB;
     float* US = Hk + cols * cols;
     float* hd = US + cols * std::max<int64_t>(k, 1);
-    double* part = reinterpret_cast<double*>((reinterpret_cast<uintptr_t>(hd + cols) + 255) & ~(uintptr_t)255);
+    float* split_part = hd + cols;
+    double* part = reinterpret_cast<double*>(
+        (reinterpret_cast<uintptr_t>(split_part + GSPLIT * rows * GSB) + 255) & ~(uintptr_t)255);
     // Hk = U_k diag(s_k) U_k^T
     if (k == 0) {
         IC_CHECK_HIP(hipMemsetAsync(Hk, 0, cols * cols * sizeof(float), st));
@@ -493,7 +527,7 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     double prev = 0.0;
     int done = 0;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, D, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, D, split_part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
         done = p + 1;
         if (p + 1 == passes) break;   // a stall test after the last pass changes nothing
