@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void damp_kernel(float* H, int64_t n, int64_t 
 
 // Factor the diagonal block [k0, k0+nb) of matrix blockIdx.x in place (lower,
 // upper part of the block set to 0) and write Dinv = L_kk^-1 (lower, upper 0)
-// to dinv (fp32, pitch NB) and dinv64 (fp64, pitch NB).  info[b] gets the
+// to dinv64 (fp64, pitch NB).  info[b] gets the
 // 1-based column of the first non-positive pivot (LAPACK convention) if it
 // is still 0.  A partial block (nb < 128) is padded with the identity.
 //
@@ -198,9 +198,9 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Rows 8 p .. 8 p + 7 of X = L^-1, column q: forward substitution with panel
 // p's 8x8 diagonal block of L from the published rows of R; the result goes
-// to rowXt (for the R updates) and to Dinv / Dinv64 (whole rows: coalesced
-// over the lanes).  Phase A splits the columns over waves 0 and 1.
-__device__ __forceinline__ void x_rows(DiagShared& sh, int p, int q, int nb, float* D, double* D64) {
+// to rowXt (for the R updates) and to Dinv64 (whole rows: coalesced over the
+// lanes).  Phase A splits the columns over waves 0 and 1.
+__device__ __forceinline__ void x_rows(DiagShared& sh, int p, int q, int nb, double* D64) {
     const int x0 = p * 8, xb = p & 1;
     double x[8], l[8][8], ri[8];
 #pragma unroll
@@ -220,9 +220,7 @@ __device__ __forceinline__ void x_rows(DiagShared& sh, int p, int q, int nb, flo
     for (int c = 0; c < 8; ++c) {
         sh.rowXt[q][kperm(c)] = x[c];
         const int row = x0 + c;
-        const double o = (row < nb && q < nb) ? x[c] : 0.0;
-        D[row * NB + q] = (float)o;
-        D64[row * NB + q] = o;
+        D64[row * NB + q] = (row < nb && q < nb) ? x[c] : 0.0;
     }
 }
 
@@ -292,12 +290,12 @@ __device__ __forceinline__ void factor_panel(DiagShared& sh, int it, int lane, i
 // Wave 0: phase U factors panel it, phase A finishes columns 0..63 of the
 // rows of X of panel it - 1.  Two barriers per iteration, matching
 // diag_tile_wave.
-__device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, float* D, double* D64, int lane, int& bad) {
+__device__ __forceinline__ void diag_factor_wave(DiagShared& sh, int nb, double* D64, int lane, int& bad) {
     for (int it = 0; it <= 16; ++it) {
         if (it < 8) factor_panel<true>(sh, it, lane, bad);
         else if (it < 16) factor_panel<false>(sh, it, lane, bad);
         lds_barrier();
-        if (it >= 1) x_rows(sh, it - 1, lane, nb, D, D64);
+        if (it >= 1) x_rows(sh, it - 1, lane, nb, D64);
         lds_barrier();
     }
 }
@@ -312,8 +310,8 @@ __device__ __forceinline__ void load_op(const double (*P)[DP], int r, int lr, in
 // Waves 1..7: the tiles of A and R.  Every tile coordinate is a compile-time
 // constant, so accumulators are indexed statically.
 template <int W>
-__device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, int64_t ld, int nb, float* D,
-                                               double* D64, int lane) {
+__device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, int64_t ld, int nb, double* D64,
+                                               int lane) {
     const int lr = lane >> 4, lj = lane & 15;   // accumulator v holds row lr + 4 v, column lj
     ddoublex4 accA[DSLOTS], accX[DSLOTS];
     // all loads in flight at once: addresses are clamped into the block (no
@@ -437,18 +435,17 @@ __device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, i
             });
         }
         // columns 64..127 of the rows of X of panel it - 1 (wave 0 does 0..63)
-        if (W == 1 && it >= 1) x_rows(sh, it - 1, 64 + lane, nb, D, D64);
+        if (W == 1 && it >= 1) x_rows(sh, it - 1, 64 + lane, nb, D64);
         lds_barrier();
     }
 }
 
 __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0,
-                                                                    int nb, float* dinv, double* dinv64,
-                                                                    int64_t dstride, int* info) {
+                                                                    int nb, double* dinv64, int64_t dstride,
+                                                                    int* info) {
     __shared__ __attribute__((aligned(16))) DiagShared sh;
     const int b = blockIdx.x;
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
-    float* D = dinv + (int64_t)b * dstride;
     double* D64 = dinv64 + (int64_t)b * dstride;
     const int lane = threadIdx.x & 63;
     // uniform in the wave; every wave runs 1 + 2 * 17 barriers
@@ -457,14 +454,14 @@ __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, i
     if (threadIdx.x < RP) sh.pRaw[NB][threadIdx.x] = 0.0;
     int bad = 0;
     switch (wave) {
-        case 0: __syncthreads(); diag_factor_wave(sh, nb, D, D64, lane, bad); break;
-        case 1: diag_tile_wave<1>(sh, A, ld, nb, D, D64, lane); break;
-        case 2: diag_tile_wave<2>(sh, A, ld, nb, D, D64, lane); break;
-        case 3: diag_tile_wave<3>(sh, A, ld, nb, D, D64, lane); break;
-        case 4: diag_tile_wave<4>(sh, A, ld, nb, D, D64, lane); break;
-        case 5: diag_tile_wave<5>(sh, A, ld, nb, D, D64, lane); break;
-        case 6: diag_tile_wave<6>(sh, A, ld, nb, D, D64, lane); break;
-        default: diag_tile_wave<7>(sh, A, ld, nb, D, D64, lane); break;
+        case 0: __syncthreads(); diag_factor_wave(sh, nb, D64, lane, bad); break;
+        case 1: diag_tile_wave<1>(sh, A, ld, nb, D64, lane); break;
+        case 2: diag_tile_wave<2>(sh, A, ld, nb, D64, lane); break;
+        case 3: diag_tile_wave<3>(sh, A, ld, nb, D64, lane); break;
+        case 4: diag_tile_wave<4>(sh, A, ld, nb, D64, lane); break;
+        case 5: diag_tile_wave<5>(sh, A, ld, nb, D64, lane); break;
+        case 6: diag_tile_wave<6>(sh, A, ld, nb, D64, lane); break;
+        default: diag_tile_wave<7>(sh, A, ld, nb, D64, lane); break;
     }
     __syncthreads();
     // write L, row-coalesced: Lfin holds every element on and below the
@@ -589,7 +586,7 @@ double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
 }
 
 // Lower Cholesky in place of `batch` matrices [n, n] (pitch ld, stride sH);
-// dinv / dinv64 receive every Dinv_k (batch x nblk x NB x NB, fp32 / fp64).
+// dinv64 receives every Dinv_k (batch x nblk x NB x NB, fp64).
 //
 // Two-level right-looking: columns are taken in super-blocks of up to
 // SUPER_NB columns.  After each block's panel, only the rest of the
@@ -599,8 +596,7 @@ double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
 // super-block.
 constexpr int64_t SUPER_NB = 1024;
 
-int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* dinv, double* dinv64, int* info,
-                 hipStream_t st) {
+int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, double* dinv64, int* info, hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
     for (int64_t s0 = 0; s0 < n; s0 += SUPER_NB) {
@@ -608,11 +604,10 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* din
         for (int64_t k0 = s0; k0 < s1; k0 += NB) {
             const int64_t kb = k0 / NB;
             const int nb = (int)std::min<int64_t>(NB, n - k0);
-            float* Dk = dinv + kb * NB * NB;
             double* Dk64 = dinv64 + kb * NB * NB;
             {
                 ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
-                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(DIAG_WAVES * 64), 0, st, H, ld, sH, k0, nb, Dk,
+                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(DIAG_WAVES * 64), 0, st, H, ld, sH, k0, nb,
                                    Dk64, dstride, info);
                 IC_CHECK_LAUNCH();
             }
@@ -662,24 +657,27 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, float* din
 // upper block of the merged square.  All pairs of one level that have the same shape run as one
 // batched GEMM, so the whole inverse takes ~2 log2(n/128) launches of
 // large-K GEMMs instead of 2 n/128 rank-128 updates.
-__global__ void put_diag_all_kernel(float* X, int64_t n, int64_t ld, int64_t stride, const float* dinv,
+__global__ void put_diag_all_kernel(float* X, int64_t n, int64_t ld, int64_t stride, const double* dinv64,
                                     int64_t dstride) {
     const int64_t k0 = (int64_t)blockIdx.x * NB;
     const int b = blockIdx.y;
-    const float* D = dinv + (int64_t)b * dstride + (int64_t)blockIdx.x * NB * NB;
+    const double* D = dinv64 + (int64_t)b * dstride + (int64_t)blockIdx.x * NB * NB;
     float* P = X + (int64_t)b * stride + k0 * ld + k0;
     const int nb = (int)std::min<int64_t>(NB, n - k0);
     if (nb == NB && ld % 4 == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0) {
-        // whole block, 16-byte rows: 32 float4 per row
+        // whole block, 16-byte rows: 32 float4 per row, each from 4 doubles
         for (int idx = threadIdx.x; idx < NB * NB / 4; idx += blockDim.x) {
             const int i = idx >> 5, j4 = (idx & 31) * 4;
-            *reinterpret_cast<float4*>(&P[(int64_t)i * ld + j4]) = *reinterpret_cast<const float4*>(&D[i * NB + j4]);
+            const double2 a = *reinterpret_cast<const double2*>(&D[i * NB + j4]);
+            const double2 c = *reinterpret_cast<const double2*>(&D[i * NB + j4 + 2]);
+            *reinterpret_cast<float4*>(&P[(int64_t)i * ld + j4]) =
+                make_float4((float)a.x, (float)a.y, (float)c.x, (float)c.y);
         }
         return;
     }
     for (int idx = threadIdx.x; idx < nb * nb; idx += blockDim.x) {
         const int i = idx / nb, j = idx - i * nb;
-        P[(int64_t)i * ld + j] = D[i * NB + j];
+        P[(int64_t)i * ld + j] = (float)D[i * NB + j];
     }
 }
 
@@ -725,12 +723,12 @@ static int merge_pairs(const float* L, float* X, int64_t ld, int64_t r0, int64_t
     return IC_OK;
 }
 
-int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const float* dinv,
-                 hipStream_t st) {
+int trtri(const float* L, float* X, int64_t batch, int64_t n, int64_t ld, int64_t sH, const double* dinv64,
+          hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
     hipLaunchKernelGGL(put_diag_all_kernel, dim3((unsigned)nblk, (unsigned)batch), dim3(256), 0, st, X, n, ld, sH,
-                       dinv, dstride);
+                       dinv64, dstride);
     IC_CHECK_LAUNCH();
     // segments of rows [start, start + len); merged pairwise per level
     std::vector<int64_t> seg;
@@ -784,9 +782,9 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
     hipLaunchKernelGGL(damp_kernel, dim3((unsigned)batch), dim3(256), 0, st, H, n, ld, sH, damping);
     IC_CHECK_LAUNCH();
-    int rc = potrf(H, batch, n, ld, sH, dinv, dinv64, info, st);
+    int rc = potrf(H, batch, n, ld, sH, dinv64, info, st);
     if (rc) return rc;
-    rc = trtri(H, X, batch, n, ld, sH, dinv, st);
+    rc = trtri(H, X, batch, n, ld, sH, dinv64, st);
     if (rc) return rc;
     // H^-1 (upper triangle incl. diagonal) = X^T X  -> H
     GemmArgs u{n, n, n, 1.0f, 0.0f, X, ld, sH, X, ld, sH, H, ld, sH, 1, 0, CMASK_UPPER, KR_FROM_MAXIJ, batch,
@@ -799,7 +797,7 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     IC_CHECK_LAUNCH();
     if (method == 1) {
         // upper Cholesky factor of H^-1 (converter/gptq.py:91-110): L2 = chol(H^-1), return L2^T
-        rc = potrf(H, batch, n, ld, sH, dinv, dinv64, info + batch, st);
+        rc = potrf(H, batch, n, ld, sH, dinv64, info + batch, st);
         if (rc) return rc;
         hipLaunchKernelGGL(lower_to_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
         IC_CHECK_LAUNCH();
@@ -823,5 +821,5 @@ extern "C" int ic_cholesky(float* H, int64_t batch, int64_t n, int* info, void* 
     IC_CHECK_HIP(hipMemsetAsync(info, 0, batch * sizeof(int), st));
     float* dinv = reinterpret_cast<float*>(workspace) + batch * n * n;
     double* dinv64 = dinv64_of(dinv, batch, n);
-    return potrf(H, batch, n, n, n * n, dinv, dinv64, info, st);
+    return potrf(H, batch, n, n, n * n, dinv64, info, st);
 }

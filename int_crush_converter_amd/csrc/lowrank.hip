@@ -372,8 +372,8 @@ static int cholqr_pass(const float* Y, float* Q, int64_t n, int64_t p, float shi
         hipLaunchKernelGGL(shift_diag_kernel, dim3(1), dim3(256), 0, st, w.G, p, shift_rel);
         IC_CHECK_LAUNCH();
     }
-    if ((rc = potrf(w.G, 1, p, p, p * p, w.dinv, w.dinv64, w.info, st))) return rc;
-    if ((rc = trtri(w.G, w.X, 1, p, p, p * p, w.dinv, st))) return rc;
+    if ((rc = potrf(w.G, 1, p, p, p * p, w.dinv64, w.info, st))) return rc;
+    if ((rc = trtri(w.G, w.X, 1, p, p, p * p, w.dinv64, st))) return rc;
     hipLaunchKernelGGL(zero_upper_kernel, dim3(egrid_lr(p * p)), dim3(256), 0, st, w.X, p);
     IC_CHECK_LAUNCH();
     // Q = Y X^T  (X = L^-1 lower, so op(B) = X^T is upper triangular)
@@ -454,7 +454,7 @@ extern "C" int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, 
             hipLaunchKernelGGL(sub_frob_diag_kernel, dim3(1), dim3(256), 0, st, w.T, p, w.part, LR_PARTS,
                                (double)refuse_rel);
             IC_CHECK_LAUNCH();
-            if ((rc = potrf(w.T, 1, p, p, p * p, w.dinv, w.dinv64, w.info + 1, st))) return rc;
+            if ((rc = potrf(w.T, 1, p, p, p * p, w.dinv64, w.info + 1, st))) return rc;
             int pd_info = 0;
             IC_CHECK_HIP(hipMemcpyAsync(&pd_info, w.info + 1, sizeof(int), hipMemcpyDeviceToHost, st));
             IC_CHECK_HIP(hipStreamSynchronize(st));
