@@ -14,7 +14,7 @@
 namespace icq {
 
 constexpr int GB = 64;          // greedy column block
-constexpr int GL = 16;          // lanes per row in the greedy block kernel
+constexpr int GQ = 4;           // lanes per row in the greedy block kernel
 
 __device__ __forceinline__ float nclampmin(float x, float lo) { return x != x ? x : (x < lo ? lo : x); }
 
@@ -139,157 +139,175 @@ __global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const floa
     }
 }
 
-// One 64-column block of a greedy pass for GROWS rows.  The block's err,
-// codes and cross terms are staged in LDS (all loads in flight at once), so
-// the column loop touches no global memory; at the end the new err and codes
-// and the changes d (D [rows, 64]) are written back.  C holds, for the
-// block's columns, err @ H[:, j] as of the start of the block.
-// GL lanes per row: lane l keeps the changes d_j' of the columns
-// j' = l (mod GL) and their share of the correction sum, and scans the
-// candidates g = qmin + l + GL m in increasing order; the lanes' best
-// (cost, g) pairs are then merged, the lower g winning a tie, which is the
-// sequential first-minimum scan.  H is the matrix of the cross terms (the
-// Hessian, or its low-rank truncation) and hd its exact diagonal H_jj (null:
-// the diagonal of H).
-constexpr int GROWS = 256 / GL;
-constexpr int GSTAGE = GROWS * GB / 256;   // staged elements per thread
+// One 64-column block of a greedy pass for GQR rows: one wave, GQ = 4 lanes
+// (a DPP quad) per row.  Lane p of a row owns the block columns j = 4 m + p
+// (m = 0..15) and keeps, in registers, their err, code and cross term
+//   c_j = err @ H[:, j] as of the start of the block (C)
+//         + sum over the block columns j' < j decided so far of
+//           (err_new - err_old)_j' * H[j', j],
+// added one column at a time in the column order, each product rounded
+// before it is added (the rank-1 corrections of converter/greedy.py:255-258).
+// Column jl's decision (converter/greedy.py:80-95: the grid value with the
+// least (e + d)^2 H_jj + 2 (e + d) cross, cross = c_j - e H_jj, the first
+// one on a tie) is made by its owner from the two grid values around the
+// continuous minimiser t = q - (cross / H_jj + e) / s: the cost is a convex
+// quadratic in the grid value, so when its fp32 rounding is small against
+// the gap H_jj s^2 between neighbouring grid values (|cross| <= 128 H_jj s,
+// |t| < 2^16, H_jj and s^2 in a normal range) no other grid value can tie or
+// beat the better of the two, and the full scan's answer is that one.
+// Otherwise the owner scans the whole grid in increasing order, as the
+// reference does.  The change is then broadcast over the quad and every
+// lane adds its products to the cross terms of its later columns.  H is the
+// matrix of the cross terms (the Hessian, or its low-rank truncation) and hd
+// its exact diagonal H_jj (null: the diagonal of H).
+constexpr int GQR = 64 / GQ;      // rows per work-group
+constexpr int GSLOT = GB / GQ;    // block columns per lane
+constexpr float GREEDY_GAMMA = 128.0f;
+constexpr float GREEDY_TMAX = 65536.0f;
 
-// Exchanges inside a 16-lane DPP row (one greedy row): rotations by 8 and 4
-// within the row, then quad swaps; after the four steps of a commutative,
-// associative merge every lane of the row holds the merge of all 16.
-template <int CTRL>
-__device__ __forceinline__ float rdpp(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-constexpr int DPP_ROR8 = 0x128, DPP_ROR4 = 0x124, DPP_QXOR2 = 0x4E, DPP_QXOR1 = 0xB1;
-static_assert(GL == 16, "the row exchanges assume one greedy row per 16-lane DPP row");
-
-__device__ __forceinline__ float row_sum16(float v) {
-    v = v + rdpp<DPP_ROR8>(v);
-    v = v + rdpp<DPP_ROR4>(v);
-    v = v + rdpp<DPP_QXOR2>(v);
-    return v + rdpp<DPP_QXOR1>(v);
-}
-
-// Merge (cost, g) pairs: the lower cost, on a tie the lower g (branch-free).
-template <int CTRL>
-__device__ __forceinline__ void argmin_step(float& best, float& bq) {
-    const float ob = rdpp<CTRL>(best), oq = rdpp<CTRL>(bq);
-    const bool take = (ob < best) | ((ob == best) & (oq < bq));
-    best = take ? ob : best;
-    bq = take ? oq : bq;
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
 }
 
-template <int NG>
-__global__ __launch_bounds__(256) void greedy_block_kernel(float* err, float* Qf, const float* srow, const float* H,
-                                                           int64_t ldh, const float* hd, const float* C,
-                                                           int64_t ldc, float* D, int64_t rows, int64_t cols,
-                                                           int64_t j0, int nb, float qmin, float qmax) {
-    constexpr int HP = GB + 1;                 // pitch of the transposed H tile
-    __shared__ float HsT[GB * HP];             // HsT[j][j'] = H[j0 + j'][j0 + j]
-    __shared__ float Es[GROWS][GB + 1];
-    __shared__ float Qs[GROWS][GB + 1];
-    __shared__ float Cs[GROWS][GB + 1];
-    __shared__ float hds[GB];
-    const int t = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * GROWS;
-    if (t < GB) hds[t] = t < nb ? (hd ? hd[j0 + t] : H[(j0 + t) * ldh + j0 + t]) : 1.0f;
+template <int P>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), P * 0x55, 0xf, 0xf, false));
+}
+
+// The reference's scan over the whole grid (first minimum, codes start at
+// q): {code, new err}.
+__device__ __forceinline__ float2 greedy_scan(float e, float q, float s, float h, float cross, float qmin,
+                                              float qmax) {
+    float best = 1e30f, bq = q;
+    for (float g = qmin; g <= qmax; g += 1.0f) {
+        const float ne = e + (g - q) * s;
+        const float cost = ne * ne * h + 2.0f * ne * cross;
+        if (cost < best) {
+            best = cost;
+            bq = g;
+        }
+    }
+    bq = clampf(bq, qmin, qmax);
+    return make_float2(bq, e + (bq - q) * s);
+}
+
+// FULL: nb == GB (no column bound checks).
+template <bool FULL>
+__global__ __launch_bounds__(64) void greedy_block_kernel(float* err, float* Qf, const float* srow, const float* H,
+                                                          int64_t ldh, const float* hd, const float* C, int64_t ldc,
+                                                          float* D, int64_t rows, int64_t cols, int64_t j0, int nb,
+                                                          float qmin, float qmax) {
+    __shared__ __align__(16) float Hl[GB][GQ][GSLOT];   // Hl[j'][p][m] = H[j0 + j'][j0 + 4 m + p]
+    __shared__ __align__(16) float4 colv[GB];           // {H_jj, H_jj or NaN (guard), 1 / H_jj, 0}
+    const int t = threadIdx.x, p = t & (GQ - 1);
     {
-        float e[GSTAGE], q[GSTAGE], c[GSTAGE], h[GB * GB / 256];
+        float hv[GB];
 #pragma unroll
-        for (int k = 0; k < GSTAGE; ++k) {
-            const int idx = t + 256 * k, rr = idx / GB, cc = idx % GB;
-            const int64_t r = r0 + rr;
-            const bool ok = r < rows && cc < nb;
-            e[k] = ok ? err[r * cols + j0 + cc] : 0.0f;
-            q[k] = ok ? Qf[r * cols + j0 + cc] : 0.0f;
-            c[k] = ok ? C[r * ldc + cc] : 0.0f;
-        }
+        for (int a = 0; a < GB; ++a) hv[a] = (FULL || (a < nb && t < nb)) ? H[(j0 + a) * ldh + j0 + t] : 0.0f;
 #pragma unroll
-        for (int k = 0; k < GB * GB / 256; ++k) {
-            const int idx = t + 256 * k, a = idx / GB, b = idx % GB;
-            h[k] = (a < nb && b < nb) ? H[(j0 + a) * ldh + j0 + b] : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < GSTAGE; ++k) {
-            const int idx = t + 256 * k, rr = idx / GB, cc = idx % GB;
-            Es[rr][cc] = e[k];
-            Qs[rr][cc] = q[k];
-            Cs[rr][cc] = c[k];
-        }
-#pragma unroll
-        for (int k = 0; k < GB * GB / 256; ++k) {
-            const int idx = t + 256 * k, a = idx / GB, b = idx % GB;
-            HsT[b * HP + a] = h[k];
-        }
+        for (int a = 0; a < GB; ++a) Hl[a][t & (GQ - 1)][t / GQ] = hv[a];
+        const float h = (FULL || t < nb) ? (hd ? hd[j0 + t] : H[(j0 + t) * ldh + j0 + t]) : 1.0f;
+        const bool hok = h >= 0x1p-60f && h <= 0x1p30f;
+        colv[t] = make_float4(h, hok ? h : __builtin_nanf(""), 1.0f / h, 0.0f);
     }
+    const int64_t r = (int64_t)blockIdx.x * GQR + t / GQ;
+    const bool live = r < rows;
+    const float s = live ? srow[r] : 1.0f;
+    const float is = 1.0f / s, s2 = s * s;
+    const float sg = (s > 0.0f && s2 >= 0x1p-40f && s2 <= 0x1p30f) ? GREEDY_GAMMA * s : __builtin_nanf("");
+    float er[GSLOT], e0[GSLOT], qr[GSLOT], cr[GSLOT];
+    auto load_state = [&]() {
+#pragma unroll
+        for (int m = 0; m < GSLOT; ++m) {
+            const int col = GQ * m + p;
+            const bool ok = live && (FULL || col < nb);
+            er[m] = ok ? err[r * cols + j0 + col] : 0.0f;
+            qr[m] = ok ? Qf[r * cols + j0 + col] : 0.0f;
+            cr[m] = ok ? C[r * ldc + col] : 0.0f;
+        }
+    };
+    load_state();
+#pragma unroll
+    for (int m = 0; m < GSLOT; ++m) e0[m] = er[m];
     __syncthreads();
-    const int lane = t % GL, rr = t / GL;
-    const int64_t r = r0 + rr;
-    const float s = r < rows ? srow[r] : 1.0f;
-    float dl[GB / GL];
-#pragma unroll
-    for (int i = 0; i < GB / GL; ++i) dl[i] = 0.0f;
-    // operands of column 0; each iteration fetches those of the next column
-    float hv[GB / GL];
-#pragma unroll
-    for (int i = 0; i < GB / GL; ++i) hv[i] = HsT[i * GL + lane];
-    float e = Es[rr][0], qo = Qs[rr][0], cc0 = Cs[rr][0], hjj = hds[0];
-    for (int jl = 0; jl < nb; ++jl) {
-        const int jn = jl + 1 < GB ? jl + 1 : jl;
-        float hn[GB / GL];
-#pragma unroll
-        for (int i = 0; i < GB / GL; ++i) hn[i] = HsT[jn * HP + i * GL + lane];
-        const float en = Es[rr][jn], qn = Qs[rr][jn], cn = Cs[rr][jn], hjn = hds[jn];
-        // correction: sum over earlier block columns of d_j' * H[j', j]
-        // (branch-free; columns j' >= j add +0)
-        float part = 0.0f;
-#pragma unroll
-        for (int i = 0; i < GB / GL; ++i) {
-            const float pr = dl[i] * hv[i];
-            part = part + (i * GL + lane < jl ? pr : 0.0f);
+    // Column jl of the block (jl a compile-time constant: register slots).
+    // GUARDED: a lane outside the window's domain scans the whole grid;
+    // otherwise such a lane only sets `bad` (and the block is run again
+    // guarded), so the common path has no branch.
+    bool bad = false;
+    float4 cvn, hc[GSLOT / 4], hn[GSLOT / 4];   // column data and H row share, one column ahead
+    const float4* Hl4 = reinterpret_cast<const float4*>(&Hl[0][p][0]);   // + jl * GQ * GSLOT / 4
+    auto column = [&](auto JL, auto GUARDED) {
+        constexpr int jl = decltype(JL)::value, m = jl / GQ, o = jl % GQ;
+        if constexpr (!FULL) {
+            if (jl >= nb) return;
         }
-        part = row_sum16(part);
-        const float c = (cc0 + part) - e * hjj;
-        float best = 1e30f, bq = qo;
+        const float4 cv = cvn;
+        if constexpr (jl + 1 < GB) {
+            cvn = colv[jl + 1];
 #pragma unroll
-        for (int m = 0; m < NG / GL; ++m) {
-            const float g = qmin + (float)(m * GL + lane);
-            const float ne = e + (g - qo) * s;
-            const float cost = ne * ne * hjj + 2.0f * ne * c;
-            const bool better = cost < best;
-            best = better ? cost : best;
-            bq = better ? g : bq;
+            for (int g = (jl + 1) / 16; g < GSLOT / 4; ++g) hn[g] = Hl4[(jl + 1) * (GQ * GSLOT / 4) + g];
         }
-        argmin_step<DPP_ROR8>(best, bq);
-        argmin_step<DPP_ROR4>(best, bq);
-        argmin_step<DPP_QXOR2>(best, bq);
-        argmin_step<DPP_QXOR1>(best, bq);
-        bq = clampf(bq, qmin, qmax);
-        const float d = (bq - qo) * s;
-        if (lane == 0) {   // column jl is not read again in this block; Cs[.][jl] now keeps d
-            Qs[rr][jl] = bq;
-            Es[rr][jl] = e + d;
-            Cs[rr][jl] = d;
+        const float h = cv.x;
+        const float xe = er[m], xq = qr[m];
+        const float cross = cr[m] - xe * h;
+        const float tt = xq - fmaf(cross, cv.z, xe) * is;
+        const float g0 = __builtin_amdgcn_fmed3f(floorf(tt), qmin, qmax - 1.0f), g1 = g0 + 1.0f;
+        const float n0 = xe + (g0 - xq) * s, n1 = xe + (g1 - xq) * s;
+        const float c0 = n0 * n0 * h + 2.0f * n0 * cross, c1 = n1 * n1 * h + 2.0f * n1 * cross;
+        const bool up = c1 < c0;
+        float bq = up ? g1 : g0, ne = up ? n1 : n0;
+        const bool fast = fabsf(cross) <= cv.y * sg && fabsf(tt) < GREEDY_TMAX;
+        if constexpr (decltype(GUARDED)::value) {
+            if (!fast) {
+                const float2 sc = greedy_scan(xe, xq, s, h, cross, qmin, qmax);
+                bq = sc.x;
+                ne = sc.y;
+            }
+        } else {
+            bad = bad | !fast;
+        }
+        const float d = quad_bcast<o>(ne - xe);
+        if (p == o) {
+            er[m] = ne;
+            qr[m] = bq;
         }
 #pragma unroll
-        for (int i = 0; i < GB / GL; ++i) dl[i] = i * GL + lane == jl ? d : dl[i];
+        for (int m2 = m; m2 < GSLOT; ++m2) {
+            const float4 h4 = hc[m2 / 4];
+            const float hv = m2 % 4 == 0 ? h4.x : m2 % 4 == 1 ? h4.y : m2 % 4 == 2 ? h4.z : h4.w;
+            cr[m2] = cr[m2] + d * hv;
+        }
 #pragma unroll
-        for (int i = 0; i < GB / GL; ++i) hv[i] = hn[i];
-        e = en;
-        qo = qn;
-        cc0 = cn;
-        hjj = hjn;
+        for (int g = 0; g < GSLOT / 4; ++g) hc[g] = hn[g];
+        __builtin_amdgcn_sched_barrier(0);   // keep the one-column-ahead loads where they are
+    };
+    auto start = [&]() {
+        cvn = colv[0];
+#pragma unroll
+        for (int g = 0; g < GSLOT / 4; ++g) hc[g] = Hl4[g];
+    };
+    start();
+    auto fast_column = [&](auto JL) { column(JL, std::false_type{}); };
+    static_for<0, GB>(fast_column);
+    if (__builtin_amdgcn_ballot_w64(bad)) {   // rare: this wave's rows again, guarded
+        __asm__ volatile("" ::: "memory");   // reload, rather than keep the first loads live
+        load_state();
+        start();
+        auto guarded_column = [&](auto JL) { column(JL, std::true_type{}); };
+        static_for<0, GB>(guarded_column);
     }
-    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < GSTAGE; ++k) {
-        const int idx = t + 256 * k, rr2 = idx / GB, c2 = idx % GB;
-        const int64_t r2 = r0 + rr2;
-        if (r2 < rows && c2 < nb) {
-            err[r2 * cols + j0 + c2] = Es[rr2][c2];
-            Qf[r2 * cols + j0 + c2] = Qs[rr2][c2];
-            D[r2 * GB + c2] = Cs[rr2][c2];
+    for (int m = 0; m < GSLOT; ++m) {
+        const int col = GQ * m + p;
+        if (live && (FULL || col < nb)) {
+            err[r * cols + j0 + col] = er[m];
+            Qf[r * cols + j0 + col] = qr[m];
+            D[r * GB + col] = er[m] - e0[m];
         }
     }
 }
@@ -383,12 +401,11 @@ static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc
             {
                 ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)),
                                      (double)rows * nb * 20);
-                if (qmax - qmin + 1.0f == 16.0f)
-                    hipLaunchKernelGGL(greedy_block_kernel<16>, dim3((unsigned)cdiv(rows, GROWS)), dim3(256), 0, st,
-                                       err, Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin,
-                                       qmax);
+                if (nb == GB)
+                    hipLaunchKernelGGL(greedy_block_kernel<true>, dim3((unsigned)cdiv(rows, GQR)), dim3(64), 0, st, err,
+                                       Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin, qmax);
                 else
-                    hipLaunchKernelGGL(greedy_block_kernel<256>, dim3((unsigned)cdiv(rows, GROWS)), dim3(256), 0, st,
+                    hipLaunchKernelGGL(greedy_block_kernel<false>, dim3((unsigned)cdiv(rows, GQR)), dim3(64), 0, st,
                                        err, Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin,
                                        qmax);
                 IC_CHECK_LAUNCH();

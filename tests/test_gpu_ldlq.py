@@ -106,6 +106,33 @@ def test_greedy_matches_oracle(gpu_dev):
     assert agree >= 0.999
 
 
+def test_greedy_outside_window_domain(gpu_dev):
+    """Decisions the two-candidate window does not cover go through the full
+    grid scan: a dead input channel (its row and column of H zero, no
+    damping: every candidate costs 0 and the first grid value wins, as in the
+    reference's argmin), rows whose scale is 1000x below their weights'
+    spread (|cross| far above H_jj s), and a partial last column block."""
+    from int_crush_converter_amd.ldlq import greedy_local_search
+    g = torch.Generator().manual_seed(11)
+    M, N = 80, 200
+    W = torch.randn(M, N, generator=g) * 0.02
+    X = torch.randn(4 * N, N, generator=g)
+    X[:, 5] = 0.0
+    H = X.T @ X / (4 * N)
+    s = (W.abs().amax(dim=1) / 7).clamp(min=1e-5)
+    odd = [3, 40, 77]
+    s[odd] *= 1e-3
+    Q0 = ref.rhaz(W / s[:, None]).clamp(-8, 7)
+    want = ref.greedy_pytorch(W, Q0.clone(), s[:, None].expand(M, N), H, 2, -8, 7)
+    got = greedy_local_search(W.to(gpu_dev), Q0.to(torch.int8).to(gpu_dev), s.to(gpu_dev), H.to(gpu_dev), 2, 4).cpu()
+    assert torch.equal(want[:, 5], torch.full((M,), -8, dtype=torch.int8))
+    assert torch.equal(got[:, 5], want[:, 5])
+    agree = (got == want).float().mean().item()
+    agree_odd = (got[odd] == want[odd]).float().mean().item()
+    print(f"[parity] greedy_outside_window agreement={agree:.6f} odd_rows={agree_odd:.6f}", flush=True)
+    assert agree >= 0.999 and agree_odd >= 0.99
+
+
 def test_ldlq_layer_vs_oracle_moderate(gpu_dev):
     from int_crush_converter_amd.ldlq import ldlq_quantize_layer
     g = torch.Generator().manual_seed(8)
