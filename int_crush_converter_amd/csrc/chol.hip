@@ -185,16 +185,9 @@ struct DiagShared {
     float Lfin[NB + 1][NB + 1];    // L as it is finalised (on and below the diagonal)
 };
 
-// Barrier between the phases of the diagonal-block kernel: the waves hand
-// data to each other only through LDS, so each waits for its own LDS
-// operations and no more.  (__syncthreads() would also wait for the global
-// stores of the Dinv rows, which only later kernels read: a store round trip
-// per phase.)
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// The phases of the diagonal-block kernel hand data to each other only
+// through LDS, so they are separated by lds_barrier() (common.hpp), which
+// does not wait for the global stores of the Dinv rows.
 
 // Rows 8 p .. 8 p + 7 of X = L^-1, column q: forward substitution with panel
 // p's 8x8 diagonal block of L from the published rows of R; the result goes

@@ -113,6 +113,16 @@ __device__ __forceinline__ float rhaz_trunc(float x) {
     return truncf(x + __builtin_copysignf(0.5f, x));
 }
 
+// Work-group barrier for waves that hand data to each other only through
+// LDS: each waits for its own LDS operations and no more (__syncthreads()
+// also waits for outstanding global memory operations, e.g. loads issued
+// early to hide their latency, or stores that only later kernels read).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // clampf as a median of three (NaN still propagates).
 __device__ __forceinline__ float clampf_med3(float x, float lo, float hi) {
     return x != x ? x : __builtin_amdgcn_fmed3f(x, lo, hi);

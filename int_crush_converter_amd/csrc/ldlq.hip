@@ -15,6 +15,7 @@ namespace icq {
 
 constexpr int GB = 64;          // greedy column block
 constexpr int GQ = 4;           // lanes per row in the greedy block kernel
+constexpr int64_t GSB = 512;    // greedy super-block (columns)
 
 __device__ __forceinline__ float nclampmin(float x, float lo) { return x != x ? x : (x < lo ? lo : x); }
 
@@ -139,14 +140,15 @@ __global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const floa
     }
 }
 
-// One 64-column block of a greedy pass for GQR rows: one wave, GQ = 4 lanes
-// (a DPP quad) per row.  Lane p of a row owns the block columns j = 4 m + p
-// (m = 0..15) and keeps, in registers, their err, code and cross term
-//   c_j = err @ H[:, j] as of the start of the block (C)
+// A 64-column block of a greedy pass for GQR rows is run by one wave, GQ = 4
+// lanes (a DPP quad) per row.  Lane p of a row owns the block columns
+// j = 4 m + p (m = 0..15) and keeps, in registers, their err, code and cross
+// term
+//   c_j = err @ H[:, j] as of the start of the block
 //         + sum over the block columns j' < j decided so far of
 //           (err_new - err_old)_j' * H[j', j],
-// added one column at a time in the column order, each product rounded
-// before it is added (the rank-1 corrections of converter/greedy.py:255-258).
+// the changes added one column at a time in the column order (the rank-1
+// corrections of converter/greedy.py:255-258, as fused multiply-adds).
 // Column jl's decision (converter/greedy.py:80-95: the grid value with the
 // least (e + d)^2 H_jj + 2 (e + d) cross, cross = c_j - e H_jj, the first
 // one on a tie) is made by its owner from the two grid values around the
@@ -155,11 +157,11 @@ __global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const floa
 // the gap H_jj s^2 between neighbouring grid values (|cross| <= 128 H_jj s,
 // |t| < 2^16, H_jj and s^2 in a normal range) no other grid value can tie or
 // beat the better of the two, and the full scan's answer is that one.
-// Otherwise the owner scans the whole grid in increasing order, as the
-// reference does.  The change is then broadcast over the quad and every
-// lane adds its products to the cross terms of its later columns.  H is the
-// matrix of the cross terms (the Hessian, or its low-rank truncation) and hd
-// its exact diagonal H_jj (null: the diagonal of H).
+// Otherwise the whole grid is scanned in increasing order, as the reference
+// does.  The change is then broadcast over the quad and every lane adds its
+// products to the cross terms of its later columns.  H is the matrix of the
+// cross terms (the Hessian, or its low-rank truncation) and hd its exact
+// diagonal H_jj (null: the diagonal of H).
 constexpr int GQR = 64 / GQ;      // rows per work-group
 constexpr int GSLOT = GB / GQ;    // block columns per lane
 constexpr float GREEDY_GAMMA = 128.0f;
@@ -195,120 +197,253 @@ __device__ __forceinline__ float2 greedy_scan(float e, float q, float s, float h
     return make_float2(bq, e + (bq - q) * s);
 }
 
-// FULL: nb == GB (no column bound checks).
+// The window decision for one column of one row: err e, code q, running
+// cross-term sum c (before the diagonal term), column data cv = {H_jj,
+// H_jj or NaN, 1 / H_jj}, row scale s, 1 / s and the guard scale sg
+// (GREEDY_GAMMA s, or NaN for a row outside the domain).  {code, new err};
+// fast: the window's answer is the full scan's.
+__device__ __forceinline__ float2 greedy_decide(float e, float q, float c, float4 cv, float s, float is, float sg,
+                                                float qmin, float qmax, bool& fast) {
+    const float h = cv.x;
+    const float cross = c - e * h;
+    const float tt = q - fmaf(cross, cv.z, e) * is;
+    const float g0 = __builtin_amdgcn_fmed3f(floorf(tt), qmin, qmax - 1.0f), g1 = g0 + 1.0f;
+    const float n0 = e + (g0 - q) * s, n1 = e + (g1 - q) * s;
+    const float c0 = n0 * n0 * h + 2.0f * n0 * cross, c1 = n1 * n1 * h + 2.0f * n1 * cross;
+    const bool up = c1 < c0;
+    fast = fabsf(cross) <= cv.y * sg && fabsf(tt) < GREEDY_TMAX;
+    return up ? make_float2(g1, n1) : make_float2(g0, n0);
+}
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Orders a wave's own LDS accesses (exchanges between its lanes), with no
+// work-group barrier.
+__device__ __forceinline__ void lds_wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One super-block of a greedy pass (columns s0 .. s0 + sw, sw <= GSB) for
+// GQR rows, one launch per super-block.  Csb [rows, GSB] holds
+// err @ H[:, j] for the super-block's columns as of its start.  Block b's
+// cross terms are Csb plus the changes D of the super-block's earlier
+// blocks, D [16 rows, 64 b] kept in LDS, times H[earlier, block]: on the
+// matrix cores as (H^T D^T) in 16 x 16 tiles, tile t holding the block
+// columns 4 u + t (u = 0..15), the columns lane p = t owns, so that each lane
+// fetches H[j'][j0 + 4 u .. + 3] as one vector for the four tiles.
+// Two waves: wave 0 runs the blocks' columns; meanwhile wave 1 stages the
+// next block's H tile and sums the next block's corrections from all but
+// the current block, then, once the current block's changes are in LDS,
+// adds those (one accumulation in block order).
+// FULL: every block whole and the pitch of H a multiple of 4.
 template <bool FULL>
-__global__ __launch_bounds__(64) void greedy_block_kernel(float* err, float* Qf, const float* srow, const float* H,
-                                                          int64_t ldh, const float* hd, const float* C, int64_t ldc,
-                                                          float* D, int64_t rows, int64_t cols, int64_t j0, int nb,
-                                                          float qmin, float qmax) {
-    __shared__ __align__(16) float Hl[GB][GQ][GSLOT];   // Hl[j'][p][m] = H[j0 + j'][j0 + 4 m + p]
-    __shared__ __align__(16) float4 colv[GB];           // {H_jj, H_jj or NaN (guard), 1 / H_jj, 0}
-    const int t = threadIdx.x, p = t & (GQ - 1);
-    {
+__global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, const float* srow, const float* H,
+                                                        int64_t ldh, const float* hd, const float* Csb,
+                                                        int64_t rows, int64_t cols, int64_t s0, int sw, float qmin,
+                                                        float qmax) {
+    __shared__ __align__(16) float Hl[2][GB][GQ][GSLOT];   // Hl[b & 1][j'][p][m] = H[j0 + j'][j0 + 4 m + p]
+    __shared__ __align__(16) float4 colv[2][GB];           // {H_jj, H_jj or NaN (guard), 1 / H_jj, 0}
+    __shared__ __align__(16) float Dl[GSB][GQR];           // Dl[j - s0][row]: the block's change of err
+    __shared__ __align__(16) float Xs[GQR][GQ][GSLOT];     // corrections of the next block, Xs[row][p][m]
+    __shared__ float Gs[GQR][3][GB];                       // guarded rerun: err, codes, cross terms
+    const int w = threadIdx.x >> 6, t = threadIdx.x & 63;
+    const int nblk = (sw + GB - 1) / GB;
+    auto width = [&](int b) { return FULL ? GB : (int)min((int64_t)GB, (int64_t)sw - (int64_t)b * GB); };
+
+    // ---- wave 1: H tiles and corrections ----
+    auto put_tile = [&](int b) {   // H[blk, blk] of block b and its diagonal, into buffer b & 1
+        const int64_t jb = s0 + (int64_t)b * GB;
+        const int nbb = width(b);
         float hv[GB];
 #pragma unroll
-        for (int a = 0; a < GB; ++a) hv[a] = (FULL || (a < nb && t < nb)) ? H[(j0 + a) * ldh + j0 + t] : 0.0f;
+        for (int a = 0; a < GB; ++a) hv[a] = (FULL || (a < nbb && t < nbb)) ? H[(jb + a) * ldh + jb + t] : 0.0f;
+        const float h = (FULL || t < nbb) ? (hd ? hd[jb + t] : H[(jb + t) * ldh + jb + t]) : 1.0f;
 #pragma unroll
-        for (int a = 0; a < GB; ++a) Hl[a][t & (GQ - 1)][t / GQ] = hv[a];
-        const float h = (FULL || t < nb) ? (hd ? hd[j0 + t] : H[(j0 + t) * ldh + j0 + t]) : 1.0f;
+        for (int a = 0; a < GB; ++a) Hl[b & 1][a][t & (GQ - 1)][t / GQ] = hv[a];
         const bool hok = h >= 0x1p-60f && h <= 0x1p30f;
-        colv[t] = make_float4(h, hok ? h : __builtin_nanf(""), 1.0f / h, 0.0f);
-    }
-    const int64_t r = (int64_t)blockIdx.x * GQR + t / GQ;
-    const bool live = r < rows;
+        colv[b & 1][t] = make_float4(h, hok ? h : __builtin_nanf(""), 1.0f / h, 0.0f);
+    };
+    floatx4 acc[GQ];
+    const int lr = t & 15, lk = t >> 4;
+    // acc += D[:, 4 ks .. 4 ks + 3] H[s0 + 4 ks .., block b] for ks in [k_lo, k_hi) (multiples of 16)
+    auto corrections = [&](int b, int k_lo, int k_hi) {
+        const int64_t c = s0 + (int64_t)b * GB + 4 * lr;
+        auto hload = [&](int ks) -> float4 {
+            const float* src = H + (s0 + 4 * ks + lk) * ldh + c;
+            if (FULL) return *reinterpret_cast<const float4*>(src);
+            return make_float4(c < cols ? src[0] : 0.0f, c + 1 < cols ? src[1] : 0.0f, c + 2 < cols ? src[2] : 0.0f,
+                               c + 3 < cols ? src[3] : 0.0f);
+        };
+        constexpr int PF = 8;
+        auto group = [&](int k0, const float4 (&hv)[PF]) {
+            float bv[PF];
+#pragma unroll
+            for (int i = 0; i < PF; ++i) bv[i] = Dl[4 * (k0 + i) + lk][lr];
+#pragma unroll
+            for (int i = 0; i < PF; ++i) {
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i].x, bv[i], acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i].y, bv[i], acc[1], 0, 0, 0);
+                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i].z, bv[i], acc[2], 0, 0, 0);
+                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i].w, bv[i], acc[3], 0, 0, 0);
+            }
+        };
+        auto fetch = [&](int k0, float4 (&hv)[PF]) {   // clamped: past the range, in-bounds filler
+#pragma unroll
+            for (int i = 0; i < PF; ++i) hv[i] = hload(min(k0 + i, k_hi - 1));
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        float4 ha[PF], hb[PF];
+        fetch(k_lo, ha);
+        for (int k0 = k_lo; k0 < k_hi; k0 += 2 * PF) {
+            fetch(k0 + PF, hb);
+            group(k0, ha);
+            fetch(k0 + 2 * PF, ha);
+            group(k0 + PF, hb);
+        }
+    };
+
+    // ---- wave 0: the columns ----
+    const int p = t & (GQ - 1), rr = t / GQ;
+    const int64_t r = (int64_t)blockIdx.x * GQR + rr;
+    const bool live = w == 0 && r < rows;
     const float s = live ? srow[r] : 1.0f;
     const float is = 1.0f / s, s2 = s * s;
     const float sg = (s > 0.0f && s2 >= 0x1p-40f && s2 <= 0x1p30f) ? GREEDY_GAMMA * s : __builtin_nanf("");
     float er[GSLOT], e0[GSLOT], qr[GSLOT], cr[GSLOT];
-    auto load_state = [&]() {
+    auto load_raw = [&](int b) {   // block b's err, codes and super-block cross terms
+        const int64_t j0 = s0 + (int64_t)b * GB;
+        const int nb = width(b);
 #pragma unroll
         for (int m = 0; m < GSLOT; ++m) {
             const int col = GQ * m + p;
             const bool ok = live && (FULL || col < nb);
             er[m] = ok ? err[r * cols + j0 + col] : 0.0f;
             qr[m] = ok ? Qf[r * cols + j0 + col] : 0.0f;
-            cr[m] = ok ? C[r * ldc + col] : 0.0f;
+            cr[m] = ok ? Csb[r * GSB + (j0 - s0) + col] : 0.0f;
         }
     };
-    load_state();
+    auto add_corr = [&](int b) {
+        if (b > 0) {
 #pragma unroll
-    for (int m = 0; m < GSLOT; ++m) e0[m] = er[m];
-    __syncthreads();
-    // Column jl of the block (jl a compile-time constant: register slots).
-    // GUARDED: a lane outside the window's domain scans the whole grid;
-    // otherwise such a lane only sets `bad` (and the block is run again
-    // guarded), so the common path has no branch.
-    bool bad = false;
-    float4 cvn, hc[GSLOT / 4], hn[GSLOT / 4];   // column data and H row share, one column ahead
-    const float4* Hl4 = reinterpret_cast<const float4*>(&Hl[0][p][0]);   // + jl * GQ * GSLOT / 4
-    auto column = [&](auto JL, auto GUARDED) {
-        constexpr int jl = decltype(JL)::value, m = jl / GQ, o = jl % GQ;
-        if constexpr (!FULL) {
-            if (jl >= nb) return;
+            for (int m = 0; m < GSLOT; ++m) cr[m] = cr[m] + Xs[rr][p][m];
         }
-        const float4 cv = cvn;
-        if constexpr (jl + 1 < GB) {
-            cvn = colv[jl + 1];
+    };
+
+    if (w == 1) put_tile(0);
+    else load_raw(0);
+    lds_barrier();
+    for (int b = 0; b < nblk; ++b) {
+        if (w == 0) {
+            const int64_t j0 = s0 + (int64_t)b * GB;
+            const int nb = width(b);
+            const int buf = b & 1;
+            add_corr(b);
 #pragma unroll
-            for (int g = (jl + 1) / 16; g < GSLOT / 4; ++g) hn[g] = Hl4[(jl + 1) * (GQ * GSLOT / 4) + g];
-        }
-        const float h = cv.x;
-        const float xe = er[m], xq = qr[m];
-        const float cross = cr[m] - xe * h;
-        const float tt = xq - fmaf(cross, cv.z, xe) * is;
-        const float g0 = __builtin_amdgcn_fmed3f(floorf(tt), qmin, qmax - 1.0f), g1 = g0 + 1.0f;
-        const float n0 = xe + (g0 - xq) * s, n1 = xe + (g1 - xq) * s;
-        const float c0 = n0 * n0 * h + 2.0f * n0 * cross, c1 = n1 * n1 * h + 2.0f * n1 * cross;
-        const bool up = c1 < c0;
-        float bq = up ? g1 : g0, ne = up ? n1 : n0;
-        const bool fast = fabsf(cross) <= cv.y * sg && fabsf(tt) < GREEDY_TMAX;
-        if constexpr (decltype(GUARDED)::value) {
-            if (!fast) {
-                const float2 sc = greedy_scan(xe, xq, s, h, cross, qmin, qmax);
-                bq = sc.x;
-                ne = sc.y;
+            for (int m = 0; m < GSLOT; ++m) e0[m] = er[m];
+            // Column jl of the block (jl a compile-time constant: register
+            // slots).  A lane outside the window's domain only sets `bad`,
+            // so the common path has no branch; the wave's rows are then run
+            // again below.  Columns past a partial block (and rows past the
+            // matrix) run on zeros (err, code, cross terms and H; H_jj = 1):
+            // they decide code 0 with no change, add nothing to the real
+            // columns and are not stored.
+            uint64_t bad = 0;   // lanes that left the window's domain
+            float4 cvn, hc[GSLOT / 4], hn[GSLOT / 4];   // column data and H row share, one column ahead
+            const float4* Hl4 = reinterpret_cast<const float4*>(&Hl[buf][0][p][0]);
+            const float4* cvp = &colv[buf][0];
+            auto column = [&](auto JL) {
+                constexpr int jl = decltype(JL)::value, m = jl / GQ, o = jl % GQ;
+                const float4 cv = cvn;
+                if constexpr (jl + 1 < GB) {
+                    cvn = cvp[jl + 1];
+#pragma unroll
+                    for (int g = (jl + 1) / 16; g < GSLOT / 4; ++g) hn[g] = Hl4[(jl + 1) * (GQ * GSLOT / 4) + g];
+                }
+                const float xe = er[m];
+                bool fast;
+                const float2 dec = greedy_decide(xe, qr[m], cr[m], cv, s, is, sg, qmin, qmax, fast);
+                bad |= __builtin_amdgcn_ballot_w64(!fast);
+                __asm__ volatile("" : "+s"(bad));   // fold this column's test in now, not at the end
+                const float d = quad_bcast<o>(dec.y - xe);
+                if (p == o) {
+                    er[m] = dec.y;
+                    qr[m] = dec.x;
+                }
+#pragma unroll
+                for (int m2 = m; m2 < GSLOT; ++m2) {
+                    const float4 h4 = hc[m2 / 4];
+                    const float hv = m2 % 4 == 0 ? h4.x : m2 % 4 == 1 ? h4.y : m2 % 4 == 2 ? h4.z : h4.w;
+                    cr[m2] = fmaf(d, hv, cr[m2]);
+                }
+#pragma unroll
+                for (int g = 0; g < GSLOT / 4; ++g) hc[g] = hn[g];
+                __builtin_amdgcn_sched_barrier(0);   // keep the one-column-ahead loads where they are
+            };
+            cvn = cvp[0];
+#pragma unroll
+            for (int g = 0; g < GSLOT / 4; ++g) hc[g] = Hl4[g];
+            static_for<0, GB>(column);
+            if (bad) {
+                // Rare: the block again from its start for this wave's rows,
+                // one lane per row, the same arithmetic in the same order,
+                // with the whole-grid scan where the window does not apply.
+                __asm__ volatile("" ::: "memory");   // reload, rather than keep the first loads live
+                load_raw(b);
+                add_corr(b);
+#pragma unroll
+                for (int m = 0; m < GSLOT; ++m) {
+                    Gs[rr][0][GQ * m + p] = er[m];
+                    Gs[rr][1][GQ * m + p] = qr[m];
+                    Gs[rr][2][GQ * m + p] = cr[m];
+                }
+                lds_wave_fence();
+                if (p == 0) {
+                    for (int jl = 0; jl < nb; ++jl) {
+                        const float4 cv = colv[buf][jl];
+                        const float xe = Gs[rr][0][jl], xq = Gs[rr][1][jl];
+                        bool fast;
+                        float2 dec = greedy_decide(xe, xq, Gs[rr][2][jl], cv, s, is, sg, qmin, qmax, fast);
+                        if (!fast) dec = greedy_scan(xe, xq, s, cv.x, Gs[rr][2][jl] - xe * cv.x, qmin, qmax);
+                        Gs[rr][0][jl] = dec.y;
+                        Gs[rr][1][jl] = dec.x;
+                        const float d = dec.y - xe;
+                        for (int j = jl + 1; j < nb; ++j)
+                            Gs[rr][2][j] = fmaf(d, Hl[buf][jl][j % GQ][j / GQ], Gs[rr][2][j]);
+                    }
+                }
+                lds_wave_fence();
+#pragma unroll
+                for (int m = 0; m < GSLOT; ++m) {
+                    er[m] = Gs[rr][0][GQ * m + p];
+                    qr[m] = Gs[rr][1][GQ * m + p];
+                }
             }
-        } else {
-            bad = bad | !fast;
-        }
-        const float d = quad_bcast<o>(ne - xe);
-        if (p == o) {
-            er[m] = ne;
-            qr[m] = bq;
-        }
 #pragma unroll
-        for (int m2 = m; m2 < GSLOT; ++m2) {
-            const float4 h4 = hc[m2 / 4];
-            const float hv = m2 % 4 == 0 ? h4.x : m2 % 4 == 1 ? h4.y : m2 % 4 == 2 ? h4.z : h4.w;
-            cr[m2] = cr[m2] + d * hv;
+            for (int m = 0; m < GSLOT; ++m) {
+                const int col = GQ * m + p;
+                if (b + 1 < nblk) Dl[b * GB + col][rr] = er[m] - e0[m];
+                if (live && (FULL || col < nb)) {
+                    err[r * cols + j0 + col] = er[m];
+                    Qf[r * cols + j0 + col] = qr[m];
+                }
+            }
+            if (b + 1 < nblk) load_raw(b + 1);   // in flight through the corrections
+        } else if (b + 1 < nblk) {
+#pragma unroll
+            for (int u = 0; u < GQ; ++u) acc[u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            put_tile(b + 1);
+            if (b > 0) corrections(b + 1, 0, 16 * b);
         }
+        lds_barrier();   // block b's changes are in Dl, block b + 1's tile in place
+        if (w == 1 && b + 1 < nblk) {
+            corrections(b + 1, 16 * b, 16 * b + 16);
+            // acc[u][v] = correction of row lr, column 4 (4 lk + v) + u
 #pragma unroll
-        for (int g = 0; g < GSLOT / 4; ++g) hc[g] = hn[g];
-        __builtin_amdgcn_sched_barrier(0);   // keep the one-column-ahead loads where they are
-    };
-    auto start = [&]() {
-        cvn = colv[0];
-#pragma unroll
-        for (int g = 0; g < GSLOT / 4; ++g) hc[g] = Hl4[g];
-    };
-    start();
-    auto fast_column = [&](auto JL) { column(JL, std::false_type{}); };
-    static_for<0, GB>(fast_column);
-    if (__builtin_amdgcn_ballot_w64(bad)) {   // rare: this wave's rows again, guarded
-        __asm__ volatile("" ::: "memory");   // reload, rather than keep the first loads live
-        load_state();
-        start();
-        auto guarded_column = [&](auto JL) { column(JL, std::true_type{}); };
-        static_for<0, GB>(guarded_column);
-    }
-#pragma unroll
-    for (int m = 0; m < GSLOT; ++m) {
-        const int col = GQ * m + p;
-        if (live && (FULL || col < nb)) {
-            err[r * cols + j0 + col] = er[m];
-            Qf[r * cols + j0 + col] = qr[m];
-            D[r * GB + col] = er[m] - e0[m];
+            for (int u = 0; u < GQ; ++u)
+                *reinterpret_cast<float4*>(&Xs[lr][u][4 * lk]) = make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
         }
+        lds_barrier();   // block b + 1's corrections are in Xs
     }
 }
 
@@ -351,11 +486,11 @@ constexpr int PROXY_PARTS = 1024;
 
 // Two-level pass.  Columns go in super-blocks of GSB: one GEMM gives the
 // cross terms of a whole super-block, C = err @ Hc[sb, :]^T (K = cols, full
-// tiles), and after each 64-column block its changes D update the rest of
-// the super-block, C[:, rest] += D @ Hc[blk, rest] (K = 64).  Cross terms of
-// later super-blocks come from the updated err.  Same sums as one GEMM per
-// block over all of err, in another fp32 order.
-constexpr int64_t GSB = 512;
+// tiles), and one launch of greedy_sb_kernel runs the super-block's 64-column
+// blocks, adding each block's changes to the later blocks' cross terms on
+// the way.  Cross terms of later super-blocks come from the updated err.
+// Same sums as the reference's GEMM per block over all of err, in another
+// fp32 order.
 // The cross-term GEMM of a super-block has few 128-tiles (rows / 128 x 4)
 // and a long K (= cols): it runs as GSPLIT products over K / GSPLIT each
 // (GSPLIT times the tiles, two per CU), summed in order by split_sum_kernel.
@@ -377,7 +512,7 @@ __global__ void split_sum_kernel(const float* __restrict__ P, int64_t rows, int6
 
 // part: scratch for the split products (GSPLIT * rows * GSB floats), or null.
 static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* C,
-                       float* D, float* part, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
+                       float* part, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
     for (int64_t s0 = 0; s0 < cols; s0 += GSB) {
         const int64_t sw = std::min<int64_t>(GSB, cols - s0);
         const int64_t ks = cols / GSPLIT;
@@ -396,26 +531,16 @@ static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc
                        CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
             if ((rc = gemm_f32(g, st))) return rc;
         }
-        for (int64_t j0 = s0; j0 < s0 + sw; j0 += GB) {
-            const int nb = (int)std::min<int64_t>(GB, s0 + sw - j0);
-            {
-                ProfScope prof_scope(st, PT_GREEDY, (double)rows * nb * (nb + 4.0 * (qmax - qmin + 1)),
-                                     (double)rows * nb * 20);
-                if (nb == GB)
-                    hipLaunchKernelGGL(greedy_block_kernel<true>, dim3((unsigned)cdiv(rows, GQR)), dim3(64), 0, st, err,
-                                       Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin, qmax);
-                else
-                    hipLaunchKernelGGL(greedy_block_kernel<false>, dim3((unsigned)cdiv(rows, GQR)), dim3(64), 0, st,
-                                       err, Qf, srow, Hc, cols, hd, C + (j0 - s0), GSB, D, rows, cols, j0, nb, qmin,
-                                       qmax);
-                IC_CHECK_LAUNCH();
-            }
-            const int64_t rest = s0 + sw - (j0 + nb);
-            if (rest > 0) {
-                GemmArgs u{rows, rest, nb, 1.0f, 1.0f, D, GB, 0, Hc + j0 * cols + j0 + nb, cols, 0,
-                           C + (j0 + nb - s0), GSB, 0, 0, 0, CMASK_FULL, KR_FULL, 1, PT_GEMM_GREEDY};
-                if ((rc = gemm_f32(u, st))) return rc;
-            }
+        {
+            ProfScope prof_scope(st, PT_GREEDY, (double)rows * sw * (GB + 2.0 * sw), (double)rows * sw * 20);
+            const bool full = sw % GB == 0 && cols % 4 == 0;
+            if (full)
+                hipLaunchKernelGGL(greedy_sb_kernel<true>, dim3((unsigned)cdiv(rows, GQR)), dim3(128), 0, st, err, Qf,
+                                   srow, Hc, cols, hd, C, rows, cols, s0, (int)sw, qmin, qmax);
+            else
+                hipLaunchKernelGGL(greedy_sb_kernel<false>, dim3((unsigned)cdiv(rows, GQR)), dim3(128), 0, st, err, Qf,
+                                   srow, Hc, cols, hd, C, rows, cols, s0, (int)sw, qmin, qmax);
+            IC_CHECK_LAUNCH();
         }
     }
     return IC_OK;
@@ -475,7 +600,7 @@ extern "C" int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64
 }
 
 extern "C" int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols) {
-    return (2 * rows * cols + rows * (GSB + GB) + GSPLIT * rows * GSB) * (int64_t)sizeof(float) + 256;
+    return (2 * rows * cols + rows * GSB + GSPLIT * rows * GSB) * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
@@ -490,9 +615,9 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
     float* cross = Qf + rows * cols;
     hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
     IC_CHECK_LAUNCH();
-    float* part = cross + rows * (GSB + GB);
+    float* part = cross + rows * GSB;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, cross + rows * GSB, part, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
@@ -501,7 +626,7 @@ extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const flo
 }
 
 extern "C" int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k) {
-    return (3 * rows * cols + rows * (GSB + GB) + cols * cols + cols * std::max<int64_t>(k, 1) + cols +
+    return (3 * rows * cols + rows * GSB + cols * cols + cols * std::max<int64_t>(k, 1) + cols +
             GSPLIT * rows * GSB) * (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
 }
 
@@ -519,8 +644,7 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     float* Qf = err + rows * cols;
     float* EH = Qf + rows * cols;
     float* cross = EH + rows * cols;
-    float* D = cross + rows * GSB;
-    float* Hk = D + rows * GB;
+    float* Hk = cross + rows * GSB;
     float* US = Hk + cols * cols;
     float* hd = US + cols * std::max<int64_t>(k, 1);
     float* split_part = hd + cols;
@@ -544,7 +668,7 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     double prev = 0.0;
     int done = 0;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, D, split_part, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, split_part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
         done = p + 1;
         if (p + 1 == passes) break;   // a stall test after the last pass changes nothing
