@@ -179,6 +179,13 @@ int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damping, int me
  * greedy search).  ic_hessian_inverse applies the same damping first. */
 int ic_damp_hessian(float* H, int64_t batch, int64_t n, float damping, void* stream);
 
+/* C [N, N] = alpha * W^T W (full symmetric; W [M, N] at row pitch ldw):
+ * the upper triangle on the matrix cores, with ic_sgemm's accumulation
+ * order, mirrored onto the lower one (each pair of entries is the same sum
+ * of the same products).  Replaces converter/ldlq.py:186 (the weight-only
+ * Hessian H = W.T @ W / M). */
+int ic_gram_tn(const float* W, int64_t M, int64_t N, int64_t ldw, float alpha, float* C, void* stream);
+
 /* Lower Cholesky factor in place (upper part of the diagonal 128-blocks set
  * to 0, the rest of the upper triangle untouched); info as above; workspace
  * as for ic_hessian_inverse.  Replaces torch.linalg.cholesky. */

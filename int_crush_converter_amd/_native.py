@@ -49,6 +49,7 @@ _SIGS = {
     "ic_hessian_inverse": (_i32, [_vp, _i64, _i64, _f32, _i32, _vp, _vp, _vp]),
     "ic_cholesky": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "ic_damp_hessian": (_i32, [_vp, _i64, _i64, _f32, _vp]),
+    "ic_gram_tn": (_i32, [_vp, _i64, _i64, _i64, _f32, _vp, _vp]),
     "ic_gptq_row_params": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ic_gptq_workspace_bytes": (_i64, [_i64, _i64, _i32]),
     "ic_gptq_quantize": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),

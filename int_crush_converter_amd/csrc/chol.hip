@@ -550,12 +550,33 @@ __global__ __launch_bounds__(256) void panel64_kernel(float* A21, int64_t m, int
         }
 }
 
-// Copy the upper triangle onto the lower one (in place), per matrix.
-__global__ void mirror_upper_kernel(float* H, int64_t n, int64_t ld, int64_t stride) {
+// Copy the upper triangle onto the lower one (in place), per matrix, in
+// 32 x 32 tiles through LDS: both the upper source tile and the lower target
+// tile are read and written along rows.  Grid (tiles, tiles, batch), block
+// (32, 8); work-groups above the diagonal exit.
+__global__ void mirror_upper_tiled_kernel(float* H, int64_t n, int64_t ld, int64_t stride) {
+    const int ti = blockIdx.y, tj = blockIdx.x;   // target tile: rows ti, columns tj (ti >= tj)
+    if (ti < tj) return;
+    __shared__ float S[32][33];
     float* A = H + (int64_t)blockIdx.z * stride;
-    const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.y;
-    const int64_t j = (int64_t)blockIdx.x * 16 + threadIdx.x;
-    if (i < n && j < n && i > j) A[i * ld + j] = A[j * ld + i];
+    const int tx = threadIdx.x, ty = threadIdx.y;
+    for (int r = ty; r < 32; r += 8) {   // source: rows tj, columns ti (upper)
+        const int64_t i = (int64_t)tj * 32 + r, j = (int64_t)ti * 32 + tx;
+        if (i < n && j < n) S[r][tx] = A[i * ld + j];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int64_t i = (int64_t)ti * 32 + r, j = (int64_t)tj * 32 + tx;
+        if (i < n && j < n && i > j) A[i * ld + j] = S[tx][r];
+    }
+}
+
+static int mirror_upper(float* H, int64_t batch, int64_t n, int64_t ld, int64_t stride, hipStream_t st) {
+    IC_REQUIRE(batch <= 65535 && cdiv(n, 32) < 65536, "mirror_upper: too large");
+    const dim3 tg((unsigned)cdiv(n, 32), (unsigned)cdiv(n, 32), (unsigned)batch);
+    hipLaunchKernelGGL(mirror_upper_tiled_kernel, tg, dim3(32, 8), 0, st, H, n, ld, stride);
+    IC_CHECK_LAUNCH();
+    return IC_OK;
 }
 
 // Transpose the lower triangle into the upper one and zero the lower (in place):
@@ -786,8 +807,7 @@ extern "C" int ic_hessian_inverse(float* H, int64_t batch, int64_t n, float damp
     if (rc) return rc;
     dim3 tb(16, 16), tg((unsigned)cdiv(n, 16), (unsigned)cdiv(n, 16), (unsigned)batch);
     if (method == 2) return IC_OK;   // the lower part keeps L: finite, never read by such callers
-    hipLaunchKernelGGL(mirror_upper_kernel, tg, tb, 0, st, H, n, ld, sH);
-    IC_CHECK_LAUNCH();
+    if ((rc = mirror_upper(H, batch, n, ld, sH, st))) return rc;
     if (method == 1) {
         // upper Cholesky factor of H^-1 (converter/gptq.py:91-110): L2 = chol(H^-1), return L2^T
         rc = potrf(H, batch, n, ld, sH, dinv64, info + batch, st);
@@ -805,6 +825,20 @@ extern "C" int ic_damp_hessian(float* H, int64_t batch, int64_t n, float damping
     hipLaunchKernelGGL(damp_kernel, dim3((unsigned)batch), dim3(256), 0, as_stream(stream), H, n, n, n * n, damping);
     IC_CHECK_LAUNCH();
     return IC_OK;
+}
+
+extern "C" int ic_gram_tn(const float* W, int64_t M, int64_t N, int64_t ldw, float alpha, float* C, void* stream) {
+    IC_REQUIRE(W && C, "ic_gram_tn: null pointer");
+    IC_REQUIRE(M >= 0 && N >= 0 && ldw >= N, "ic_gram_tn: bad size");
+    if (N == 0) return IC_OK;
+    hipStream_t st = as_stream(stream);
+    // C[i][j] and C[j][i] are the same products summed in the same order:
+    // the upper triangle on the matrix cores, then mirrored
+    GemmArgs g{N, N, M, alpha, 0.0f, W, ldw, 0, W, ldw, 0, C, N, 0, 1, 0, CMASK_UPPER, KR_FULL, 1, PT_OTHER,
+               (double)N * (N + 1) * M};
+    int rc = gemm_f32(g, st);
+    if (rc) return rc;
+    return mirror_upper(C, 1, N, N, N * N, st);
 }
 
 extern "C" int ic_cholesky(float* H, int64_t batch, int64_t n, int* info, void* workspace, void* stream) {

@@ -516,6 +516,18 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
 // there the 128-tile's few long stages leave the tail of the launch on a
 // fraction of the chip.
 constexpr int64_t SMALL_TILE_LIMIT = 256;
+constexpr int64_t CHIP_CUS = 256;
+// C = X^T X with K from max(tile row, tile column) (the inverse's X^T X on a
+// triangular grid): the (0, 0) tile runs all of K.  When that one tile,
+// sharing its CU with a second work-group, outlasts the average 128-tile
+// work per CU, the launch is bound by it, and 64-tiles cut it to a quarter
+// (same chunks of K, same order of accumulation).
+static bool long_tile_bound(const GemmArgs& g) {
+    const int64_t tm = cdiv(g.M, 128);
+    double total = 0.0;   // K stages over all kept tiles
+    for (int64_t j = 0; j < tm; ++j) total += (double)(j + 1) * std::max<int64_t>(0, g.K - 128 * j) / BK;
+    return 2.0 * g.K / BK > total * g.batch / CHIP_CUS;
+}
 constexpr int64_t SHORT_K = 256, SHORT_K_TILE_LIMIT = 1024;
 
 int gemm_f32(const GemmArgs& g, hipStream_t st) {
@@ -532,6 +544,7 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     bool tri;
     const int64_t t128 = tile_count<128>(g, tri) * g.batch;
     if (t128 < SMALL_TILE_LIMIT || (g.K <= SHORT_K && t128 < SHORT_K_TILE_LIMIT)) return launch_gemm<64>(g, aligned, st);
+    if (tri && g.krange == KR_FROM_MAXIJ && long_tile_bound(g)) return launch_gemm<64>(g, aligned, st);
     return launch_gemm<128>(g, aligned, st);
 }
 

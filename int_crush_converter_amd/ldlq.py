@@ -41,11 +41,10 @@ def _row_absmax(W):
 
 
 def _gemm_tn(W: torch.Tensor, alpha: float) -> torch.Tensor:
-    """alpha * W^T W on the matrix cores (fp32)."""
+    """alpha * W^T W on the matrix cores (fp32; one triangle computed, mirrored)."""
     M, N = W.shape
     C = torch.empty(N, N, dtype=torch.float32, device=W.device)
-    nat.check(_lib().ic_sgemm(1, 0, N, N, M, alpha, W.data_ptr(), N, W.data_ptr(), N, 0.0, C.data_ptr(), N, 0, 0,
-                              nat.stream()), "ic_sgemm")
+    nat.check(_lib().ic_gram_tn(W.data_ptr(), M, N, N, alpha, C.data_ptr(), nat.stream()), "ic_gram_tn")
     return C
 
 

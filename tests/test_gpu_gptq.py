@@ -66,16 +66,23 @@ def test_sgemm_large_tiles_match_fp64(gpu_dev, M, N, K, ta, tb):
 
 @pytest.mark.parametrize("n", [300, 2900])
 def test_sgemm_masks_both_tiles(gpu_dev, n):
-    # n = 2900: 276 lower tiles of 128 (128-tile kernel); n = 300: 64-tile kernel
+    # n = 2900: 276 upper tiles of 128; with K from max(i0, j0) the (0, 0)
+    # tile's full K bounds the launch and it runs 64-tiles, with the whole K
+    # range the 128-tile kernel.  n = 300: 64-tile kernel.  The two results
+    # are the same sums in the same order.
     g = torch.Generator().manual_seed(n)
     X = torch.tril(torch.randn(n, n, generator=g)) / n ** 0.5
-    C = torch.full((n, n), float("nan"))
-    got = _sgemm(X.to(gpu_dev), X.to(gpu_dev), C.to(gpu_dev), 1, 0, 1.0, 0.0, cmask=2, krange=1).cpu()
     want = X.double().T @ X.double()
     iu = torch.triu_indices(n, n)
-    assert torch.allclose(got[iu[0], iu[1]].double(), want[iu[0], iu[1]], atol=3e-5)
     il = torch.tril_indices(n, n, -1)
-    assert torch.isnan(got[il[0], il[1]]).all()
+    outs = []
+    for krange in (1, 0):
+        C = torch.full((n, n), float("nan"))
+        got = _sgemm(X.to(gpu_dev), X.to(gpu_dev), C.to(gpu_dev), 1, 0, 1.0, 0.0, cmask=2, krange=krange).cpu()
+        assert torch.allclose(got[iu[0], iu[1]].double(), want[iu[0], iu[1]], atol=3e-5)
+        assert torch.isnan(got[il[0], il[1]]).all()
+        outs.append(got[iu[0], iu[1]])
+    assert torch.equal(outs[0], outs[1])
     A = torch.randn(n, 160, generator=g)
     C = torch.randn(n, n, generator=g)
     got = _sgemm(A.to(gpu_dev), A.to(gpu_dev), C.clone().to(gpu_dev), 0, 1, -1.0, 1.0, cmask=1).cpu()
@@ -84,6 +91,22 @@ def test_sgemm_masks_both_tiles(gpu_dev, n):
     assert torch.allclose(got[il[0], il[1]].double(), want[il[0], il[1]], atol=1e-4)
     iu = torch.triu_indices(n, n, 1)
     assert torch.equal(got[iu[0], iu[1]], C[iu[0], iu[1]])
+
+
+@pytest.mark.parametrize("M,N", [(300, 200), (1000, 2900), (257, 4096)])
+def test_gram_tn_is_the_full_product(gpu_dev, M, N):
+    """ic_gram_tn (one triangle, mirrored) equals ic_sgemm's full W^T W bit
+    for bit, and the fp64 product to fp32 accuracy."""
+    from int_crush_converter_amd import _native as nat
+    g = torch.Generator().manual_seed(M + N)
+    W = (torch.randn(M, N, generator=g) * torch.exp(torch.randn(1, N, generator=g))).to(gpu_dev)
+    full = _sgemm(W, W, torch.empty(N, N, device=gpu_dev), 1, 0, 1.0 / M, 0.0)
+    C = torch.full((N, N), float("nan"), device=gpu_dev)
+    nat.check(nat.lib().ic_gram_tn(W.data_ptr(), M, N, N, 1.0 / M, C.data_ptr(), nat.stream()), "ic_gram_tn")
+    assert torch.equal(C, full)
+    want = W.double().T @ W.double() / M
+    scale = (W.abs().double().T @ W.abs().double() / M).max().item()
+    assert (C.double() - want).abs().max().item() <= 2e-6 * scale * max(1, M ** 0.5)
 
 
 def test_sgemm_masks(gpu_dev):
