@@ -125,10 +125,10 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
             for (int r = r0; r < R; ++r) hn[r] = Hs[jn * SW_NB + r * SW_HALF + p];
             const float hdn = hjj[jn], dvn = dinv[jn];
             const bool dkn = dok[jn] != 0;
-            // the owner's value of this lane's row
-            const float x = row_owner<LPR>(w[r0], o, half);
             float q, e;
             if (MODE == SWEEP_GPTQ) {
+                // the owner's value of this lane's row
+                const float x = row_owner<LPR>(w[r0], o, half);
                 float y;
                 if (EXACT) {
                     y = div_rn_wave(x, s_row, s_rrow, srow_ok);
@@ -149,8 +149,13 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
                 }
                 e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
             } else {
-                const float s_el = row_owner<LPR>(sc[r0], o, half);
-                const float s_rc = row_owner<LPR>(scr[r0], o, half);
+                // Every lane quantises its own column of register r0 (the
+                // owner's is column j) with its own element scale; the
+                // owner's error is then broadcast over the row.  The
+                // reference's sign-flip correction is inert here: the scales
+                // are clamped to >= 1e-8 (or NaN), so the rounded, clamped
+                // code has the sign of x or is 0, and it is left out.
+                const float x = w[r0], s_el = sc[r0], s_rc = scr[r0];
                 float y;
                 if (EXACT) {
                     y = div_rn_wave(x, s_el, s_rc, div_b_ok(s_el));
@@ -159,17 +164,8 @@ __device__ __forceinline__ void sweep_cols(float (&w)[SW_NB / LPR], float (&qv)[
                     y = fabsf(x) < 0x1p61f ? y : x * s_rc;
                     bad = bad || !div_b_ok(s_el);
                 }
-                q = clampf_med3(rhaz_trunc(y), qmin, qmax);
-                // sign-flip correction (inert for positive scales)
-                const float ws = fabsf(x) > 1e-8f ? (x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f))
-                                                  : (q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f));
-                const float qs = q > 0.0f ? 1.0f : (q < 0.0f ? -1.0f : 0.0f);
-                const bool flip = ws * qs < 0.0f;
-                const bool can = flip && (q > qmin);
-                if (flip && q == qmin) q = qmax;
-                if (can) q = -q;
-                q = clampf(q, qmin, qmax);
-                e = (x - q * s_el) * dvj;
+                q = clampf(clampf_med3(rhaz_trunc(y), qmin, qmax), qmin, qmax);
+                e = row_owner<LPR>((x - q * s_el) * dvj, o, half);
             }
             const bool own = p == o;
             qv[r0] = own ? q : qv[r0];
