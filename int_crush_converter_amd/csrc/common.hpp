@@ -11,6 +11,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
+#include <type_traits>
 #include <string>
 
 #include "../../include/ic_abi.h"
@@ -121,6 +122,29 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Orders a wave's own LDS accesses (exchanges between its lanes), with no
+// work-group barrier.
+__device__ __forceinline__ void lds_wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// f(std::integral_constant<int, i>) for i = I .. N-1: a loop whose index
+// is a compile-time constant in the body (register-array slots).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// Lane P's value of v in every lane of its DPP quad (lanes 4k .. 4k+3).
+template <int P>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), P * 0x55, 0xf, 0xf, false));
 }
 
 // clampf as a median of three (NaN still propagates).

@@ -167,19 +167,6 @@ constexpr int GSLOT = GB / GQ;    // block columns per lane
 constexpr float GREEDY_GAMMA = 128.0f;
 constexpr float GREEDY_TMAX = 65536.0f;
 
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
-template <int P>
-__device__ __forceinline__ float quad_bcast(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), P * 0x55, 0xf, 0xf, false));
-}
-
 // The reference's scan over the whole grid (first minimum, codes start at
 // q): {code, new err}.
 __device__ __forceinline__ float2 greedy_scan(float e, float q, float s, float h, float cross, float qmin,
@@ -216,13 +203,6 @@ __device__ __forceinline__ float2 greedy_decide(float e, float q, float c, float
 }
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-// Orders a wave's own LDS accesses (exchanges between its lanes), with no
-// work-group barrier.
-__device__ __forceinline__ void lds_wave_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // One super-block of a greedy pass (columns s0 .. s0 + sw, sw <= GSB) for
 // GQR rows, one launch per super-block.  Csb [rows, GSB] holds
