@@ -472,6 +472,191 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
     }
 }
 
+// Row sweep: full 128-column blocks of one matrix (groups == 1), 16 lanes (a
+// DPP row) per row, 4 rows per wave.  Lane p of a row owns the block
+// columns j = 16 m + p (m = 0..7): their weights, codes and errors stay in
+// registers.  At column j the owner (p = j mod 16) quantises its weight and
+// forms the error, one DPP row broadcast (row_newbcast) hands the error to
+// the row's lanes, and each lane updates its later columns,
+// w <- w - RN(e Hinv[j][k]) (the product rounded, then subtracted, in column
+// order: the reference's sequence of roundings).  The column loop is
+// unrolled (the slots are registers) and Hinv's next row share and pivot
+// are fetched a column ahead.  The other lanes of the row run the same
+// steps on their own columns, results unused, so the common path has no
+// branch.  Division uses the fast correctly rounded quotient; a value
+// outside its exact domain (as in sweep_cols, plus LDLQ dividends outside
+// [2^-60, 2^61)) sends the wave's rows through the block once more, one lane
+// per row from LDS, with the IEEE-exact test on every division (rare).  WV
+// waves share the staged Hinv block.
+constexpr int SR_L = 16;             // lanes per row
+constexpr int SR_M = SW_NB / SR_L;   // columns per lane
+constexpr int SR_ROWS = 64 / SR_L;   // rows per wave
+
+// Lane L's value of v in every lane of its 16-lane DPP row.
+template <int L>
+__device__ __forceinline__ float row_bcast16(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xf, 0xf, false));
+}
+
+template <int MODE, bool ZP, int WV>
+__global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
+    __shared__ __align__(16) float Hq[SW_NB][SR_L][SR_M];   // Hq[j][p][m] = Hinv[j][16 m + p]
+    __shared__ __align__(16) float4 piv[SW_NB];          // {Hinv_jj, 1 / d_j, d_j in the fast domain, 0}
+    __shared__ float Xr[WV * SR_ROWS][SW_NB + 1];        // exact rerun: weights, then errors
+    __shared__ signed char Qr[WV * SR_ROWS][SW_NB];      //              codes
+    const int tid = threadIdx.x, t = tid & 63, p = t & (SR_L - 1);
+    const int rw = (tid >> 6) * SR_ROWS + t / SR_L;      // row within the work-group
+    {
+        // the Hinv block: 32 loads per thread in flight, then their LDS stores
+        constexpr int NT = 64 * WV, CH = 32, ALL = SW_NB * SW_NB;
+#pragma unroll
+        for (int base = 0; base < ALL; base += NT * CH) {
+            float tmp[CH];
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                const int idx = base + tid + k * NT;
+                tmp[k] = idx < ALL ? a.H[(int64_t)(idx / SW_NB) * a.ldh + (idx % SW_NB)] : 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                const int idx = base + tid + k * NT, c = idx % SW_NB;
+                if (idx < ALL) Hq[idx / SW_NB][c % SR_L][c / SR_L] = tmp[k];
+            }
+        }
+        for (int j = tid; j < SW_NB; j += 64 * WV) {
+            const float hd = a.H[(int64_t)j * a.ldh + j];
+            float d = hd;
+            if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
+            piv[j] = make_float4(hd, 1.0f / d, div_b_ok(d) ? 1.0f : 0.0f, 0.0f);
+        }
+    }
+    __syncthreads();
+    const int64_t row = (int64_t)blockIdx.x * (WV * SR_ROWS) + rw;
+    const bool rv = row < a.rows;
+    const int64_t rrow = rv ? row : a.rows - 1;   // a row that exists (results not stored)
+    const float* wrow = a.W + rrow * a.ldw + a.col0;
+    float w[SR_M];
+#pragma unroll
+    for (int m = 0; m < SR_M; ++m) w[m] = wrow[SR_L * m + p];
+    float s_row = 1.0f, z_row = 0.0f;
+    float sc[MODE == SWEEP_LDLQ ? SR_M : 1], scr[MODE == SWEEP_LDLQ ? SR_M : 1];
+    if (MODE == SWEEP_GPTQ) {
+        s_row = a.s[rrow];
+        if (ZP) z_row = a.zp[rrow];
+    } else {
+#pragma unroll
+        for (int m = 0; m < SR_M; ++m) {
+            float v = a.s[rrow * a.lds + a.col0 + SR_L * m + p];
+            v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
+            sc[m] = v;
+            scr[m] = 1.0f / v;
+        }
+    }
+    const float s_rrow = 1.0f / s_row;
+    const bool srow_ok = div_b_ok(s_row);
+    float qv[SR_M], ev[SR_M];
+    uint64_t badm = 0;   // LDLQ: lanes with a value outside the fast division's domain
+    float amax = 0.0f, amin = INFINITY;   // GPTQ: the dividends' range (amin = 0: a pivot outside)
+    float4 pvn = piv[0], hc[SR_M / 4], hn[SR_M / 4];
+    const float4* Hq4 = reinterpret_cast<const float4*>(&Hq[0][p][0]);   // + j * SW_NB / 4
+#pragma unroll
+    for (int g = 0; g < SR_M / 4; ++g) hc[g] = Hq4[g];
+    auto column = [&](auto J) {
+        constexpr int j = decltype(J)::value, m = j / SR_L, o = j % SR_L;
+        const float4 pv = pvn;
+        if constexpr (j + 1 < SW_NB) {
+            pvn = piv[j + 1];
+#pragma unroll
+            for (int g = (j + 1) / (4 * SR_L); g < SR_M / 4; ++g) hn[g] = Hq4[(j + 1) * (SW_NB / 4) + g];
+        }
+        const float x = w[m];
+        float q, e;
+        if (MODE == SWEEP_GPTQ) {
+            float y = div_rn_fast(x, s_row, s_rrow);
+            if (ZP) y = y + z_row;
+            q = clampf_med3(rhaz_trunc(y), a.qmin, a.qmax);
+            const float deq = ZP ? (q - z_row) * s_row : q * s_row;
+            const float num = x - deq;
+            e = div_rn_fast(num, pv.x, pv.y);
+            const float an = fabsf(num);
+            amax = fmaxf(amax, fmaxf(fabsf(x), an));
+            amin = fminf(amin, an == 0.0f ? INFINITY : an);
+            amin = pv.z == 0.0f ? 0.0f : amin;   // a pivot outside the domain
+            __asm__ volatile("" : "+v"(amax), "+v"(amin));   // fold this column in now, not at the end
+            e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
+        } else {
+            const float y = div_rn_fast(x, sc[m], scr[m]);
+            const float ax = fabsf(x);
+            badm |= __builtin_amdgcn_ballot_w64(!div_b_ok(sc[m]) || ax >= 0x1p61f || (ax < 0x1p-60f && ax != 0.0f));
+            __asm__ volatile("" : "+s"(badm));   // fold this column in now, not at the end
+            q = clampf(clampf_med3(rhaz_trunc(y), a.qmin, a.qmax), a.qmin, a.qmax);
+            e = (x - q * sc[m]) * pv.y;
+        }
+        const float d = row_bcast16<o>(e);
+        if (p == o) {
+            qv[m] = q;
+            ev[m] = e;
+        }
+#pragma unroll
+        for (int m2 = m; m2 < SR_M; ++m2) {
+            const float4 h4 = hc[m2 / 4];
+            const float hv = m2 % 4 == 0 ? h4.x : m2 % 4 == 1 ? h4.y : m2 % 4 == 2 ? h4.z : h4.w;
+            w[m2] = w[m2] - d * hv;
+        }
+#pragma unroll
+        for (int g = 0; g < SR_M / 4; ++g) hc[g] = hn[g];
+        __builtin_amdgcn_sched_barrier(0);   // keep the one-column-ahead loads where they are
+    };
+    static_for<0, SW_NB>(column);
+    const bool bad = MODE == SWEEP_GPTQ ? !srow_ok || amax >= 0x1p61f || amin < 0x1p-60f : false;
+    if (__builtin_expect((__builtin_amdgcn_ballot_w64(bad) | badm) != 0, 0)) {
+        // the wave's rows again from the block's start, one lane per row,
+        // every division IEEE-exact (div_rn tests its domain per value)
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < SR_M; ++m) Xr[rw][SR_L * m + p] = wrow[SR_L * m + p];
+        lds_wave_fence();
+        if (p == 0) {
+            for (int j = 0; j < SW_NB; ++j) {
+                const float x = Xr[rw][j];
+                const float4 pv = piv[j];
+                float q, e;
+                if (MODE == SWEEP_GPTQ) {
+                    float y = div_rn(x, s_row, s_rrow, srow_ok);
+                    if (ZP) y = y + z_row;
+                    q = clampf_med3(rhaz_trunc(y), a.qmin, a.qmax);
+                    const float deq = ZP ? (q - z_row) * s_row : q * s_row;
+                    e = div_rn(x - deq, pv.x, pv.y, pv.z != 0.0f);
+                    e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
+                } else {
+                    float v = a.s[rrow * a.lds + a.col0 + j];
+                    v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
+                    const float y = div_rn(x, v, 1.0f / v, div_b_ok(v));
+                    q = clampf(clampf_med3(rhaz_trunc(y), a.qmin, a.qmax), a.qmin, a.qmax);
+                    e = (x - q * v) * pv.y;
+                }
+                Qr[rw][j] = (signed char)(int)q;
+                Xr[rw][j] = e;
+                for (int k = j + 1; k < SW_NB; ++k) Xr[rw][k] = Xr[rw][k] - e * Hq[j][k % SR_L][k / SR_L];
+            }
+        }
+        lds_wave_fence();
+#pragma unroll
+        for (int m = 0; m < SR_M; ++m) {
+            qv[m] = (float)Qr[rw][SR_L * m + p];
+            ev[m] = Xr[rw][SR_L * m + p];
+        }
+    }
+    if (rv) {
+#pragma unroll
+        for (int m = 0; m < SR_M; ++m) {
+            const int c = SR_L * m + p;
+            a.Q[row * a.ldq + a.col0 + c] = (int8_t)(int)qv[m];
+            a.E[row * a.lde + c] = ev[m];
+        }
+    }
+}
+
 static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
     const bool wide = a.rows * groups >= SW_THROUGHPUT_ROWS;
@@ -479,22 +664,33 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
                  (double)groups * (a.rows * a.nb * 9.0 + 4.0 * a.nb * a.nb));
     if (groups == 1 && a.nb == SW_NB) {
-        // whole blocks of one matrix: the quad sweep, two waves per
-        // work-group (measured: 2.80 ms per headline layer against 3.05 with
-        // one and 3.38 with four), four sharing Hinv when there are more rows
-        // than one work-group per CU covers
-        const bool two = a.rows <= 256 * 2 * SQ_ROWS;
-        const dim3 g4((unsigned)cdiv(a.rows, (two ? 2 : 4) * SQ_ROWS));
+        // whole blocks of one matrix: the row sweep (16 lanes per row, four
+        // waves per work-group sharing the staged Hinv block) while two
+        // work-groups per CU cover the rows; beyond that the quad sweep's 64
+        // rows per work-group (measured at 12288 rows: 0.92 ms per layer
+        // against 0.97)
         const bool zp = a.zp != nullptr;
-#define ICQ_SWEEP4(M, Z, W) hipLaunchKernelGGL((sweep4_kernel<M, Z, W>), g4, dim3(64 * W), 0, st, a)
-        if (a.mode == SWEEP_GPTQ) {
-            if (two) { if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true, 2); else ICQ_SWEEP4(SWEEP_GPTQ, false, 2); }
-            else { if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true, 4); else ICQ_SWEEP4(SWEEP_GPTQ, false, 4); }
+        if (a.rows <= 2 * 256 * 4 * SR_ROWS) {
+            const dim3 g16((unsigned)cdiv(a.rows, 4 * SR_ROWS));
+#define ICQ_SWEEP16(M, Z) hipLaunchKernelGGL((sweep16_kernel<M, Z, 4>), g16, dim3(256), 0, st, a)
+            if (a.mode == SWEEP_GPTQ) {
+                if (zp) ICQ_SWEEP16(SWEEP_GPTQ, true);
+                else ICQ_SWEEP16(SWEEP_GPTQ, false);
+            } else {
+                ICQ_SWEEP16(SWEEP_LDLQ, false);
+            }
+#undef ICQ_SWEEP16
         } else {
-            if (two) ICQ_SWEEP4(SWEEP_LDLQ, false, 2);
-            else ICQ_SWEEP4(SWEEP_LDLQ, false, 4);
-        }
+            const dim3 g4((unsigned)cdiv(a.rows, 4 * SQ_ROWS));
+#define ICQ_SWEEP4(M, Z) hipLaunchKernelGGL((sweep4_kernel<M, Z, 4>), g4, dim3(256), 0, st, a)
+            if (a.mode == SWEEP_GPTQ) {
+                if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true);
+                else ICQ_SWEEP4(SWEEP_GPTQ, false);
+            } else {
+                ICQ_SWEEP4(SWEEP_LDLQ, false);
+            }
 #undef ICQ_SWEEP4
+        }
         IC_CHECK_LAUNCH();
         return IC_OK;
     }
