@@ -294,8 +294,8 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
     }
 }
 
-// Quad sweep: full 128-column blocks of one matrix (groups == 1), 4 lanes (a
-// DPP quad) per row, 16 rows per wave.  Lane p of a row owns the block
+// Quad sweep: full 128-column blocks, 4 lanes (a DPP quad) per row, 16 rows
+// per wave.  Lane p of a row owns the block
 // columns j = 4 m + p (m = 0..31): their weights, codes and errors stay in
 // registers.  At column j the owner (p = j mod 4) quantises its weight and
 // forms the error, one quad broadcast hands the error to the row's lanes,
@@ -307,20 +307,25 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 // columns, results unused, so the common path has no branch.  Division
 // uses the fast correctly rounded quotient; a value outside its exact
 // domain (as in sweep_cols, plus LDLQ dividends outside [2^-60, 2^61))
-// sends the wave's rows through the block once more, one lane per row from
-// LDS, with the IEEE-exact test on every division (rare).  WV waves share
-// the staged Hinv block.
+// sends the wave's rows through the block once more, one lane per row with
+// the row's error output as its working row, with the IEEE-exact test on
+// every division (rare).  WV waves share the staged Hinv block; blockIdx.y
+// is the column group of a block-diagonal Hessian.  Two work-groups fit a
+// CU (LDS and at most 256 VGPRs), so batched launches keep two waves per
+// SIMD.
 constexpr int SQ_M = SW_NB / 4;   // columns per lane
 constexpr int SQ_ROWS = 16;       // rows per wave
 
 template <int MODE, bool ZP, int WV>
-__global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
+__global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
     __shared__ __align__(16) float Hq[SW_NB][4][SQ_M];   // Hq[j][p][m] = Hinv[j][4 m + p]
     __shared__ __align__(16) float4 piv[SW_NB];          // {Hinv_jj, 1 / d_j, d_j in the fast domain, 0}
-    __shared__ float Xr[WV * SQ_ROWS][SW_NB + 1];        // exact rerun: weights, then errors
-    __shared__ signed char Qr[WV * SQ_ROWS][SW_NB];      //              codes
     const int tid = threadIdx.x, t = tid & 63, p = t & 3;
     const int rw = (tid >> 6) * SQ_ROWS + (t >> 2);      // row within the work-group
+    const int g = blockIdx.y;                            // column group (block-diagonal Hessians)
+    const int64_t col0 = a.col0 + (int64_t)g * a.gcol;
+    const float* Hg = a.H + (int64_t)g * a.hg;
+    float* Eg = a.E + (int64_t)g * a.eg;
     {
         // the Hinv block: 32 loads per thread in flight, then their LDS stores
         constexpr int NT = 64 * WV, CH = 32, PER = SW_NB * SW_NB / NT;
@@ -330,7 +335,7 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
                 const int idx = tid + (k0 + k) * NT;
-                tmp[k] = a.H[(int64_t)(idx / SW_NB) * a.ldh + (idx % SW_NB)];
+                tmp[k] = Hg[(int64_t)(idx / SW_NB) * a.ldh + (idx % SW_NB)];
             }
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
             }
         }
         for (int j = tid; j < SW_NB; j += 64 * WV) {
-            const float hd = a.H[(int64_t)j * a.ldh + j];
+            const float hd = Hg[(int64_t)j * a.ldh + j];
             float d = hd;
             if (MODE == SWEEP_LDLQ) d = d > 1e-8f ? d : (d != d ? d : 1e-8f);
             piv[j] = make_float4(hd, 1.0f / d, div_b_ok(d) ? 1.0f : 0.0f, 0.0f);
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
     const int64_t row = (int64_t)blockIdx.x * (WV * SQ_ROWS) + rw;
     const bool rv = row < a.rows;
     const int64_t rrow = rv ? row : a.rows - 1;   // a row that exists (results not stored)
-    const float* wrow = a.W + rrow * a.ldw + a.col0;
+    const float* wrow = a.W + rrow * a.ldw + col0;
     float w[SQ_M];
 #pragma unroll
     for (int m = 0; m < SQ_M; ++m) w[m] = wrow[4 * m + p];
@@ -361,7 +366,7 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
     } else {
 #pragma unroll
         for (int m = 0; m < SQ_M; ++m) {
-            float v = a.s[rrow * a.lds + a.col0 + 4 * m + p];
+            float v = a.s[rrow * a.lds + col0 + 4 * m + p];
             v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
             sc[m] = v;
             scr[m] = 1.0f / v;
@@ -426,14 +431,15 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
     const bool bad = MODE == SWEEP_GPTQ ? !srow_ok || amax >= 0x1p61f || amin < 0x1p-60f : false;
     if (__builtin_expect((__builtin_amdgcn_ballot_w64(bad) | badm) != 0, 0)) {
         // the wave's rows again from the block's start, one lane per row,
-        // every division IEEE-exact (div_rn tests its domain per value)
+        // every division IEEE-exact (div_rn tests its domain per value); the
+        // row's error output is the working row, and that lane writes the
+        // row's codes and errors itself
         __asm__ volatile("" ::: "memory");
-#pragma unroll
-        for (int m = 0; m < SQ_M; ++m) Xr[rw][4 * m + p] = wrow[4 * m + p];
-        lds_wave_fence();
-        if (p == 0) {
+        if (rv && p == 0) {
+            float* xr = Eg + row * a.lde;
+            for (int c = 0; c < SW_NB; ++c) xr[c] = wrow[c];
             for (int j = 0; j < SW_NB; ++j) {
-                const float x = Xr[rw][j];
+                const float x = xr[j];
                 const float4 pv = piv[j];
                 float q, e;
                 if (MODE == SWEEP_GPTQ) {
@@ -444,30 +450,25 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
                     e = div_rn(x - deq, pv.x, pv.y, pv.z != 0.0f);
                     e = e != e ? 0.0f : __builtin_amdgcn_fmed3f(e, -100.0f, 100.0f);
                 } else {
-                    float v = a.s[rrow * a.lds + a.col0 + j];
+                    float v = a.s[rrow * a.lds + col0 + j];
                     v = v > 1e-8f ? v : (v != v ? v : 1e-8f);
                     const float y = div_rn(x, v, 1.0f / v, div_b_ok(v));
                     q = clampf(clampf_med3(rhaz_trunc(y), a.qmin, a.qmax), a.qmin, a.qmax);
                     e = (x - q * v) * pv.y;
                 }
-                Qr[rw][j] = (signed char)(int)q;
-                Xr[rw][j] = e;
-                for (int k = j + 1; k < SW_NB; ++k) Xr[rw][k] = Xr[rw][k] - e * Hq[j][k & 3][k >> 2];
+                a.Q[row * a.ldq + col0 + j] = (int8_t)(int)q;
+                xr[j] = e;
+                for (int k = j + 1; k < SW_NB; ++k) xr[k] = xr[k] - e * Hq[j][k & 3][k >> 2];
             }
         }
-        lds_wave_fence();
-#pragma unroll
-        for (int m = 0; m < SQ_M; ++m) {
-            qv[m] = (float)Qr[rw][4 * m + p];
-            ev[m] = Xr[rw][4 * m + p];
-        }
+        return;
     }
     if (rv) {
 #pragma unroll
         for (int m = 0; m < SQ_M; ++m) {
             const int c = 4 * m + p;
-            a.Q[row * a.ldq + a.col0 + c] = (int8_t)(int)qv[m];
-            a.E[row * a.lde + c] = ev[m];
+            a.Q[row * a.ldq + col0 + c] = (int8_t)(int)qv[m];
+            Eg[row * a.lde + c] = ev[m];
         }
     }
 }
@@ -663,6 +664,23 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     const int64_t wgs = cdiv(a.rows, wide ? sw_rows<SW_LPR_THROUGHPUT>() : sw_rows<SW_LPR_LATENCY>());
     ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
                  (double)groups * (a.rows * a.nb * 9.0 + 4.0 * a.nb * a.nb));
+    if (groups > 1 && a.nb == SW_NB) {
+        // batched column groups (block-diagonal Hessians): many work-groups per
+        // CU over the launch, where the quad sweep's few instructions per
+        // row and column count (two work-groups per CU)
+        const dim3 g4((unsigned)cdiv(a.rows, 4 * SQ_ROWS), (unsigned)groups);
+        const bool zp = a.zp != nullptr;
+#define ICQ_SWEEP4(M, Z) hipLaunchKernelGGL((sweep4_kernel<M, Z, 4>), g4, dim3(256), 0, st, a)
+        if (a.mode == SWEEP_GPTQ) {
+            if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true);
+            else ICQ_SWEEP4(SWEEP_GPTQ, false);
+        } else {
+            ICQ_SWEEP4(SWEEP_LDLQ, false);
+        }
+#undef ICQ_SWEEP4
+        IC_CHECK_LAUNCH();
+        return IC_OK;
+    }
     if (groups == 1 && a.nb == SW_NB) {
         // whole blocks of one matrix: the row sweep (16 lanes per row, four
         // waves per work-group sharing the staged Hinv block) while two
