@@ -417,6 +417,7 @@ __global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
             qv[m] = q;
             ev[m] = e;
         }
+        __asm__ volatile("" : "+v"(qv[m]), "+v"(ev[m]));   // select now: keeps the columns' q, e dead
 #pragma unroll
         for (int m2 = m; m2 < SQ_M; ++m2) {
             const float4 h4 = hc[m2 / 4];
@@ -508,15 +509,17 @@ __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
     const int tid = threadIdx.x, t = tid & 63, p = t & (SR_L - 1);
     const int rw = (tid >> 6) * SR_ROWS + t / SR_L;      // row within the work-group
     {
-        // the Hinv block: 32 loads per thread in flight, then their LDS stores
+        // the Hinv block: 32 loads per thread in flight (32-bit offsets from
+        // the block's corner), then their LDS stores
         constexpr int NT = 64 * WV, CH = 32, ALL = SW_NB * SW_NB;
-#pragma unroll
+        const int ldh = (int)a.ldh;   // the block spans < 2^31 elements (checked on the host)
+#pragma unroll 1
         for (int base = 0; base < ALL; base += NT * CH) {
             float tmp[CH];
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
                 const int idx = base + tid + k * NT;
-                tmp[k] = idx < ALL ? a.H[(int64_t)(idx / SW_NB) * a.ldh + (idx % SW_NB)] : 0.0f;
+                tmp[k] = idx < ALL ? a.H[(idx / SW_NB) * ldh + (idx % SW_NB)] : 0.0f;
             }
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
@@ -598,6 +601,7 @@ __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
             qv[m] = q;
             ev[m] = e;
         }
+        __asm__ volatile("" : "+v"(qv[m]), "+v"(ev[m]));   // select now: keeps the columns' q, e dead
 #pragma unroll
         for (int m2 = m; m2 < SR_M; ++m2) {
             const float4 h4 = hc[m2 / 4];
@@ -682,33 +686,29 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
         return IC_OK;
     }
     if (groups == 1 && a.nb == SW_NB) {
-        // whole blocks of one matrix: the row sweep (16 lanes per row, four
-        // waves per work-group sharing the staged Hinv block) while two
-        // work-groups per CU cover the rows; beyond that the quad sweep's 64
-        // rows per work-group (measured at 12288 rows: 0.92 ms per layer
-        // against 0.97)
+        // whole blocks of one matrix: the row sweep (16 lanes per row), with
+        // 4 to 16 waves per work-group sharing the staged Hinv block, as many
+        // as one work-group per CU needs to cover the rows
+        const int64_t need = cdiv(cdiv(a.rows, SR_ROWS), 256);
+        const int WVs = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
+        const dim3 g16((unsigned)cdiv(a.rows, WVs * SR_ROWS));
         const bool zp = a.zp != nullptr;
-        if (a.rows <= 2 * 256 * 4 * SR_ROWS) {
-            const dim3 g16((unsigned)cdiv(a.rows, 4 * SR_ROWS));
-#define ICQ_SWEEP16(M, Z) hipLaunchKernelGGL((sweep16_kernel<M, Z, 4>), g16, dim3(256), 0, st, a)
-            if (a.mode == SWEEP_GPTQ) {
-                if (zp) ICQ_SWEEP16(SWEEP_GPTQ, true);
-                else ICQ_SWEEP16(SWEEP_GPTQ, false);
-            } else {
-                ICQ_SWEEP16(SWEEP_LDLQ, false);
-            }
-#undef ICQ_SWEEP16
+#define ICQ_SWEEP16(M, Z, W) hipLaunchKernelGGL((sweep16_kernel<M, Z, W>), g16, dim3(64 * W), 0, st, a)
+#define ICQ_SWEEP16_WV(M, Z)                    \
+    switch (WVs) {                              \
+        case 4: ICQ_SWEEP16(M, Z, 4); break;    \
+        case 8: ICQ_SWEEP16(M, Z, 8); break;    \
+        case 12: ICQ_SWEEP16(M, Z, 12); break;  \
+        default: ICQ_SWEEP16(M, Z, 16); break;  \
+    }
+        if (a.mode == SWEEP_GPTQ) {
+            if (zp) ICQ_SWEEP16_WV(SWEEP_GPTQ, true)
+            else ICQ_SWEEP16_WV(SWEEP_GPTQ, false)
         } else {
-            const dim3 g4((unsigned)cdiv(a.rows, 4 * SQ_ROWS));
-#define ICQ_SWEEP4(M, Z) hipLaunchKernelGGL((sweep4_kernel<M, Z, 4>), g4, dim3(256), 0, st, a)
-            if (a.mode == SWEEP_GPTQ) {
-                if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true);
-                else ICQ_SWEEP4(SWEEP_GPTQ, false);
-            } else {
-                ICQ_SWEEP4(SWEEP_LDLQ, false);
-            }
-#undef ICQ_SWEEP4
+            ICQ_SWEEP16_WV(SWEEP_LDLQ, false)
         }
+#undef ICQ_SWEEP16_WV
+#undef ICQ_SWEEP16
         IC_CHECK_LAUNCH();
         return IC_OK;
     }

@@ -350,6 +350,7 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
                     er[m] = dec.y;
                     qr[m] = dec.x;
                 }
+                __asm__ volatile("" : "+v"(er[m]), "+v"(qr[m]));   // select now: keeps the columns' results dead
 #pragma unroll
                 for (int m2 = m; m2 < GSLOT; ++m2) {
                     const float4 h4 = hc[m2 / 4];
