@@ -310,15 +310,27 @@ __global__ __launch_bounds__(SW_THREADS) void sweep_kernel(SweepArgs a) {
 // sends the wave's rows through the block once more, one lane per row with
 // the row's error output as its working row, with the IEEE-exact test on
 // every division (rare).  WV waves share the staged Hinv block; blockIdx.y
-// is the column group of a block-diagonal Hessian.  Two work-groups fit a
-// CU (LDS and at most 256 VGPRs), so batched launches keep two waves per
-// SIMD.
+// is the column group of a block-diagonal Hessian.
 constexpr int SQ_M = SW_NB / 4;   // columns per lane
 constexpr int SQ_ROWS = 16;       // rows per wave
 
+// The quad sweep's Hinv block in LDS, packed: row j keeps only the
+// 16-column groups g >= j / 16 (the later columns its update reaches), as
+// [p][g - j/16] float4s (lane p's four columns 16 g + 4 s + p, s = 0..3):
+// 36 KB instead of 64, so four work-groups share a CU.
+__host__ __device__ constexpr int qp_row4(int j) {   // float4 offset of row j
+    return 4 * (16 * (8 * (j / 16) - (j / 16) * (j / 16 - 1) / 2) + (j % 16) * (8 - j / 16));
+}
+constexpr int QP_F4 = qp_row4(SW_NB);
+static_assert(QP_F4 == 2304, "packed quad-sweep Hinv block");
+__device__ __forceinline__ int qp_idx(int j, int c) {   // float index of Hinv[j][c], c >= 16 (j / 16)
+    const int m = c >> 2, p = c & 3, g0 = j >> 4;
+    return 4 * (qp_row4(j) + p * (8 - g0) + (m >> 2) - g0) + (m & 3);
+}
+
 template <int MODE, bool ZP, int WV>
-__global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
-    __shared__ __align__(16) float Hq[SW_NB][4][SQ_M];   // Hq[j][p][m] = Hinv[j][4 m + p]
+__global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
+    __shared__ __align__(16) float4 Hq4[QP_F4];          // packed Hinv block (qp_idx)
     __shared__ __align__(16) float4 piv[SW_NB];          // {Hinv_jj, 1 / d_j, d_j in the fast domain, 0}
     const int tid = threadIdx.x, t = tid & 63, p = t & 3;
     const int rw = (tid >> 6) * SQ_ROWS + (t >> 2);      // row within the work-group
@@ -339,8 +351,8 @@ __global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
             }
 #pragma unroll
             for (int k = 0; k < CH; ++k) {
-                const int idx = tid + (k0 + k) * NT, c = idx % SW_NB;
-                Hq[idx / SW_NB][c & 3][c >> 2] = tmp[k];
+                const int idx = tid + (k0 + k) * NT, i = idx / SW_NB, c = idx % SW_NB;
+                if (c >= 16 * (i / 16)) reinterpret_cast<float*>(Hq4)[qp_idx(i, c)] = tmp[k];
             }
         }
         for (int j = tid; j < SW_NB; j += 64 * WV) {
@@ -378,16 +390,16 @@ __global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
     uint64_t badm = 0;   // LDLQ: lanes with a value outside the fast division's domain
     float amax = 0.0f, amin = INFINITY;   // GPTQ: the dividends' range (amin = 0: a pivot outside)
     float4 pvn = piv[0], hc[SQ_M / 4], hn[SQ_M / 4];
-    const float4* Hq4 = reinterpret_cast<const float4*>(&Hq[0][p][0]);   // + j * SW_NB / 4
 #pragma unroll
-    for (int g = 0; g < SQ_M / 4; ++g) hc[g] = Hq4[g];
+    for (int g = 0; g < SQ_M / 4; ++g) hc[g] = Hq4[qp_row4(0) + p * 8 + g];
     auto column = [&](auto J) {
         constexpr int j = decltype(J)::value, m = j / 4, o = j % 4;
         const float4 pv = pvn;
         if constexpr (j + 1 < SW_NB) {
             pvn = piv[j + 1];
 #pragma unroll
-            for (int g = (j + 1) / 16; g < SQ_M / 4; ++g) hn[g] = Hq4[(j + 1) * (SW_NB / 4) + g];
+            for (int g = (j + 1) / 16; g < SQ_M / 4; ++g)
+                hn[g] = Hq4[qp_row4(j + 1) + p * (8 - (j + 1) / 16) + g - (j + 1) / 16];
         }
         const float x = w[m];
         float q, e;
@@ -459,7 +471,7 @@ __global__ __launch_bounds__(64 * WV, 2) void sweep4_kernel(SweepArgs a) {
                 }
                 a.Q[row * a.ldq + col0 + j] = (int8_t)(int)q;
                 xr[j] = e;
-                for (int k = j + 1; k < SW_NB; ++k) xr[k] = xr[k] - e * Hq[j][k & 3][k >> 2];
+                for (int k = j + 1; k < SW_NB; ++k) xr[k] = xr[k] - e * reinterpret_cast<const float*>(Hq4)[qp_idx(j, k)];
             }
         }
         return;
