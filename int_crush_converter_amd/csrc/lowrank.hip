@@ -439,12 +439,16 @@ extern "C" int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, 
     IC_CHECK_LAUNCH();
     int rc = orth(w.Y, w.Q, n, p, w, st, /*well_conditioned=*/true);
     if (rc) return rc;
-    const int test_it = refuse_rel > 0.0f ? std::min(iters, 2) : -1;
+    // the refusal certificate is tried after one and after two steps (the
+    // random start's Ritz values sit near the mean eigenvalue; one step of
+    // (H + mu I) already lifts them for Hessians of high rank)
+    const int test_lo = refuse_rel > 0.0f ? std::min(iters, 1) : -1;
+    const int test_hi = refuse_rel > 0.0f ? std::min(iters, 2) : -1;
     for (int it = 0;; ++it) {
         // Y = H Q
         GemmArgs g{n, p, n, 1.0f, 0.0f, H, n, 0, w.Q, p, 0, w.Y, p, 0, 0, 0, CMASK_FULL, KR_FULL, 1, PT_OTHER};
         if ((rc = gemm_f32(g, st))) return rc;
-        if (it == test_it) {
+        if (it >= test_lo && it <= test_hi && test_lo >= 0) {
             // Refusal certificate: if T - refuse_rel ||H||_F I is positive definite,
             // every Ritz value exceeds refuse_rel ||H||_F >= refuse_rel lambda_max,
             // and by interlacing so do the p largest eigenvalues of H.
