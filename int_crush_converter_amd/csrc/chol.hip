@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "chol.hpp"
+#include "gemm_dev.hpp"
 #include "torchsum.hpp"
 
 namespace icq {
@@ -433,11 +434,9 @@ __device__ __forceinline__ void diag_tile_wave(DiagShared& sh, const float* A, i
     }
 }
 
-__global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0,
-                                                                    int nb, double* dinv64, int64_t dstride,
-                                                                    int* info) {
-    __shared__ __attribute__((aligned(16))) DiagShared sh;
-    const int b = blockIdx.x;
+// The diagonal block of matrix b, by a work-group of DIAG_WAVES waves.
+__device__ __forceinline__ void diag_block(DiagShared& sh, int b, float* H, int64_t ld, int64_t stride, int64_t k0,
+                                           int nb, double* dinv64, int64_t dstride, int* info) {
     float* A = H + (int64_t)b * stride + k0 * ld + k0;
     double* D64 = dinv64 + (int64_t)b * dstride;
     const int lane = threadIdx.x & 63;
@@ -468,6 +467,38 @@ __global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, i
         if (i < nb && j < nb) A[(int64_t)i * ld + j] = v;
     }
     if (threadIdx.x == 0 && bad && info[b] == 0) info[b] = (int)k0 + bad;
+}
+
+__global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_kernel(float* H, int64_t ld, int64_t stride, int64_t k0,
+                                                                    int nb, double* dinv64, int64_t dstride,
+                                                                    int* info) {
+    __shared__ __attribute__((aligned(16))) DiagShared sh;
+    diag_block(sh, blockIdx.x, H, ld, stride, k0, nb, dinv64, dstride, info);
+}
+
+// The diagonal block of matrix blockIdx.z (work-group 0) beside the
+// previous block's update of the rest of its super-block: work-group
+// t >= 1 runs tile t - 1 (REST_T x REST_T) of the GEMM g (batch entry
+// blockIdx.z) on its first four waves, in the LDS the diagonal block uses;
+// the other waves end at once (a barrier waits only for the waves still
+// running).  The two touch disjoint columns.  One launch instead of two,
+// and the update runs while the diagonal block's serial chain does.  The
+// launch holds one work-group per CU (the diagonal block's LDS), where
+// 128-tiles (a quarter as many as 64-tiles) finish the update sooner.
+constexpr int REST_T = 128;
+static_assert(2 * gk::Geo<REST_T>::TILE_F * sizeof(float) <= sizeof(DiagShared), "GEMM tile staging fits");
+__global__ __launch_bounds__(DIAG_WAVES * 64) void potrf_diag_rest_kernel(float* H, int64_t ld, int64_t stride,
+                                                                         int64_t k0, int nb, double* dinv64,
+                                                                         int64_t dstride, int* info, GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) DiagShared sh;
+    if (blockIdx.x == 0) {
+        diag_block(sh, blockIdx.z, H, ld, stride, k0, nb, dinv64, dstride, info);
+        return;
+    }
+    if (threadIdx.x >= 256) return;
+    const gk::TileRange tr = gk::tile_of<REST_T>(g, blockIdx.x - 1);
+    if (tr.skip) return;
+    gk::gemm_tile<0, 1, true, REST_T, gk::CHUNK_SUM>(g, tr, blockIdx.z, reinterpret_cast<float*>(&sh));
 }
 
 // Panel solve A21 <- A21 * Dinv^T for the m rows below a diagonal block, in
@@ -608,11 +639,22 @@ double* dinv64_of(float* dinv, int64_t batch, int64_t n) {
 // trailing matrix beyond it gets one SYRK with K = SUPER_NB.  Same flops as
 // one SYRK per block, with the trailing matrix read and written once per
 // super-block.
+//
+// Look-ahead inside a super-block: block k's update is split into the next
+// block column (before the next diagonal block) and the rest of the
+// super-block, which runs in the next diagonal block's launch
+// (potrf_diag_rest_kernel).  The next block column's update follows that
+// launch, so every element receives the same rank-NB updates in the same
+// order as with one update per block (bit-identical results).
 constexpr int64_t SUPER_NB = 1024;
 
 int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, double* dinv64, int* info, hipStream_t st) {
     const int64_t nblk = cdiv(n, NB);
     const int64_t dstride = nblk * NB * NB;
+    IC_REQUIRE(batch <= 65535, "potrf: batch too large");
+    bool rest_pending = false;   // `rest`: the previous block's update of the rest of its super-block
+    GemmArgs rest{};
+    int64_t rest_tiles = 0;
     for (int64_t s0 = 0; s0 < n; s0 += SUPER_NB) {
         const int64_t s1 = std::min<int64_t>(n, s0 + SUPER_NB);
         for (int64_t k0 = s0; k0 < s1; k0 += NB) {
@@ -620,10 +662,17 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, double* di
             const int nb = (int)std::min<int64_t>(NB, n - k0);
             double* Dk64 = dinv64 + kb * NB * NB;
             {
-                ProfScope prof_scope(st, PT_DIAG, batch * (2.0 / 3.0) * nb * nb * nb, batch * 3.0 * 4 * nb * nb);
-                hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(DIAG_WAVES * 64), 0, st, H, ld, sH, k0, nb,
-                                   Dk64, dstride, info);
+                double fl = batch * (2.0 / 3.0) * nb * nb * nb, by = batch * 3.0 * 4 * nb * nb;
+                if (rest_pending) fl += rest.algo_flops, by += 4.0 * batch * (2.0 * rest.M * rest.K + 2.0 * rest.M * rest.N);
+                ProfScope prof_scope(st, PT_DIAG, fl, by);
+                if (rest_pending)
+                    hipLaunchKernelGGL(potrf_diag_rest_kernel, dim3((unsigned)(1 + rest_tiles), 1, (unsigned)batch),
+                                       dim3(DIAG_WAVES * 64), 0, st, H, ld, sH, k0, nb, Dk64, dstride, info, rest);
+                else
+                    hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)batch), dim3(DIAG_WAVES * 64), 0, st, H, ld,
+                                       sH, k0, nb, Dk64, dstride, info);
                 IC_CHECK_LAUNCH();
+                rest_pending = false;
             }
             const int64_t k1 = k0 + nb;
             const int64_t m = n - k1;
@@ -636,15 +685,29 @@ int potrf(float* H, int64_t batch, int64_t n, int64_t ld, int64_t sH, double* di
                                    A21, m, nb, ld, sH, Dk64, dstride);
                 IC_CHECK_LAUNCH();
             }
-            // rest of the super-block: A[k1:, k1:s1] -= A21 A21[:s1-k1]^T (lower in its top square)
+            // rest of the super-block: A[k1:, k1:s1] -= A21 A21[:s1-k1]^T (lower in its top square), the
+            // next block column now, the others in the next diagonal block's launch
             const int64_t w = s1 - k1;
             if (w > 0) {
-                GemmArgs g{m, w, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, H + k1 * ld + k1, ld, sH, 0, 1,
+                const int64_t la = std::min<int64_t>(NB, w);
+                GemmArgs g{m, la, nb, -1.0f, 1.0f, A21, ld, sH, A21, ld, sH, H + k1 * ld + k1, ld, sH, 0, 1,
                            CMASK_LOWER, KR_FULL, batch, PT_GEMM_CHOL,
-                           (double)batch * 2.0 * (dtri((double)w) + (double)(m - w) * w) * nb};
+                           (double)batch * 2.0 * (dtri((double)la) + (double)(m - la) * la) * nb};
                 g.chunk_sub = 1;   // a sequence of rank-128 updates, like LAPACK's blocked potrf
                 int rc = gemm_f32(g, st);
                 if (rc) return rc;
+                if (w > la) {
+                    // one chunk (K = nb <= kc): C - P in the sum form, as gemm_f32 runs it
+                    const float* A2 = A21 + la * ld;
+                    rest = GemmArgs{m - la, w - la, nb, -1.0f, 1.0f, A2, ld, sH, A2, ld, sH,
+                                    H + (k1 + la) * ld + k1 + la, ld, sH, 0, 1, CMASK_LOWER, KR_FULL, batch,
+                                    PT_GEMM_CHOL,
+                                    (double)batch * 2.0 * (dtri((double)(w - la)) + (double)(m - w) * (w - la)) * nb};
+                    bool tri;
+                    rest_tiles = gk::tile_count<REST_T>(rest, tri);
+                    IC_REQUIRE(rest_tiles < (1LL << 30), "potrf: problem too large");
+                    rest_pending = true;
+                }
             }
         }
         // beyond the super-block: A[s1:, s1:] -= L[s1:, s0:s1] L[s1:, s0:s1]^T (lower)
