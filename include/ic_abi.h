@@ -65,6 +65,31 @@ int ic_rotate_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, i
 int ic_rotate_hessian(const float* src, float* H, int64_t batch, int64_t n, int64_t ld, int rot,
                       void* stream);
 
+/* ic_rotate_rows with the reference's own fp32 rounding: every output is one
+ * fused multiply-add chain over the group's inputs in increasing order from
+ * zero, which is how the reference's `x @ H.T` (converter/rotation.py:82-92,
+ * a CPU sgemm with K = rot) rounds; rot 512 adds the chains of its two halves,
+ * as that sgemm does.  Runs on the matrix cores (K = 1 fp32 MFMA chains).
+ * Same arguments as ic_rotate_rows; rot: power of 2 in [1, 512]; in place
+ * needs f32, equal ld and rot <= 256.
+ * Replaces converter/rotation.py:95-125 (rotate_weights) and :128-153
+ * (rotate_activations). */
+int ic_rotate_rows_exact(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                         float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
+                         unsigned long long* n_zeroed, void* stream);
+
+/* ic_rotate_hessian with the reference's rounding: per rot x rot block,
+ * T = R^T B (chains over the block's rows in increasing order), then T R
+ * (chains over T's columns), as einsum("kp,nkl,le->npe") contracts it
+ * (converter/rotation.py:237-248).  rot: 1, 4, 16, 64 or 256 (the regular
+ * matrices that rotate_hessian accepts).  lower_only (batch 1 only): write
+ * only the rot x rot blocks on or below the block diagonal - all that a lower
+ * Cholesky factorisation and the damping read; the rest of H is unspecified
+ * (in place: src's values or partial results; out of place: unwritten).
+ * Replaces converter/rotation.py:156-248 (rotate_hessian, after padding). */
+int ic_rotate_hessian_exact(const float* src, float* H, int64_t batch, int64_t n, int64_t ld, int rot,
+                            int lower_only, void* stream);
+
 /* Per-row min / max / max-abs of an fp32 matrix; NaN propagates like
  * torch.amin/amax.  Any output pointer may be NULL.
  * Replaces the amin/amax/abs().amax reductions of converter/scales.py:85,

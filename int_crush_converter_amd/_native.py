@@ -36,6 +36,8 @@ _SIGS = {
     "ic_last_error": (_c.c_char_p, []),
     "ic_rotate_rows": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _f32, _vp, _vp]),
     "ic_rotate_hessian": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp]),
+    "ic_rotate_rows_exact": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _f32, _vp, _vp]),
+    "ic_rotate_hessian_exact": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "ic_row_stats": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "ic_rtn_scales": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _c.POINTER(_f32), _i32, _vp, _vp, _vp]),
     "ic_rtn_quantize": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _vp]),

@@ -1,0 +1,484 @@
+// Group-wise Hadamard rotation in the reference's own summation order.
+//
+// converter/rotation.py:82-92 rotates weights as `x @ H.T` and :237-248 the
+// Hessian as einsum("kp,nkl,le->npe", R, H, R), which torch contracts left
+// to right: T = R^T H_blk first, then T R.  On the CPU each of these is an
+// fp32 GEMM in which every output is ONE fused multiply-add chain over the
+// contraction index in increasing order, starting from zero (checked against
+// the reference for R = 2 .. 256, 2-D and 3-D Hessians; R = 512 is two
+// 256-long chains whose results are added).  For the regular Hadamard the
+// products are exact (entries +-2^-k), so only the order of the additions
+// decides the rounding - and a fast Walsh-Hadamard transform (rotate.hip)
+// associates them differently.
+//
+// A K = 1 fp32 MFMA (v_mfma_f32_16x16x1_4b_f32) computes D = fma(A, B, C)
+// element by element, correctly rounded with denormals kept, so a chain of
+// them over k IS the sequential fma chain, at the matrix-core rate (twice
+// the VALU fma rate).  Lane layout of that instruction (block b = v / 4 of
+// the 16 accumulator registers v):
+//     A: lane 16 b + i supplies A[b][i];   B: lane 16 b + j supplies B[b][j];
+//     D[b][i][j] sits in register v = 4 b + i % 4 of lane 16 (i / 4) + j.
+//
+//  rows (weights, and the right product of the Hessian):
+//      Y[r][j] = sum_k X[r][k] Hd[k][j]  -  blocks b = 4 row tiles of 16,
+//      A = X (lane <-> row, staged in LDS), B = Hd[k][j] built in registers.
+//  cols (the Hessian's left product):
+//      T[p][l] = sum_k Hd[k][p] H[k][l]  -  blocks b = 4 column tiles of 16,
+//      A = Hd[k][p] in registers, B = H rows (lane <-> column, from LDS).
+//
+// Hd[k][j] = m * (-1)^s(k, j) with, for the regular matrix of size 4^n,
+// m = 2^-n and s = the number of base-4 digits where k_d + j_d = 3, i.e.
+// popcount(t & (t >> 1) & 0x55..) with t = k ^ j; for the Sylvester matrix
+// of size 2^n, m = fp32(1/sqrt(2^n)) and s = popcount(k & j).  Both split
+// over k = 16 k_hi + k_lo, j = 16 j_hi + j_lo: s = s(k_lo, j_lo) + s(k_hi,
+// j_hi).  A lane keeps the 16 values m (-1)^s(k_lo, j_lo) of its own j_lo and
+// flips their sign bit with the wave-uniform s(k_hi, j_hi).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "common.hpp"
+#include "prof.hpp"
+
+namespace icq {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <bool REG>
+__host__ __device__ __forceinline__ uint32_t hd_sign(uint32_t k, uint32_t j) {
+    if (REG) {
+        const uint32_t t = k ^ j;
+        return (uint32_t)__builtin_popcount(t & (t >> 1) & 0x55555555u) & 1u;
+    }
+    return (uint32_t)__builtin_popcount(k & j) & 1u;
+}
+
+__device__ __forceinline__ f32x16 mfma_k1(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+// Four consecutive source elements as fp32: one 16-byte (f32) or 8-byte
+// (bf16 / f16) load when `vec` and in bounds, else element by element with
+// zeros beyond `cols`.
+template <int DT>
+__device__ __forceinline__ void load4(const void* src, int64_t off, int64_t c, int64_t cols, bool vec, float (&v)[4]) {
+    if (vec && c + 3 < cols) {
+        if (DT == IC_DTYPE_F32) {
+            const float4 t = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(src) + off);
+            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        } else {
+            const uint2 t = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(src) + off);
+            const uint32_t u[2] = {t.x, t.y};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (DT == IC_DTYPE_BF16) {
+                    v[2 * h] = __uint_as_float(u[h] << 16);
+                    v[2 * h + 1] = __uint_as_float(u[h] & 0xffff0000u);
+                } else {
+                    v[2 * h] = f16_bits_to_f32((uint16_t)(u[h] & 0xffffu));
+                    v[2 * h + 1] = f16_bits_to_f32((uint16_t)(u[h] >> 16));
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (c + i < cols) ? load_as_f32(src, DT, off + i) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void flush_zeroed(unsigned cnt, unsigned long long* nz) {
+    if (!nz) return;
+    const unsigned long long c = wave_sum((unsigned long long)cnt);
+    if ((threadIdx.x & 63) == 0 && c) atomicAdd(nz, c);
+}
+
+// ------------------------------------------------------------------ rows
+
+constexpr int XR_ROWS = 64;            // rows per work-group (4 row tiles of 16)
+constexpr int XR_SLICE = 256;          // output columns per work-group: 4 waves x 4 tiles x 16
+constexpr int XR_LD = XR_SLICE + 4;    // LDS pitch: lanes 4 banks apart, 16-byte reads conflict-free
+
+// One work-group: rows [r0, r0 + 64) x output columns [s0, s0 + 256).  For
+// R <= 256 the slice holds whole groups and its input is the same 256
+// columns; for R = 512 the group's 512 inputs are staged in two chunks of
+// 256 whose chains are added at the end.  TRI: only blocks (bi, bj) of
+// size R with bj <= bi of the (n_tri x n_tri) matrix are needed, and a
+// work-group whose every block lies above the diagonal returns at once.
+template <int R, int DT, bool TRI>
+__global__ __launch_bounds__(256, 2) void rot_rows_exact_kernel(const void* __restrict__ src, int64_t rows, int64_t cols,
+                                                               int64_t ld_src, float* __restrict__ dst,
+                                                               int64_t cols_pad, int64_t ld_dst, int64_t n_tri,
+                                                               uint32_t mag_bits, float zero_above,
+                                                               unsigned long long* __restrict__ nz, int vec) {
+    constexpr bool REG = (R & 0x55555555) == R;
+    constexpr int KL = R < XR_SLICE ? R : XR_SLICE;        // k steps per chunk
+    constexpr int NCH = R > XR_SLICE ? R / XR_SLICE : 1;   // chunks
+    __shared__ __align__(16) float xs[XR_ROWS * XR_LD];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t r0 = (int64_t)blockIdx.x * XR_ROWS;
+    const int64_t s0 = (int64_t)blockIdx.y * XR_SLICE;
+    if (TRI && s0 / R > ((r0 % n_tri) + XR_ROWS - 1) / R) return;
+    const int64_t kb = R > XR_SLICE ? (s0 / R) * R : s0;   // first input column of chunk 0
+    // the first slice of a group counts its outliers (every input once)
+    const bool count = zero_above > 0.0f && (R <= XR_SLICE || s0 % R == 0);
+
+    uint32_t blo[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) blo[q] = mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31);
+    int acol[4], jhi[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int jt = 64 * w + 16 * c;                                  // tile's column in the slice
+        acol[c] = R <= XR_SLICE ? (jt / R) * R : 0;                       // its group's first LDS column
+        jhi[c] = (R <= XR_SLICE ? jt % R : (int)(s0 % R) + jt) >> 4;     // in-group column / 16
+    }
+    f32x16 acc[4], part[4];
+    unsigned cnt = 0;
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        if (ch) __syncthreads();   // every wave is done with the previous chunk
+        const int64_t c0 = kb + (int64_t)ch * XR_SLICE;
+        float v[16][4];
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int u = it * 256 + tid, rr = u >> 6, cq = (u & 63) * 4;
+            const int64_t r = r0 + rr, c = c0 + cq;
+            if (r < rows) load4<DT>(src, r * ld_src + c, c, cols, vec != 0, v[it]);
+            else v[it][0] = v[it][1] = v[it][2] = v[it][3] = 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            if (zero_above > 0.0f) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool out = fabsf(v[it][i]) > zero_above;
+                    cnt += (out && count) ? 1u : 0u;
+                    v[it][i] = out ? 0.0f : v[it][i];
+                }
+            }
+            const int u = it * 256 + tid, rr = u >> 6, cq = (u & 63) * 4;
+            *reinterpret_cast<float4*>(&xs[rr * XR_LD + cq]) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
+        const float* xrow = &xs[lane * XR_LD];
+        for (int kh = 0; kh < KL / 16; ++kh) {
+            uint32_t shi[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                shi[c] = hd_sign<REG>((uint32_t)(ch * (XR_SLICE / 16) + kh), (uint32_t)jhi[c]) << 31;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                float4 a4[4];
+                if (R >= 64) {
+                    a4[0] = *reinterpret_cast<const float4*>(xrow + acol[0] + 16 * kh + 4 * q4);
+                    a4[1] = a4[2] = a4[3] = a4[0];
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        a4[c] = *reinterpret_cast<const float4*>(xrow + acol[c] + 16 * kh + 4 * q4);
+                }
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int q = 4 * q4 + qq;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float a = qq == 0 ? a4[c].x : qq == 1 ? a4[c].y : qq == 2 ? a4[c].z : a4[c].w;
+                        acc[c] = mfma_k1(a, __uint_as_float(blo[q] ^ shi[c]), acc[c]);
+                    }
+                }
+            }
+        }
+        if (NCH > 1 && ch == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part[c] = acc[c];
+        }
+    }
+    if (count) flush_zeroed(cnt, nz);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t col = s0 + 64 * w + 16 * c + (lane & 15);
+        if (s0 + 64 * w + 16 * c >= cols_pad) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t r = r0 + 16 * (v >> 2) + 4 * (lane >> 4) + (v & 3);
+            float y = acc[c][v];
+            if (NCH > 1) y = part[c][v] + y;
+            if (r < rows) dst[r * ld_dst + col] = y;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ columns
+
+constexpr int XC_ROWS = 256;   // T rows per work-group: 4 waves x 4 tiles x 16
+constexpr int XC_COLS = 64;    // columns per work-group: 4 blocks of 16
+
+// One work-group: T rows [r0, r0 + 256) x columns [l0, l0 + 64) of matrix
+// blockIdx.z; R <= 256, so the rows hold whole groups.  In place is safe:
+// a work-group reads exactly the region it writes, all of it before its
+// first store.
+template <int R, bool TRI>
+__global__ __launch_bounds__(256, 2) void rot_cols_exact_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                               int64_t n, int64_t ld, int64_t bstride,
+                                                               uint32_t mag_bits, int vec) {
+    constexpr bool REG = (R & 0x55555555) == R;
+    __shared__ __align__(16) float hs[XC_ROWS * XC_COLS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t l0 = (int64_t)blockIdx.x * XC_COLS;
+    const int64_t r0 = (int64_t)blockIdx.y * XC_ROWS;
+    if (TRI && l0 / R > (r0 + XC_ROWS - 1) / R) return;
+    const float* S = src + (int64_t)blockIdx.z * bstride;
+    float* D = dst + (int64_t)blockIdx.z * bstride;
+    {
+        float v[16][4];
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int u = it * 256 + tid, rr = u >> 4, cq = (u & 15) * 4;
+            const int64_t r = r0 + rr, c = l0 + cq;
+            if (r < n) load4<IC_DTYPE_F32>(S, r * ld + c, c, n, vec != 0, v[it]);
+            else v[it][0] = v[it][1] = v[it][2] = v[it][3] = 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int u = it * 256 + tid, rr = u >> 4, cq = (u & 15) * 4;
+            *reinterpret_cast<float4*>(&hs[rr * XC_COLS + cq]) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+        }
+    }
+    __syncthreads();
+    uint32_t alo[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) alo[q] = mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31);
+    int brow[4], phi[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int pt = 64 * w + 16 * c;   // tile's first row in the work-group
+        brow[c] = (pt / R) * R;           // its group's first row (LDS)
+        phi[c] = (pt % R) >> 4;           // in-group row / 16
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
+    for (int kh = 0; kh < R / 16; ++kh) {
+        uint32_t shi[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) shi[c] = hd_sign<REG>((uint32_t)kh, (uint32_t)phi[c]) << 31;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            float b[4];
+            if (R >= 64) {
+                b[0] = b[1] = b[2] = b[3] = hs[(brow[0] + 16 * kh + q) * XC_COLS + lane];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) b[c] = hs[(brow[c] + 16 * kh + q) * XC_COLS + lane];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = mfma_k1(__uint_as_float(alo[q] ^ shi[c]), b[c], acc[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t r = r0 + 64 * w + 16 * c + 4 * (lane >> 4) + (v & 3);
+            const int64_t col = l0 + 16 * (v >> 2) + (lane & 15);
+            if (r < n && col < n) D[r * ld + col] = acc[c][v];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ small R (2, 4, 8): VALU fma chains
+
+// One thread per (row, group): reads the group's R inputs, writes its R
+// outputs (so in place is safe and every input is counted once).
+template <int R, int DT>
+__global__ __launch_bounds__(256) void rot_rows_small_kernel(const void* __restrict__ src, int64_t rows, int64_t cols,
+                                                             int64_t ld_src, float* dst, int64_t groups,
+                                                             int64_t ld_dst, float mag, float zero_above,
+                                                             unsigned long long* __restrict__ nz) {
+    constexpr bool REG = (R & 0x55555555) == R;
+    unsigned cnt = 0;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < rows * groups;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t / groups, g = t % groups;
+        float x[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int64_t c = g * R + k;
+            float v = c < cols ? load_as_f32(src, DT, r * ld_src + c) : 0.0f;
+            if (zero_above > 0.0f && fabsf(v) > zero_above) { v = 0.0f; ++cnt; }
+            x[k] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            float y = 0.0f;
+#pragma unroll
+            for (int k = 0; k < R; ++k) y = __builtin_fmaf(x[k], hd_sign<REG>(k, j) ? -mag : mag, y);
+            dst[r * ld_dst + g * R + j] = y;
+        }
+    }
+    if (zero_above > 0.0f) flush_zeroed(cnt, nz);
+}
+
+// One thread per (matrix, group, column): T[g R + p][l] = sum_k Hd[k][p] H[g R + k][l].
+template <int R>
+__global__ __launch_bounds__(256) void rot_cols_small_kernel(const float* __restrict__ src, float* dst, int64_t batch,
+                                                             int64_t n, int64_t ld, int64_t bstride, float mag) {
+    constexpr bool REG = (R & 0x55555555) == R;
+    const int64_t per = (n / R) * n;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < batch * per;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = t / per, g = (t % per) / n, l = t % n;
+        const float* S = src + b * bstride;
+        float* D = dst + b * bstride;
+        float x[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) x[k] = S[(g * R + k) * ld + l];
+#pragma unroll
+        for (int p = 0; p < R; ++p) {
+            float y = 0.0f;
+#pragma unroll
+            for (int k = 0; k < R; ++k) y = __builtin_fmaf(hd_sign<REG>(k, p) ? -mag : mag, x[k], y);
+            D[(g * R + p) * ld + l] = y;
+        }
+    }
+}
+
+static bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
+static bool pow4(int64_t n) { return pow2(n) && (n & 0x55555555) == n; }
+
+// fp32 magnitude of the entries: 2^-log4(R) (regular) or fp32(1/sqrt(R)).
+static float hd_mag(int rot) {
+    if (pow4(rot)) {
+        float m = 1.0f;
+        for (int r = rot; r > 1; r >>= 2) m *= 0.5f;
+        return m;
+    }
+    return (float)(1.0 / std::sqrt((double)rot));
+}
+
+static int small_grid(int64_t work) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 256 * 32));
+}
+
+static int rows_exact(const void* src, int dt, int64_t rows, int64_t cols, int64_t ld_src, float* dst,
+                      int64_t cols_pad, int64_t ld_dst, int rot, float zero_above, unsigned long long* nz,
+                      int64_t n_tri, hipStream_t st, int tag) {
+    const float mag = hd_mag(rot);
+    if (rot <= 8) {
+        const int64_t groups = cols_pad / rot;
+        const int grid = small_grid(rows * groups);
+        ProfScope prof_scope(st, tag, 2.0 * rot * rows * cols_pad, 4.0 * rows * cols_pad + (dt ? 2.0 : 4.0) * rows * cols);
+#define ICQ_SMALL(RR, D) hipLaunchKernelGGL((rot_rows_small_kernel<RR, D>), dim3(grid), dim3(256), 0, st, src, rows, \
+                                            cols, ld_src, dst, groups, ld_dst, mag, zero_above, nz)
+#define ICQ_SMALL_DT(RR) do { if (dt == IC_DTYPE_F32) ICQ_SMALL(RR, IC_DTYPE_F32); \
+                              else if (dt == IC_DTYPE_BF16) ICQ_SMALL(RR, IC_DTYPE_BF16); \
+                              else ICQ_SMALL(RR, IC_DTYPE_F16); } while (0)
+        if (rot == 2) ICQ_SMALL_DT(2);
+        else if (rot == 4) ICQ_SMALL_DT(4);
+        else ICQ_SMALL_DT(8);
+#undef ICQ_SMALL_DT
+#undef ICQ_SMALL
+        IC_CHECK_LAUNCH();
+        return IC_OK;
+    }
+    const size_t esz = dt == IC_DTYPE_F32 ? 4 : 2;
+    const int vec = ((uintptr_t)src % (4 * esz) == 0) && ((ld_src * esz) % (4 * esz) == 0);
+    const bool tri = n_tri > 0;
+    IC_REQUIRE(!tri || n_tri % XR_ROWS == 0, "rotate_exact: the triangle needs n % 64 == 0");
+    IC_REQUIRE(cdiv(rows, XR_ROWS) < (1LL << 31) && cdiv(cols_pad, XR_SLICE) <= 65535, "rotate_exact: too large");
+    dim3 grid((unsigned)cdiv(rows, XR_ROWS), (unsigned)cdiv(cols_pad, XR_SLICE));
+    ProfScope prof_scope(st, tag, 2.0 * rot * rows * cols_pad * (tri ? 0.5 : 1.0),
+                         4.0 * rows * cols_pad * (tri ? 0.5 : 1.0) + (double)esz * rows * cols * (tri ? 0.5 : 1.0));
+    uint32_t mb;
+    std::memcpy(&mb, &mag, 4);
+#define ICQ_XR(RR, D, T) hipLaunchKernelGGL((rot_rows_exact_kernel<RR, D, T>), grid, dim3(256), 0, st, src, rows, \
+                                            cols, ld_src, dst, cols_pad, ld_dst, n_tri, mb, zero_above, nz, vec)
+#define ICQ_XR_DT(RR) do { if (tri) ICQ_XR(RR, IC_DTYPE_F32, true); \
+                           else if (dt == IC_DTYPE_F32) ICQ_XR(RR, IC_DTYPE_F32, false); \
+                           else if (dt == IC_DTYPE_BF16) ICQ_XR(RR, IC_DTYPE_BF16, false); \
+                           else ICQ_XR(RR, IC_DTYPE_F16, false); } while (0)
+    switch (rot) {
+        case 16: ICQ_XR_DT(16); break;
+        case 32: ICQ_XR_DT(32); break;
+        case 64: ICQ_XR_DT(64); break;
+        case 128: ICQ_XR_DT(128); break;
+        case 256: ICQ_XR_DT(256); break;
+        default: ICQ_XR_DT(512); break;
+    }
+#undef ICQ_XR_DT
+#undef ICQ_XR
+    IC_CHECK_LAUNCH();
+    return IC_OK;
+}
+
+}  // namespace icq
+
+using namespace icq;
+
+extern "C" int ic_rotate_rows_exact(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                                    float* dst, int64_t cols_pad, int64_t ld_dst, int rot, float zero_above,
+                                    unsigned long long* n_zeroed, void* stream) {
+    IC_REQUIRE(src && dst, "ic_rotate_rows_exact: null pointer");
+    IC_REQUIRE(src_dtype >= 0 && src_dtype <= 2, "ic_rotate_rows_exact: bad dtype");
+    IC_REQUIRE(rot >= 1 && rot <= 512 && pow2(rot), "ic_rotate_rows_exact: rot must be a power of 2 <= 512");
+    IC_REQUIRE(rows >= 0 && cols >= 0 && cols_pad == cdiv(cols, rot) * rot, "ic_rotate_rows_exact: cols_pad mismatch");
+    IC_REQUIRE(ld_src >= cols && ld_dst >= cols_pad, "ic_rotate_rows_exact: bad leading dimension");
+    IC_REQUIRE(src != (const void*)dst || (src_dtype == IC_DTYPE_F32 && ld_src == ld_dst && rot <= 256),
+               "ic_rotate_rows_exact: in place needs f32, equal ld and rot <= 256");
+    if (rot == 1)
+        return ic_rotate_rows(src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, 1, zero_above, n_zeroed,
+                              stream);
+    if (rows == 0 || cols_pad == 0) return IC_OK;
+    return rows_exact(src, src_dtype, rows, cols, ld_src, dst, cols_pad, ld_dst, rot, zero_above, n_zeroed, 0,
+                      as_stream(stream), PT_ROTATE);
+}
+
+extern "C" int ic_rotate_hessian_exact(const float* src, float* H, int64_t batch, int64_t n, int64_t ld, int rot,
+                                       int lower_only, void* stream) {
+    IC_REQUIRE(src && H, "ic_rotate_hessian_exact: null pointer");
+    IC_REQUIRE(rot == 1 || (pow4(rot) && rot <= 256), "ic_rotate_hessian_exact: rot must be 1, 4, 16, 64 or 256");
+    IC_REQUIRE(batch >= 0 && n >= 0 && n % rot == 0 && ld >= n, "ic_rotate_hessian_exact: n must be a multiple of rot");
+    IC_REQUIRE(!lower_only || batch == 1, "ic_rotate_hessian_exact: lower_only needs batch == 1");
+    IC_REQUIRE(batch <= 65535, "ic_rotate_hessian_exact: batch too large");
+    if (batch == 0 || n == 0) return IC_OK;
+    hipStream_t st = as_stream(stream);
+    if (rot == 1) {
+        if (src != H)
+            IC_CHECK_HIP(hipMemcpy2DAsync(H, ld * sizeof(float), src, ld * sizeof(float), n * sizeof(float),
+                                          batch * n, hipMemcpyDeviceToDevice, st));
+        return IC_OK;
+    }
+    const float mag = hd_mag(rot);
+    const bool tri = lower_only && rot >= 16 && n % XR_ROWS == 0;   // else the full matrix (a superset)
+    // left product: H <- R^T src (column pass; src -> H, or in place)
+    if (rot == 4) {
+        ProfScope prof_scope(st, PT_ROTATE_H, 2.0 * rot * batch * n * n, 8.0 * batch * n * n);
+        hipLaunchKernelGGL((rot_cols_small_kernel<4>), dim3(small_grid(batch * (n / 4) * n)), dim3(256), 0, st, src,
+                           H, batch, n, ld, n * ld, mag);
+        IC_CHECK_LAUNCH();
+    } else {
+        IC_REQUIRE(cdiv(n, XC_COLS) < (1LL << 31) && cdiv(n, XC_ROWS) <= 65535, "ic_rotate_hessian_exact: too large");
+        const int vec = ((uintptr_t)src % 16 == 0) && (ld % 4 == 0);
+        uint32_t mb;
+        std::memcpy(&mb, &mag, 4);
+        dim3 grid((unsigned)cdiv(n, XC_COLS), (unsigned)cdiv(n, XC_ROWS), (unsigned)batch);
+        ProfScope prof_scope(st, PT_ROTATE_H, 2.0 * rot * batch * n * n * (tri ? 0.5 : 1.0),
+                             8.0 * batch * n * n * (tri ? 0.5 : 1.0));
+#define ICQ_XC(RR) do { if (tri) hipLaunchKernelGGL((rot_cols_exact_kernel<RR, true>), grid, dim3(256), 0, st, src, H, \
+                                                    n, ld, n * ld, mb, vec); \
+                        else hipLaunchKernelGGL((rot_cols_exact_kernel<RR, false>), grid, dim3(256), 0, st, src, H, \
+                                                n, ld, n * ld, mb, vec); } while (0)
+        if (rot == 16) ICQ_XC(16);
+        else if (rot == 64) ICQ_XC(64);
+        else ICQ_XC(256);
+#undef ICQ_XC
+        IC_CHECK_LAUNCH();
+    }
+    // right product: H <- H R (row pass, in place); batch * n rows of pitch ld
+    return rows_exact(H, IC_DTYPE_F32, batch * n, n, ld, H, n, ld, rot, 0.0f, nullptr, tri ? n : 0, st,
+                      PT_ROTATE_H);
+}

@@ -92,7 +92,12 @@ def gptq_codes(W_work: torch.Tensor, H: torch.Tensor, *, rotate_h: int, block_si
             return Q, s16.reshape(M, 1), None if z8 is None else z8.reshape(M, 1)
         H = dlr_to_dense(H["D"], H["U"])
     Hsrc = nat.to_gpu(H).float()
-    Hg = rotate_hessian_gpu(Hsrc, rotate_h) if rotate_h > 0 else Hsrc
+    # a 2-D Hessian is factored from its lower triangle only, so only the
+    # blocks on and below the diagonal are rotated (the fallback chain's
+    # restore() below rotates the whole matrix); a copy made here is rotated
+    # in place
+    Hg = (rotate_hessian_gpu(Hsrc, rotate_h, lower_only=Hsrc.dim() == 2, inplace=Hsrc.data_ptr() != H.data_ptr())
+          if rotate_h > 0 else Hsrc)
     # a Hessian this function created (rotated, or copied to the GPU / fp32)
     # is inverted in place; the fallback chain rebuilds it from the caller's
     # untouched one

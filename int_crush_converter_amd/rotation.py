@@ -1,15 +1,30 @@
 """ConvRot group-wise Hadamard rotation (API of ``converter/rotation.py``).
 
 ``make_hadamard_*`` / ``get_hadamard`` build the dense matrices (used for
-reference and inverse transforms by callers); the rotations themselves run as
-a fast Walsh-Hadamard transform in the HIP library (``ic_rotate_rows``,
-``ic_rotate_hessian``): 2·log4(R) flops per element instead of the dense
-R-wide dot product.
+reference and inverse transforms by callers).  The rotations run in the HIP
+library with one of two kernels:
+
+* ``"exact"`` (the default): the dense product in the reference's own fp32
+  summation order - every output one fused multiply-add chain over the
+  group in increasing order, as the reference's CPU ``x @ H.T`` and its
+  Hessian einsum round (``ic_rotate_rows_exact``,
+  ``ic_rotate_hessian_exact``, K = 1 MFMA chains on the matrix cores).
+  Results are bit-identical to the reference's for rot <= 512 (weights) and
+  rot <= 256 (Hessians); 2·R flops per element.
+* ``"fwht"``: a fast Walsh-Hadamard transform (``ic_rotate_rows``,
+  ``ic_rotate_hessian``): 2·log4(R) flops per element, HBM-bound; equal to
+  the reference's within a few fp32 ulps, not bit for bit.
+
+Sizes the exact kernels do not cover (rot >= 1024, where the reference's
+CPU GEMM splits the sum in a way of its own) use the FWHT.  The choice is
+process-wide: ``set_rotation_kernel()``, or the environment variable
+``IC_ROTATION_KERNEL`` read at import.
 """
 
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 import torch.nn.functional as F
@@ -63,6 +78,26 @@ def clear_hadamard_cache() -> None:
     _hadamard_cache.clear()
 
 
+_KERNELS = ("exact", "fwht")
+_kernel = os.environ.get("IC_ROTATION_KERNEL", "exact")
+if _kernel not in _KERNELS:
+    raise ValueError(f"IC_ROTATION_KERNEL must be one of {_KERNELS}, got {_kernel!r}")
+
+
+def set_rotation_kernel(kind: str) -> str:
+    """Select the rotation kernel ("exact" or "fwht") for every later call;
+    returns the previous choice."""
+    global _kernel
+    if kind not in _KERNELS:
+        raise ValueError(f"rotation kernel must be one of {_KERNELS}, got {kind!r}")
+    prev, _kernel = _kernel, kind
+    return prev
+
+
+def rotation_kernel() -> str:
+    return _kernel
+
+
 def _check_rot(rot_size: int) -> None:
     if not _is_power_of_two(rot_size):
         raise ValueError(f"rot_size must be a power of 2, got {rot_size}")
@@ -81,9 +116,10 @@ def rotate_rows_gpu(W: torch.Tensor, rot_size: int, zero_above: float = 0.0,
     cols_pad = -(-cols // rot_size) * rot_size
     out = torch.empty(rows, cols_pad, dtype=torch.float32, device=W.device)
     L = nat.lib()
-    nat.check(L.ic_rotate_rows(W.data_ptr(), nat.dtype_code(W), rows, cols, cols, out.data_ptr(),
-                               cols_pad, cols_pad, rot_size, float(zero_above), nat.ptr(n_zeroed), nat.stream()),
-              "ic_rotate_rows")
+    exact = _kernel == "exact" and rot_size <= 512
+    fn, name = (L.ic_rotate_rows_exact, "ic_rotate_rows_exact") if exact else (L.ic_rotate_rows, "ic_rotate_rows")
+    nat.check(fn(W.data_ptr(), nat.dtype_code(W), rows, cols, cols, out.data_ptr(), cols_pad, cols_pad, rot_size,
+                 float(zero_above), nat.ptr(n_zeroed), nat.stream()), name)
     return out
 
 
@@ -112,19 +148,41 @@ def rotate_activations(x: torch.Tensor, rot_size: int) -> torch.Tensor:
     return out.reshape(*lead, out.shape[-1])
 
 
-def rotate_hessian_gpu(H: torch.Tensor, rot_size: int) -> torch.Tensor:
-    """R^T H R of a 2-D or 3-D fp32 GPU Hessian (padded first for 2-D); a new
-    tensor.  Internal fast path used by the GPTQ/LDLQ drivers."""
+def _check_hessian_rot(rot_size: int) -> None:
+    # rotate_hessian takes the regular (power-of-4) matrix only
+    # (converter/rotation.py:247 -> get_hadamard -> make_hadamard_regular)
+    if not _is_power_of_four(rot_size):
+        raise ValueError(f"Regular Hadamard requires power of 4, got {rot_size}. Use rot_size=16/64/256.")
+
+
+def rotate_hessian_gpu(H: torch.Tensor, rot_size: int, lower_only: bool = False,
+                       inplace: bool = False) -> torch.Tensor:
+    """R^T H R of a 2-D or 3-D fp32 GPU Hessian (padded first for 2-D).
+    Internal fast path used by the GPTQ/LDLQ drivers.  ``inplace``: H (a
+    contiguous fp32 tensor the caller owns) is overwritten when no padding
+    is needed.  ``lower_only`` (2-D, exact kernel): only the rot x rot blocks
+    on and below the block diagonal are rotated - all that the lower Cholesky
+    factorisation and the damping read; the other entries are unspecified
+    (in place: input values or partial results, out of place: unset)."""
+    _check_hessian_rot(rot_size)
     H = H.float().contiguous()
     if H.dim() == 2 and H.shape[0] % rot_size:
         p = rot_size - H.shape[0] % rot_size
         src = out = F.pad(H, (0, p, 0, p))          # a new tensor: rotated in place
+    elif inplace:
+        src = out = H
     else:
         src, out = H, torch.empty_like(H)          # the first pass reads H and writes out
     batch, n = (1, out.shape[0]) if out.dim() == 2 else (out.shape[0], out.shape[1])
     if out.numel():
-        nat.check(nat.lib().ic_rotate_hessian(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size,
-                                              nat.stream()), "ic_rotate_hessian")
+        L = nat.lib()
+        if _kernel == "exact" and rot_size <= 256:
+            nat.check(L.ic_rotate_hessian_exact(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size,
+                                                int(bool(lower_only) and batch == 1), nat.stream()),
+                      "ic_rotate_hessian_exact")
+        else:
+            nat.check(L.ic_rotate_hessian(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size, nat.stream()),
+                      "ic_rotate_hessian")
     return out
 
 
@@ -132,7 +190,8 @@ def rotate_hessian(H, rot_size: int):
     """Hessian in the rotated weight space: H_rot = R^T H R (reference
     rotation.py:156-248).  2-D input is zero-padded to a multiple of
     ``rot_size``; 3-D [blocks, bs, bs] input needs bs % rot_size == 0; a DLR
-    dict becomes the rotated dense 2-D Hessian (on the GPU)."""
+    dict becomes the rotated dense 2-D Hessian (on the GPU).  Like the
+    reference, only powers of 4 are accepted (its get_hadamard)."""
     if not _is_power_of_two(rot_size):
         raise ValueError(f"rot_size must be a power of 2, got {rot_size}")
     if isinstance(H, dict):

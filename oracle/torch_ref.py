@@ -15,8 +15,12 @@ Parity pinning (how each function is checked against something other than
 itself; see tests/test_oracle.py):
   * hadamard_regular / hadamard_sylvester: closed form (involution, entries
     +-2^-k, Kronecker structure), reference KATs of tests/test_rotation.py.
-  * rotate_weights / rotate_hessian: brute-force dense R, norm and trace
-    preservation, (XR)^T(XR) identity.
+  * rotate_weights / rotate_hessian: the reference's own outputs, bit for
+    bit (tests/golden/golden_rotation.safetensors: every rot to 512, 2-D /
+    3-D Hessians); an independent numpy restatement of the sequential fp32
+    chains; brute-force dense R, norm and trace preservation, (XR)^T(XR)
+    identity.  The products run in rotation_seq.c (C, no BLAS) so the
+    oracle rounds like the reference on any host.
   * rhaz: reference KATs (tests/unit/test_ldlq_hessian.py:34-49), numpy.
   * rtn_* scale/quantize functions: reference KAT (tests/test_scales.py:48-55),
     numpy float32 restatement of every formula, brute-force clip search.
@@ -112,23 +116,69 @@ def _hadamard_for(n: int, dtype) -> torch.Tensor:
     return hadamard_regular(n, dtype) if is_pow4(n) else hadamard_sylvester(n, dtype)
 
 
+_ROT_LIB = None
+
+
+def _rot_lib():
+    """ctypes handle of rotation_seq.c (built by oracle/build.py, on demand
+    where gcc exists)."""
+    global _ROT_LIB
+    if _ROT_LIB is None:
+        import ctypes
+        import os
+        from oracle import build as _b
+        if not os.path.exists(_b.LIB):
+            _b.build()
+        lib = ctypes.CDLL(_b.LIB)
+        for fn in (lib.oracle_rotate_rows, lib.oracle_rotate_blocks):
+            fn.restype = ctypes.c_int
+        lib.oracle_rotate_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_int]
+        lib.oracle_rotate_blocks.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_int]
+        _ROT_LIB = lib
+    return _ROT_LIB
+
+
 def rotate_weights(W: torch.Tensor, rot: int) -> torch.Tensor:
     """Pad the last dim to a multiple of ``rot``, then ``x @ H.T`` per group
-    (rotation.py:95-125)."""
+    (rotation.py:95-125).  For fp32 and rot 2 .. 512 the product is the C
+    restatement of the reference's rounding (rotation_seq.c: sequential fma
+    chains, as the reference's CPU sgemm rounds); otherwise torch's matmul."""
     M, N = W.shape
     if N % rot:
         W = F.pad(W, (0, rot - N % rot))
     g = W.shape[1] // rot
+    if W.dtype == torch.float32 and 2 <= rot <= 512 and W.numel():
+        x = W.contiguous()
+        out = torch.empty_like(x)
+        if _rot_lib().oracle_rotate_rows(x.data_ptr(), M, x.shape[1], out.data_ptr(), rot,
+                                         torch.get_num_threads()) != 0:
+            raise RuntimeError("oracle_rotate_rows failed")
+        return out
     Hm = _hadamard_for(rot, W.dtype)
     return (W.reshape(M, g, rot) @ Hm.T).reshape(M, -1)
 
 
 def rotate_hessian(H: torch.Tensor, rot: int) -> torch.Tensor:
-    """R^T H R on 2-D or 3-D Hessians (rotation.py:156-248)."""
+    """R^T H R on 2-D or 3-D Hessians (rotation.py:156-248).  Only the
+    regular matrix: rotation.py:247 takes it from get_hadamard, which raises
+    for sizes that are not powers of 4 (rotation.py:45-47)."""
+    if not is_pow4(rot):
+        raise ValueError(f"Regular Hadamard requires power of 4, got {rot}. Use rot_size=16/64/256.")
     H = H.float()
-    R = hadamard_regular(rot, H.dtype) if is_pow4(rot) else hadamard_sylvester(rot, H.dtype)
+    R = hadamard_regular(rot, H.dtype)
 
     def blocks(h3):
+        # the einsum's two products, each as sequential fma chains
+        # (rotation_seq.c), for the sizes whose order is pinned
+        if rot <= 256 and h3.numel():
+            h3 = h3.contiguous()
+            out = torch.empty_like(h3)
+            if _rot_lib().oracle_rotate_blocks(h3.data_ptr(), h3.shape[0], out.data_ptr(), rot,
+                                               torch.get_num_threads()) != 0:
+                raise RuntimeError("oracle_rotate_blocks failed")
+            return out
         return torch.einsum("kp, nkl, le -> npe", R, h3, R)
 
     if H.dim() == 2:

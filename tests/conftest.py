@@ -45,6 +45,17 @@ def golden_greedy_gpu():
     return tensors, meta
 
 
+@pytest.fixture(scope="session")
+def golden_rotation():
+    """Inputs and outputs of the reference's rotate_weights / rotate_hessian,
+    written by tests/golden/make_golden.py --rotation."""
+    from safetensors.torch import load_file
+    tensors = load_file(os.path.join(GOLDEN_DIR, "golden_rotation.safetensors"))
+    with open(os.path.join(GOLDEN_DIR, "golden_rotation.json")) as f:
+        meta = json.load(f)
+    return tensors, meta
+
+
 @pytest.fixture
 def one_thread():
     """Pin torch to one intra-op thread (MKL rounding depends on blocking)."""

@@ -13,6 +13,17 @@ the outputs are stored as ``.safetensors`` next to this script.
 
     PYTHONPATH=/root/reference python tests/golden/make_golden.py --greedy-gpu
 
+    PYTHONPATH=/root/reference python tests/golden/make_golden.py --rotation
+
+writes ``golden_rotation.safetensors`` / ``.json``: inputs and outputs of
+the reference's ``rotate_weights`` (every power of 2 up to 512, fp32 and
+bf16 sources, padding, the pipeline's outlier zeroing first) and
+``rotate_hessian`` (2-D with padding, 3-D whole blocks and sub-blocks), plus
+the raw W and H of the rotated GPTQ golden cases with their rotations.
+These pin the fp32 rounding of the rotation itself.
+
+    PYTHONPATH=/root/reference python tests/golden/make_golden.py --greedy-gpu
+
 writes ``golden_greedy_gpu.safetensors`` / ``.json`` instead: the
 reference's GPU greedy backends (the low-rank kernel of
 converter/greedy.py:99-199, 369-479 and the full-rank v2 path of
@@ -29,6 +40,7 @@ import sys
 import tempfile
 
 GREEDY_GPU = "--greedy-gpu" in sys.argv
+ROTATION = "--rotation" in sys.argv
 if GREEDY_GPU:
     os.environ["TRITON_INTERPRET"] = "1"   # must precede the first triton import
 
@@ -47,6 +59,7 @@ from converter.scales import (  # noqa: E402
 )
 from converter.rotation import rotate_weights, rotate_hessian  # noqa: E402
 from converter.pipeline import quantize_model  # noqa: E402
+from converter.config import WEIGHT_OUTLIER_CLAMP  # noqa: E402
 from converter.types import QuantizeConfig  # noqa: E402
 
 
@@ -179,6 +192,53 @@ def pipeline_cases(out: dict, meta: dict) -> None:
             out[f"pipe_in/{k}"] = v
 
 
+def rotation_cases(out: dict, meta: dict) -> None:
+    # weights: every power of 2 up to 512 (regular for powers of 4, else
+    # Sylvester), fp32 source with padding (300 columns)
+    for rot in (2, 4, 8, 16, 32, 64, 128, 256, 512):
+        W = weights(33, 300, 600 + rot, std=1.0)
+        out[f"rw{rot}.W"] = W
+        out[f"rw{rot}.out"] = rotate_weights(W, rot)
+        meta[f"rw{rot}"] = dict(kind="rotate_weights", rot=rot)
+    # bf16 source (cast to fp32 first, converter/pipeline.py:524) at R = 256 and 64
+    for rot in (64, 256):
+        Wb = weights(20, 512, 700 + rot).to(torch.bfloat16)
+        out[f"rwb{rot}.W"] = Wb
+        out[f"rwb{rot}.out"] = rotate_weights(Wb.float(), rot)
+        meta[f"rwb{rot}"] = dict(kind="rotate_weights", rot=rot, source="bf16")
+    # the pipeline's outlier zeroing before rotation (converter/pipeline.py:527-555)
+    W = weights(16, 256, 800)
+    W[0, 3], W[5, 100], W[15, 255] = 5000.0, -1500.0, 1000.5
+    Wz = W.masked_fill(W.abs() > WEIGHT_OUTLIER_CLAMP, 0.0)
+    out["rwz.W"] = W
+    out["rwz.out"] = rotate_weights(Wz, 256)
+    meta["rwz"] = dict(kind="rotate_weights", rot=256, zero_above=WEIGHT_OUTLIER_CLAMP, zeroed=3)
+    # Hessians: 2-D (padded when n % rot), 3-D whole blocks and sub-blocks
+    for name, rot, n in (("rh16", 16, 64), ("rh64", 64, 200), ("rh256", 256, 300)):
+        H = lognormal_hessian(n, 2 * n, 900 + n + rot)
+        out[f"{name}.H"] = H
+        out[f"{name}.out"] = rotate_hessian(H, rot)
+        meta[name] = dict(kind="rotate_hessian", rot=rot, n=n)
+    for name, rot, nb, bs in (("rh3_256", 256, 1, 256), ("rh3_64", 64, 2, 128), ("rh3_16", 16, 3, 64)):
+        H3 = torch.stack([lognormal_hessian(bs, 2 * bs, 950 + b) for b in range(nb)])
+        out[f"{name}.H"] = H3
+        out[f"{name}.out"] = rotate_hessian(H3, rot)
+        meta[name] = dict(kind="rotate_hessian", rot=rot, blocks=nb, bs=bs)
+    # the raw inputs of rotated GPTQ golden cases (gptq_cases above); their
+    # rotations are that file's <name>.W / <name>.H, checked equal here
+    gold = load_file(os.path.join(HERE, "golden.safetensors"))
+    for name, k, M, N, S, rot in (("gptq_b", 1, 48, 256, 128, 256), ("gptq_d", 3, 32, 192, 400, 64),
+                                  ("gptq_e", 4, 32, 256, 400, 16)):
+        W = weights(M, N, 100 + k)
+        H = lognormal_hessian(N, S, 200 + k)
+        if not (torch.equal(rotate_weights(W, rot), gold[f"{name}.W"])
+                and torch.equal(rotate_hessian(H, rot), gold[f"{name}.H"])):
+            raise SystemExit(f"{name}: regenerated inputs do not rotate to the stored golden case")
+        out[f"{name}_raw.W"] = W
+        out[f"{name}_raw.H"] = H
+        meta[f"{name}_raw"] = dict(kind="gptq_raw", rot=rot)
+
+
 def greedy_gpu_cases(out: dict, meta: dict) -> None:
     """Reference GPU greedy backends on seeded inputs.  Each case starts from
     RTN codes of W and the per-row least-squares scales of those codes (what
@@ -246,6 +306,16 @@ def main() -> None:
         with open(os.path.join(HERE, "golden_greedy_gpu.json"), "w") as f:
             json.dump(meta, f, indent=1, sort_keys=True)
         print(f"wrote {len(out)} tensors, {len(meta)} cases: {meta}")
+        return
+    if ROTATION:
+        out: dict[str, torch.Tensor] = {}
+        meta: dict = {}
+        rotation_cases(out, meta)
+        out = {k: v.contiguous() for k, v in out.items()}
+        save_file(out, os.path.join(HERE, "golden_rotation.safetensors"))
+        with open(os.path.join(HERE, "golden_rotation.json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
+        print(f"wrote {len(out)} tensors, {len(meta)} cases")
         return
     out: dict[str, torch.Tensor] = {}
     meta: dict = {}

@@ -213,19 +213,28 @@ def test_hessian_in_place_fallback_uses_restore(gpu_dev):
     assert torch.allclose(got, torch.linalg.inv(ref.damp(H, 0.01)), atol=1e-5)
 
 
-def test_rotate_hessian_out_of_place(gpu_dev):
-    from int_crush_converter_amd.rotation import rotate_hessian_gpu
+@pytest.mark.parametrize("kernel", ["exact", "fwht"])
+def test_rotate_hessian_out_of_place(gpu_dev, kernel):
+    from int_crush_converter_amd.rotation import rotate_hessian_gpu, set_rotation_kernel
     H = lognormal_hessian(512, 600, 5).to(gpu_dev)
     H0 = H.clone()
-    got = rotate_hessian_gpu(H, 256)
+    prev = set_rotation_kernel(kernel)
+    try:
+        got = rotate_hessian_gpu(H, 256)
+    finally:
+        set_rotation_kernel(prev)
     assert torch.equal(H, H0) and got.data_ptr() != H.data_ptr()
     want = ref.rotate_hessian(H0.cpu(), 256)
     assert torch.allclose(got.cpu(), want, atol=2e-6 * want.abs().max().item(), rtol=0)
     # src == dst through the C ABI (what the padded path does): the same bits
     from int_crush_converter_amd import _native as nat
     inplace = H0.clone()
-    nat.check(nat.lib().ic_rotate_hessian(inplace.data_ptr(), inplace.data_ptr(), 1, 512, 512, 256,
-                                          nat.stream()), "ic_rotate_hessian")
+    if kernel == "exact":
+        nat.check(nat.lib().ic_rotate_hessian_exact(inplace.data_ptr(), inplace.data_ptr(), 1, 512, 512, 256, 0,
+                                                    nat.stream()), "ic_rotate_hessian_exact")
+    else:
+        nat.check(nat.lib().ic_rotate_hessian(inplace.data_ptr(), inplace.data_ptr(), 1, 512, 512, 256,
+                                              nat.stream()), "ic_rotate_hessian")
     assert torch.equal(inplace, got)
 
 

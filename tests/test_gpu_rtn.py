@@ -2,9 +2,11 @@
 the verification error, HIP library vs the CPU oracle.
 
 Bars: codes, packed bytes and fp16 scales bit-exact given the same fp32
-input (RTN is integer-valued arithmetic on identical fp32 operands);
-rotation within 2e-6 relative to the row norm (the FWHT and the reference's
-dense GEMM round differently); fp64 MSE within 1e-9 relative.
+input (RTN is integer-valued arithmetic on identical fp32 operands); the
+exact rotation kernels bit-exact against the reference's own rotated tensors
+(tests/golden/golden_rotation.safetensors); the FWHT kernels within 2e-6
+relative to the row norm (they associate the sums differently); fp64 MSE
+within 1e-9 relative.
 """
 
 from __future__ import annotations
@@ -29,9 +31,17 @@ def _w(m, n, seed, std=0.02, outliers=0):
     return W
 
 
+@pytest.fixture(params=["exact", "fwht"])
+def rot_kernel(request):
+    from int_crush_converter_amd.rotation import set_rotation_kernel
+    prev = set_rotation_kernel(request.param)
+    yield request.param
+    set_rotation_kernel(prev)
+
+
 @pytest.mark.parametrize("rot", [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024])
 @pytest.mark.parametrize("n", [256, 300])
-def test_rotate_weights_matches_oracle(gpu_dev, rot, n):
+def test_rotate_weights_matches_oracle(gpu_dev, rot_kernel, rot, n):
     from int_crush_converter_amd.rotation import rotate_weights
     W = _w(33, n, rot + n, std=1.0)
     want = ref.rotate_weights(W, rot)
@@ -41,7 +51,7 @@ def test_rotate_weights_matches_oracle(gpu_dev, rot, n):
     assert torch.all((got - want).abs() <= tol), (got - want).abs().max()
 
 
-def test_rotate_weights_bf16_source(gpu_dev):
+def test_rotate_weights_bf16_source(gpu_dev, rot_kernel):
     from int_crush_converter_amd.rotation import rotate_rows_gpu
     W = _w(64, 4096, 3).to(torch.bfloat16)
     want = ref.rotate_weights(W.float(), 256)
@@ -49,7 +59,7 @@ def test_rotate_weights_bf16_source(gpu_dev):
     assert torch.allclose(got, want, atol=1e-7, rtol=0)
 
 
-def test_rotate_weights_deterministic(gpu_dev):
+def test_rotate_weights_deterministic(gpu_dev, rot_kernel):
     from int_crush_converter_amd.rotation import rotate_rows_gpu
     W = _w(128, 1024, 4).to(gpu_dev)
     a = rotate_rows_gpu(W, 256)
@@ -93,8 +103,8 @@ def test_rotate256_coalesced_equals_register_kernel(gpu_dev, dtype, rows, cols):
     assert int(nz_a.item()) == int(nz_b.item()) == 2
 
 
-@pytest.mark.parametrize("rot,n", [(16, 64), (64, 192), (256, 512), (256, 300), (128, 256)])
-def test_rotate_hessian_2d(gpu_dev, rot, n):
+@pytest.mark.parametrize("rot,n", [(16, 64), (64, 192), (256, 512), (256, 300), (4, 40)])
+def test_rotate_hessian_2d(gpu_dev, rot_kernel, rot, n):
     from int_crush_converter_amd.rotation import rotate_hessian
     H = lognormal_hessian(n, 2 * n, 5)
     want = ref.rotate_hessian(H, rot)
@@ -103,12 +113,144 @@ def test_rotate_hessian_2d(gpu_dev, rot, n):
     assert torch.allclose(got, want, atol=2e-6 * want.abs().max().item(), rtol=0)
 
 
-def test_rotate_hessian_3d(gpu_dev):
+def test_rotate_hessian_3d(gpu_dev, rot_kernel):
     from int_crush_converter_amd.rotation import rotate_hessian
     H = torch.stack([lognormal_hessian(256, 300, s) for s in range(3)])
     want = ref.rotate_hessian(H, 64)
     got = rotate_hessian(H.to(gpu_dev), 64).cpu()
     assert torch.allclose(got, want, atol=2e-6 * want.abs().max().item(), rtol=0)
+
+
+# ------------------------------------------- exact rotation vs the reference
+
+def test_exact_rotate_weights_equals_reference(gpu_dev, golden_rotation):
+    """ic_rotate_rows_exact gives the reference's rotate_weights bits for
+    every rot up to 512 (regular and Sylvester), fp32 and bf16 sources and
+    padded groups."""
+    from int_crush_converter_amd.rotation import rotate_rows_gpu, set_rotation_kernel
+    t, meta = golden_rotation
+    prev = set_rotation_kernel("exact")
+    try:
+        for name, m in meta.items():
+            if m["kind"] != "rotate_weights" or "zero_above" in m:
+                continue
+            got = rotate_rows_gpu(t[f"{name}.W"].to(gpu_dev), m["rot"]).cpu()
+            assert torch.equal(got, t[f"{name}.out"]), (name, (got != t[f"{name}.out"]).sum().item())
+    finally:
+        set_rotation_kernel(prev)
+
+
+def test_exact_rotate_weights_outlier_zeroing(gpu_dev, golden_rotation):
+    """The pipeline's |w| > 1000 zeroing fused into the exact rotation
+    (converter/pipeline.py:527-555): the reference's bits and its count."""
+    from int_crush_converter_amd.layer import prepare_weights
+    from int_crush_converter_amd.rotation import set_rotation_kernel
+    t, meta = golden_rotation
+    prev = set_rotation_kernel("exact")
+    try:
+        for dtype in (torch.float32, torch.bfloat16):
+            W = t["rwz.W"].to(dtype)
+            W_work, nz = prepare_weights(W.to(gpu_dev), 256)
+            Wf = W.float()
+            want = t["rwz.out"] if dtype == torch.float32 else ref.rotate_weights(Wf.masked_fill(Wf.abs() > 1000.0, 0.0),
+                                                                                 256)
+            assert torch.equal(W_work.cpu(), want), dtype
+            # bf16 rounds 1000.5 to 1000, which is not above the threshold
+            assert int(nz.item()) == int((Wf.abs() > 1000.0).sum()), dtype
+        assert meta["rwz"]["zeroed"] == 3
+    finally:
+        set_rotation_kernel(prev)
+
+
+def test_exact_rotate_hessian_equals_reference(gpu_dev, golden_rotation):
+    """ic_rotate_hessian_exact gives the reference's rotate_hessian bits
+    (2-D with padding, 3-D whole blocks and sub-blocks)."""
+    from int_crush_converter_amd.rotation import rotate_hessian, set_rotation_kernel
+    t, meta = golden_rotation
+    prev = set_rotation_kernel("exact")
+    try:
+        for name, m in meta.items():
+            if m["kind"] != "rotate_hessian":
+                continue
+            got = rotate_hessian(t[f"{name}.H"].to(gpu_dev), m["rot"]).cpu()
+            assert torch.equal(got, t[f"{name}.out"]), (name, (got != t[f"{name}.out"]).sum().item())
+    finally:
+        set_rotation_kernel(prev)
+
+
+def test_exact_rotation_of_golden_gptq_inputs(gpu_dev, golden, golden_rotation):
+    """The raw W / H of the rotated GPTQ golden cases rotate on the GPU to
+    exactly the tensors the reference quantised."""
+    from int_crush_converter_amd.rotation import rotate_hessian_gpu, rotate_rows_gpu, set_rotation_kernel
+    g, _ = golden
+    t, meta = golden_rotation
+    prev = set_rotation_kernel("exact")
+    try:
+        for name, m in meta.items():
+            if m["kind"] != "gptq_raw":
+                continue
+            case = name[:-len("_raw")]
+            assert torch.equal(rotate_rows_gpu(t[f"{name}.W"].to(gpu_dev), m["rot"]).cpu(), g[f"{case}.W"]), name
+            assert torch.equal(rotate_hessian_gpu(t[f"{name}.H"].to(gpu_dev), m["rot"]).cpu(), g[f"{case}.H"]), name
+    finally:
+        set_rotation_kernel(prev)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rot,rows,cols", [(256, 33, 512), (64, 70, 300), (16, 5, 40), (512, 9, 1000)])
+def test_exact_rotation_unaligned_source(gpu_dev, dtype, rot, rows, cols):
+    """ic_rotate_rows_exact from a source one element in (no vector loads)
+    gives the bits of the aligned source, outlier zeroing and count included."""
+    from int_crush_converter_amd import _native as nat
+    g = torch.Generator().manual_seed(rot + rows)
+    W = torch.randn(rows, cols + 8, generator=g) * 0.02
+    W[0, 5] = 5000.0
+    W[-1, cols - 1] = -2000.0
+    code = nat.dtype_code(W.to(dtype))
+    cols_pad = -(-cols // rot) * rot
+
+    def run(ptr, ld):
+        out = torch.empty(rows, cols_pad, dtype=torch.float32, device=gpu_dev)
+        nz = torch.zeros(1, dtype=torch.int64, device=gpu_dev)
+        nat.check(nat.lib().ic_rotate_rows_exact(ptr, code, rows, cols, ld, out.data_ptr(), cols_pad, cols_pad, rot,
+                                                 1000.0, nz.data_ptr(), nat.stream()), "ic_rotate_rows_exact")
+        return out.cpu(), int(nz.item())
+
+    aligned = W[:, :cols].to(dtype).contiguous().to(gpu_dev)
+    a, na = run(aligned.data_ptr(), cols)
+    shifted = torch.cat([torch.zeros(rows, 1), W[:, :cols + 7]], 1).to(dtype).to(gpu_dev)
+    b, nb = run(shifted.data_ptr() + shifted.element_size(), cols + 8)
+    assert torch.equal(a, b) and na == nb == 2
+    Wz = W[:, :cols].to(dtype).float()
+    want = ref.rotate_weights(Wz.masked_fill(Wz.abs() > 1000.0, 0.0), rot)
+    assert torch.allclose(a, want, atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("rot,n", [(256, 768), (64, 320), (16, 128)])
+def test_exact_rotate_hessian_lower_blocks(gpu_dev, rot, n):
+    """lower_only writes the blocks on and below the block diagonal with the
+    full rotation's bits (in place, the rest stays finite: input values or
+    partial results)."""
+    from int_crush_converter_amd.rotation import rotate_hessian_gpu, set_rotation_kernel
+    prev = set_rotation_kernel("exact")
+    try:
+        H = lognormal_hessian(n, 2 * n, 40 + rot).to(gpu_dev)
+        full = rotate_hessian_gpu(H, rot)
+        part = rotate_hessian_gpu(H.clone(), rot, lower_only=True, inplace=True)
+        blk = torch.arange(n, device=gpu_dev) // rot
+        lower = blk[:, None] >= blk[None, :]
+        assert torch.equal(part[lower], full[lower])
+        assert torch.isfinite(part).all()
+        assert torch.equal(full.cpu(), ref.rotate_hessian(H.cpu(), rot))
+    finally:
+        set_rotation_kernel(prev)
+
+
+@pytest.mark.parametrize("rot", [2, 8, 32, 128])
+def test_rotate_hessian_rejects_non_power_of_four(gpu_dev, rot):
+    from int_crush_converter_amd.rotation import rotate_hessian
+    with pytest.raises(ValueError, match="power of 4"):
+        rotate_hessian(torch.eye(2 * rot, device=gpu_dev), rot)
 
 
 @pytest.mark.parametrize("bits,asym", [(4, False), (4, True), (8, False), (8, True)])

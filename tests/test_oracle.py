@@ -88,6 +88,99 @@ def test_rotate_hessian_3d_subblocks():
         assert torch.allclose(out[b], want, atol=1e-3)
 
 
+# ------------------------------------------------ rotation rounding (goldens)
+
+def _seq_rows_np(x: np.ndarray, rot: int) -> np.ndarray:
+    """Sequential fp32 chains y_j = (((0 + x_0 h_0j) + x_1 h_1j) + ...) per
+    group of ``rot`` columns, in numpy.  The regular Hadamard's entries are
+    +-2^-k, so every product is exact and an fp32 add after an fp32 multiply
+    IS the fused multiply-add: this restates, without torch, the order the
+    reference's CPU GEMM rounds in."""
+    assert ref.is_pow4(rot)
+    h = ref.hadamard_regular(rot).numpy()
+    m, n = x.shape
+    xg = x.reshape(m, n // rot, rot)
+    acc = np.zeros_like(xg, dtype=np.float32)
+    for k in range(rot):
+        acc = (acc + xg[:, :, k:k + 1] * h[k][None, None, :]).astype(np.float32)
+    return acc.reshape(m, n)
+
+
+def _pad(x: torch.Tensor, rot: int) -> torch.Tensor:
+    return torch.nn.functional.pad(x, (0, (-x.shape[1]) % rot))
+
+
+def test_rotation_golden_cases_present(golden_rotation):
+    t, meta = golden_rotation
+    kinds = {m["kind"] for m in meta.values()}
+    assert kinds == {"rotate_weights", "rotate_hessian", "gptq_raw"}
+    assert {m["rot"] for m in meta.values() if m["kind"] == "rotate_weights"} >= {2, 4, 8, 16, 32, 64, 128, 256, 512}
+
+
+def test_oracle_rotate_weights_equals_reference(golden_rotation):
+    """The oracle's x @ H.T gives the reference's bits (every rot to 512,
+    fp32 / bf16 sources, padding, the pipeline's outlier zeroing)."""
+    t, meta = golden_rotation
+    for name, m in meta.items():
+        if m["kind"] != "rotate_weights":
+            continue
+        W = t[f"{name}.W"].float()
+        if "zero_above" in m:
+            W = W.masked_fill(W.abs() > m["zero_above"], 0.0)
+        assert torch.equal(ref.rotate_weights(W, m["rot"]), t[f"{name}.out"]), name
+
+
+def test_sequential_chain_restatement_equals_reference(golden_rotation):
+    """Independent of torch: the sequential fp32 chain (numpy) reproduces the
+    reference's rotated weights and both products of its Hessian rotation
+    bit for bit - the order the exact GPU kernels implement."""
+    t, meta = golden_rotation
+    for name, m in meta.items():
+        if m["kind"] == "rotate_weights" and ref.is_pow4(m["rot"]):
+            W = t[f"{name}.W"].float()
+            if "zero_above" in m:
+                W = W.masked_fill(W.abs() > m["zero_above"], 0.0)
+            got = _seq_rows_np(_pad(W, m["rot"]).numpy(), m["rot"])
+            assert np.array_equal(got, t[f"{name}.out"].numpy()), name
+        elif m["kind"] == "rotate_hessian" and t[f"{name}.H"].dim() == 2:
+            rot = m["rot"]
+            H = t[f"{name}.H"]
+            n = H.shape[0] + (-H.shape[0]) % rot
+            Hp = torch.zeros(n, n)
+            Hp[:H.shape[0], :H.shape[0]] = H
+            # left product: T = R^T H, a chain over the rows of each block
+            # = the row chain applied to the columns (R is symmetric)
+            T = _seq_rows_np(np.ascontiguousarray(Hp.numpy().T), rot).T
+            O = _seq_rows_np(np.ascontiguousarray(T), rot)
+            assert np.array_equal(O, t[f"{name}.out"].numpy()), name
+
+
+def test_oracle_rotate_hessian_equals_reference(golden_rotation):
+    t, meta = golden_rotation
+    for name, m in meta.items():
+        if m["kind"] == "rotate_hessian":
+            assert torch.equal(ref.rotate_hessian(t[f"{name}.H"], m["rot"]), t[f"{name}.out"]), name
+
+
+def test_golden_raw_inputs_rotate_to_golden_cases(golden, golden_rotation):
+    """The stored raw W / H of the rotated GPTQ goldens rotate (oracle) to
+    the rotated inputs those cases were quantised from."""
+    g, _ = golden
+    t, meta = golden_rotation
+    for name, m in meta.items():
+        if m["kind"] == "gptq_raw":
+            case = name[:-len("_raw")]
+            assert torch.equal(ref.rotate_weights(t[f"{name}.W"], m["rot"]), g[f"{case}.W"]), name
+            assert torch.equal(ref.rotate_hessian(t[f"{name}.H"], m["rot"]), g[f"{case}.H"]), name
+
+
+@pytest.mark.parametrize("rot", [2, 8, 32, 128])
+def test_rotate_hessian_rejects_non_power_of_four(rot):
+    # converter/rotation.py:247 -> get_hadamard -> make_hadamard_regular raises
+    with pytest.raises(ValueError, match="power of 4"):
+        ref.rotate_hessian(torch.eye(2 * rot), rot)
+
+
 # ---------------------------------------------------------------- rounding
 
 def test_rhaz_reference_kats():
