@@ -309,15 +309,17 @@ int ic_ldlq_update_scales(const float* W, const int8_t* Q, const float* cur, con
 int ic_ls_scales(const int8_t* Q, const float* W, int64_t rows, int64_t cols, float* out, void* stream);
 
 /* Full-rank greedy coordinate descent on the integer grid minimising
- * tr((Q s - W) H (Q s - W)^T), `passes` sweeps over all columns, row scales
- * srow, H [cols, cols] fp32; Q (int8 [rows, cols]) updated in place.
+ * tr((Q s - W) H (Q s - W)^T), `passes` sweeps over all columns; scales
+ * per row (scale_kind 0: scale[rows]) or per element (scale_kind 1:
+ * scale[rows, cols], the reference's scale_2d), H [cols, cols] fp32;
+ * Q (int8 [rows, cols]) updated in place.
  * Column blocks of 64 take their cross terms from one fp32-MFMA GEMM plus
  * exact in-block corrections.  workspace: ic_greedy_workspace_bytes().
  * Replaces converter/greedy.py:487-541 (greedy_local_search_pytorch) and
  * 207-285 (greedy_local_search_triton). */
 int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols);
-int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
-              int passes, int bits, void* workspace, void* stream);
+int ic_greedy(const float* W, int8_t* Q, const float* scale, int scale_kind, const float* H, int64_t rows,
+              int64_t cols, int passes, int bits, void* workspace, void* stream);
 
 /* The p largest eigenpairs of a symmetric positive semi-definite H [n, n]
  * (fp32): seeded subspace iteration (`iters` steps of (H + mu I) Q with
@@ -342,8 +344,9 @@ int64_t ic_lowrank_workspace_bytes(int64_t n, int64_t p);
 int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned long long seed, float refuse_rel,
                     float* evals, float* evecs, int* sweeps, void* workspace, void* stream);
 
-/* Low-rank greedy search: the greedy of ic_greedy with the cross terms taken
- * from Hk = U_k diag(s_k) U_k^T (U [cols, >= k] pitch ldu, s [k]) and the
+/* Low-rank greedy search: the greedy of ic_greedy (same scale / scale_kind)
+ * with the cross terms taken from Hk = U_k diag(s_k) U_k^T (U [cols, >= k]
+ * pitch ldu, s [k]) and the
  * exact diagonal H_jj, i.e. cross_j = err . Hk[:, j] - err_j H_jj; after
  * every pass but the last, the proxy sum((err @ H) * err) with the full H
  * ends the search once it is >= 0.99 x the previous pass's (from the second
@@ -353,9 +356,9 @@ int ic_lowrank_eigs(const float* H, int64_t n, int64_t p, int iters, unsigned lo
  * Replaces converter/greedy.py:369-479 (greedy_lowrank_triton) and its
  * kernel 99-199 (_greedy_lowrank_kernel). */
 int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols, int64_t k);
-int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float* H, const float* U, int64_t ldu,
-                      const float* s, int64_t k, int64_t rows, int64_t cols, int passes, int bits,
-                      int* passes_run, void* workspace, void* stream);
+int ic_greedy_lowrank(const float* W, int8_t* Q, const float* scale, int scale_kind, const float* H,
+                      const float* U, int64_t ldu, const float* s, int64_t k, int64_t rows, int64_t cols,
+                      int passes, int bits, int* passes_run, void* workspace, void* stream);
 
 /* ---------------------------------------------------------------- PermuQuant */
 

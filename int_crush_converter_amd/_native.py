@@ -65,12 +65,12 @@ _SIGS = {
     "ic_ldlq_update_scales": (_i32, [_vp, _vp, _vp, _vp, _i64, _f32, _f32, _f32, _vp, _vp]),
     "ic_ls_scales": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "ic_greedy_workspace_bytes": (_i64, [_i64, _i64]),
-    "ic_greedy": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
+    "ic_greedy": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "ic_lowrank_workspace_bytes": (_i64, [_i64, _i64]),
     "ic_lowrank_eigs": (_i32, [_vp, _i64, _i64, _i32, _c.c_ulonglong, _f32, _vp, _vp, _c.POINTER(_i32), _vp,
                                _vp]),
     "ic_greedy_lowrank_workspace_bytes": (_i64, [_i64, _i64, _i64]),
-    "ic_greedy_lowrank": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32,
+    "ic_greedy_lowrank": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32,
                                  _c.POINTER(_i32), _vp, _vp]),
     "ic_hbm_stream": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "ic_profile_enable": (_i32, [_i32]),
@@ -131,6 +131,36 @@ def header_functions() -> list[str]:
     return sorted(set(re.findall(r"\b(ic_[a-z0-9_]+)\s*\(", text)))
 
 
+class _Checked:
+    """A library function that takes tensors where the C ABI takes device
+    pointers: a GPU tensor becomes its data pointer; a tensor in host memory
+    is refused with ValueError before the call, so no kernel is ever handed
+    a host address.  None (a NULL pointer) and plain integers pass through;
+    the library itself rejects a NULL where one is not allowed."""
+
+    __slots__ = ("fn", "name")
+
+    def __init__(self, fn, name: str):
+        self.fn, self.name = fn, name
+
+    def __call__(self, *args):
+        conv = list(args)
+        for i, a in enumerate(conv):
+            if isinstance(a, torch.Tensor):
+                if a.device.type != "cuda":
+                    raise ValueError(f"{self.name}: argument {i} is a {a.device.type} tensor; "
+                                     "the library takes GPU memory")
+                conv[i] = a.data_ptr()
+        return self.fn(*conv)
+
+
+class _Lib:
+    """The loaded library: one _Checked per function of _SIGS."""
+
+    def __init__(self, cdll):
+        self.cdll = cdll
+
+
 def load(require_gpu: bool = True):
     """Load the library once; raise RuntimeError if it is not built."""
     global _lib
@@ -143,11 +173,13 @@ def load(require_gpu: bool = True):
             raise RuntimeError(
                 f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
                 "(hipcc --offload-arch=gfx950).  There is no CPU fallback.")
-        lib = ctypes.CDLL(LIB_PATH)
+        cdll = ctypes.CDLL(LIB_PATH)
+        lib = _Lib(cdll)
         for name, (res, args) in _SIGS.items():
-            fn = getattr(lib, name)
+            fn = getattr(cdll, name)
             fn.restype = res
             fn.argtypes = args
+            setattr(lib, name, _Checked(fn, name))
         _lib = lib
     return _lib
 
@@ -166,8 +198,9 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
 
 
-def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+def ptr(t: torch.Tensor | None) -> torch.Tensor | None:
+    """An optional tensor argument (None = NULL); the library wrapper checks it."""
+    return t
 
 
 def stream() -> int:

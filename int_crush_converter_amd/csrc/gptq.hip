@@ -524,7 +524,7 @@ __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
         // the Hinv block: 32 loads per thread in flight (32-bit offsets from
         // the block's corner), then their LDS stores
         constexpr int NT = 64 * WV, CH = 32, ALL = SW_NB * SW_NB;
-        const int ldh = (int)a.ldh;   // the block spans < 2^31 elements (checked on the host)
+        const int ldh = (int)a.ldh;   // the block spans < 2^31 elements (launch_sweep checks it)
 #pragma unroll 1
         for (int base = 0; base < ALL; base += NT * CH) {
             float tmp[CH];
@@ -687,12 +687,10 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
         const dim3 g4((unsigned)cdiv(a.rows, 4 * SQ_ROWS), (unsigned)groups);
         const bool zp = a.zp != nullptr;
 #define ICQ_SWEEP4(M, Z) hipLaunchKernelGGL((sweep4_kernel<M, Z, 4>), g4, dim3(256), 0, st, a)
-        if (a.mode == SWEEP_GPTQ) {
-            if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true);
-            else ICQ_SWEEP4(SWEEP_GPTQ, false);
-        } else {
-            ICQ_SWEEP4(SWEEP_LDLQ, false);
-        }
+        // (LDLQ always sweeps one matrix: ic_ldlq_quantize passes groups = 1)
+        IC_REQUIRE(a.mode == SWEEP_GPTQ, "sweep: batched column groups are GPTQ only");
+        if (zp) ICQ_SWEEP4(SWEEP_GPTQ, true);
+        else ICQ_SWEEP4(SWEEP_GPTQ, false);
 #undef ICQ_SWEEP4
         IC_CHECK_LAUNCH();
         return IC_OK;
@@ -701,6 +699,8 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
         // whole blocks of one matrix: the row sweep (16 lanes per row), with
         // 4 to 16 waves per work-group sharing the staged Hinv block, as many
         // as one work-group per CU needs to cover the rows
+        // the kernel addresses the staged Hinv block with 32-bit offsets
+        IC_REQUIRE((SW_NB - 1) * a.ldh + SW_NB < (int64_t(1) << 31), "sweep: Hinv pitch too large");
         const int64_t need = cdiv(cdiv(a.rows, SR_ROWS), 256);
         const int WVs = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
         const dim3 g16((unsigned)cdiv(a.rows, WVs * SR_ROWS));
@@ -916,10 +916,14 @@ extern "C" int ic_gptq_quantize_noalloc(float* W, int64_t rows, int64_t gw, int6
     IC_REQUIRE(groups >= 1 && gw >= 0 && rows >= 0, "ic_gptq_quantize_noalloc: bad size");
     if (rows == 0 || gw == 0) return IC_OK;
     IC_REQUIRE(block >= 1 && block <= SW_NB, "ic_gptq_quantize_noalloc: block size must be in [1, 128]");
-    IC_REQUIRE(rows <= NOALLOC_SCRATCH_BYTES && groups <= NOALLOC_SCRATCH_BYTES &&
-                   groups * rows * super_cols(groups, block) * (int64_t)sizeof(float) <= NOALLOC_SCRATCH_BYTES,
-               "ic_gptq_quantize_noalloc: rows x groups x super-block columns need more than the 128 MiB "
-               "static scratch; use ic_gptq_quantize with a workspace");
+    {
+        // groups x rows x super-block columns floats must fit; bounded by
+        // division so that no product can overflow
+        const int64_t cap = NOALLOC_SCRATCH_BYTES / (int64_t)sizeof(float), sc = super_cols(groups, block);
+        IC_REQUIRE(sc >= 1 && rows <= cap / sc && groups <= cap / (rows * sc),
+                   "ic_gptq_quantize_noalloc: rows x groups x super-block columns need more than the 128 MiB "
+                   "static scratch; use ic_gptq_quantize with a workspace");
+    }
     void* ws = nullptr;
     int rc = scratch_address(&ws);
     if (rc) return rc;

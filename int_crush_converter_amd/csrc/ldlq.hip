@@ -128,15 +128,16 @@ __global__ __launch_bounds__(256) void ls_scales_kernel(const int8_t* Q, const f
     }
 }
 
-// err = Q * S - W  (S is per-row here: greedy uses least-squares row scales)
-__global__ void greedy_err_kernel(const int8_t* Q, const float* srow, const float* W, int64_t rows, int64_t cols,
-                                  float* err, float* Qf) {
+// err = Q * S - W with S per row (pe 0: sc[rows], the least-squares row
+// scales the pipeline passes) or per element (pe 1: sc[rows, cols])
+__global__ void greedy_err_kernel(const int8_t* Q, const float* sc, int pe, const float* W, int64_t rows,
+                                  int64_t cols, float* err, float* Qf) {
     const int64_t total = rows * cols;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         const float q = (float)Q[i];
         Qf[i] = q;
-        err[i] = q * srow[i / cols] - W[i];
+        err[i] = q * sc[pe ? i : i / cols] - W[i];
     }
 }
 
@@ -184,11 +185,18 @@ __device__ __forceinline__ float2 greedy_scan(float e, float q, float s, float h
     return make_float2(bq, e + (bq - q) * s);
 }
 
+// The guard scale of greedy_decide: GREEDY_GAMMA s, or NaN for a scale
+// outside the window's domain.
+__device__ __forceinline__ float greedy_guard(float s) {
+    const float s2 = s * s;
+    return (s > 0.0f && s2 >= 0x1p-40f && s2 <= 0x1p30f) ? GREEDY_GAMMA * s : __builtin_nanf("");
+}
+
 // The window decision for one column of one row: err e, code q, running
 // cross-term sum c (before the diagonal term), column data cv = {H_jj,
-// H_jj or NaN, 1 / H_jj}, row scale s, 1 / s and the guard scale sg
-// (GREEDY_GAMMA s, or NaN for a row outside the domain).  {code, new err};
-// fast: the window's answer is the full scan's.
+// H_jj or NaN, 1 / H_jj}, the scale s of this element, 1 / s and the guard
+// scale sg = greedy_guard(s).  {code, new err}; fast: the window's answer is
+// the full scan's.
 __device__ __forceinline__ float2 greedy_decide(float e, float q, float c, float4 cv, float s, float is, float sg,
                                                 float qmin, float qmax, bool& fast) {
     const float h = cv.x;
@@ -216,9 +224,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // next block's H tile and sums the next block's corrections from all but
 // the current block, then, once the current block's changes are in LDS,
 // adds those (one accumulation in block order).
-// FULL: every block whole and the pitch of H a multiple of 4.
-template <bool FULL>
-__global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, const float* srow, const float* H,
+// FULL: every block whole and the pitch of H a multiple of 4.  PE: per-element
+// scales sc[rows, cols] (each lane keeps its columns' scales with their err
+// and codes), else per-row scales sc[rows].
+template <bool FULL, bool PE>
+__global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, const float* sc, const float* H,
                                                         int64_t ldh, const float* hd, const float* Csb,
                                                         int64_t rows, int64_t cols, int64_t s0, int sw, float qmin,
                                                         float qmax) {
@@ -226,7 +236,7 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
     __shared__ __align__(16) float4 colv[2][GB];           // {H_jj, H_jj or NaN (guard), 1 / H_jj, 0}
     __shared__ __align__(16) float Dl[GSB][GQR];           // Dl[j - s0][row]: the block's change of err
     __shared__ __align__(16) float Xs[GQR][GQ][GSLOT];     // corrections of the next block, Xs[row][p][m]
-    __shared__ float Gs[GQR][3][GB];                       // guarded rerun: err, codes, cross terms
+    __shared__ float Gs[GQR][PE ? 4 : 3][GB];              // guarded rerun: err, codes, cross terms (, scales)
     const int w = threadIdx.x >> 6, t = threadIdx.x & 63;
     const int nblk = (sw + GB - 1) / GB;
     auto width = [&](int b) { return FULL ? GB : (int)min((int64_t)GB, (int64_t)sw - (int64_t)b * GB); };
@@ -287,10 +297,10 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
     const int p = t & (GQ - 1), rr = t / GQ;
     const int64_t r = (int64_t)blockIdx.x * GQR + rr;
     const bool live = w == 0 && r < rows;
-    const float s = live ? srow[r] : 1.0f;
-    const float is = 1.0f / s, s2 = s * s;
-    const float sg = (s > 0.0f && s2 >= 0x1p-40f && s2 <= 0x1p30f) ? GREEDY_GAMMA * s : __builtin_nanf("");
-    float er[GSLOT], e0[GSLOT], qr[GSLOT], cr[GSLOT];
+    const float s = (live && !PE) ? sc[r] : 1.0f;
+    const float is = 1.0f / s;
+    const float sg = greedy_guard(s);
+    float er[GSLOT], e0[GSLOT], qr[GSLOT], cr[GSLOT], sr[PE ? GSLOT : 1];
     auto load_raw = [&](int b) {   // block b's err, codes and super-block cross terms
         const int64_t j0 = s0 + (int64_t)b * GB;
         const int nb = width(b);
@@ -301,6 +311,7 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
             er[m] = ok ? err[r * cols + j0 + col] : 0.0f;
             qr[m] = ok ? Qf[r * cols + j0 + col] : 0.0f;
             cr[m] = ok ? Csb[r * GSB + (j0 - s0) + col] : 0.0f;
+            if constexpr (PE) sr[m] = ok ? sc[r * cols + j0 + col] : 1.0f;
         }
     };
     auto add_corr = [&](int b) {
@@ -342,7 +353,13 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
                 }
                 const float xe = er[m];
                 bool fast;
-                const float2 dec = greedy_decide(xe, qr[m], cr[m], cv, s, is, sg, qmin, qmax, fast);
+                float2 dec;
+                if constexpr (PE) {
+                    const float se = sr[m];
+                    dec = greedy_decide(xe, qr[m], cr[m], cv, se, 1.0f / se, greedy_guard(se), qmin, qmax, fast);
+                } else {
+                    dec = greedy_decide(xe, qr[m], cr[m], cv, s, is, sg, qmin, qmax, fast);
+                }
                 bad |= __builtin_amdgcn_ballot_w64(!fast);
                 __asm__ volatile("" : "+s"(bad));   // fold this column's test in now, not at the end
                 const float d = quad_bcast<o>(dec.y - xe);
@@ -377,15 +394,18 @@ __global__ __launch_bounds__(128) void greedy_sb_kernel(float* err, float* Qf, c
                     Gs[rr][0][GQ * m + p] = er[m];
                     Gs[rr][1][GQ * m + p] = qr[m];
                     Gs[rr][2][GQ * m + p] = cr[m];
+                    if constexpr (PE) Gs[rr][PE ? 3 : 0][GQ * m + p] = sr[m];
                 }
                 lds_wave_fence();
                 if (p == 0) {
                     for (int jl = 0; jl < nb; ++jl) {
                         const float4 cv = colv[buf][jl];
                         const float xe = Gs[rr][0][jl], xq = Gs[rr][1][jl];
+                        const float se = PE ? Gs[rr][PE ? 3 : 0][jl] : s;
+                        const float ise = PE ? 1.0f / se : is, sge = PE ? greedy_guard(se) : sg;
                         bool fast;
-                        float2 dec = greedy_decide(xe, xq, Gs[rr][2][jl], cv, s, is, sg, qmin, qmax, fast);
-                        if (!fast) dec = greedy_scan(xe, xq, s, cv.x, Gs[rr][2][jl] - xe * cv.x, qmin, qmax);
+                        float2 dec = greedy_decide(xe, xq, Gs[rr][2][jl], cv, se, ise, sge, qmin, qmax, fast);
+                        if (!fast) dec = greedy_scan(xe, xq, se, cv.x, Gs[rr][2][jl] - xe * cv.x, qmin, qmax);
                         Gs[rr][0][jl] = dec.y;
                         Gs[rr][1][jl] = dec.x;
                         const float d = dec.y - xe;
@@ -492,7 +512,8 @@ __global__ void split_sum_kernel(const float* __restrict__ P, int64_t rows, int6
 }
 
 // part: scratch for the split products (GSPLIT * rows * GSB floats), or null.
-static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc, const float* hd, float* C,
+// sc / pe: the scales, per row (pe 0) or per element (pe 1).
+static int greedy_pass(float* err, float* Qf, const float* sc, int pe, const float* Hc, const float* hd, float* C,
                        float* part, int64_t rows, int64_t cols, float qmin, float qmax, hipStream_t st) {
     for (int64_t s0 = 0; s0 < cols; s0 += GSB) {
         const int64_t sw = std::min<int64_t>(GSB, cols - s0);
@@ -515,12 +536,14 @@ static int greedy_pass(float* err, float* Qf, const float* srow, const float* Hc
         {
             ProfScope prof_scope(st, PT_GREEDY, (double)rows * sw * (GB + 2.0 * sw), (double)rows * sw * 20);
             const bool full = sw % GB == 0 && cols % 4 == 0;
-            if (full)
-                hipLaunchKernelGGL(greedy_sb_kernel<true>, dim3((unsigned)cdiv(rows, GQR)), dim3(128), 0, st, err, Qf,
-                                   srow, Hc, cols, hd, C, rows, cols, s0, (int)sw, qmin, qmax);
-            else
-                hipLaunchKernelGGL(greedy_sb_kernel<false>, dim3((unsigned)cdiv(rows, GQR)), dim3(128), 0, st, err, Qf,
-                                   srow, Hc, cols, hd, C, rows, cols, s0, (int)sw, qmin, qmax);
+#define ICQ_GSB(F, P) hipLaunchKernelGGL((greedy_sb_kernel<F, P>), dim3((unsigned)cdiv(rows, GQR)), dim3(128), 0, st, \
+                                         err, Qf, sc, Hc, cols, hd, C, rows, cols, s0, (int)sw, qmin, qmax)
+            if (full) {
+                if (pe) ICQ_GSB(true, true); else ICQ_GSB(true, false);
+            } else {
+                if (pe) ICQ_GSB(false, true); else ICQ_GSB(false, false);
+            }
+#undef ICQ_GSB
             IC_CHECK_LAUNCH();
         }
     }
@@ -584,21 +607,23 @@ extern "C" int64_t ic_greedy_workspace_bytes(int64_t rows, int64_t cols) {
     return (2 * rows * cols + rows * GSB + GSPLIT * rows * GSB) * (int64_t)sizeof(float) + 256;
 }
 
-extern "C" int ic_greedy(const float* W, int8_t* Q, const float* srow, const float* H, int64_t rows, int64_t cols,
-                         int passes, int bits, void* workspace, void* stream) {
-    IC_REQUIRE(W && Q && srow && H && workspace, "ic_greedy: null pointer");
+extern "C" int ic_greedy(const float* W, int8_t* Q, const float* scale, int scale_kind, const float* H, int64_t rows,
+                         int64_t cols, int passes, int bits, void* workspace, void* stream) {
+    IC_REQUIRE(W && Q && scale && H && workspace, "ic_greedy: null pointer");
     IC_REQUIRE(bits == 4 || bits == 8, "ic_greedy: bits must be 4 or 8");
+    IC_REQUIRE(scale_kind == 0 || scale_kind == 1, "ic_greedy: scale_kind must be 0 (per row) or 1 (per element)");
     if (rows == 0 || cols == 0 || passes <= 0) return IC_OK;
     hipStream_t st = as_stream(stream);
     const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
     float* err = reinterpret_cast<float*>(workspace);
     float* Qf = err + rows * cols;
     float* cross = Qf + rows * cols;
-    hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
+    hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, scale, scale_kind, W, rows,
+                       cols, err, Qf);
     IC_CHECK_LAUNCH();
     float* part = cross + rows * GSB;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, H, nullptr, cross, part, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, scale, scale_kind, H, nullptr, cross, part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
     }
     hipLaunchKernelGGL(to_int8_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Qf, rows * cols, qmin, qmax, Q);
@@ -611,11 +636,13 @@ extern "C" int64_t ic_greedy_lowrank_workspace_bytes(int64_t rows, int64_t cols,
             GSPLIT * rows * GSB) * (int64_t)sizeof(float) + PROXY_PARTS * (int64_t)sizeof(double) + 1024;
 }
 
-extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, const float* H, const float* U,
-                                 int64_t ldu, const float* s, int64_t k, int64_t rows, int64_t cols, int passes,
-                                 int bits, int* passes_run, void* workspace, void* stream) {
-    IC_REQUIRE(W && Q && srow && H && workspace && (k == 0 || (U && s)), "ic_greedy_lowrank: null pointer");
+extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* scale, int scale_kind, const float* H,
+                                 const float* U, int64_t ldu, const float* s, int64_t k, int64_t rows, int64_t cols,
+                                 int passes, int bits, int* passes_run, void* workspace, void* stream) {
+    IC_REQUIRE(W && Q && scale && H && workspace && (k == 0 || (U && s)), "ic_greedy_lowrank: null pointer");
     IC_REQUIRE(bits == 4 || bits == 8, "ic_greedy_lowrank: bits must be 4 or 8");
+    IC_REQUIRE(scale_kind == 0 || scale_kind == 1,
+               "ic_greedy_lowrank: scale_kind must be 0 (per row) or 1 (per element)");
     IC_REQUIRE(k >= 0 && k <= cols && ldu >= k, "ic_greedy_lowrank: bad rank");
     if (passes_run) *passes_run = 0;
     if (rows == 0 || cols == 0 || passes <= 0) return IC_OK;
@@ -644,12 +671,13 @@ extern "C" int ic_greedy_lowrank(const float* W, int8_t* Q, const float* srow, c
     }
     hipLaunchKernelGGL(diag_kernel, dim3(egrid(cols)), dim3(256), 0, st, H, cols, hd);
     IC_CHECK_LAUNCH();
-    hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, srow, W, rows, cols, err, Qf);
+    hipLaunchKernelGGL(greedy_err_kernel, dim3(egrid(rows * cols)), dim3(256), 0, st, Q, scale, scale_kind, W, rows,
+                       cols, err, Qf);
     IC_CHECK_LAUNCH();
     double prev = 0.0;
     int done = 0;
     for (int p = 0; p < passes; ++p) {
-        int rc = greedy_pass(err, Qf, srow, Hk, hd, cross, split_part, rows, cols, qmin, qmax, st);
+        int rc = greedy_pass(err, Qf, scale, scale_kind, Hk, hd, cross, split_part, rows, cols, qmin, qmax, st);
         if (rc) return rc;
         done = p + 1;
         if (p + 1 == passes) break;   // a stall test after the last pass changes nothing

@@ -89,9 +89,9 @@ def woodbury_inverse(D: torch.Tensor, U: torch.Tensor, damping: float = 0.0,
     ws = nat.workspace(nat.lib().ic_woodbury_workspace_bytes(n, r), dev)
 
     def call(minv):
-        nat.check(nat.lib().ic_woodbury_inverse(Dg.data_ptr(), Ug.data_ptr() if r else None, n, r, Ug.stride(0),
-                                                float(damping), nat.ptr(minv), int(upper_only), Hinv.data_ptr(), n,
-                                                M.data_ptr() if r else None, info.data_ptr(), ws.data_ptr(),
+        nat.check(nat.lib().ic_woodbury_inverse(Dg, Ug.data_ptr() if r else None, n, r, Ug.stride(0),
+                                                float(damping), nat.ptr(minv), int(upper_only), Hinv, n,
+                                                M.data_ptr() if r else None, info, ws,
                                                 nat.stream()), "ic_woodbury_inverse")
 
     call(None)
@@ -110,8 +110,8 @@ def dlr_to_dense(D: torch.Tensor, U: torch.Tensor) -> torch.Tensor:
     Dg, Ug = _factors(D, U)
     n, r = Ug.shape
     H = torch.empty(n, n, dtype=torch.float32, device=Dg.device)
-    nat.check(nat.lib().ic_dlr_to_dense(Dg.data_ptr(), Ug.data_ptr() if r else None, n, r, Ug.stride(0),
-                                        H.data_ptr(), n, nat.stream()), "ic_dlr_to_dense")
+    nat.check(nat.lib().ic_dlr_to_dense(Dg, Ug.data_ptr() if r else None, n, r, Ug.stride(0),
+                                        H, n, nat.stream()), "ic_dlr_to_dense")
     return H
 
 

@@ -33,14 +33,14 @@ def row_params(W: torch.Tensor, int_bits: int, asymmetric: bool):
     rmin = torch.empty(M, dtype=torch.float32, device=dev)
     rmax = torch.empty(M, dtype=torch.float32, device=dev)
     ramax = torch.empty(M, dtype=torch.float32, device=dev)
-    nat.check(L.ic_row_stats(W.data_ptr(), M, N, N, rmin.data_ptr(), rmax.data_ptr(), ramax.data_ptr(),
+    nat.check(L.ic_row_stats(W, M, N, N, rmin, rmax, ramax,
                              nat.stream()), "ic_row_stats")
     s32 = torch.empty(M, dtype=torch.float32, device=dev)
     s16 = torch.empty(M, dtype=torch.float16, device=dev)
     z32 = torch.empty(M, dtype=torch.float32, device=dev) if asym else None
     z8 = torch.empty(M, dtype=torch.int8, device=dev) if asym else None
-    nat.check(L.ic_gptq_row_params(rmin.data_ptr(), rmax.data_ptr(), ramax.data_ptr(), M, int_bits, int(asym),
-                                   s32.data_ptr(), nat.ptr(z32), s16.data_ptr(), nat.ptr(z8), nat.stream()),
+    nat.check(L.ic_gptq_row_params(rmin, rmax, ramax, M, int_bits, int(asym),
+                                   s32, nat.ptr(z32), s16, nat.ptr(z8), nat.stream()),
               "ic_gptq_row_params")
     return s32, z32, s16, z8
 
@@ -61,8 +61,8 @@ def launch_quant_error(W: torch.Tensor, Q: torch.Tensor, scale: torch.Tensor, zp
     ws = nat.workspace(nat.lib().ic_quant_error_workspace_bytes(), W.device)
     sc, kind = scale_operand(scale)
     zp = None if zp8 is None else zp8.reshape(-1).to(torch.int8).contiguous()
-    nat.check(nat.lib().ic_quant_error(W.data_ptr(), M, N, N, Q.data_ptr(), N, sc.data_ptr(), kind, nat.ptr(zp),
-                                       sumsq_ptr, max_ptr, ws.data_ptr(), nat.stream()),
+    nat.check(nat.lib().ic_quant_error(W, M, N, N, Q, N, sc, kind, nat.ptr(zp),
+                                       sumsq_ptr, max_ptr, ws, nat.stream()),
               "ic_quant_error")
 
 
@@ -88,9 +88,9 @@ def sweep(W_work: torch.Tensor, Hinv: torch.Tensor, s32: torch.Tensor, z32: torc
     R = torch.empty_like(W_work)
     blk = min(int(block_size), SWEEP_MAX_BLOCK)
     ws = nat.workspace(nat.lib().ic_gptq_workspace_bytes(M, groups, blk), W_work.device)
-    nat.check(nat.lib().ic_gptq_quantize_from(W_work.data_ptr(), R.data_ptr(), M, gw, groups, Hinv.data_ptr(),
-                                              s32.data_ptr(), nat.ptr(z32), int_bits, blk, Q.data_ptr(),
-                                              ws.data_ptr(), nat.stream()),
+    nat.check(nat.lib().ic_gptq_quantize_from(W_work, R, M, gw, groups, Hinv,
+                                              s32, nat.ptr(z32), int_bits, blk, Q,
+                                              ws, nat.stream()),
               "ic_gptq_quantize_from")
     return Q
 

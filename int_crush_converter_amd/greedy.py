@@ -14,9 +14,10 @@ minimising tr((Q s - W) H (Q s - W)^T).  Everything runs in libicq.so:
 * ``greedy_search``: the backend choice of ``converter/ldlq.py:602-647`` on
   a GPU - low-rank when the Hessian allows it, else full rank.
 
-The greedy scale is per row (the least-squares row scale broadcast over the
-row, ldlq.py:222-231); a per-element scale that is not constant along rows
-is not supported and raises.
+The scale is per element, as the reference's ``scale_2d[:, j]``
+(greedy.py:487-541): the pipeline passes the least-squares row scale
+broadcast over the row (ldlq.py:222-231), which the library takes as one
+value per row; any other [M, N] scale runs the per-element kernels.
 """
 
 from __future__ import annotations
@@ -47,14 +48,17 @@ def _bits(clamp_min: int, clamp_max: int) -> int:
     raise ValueError(f"unsupported grid [{clamp_min}, {clamp_max}]: INT4 (-8, 7) or INT8 (-128, 127)")
 
 
-def _row_scale(scale: torch.Tensor, M: int, N: int, dev) -> torch.Tensor:
-    """[M], [M, 1] or a row-constant [M, N] scale -> contiguous fp32 [M]."""
+def _scale_arg(scale: torch.Tensor, M: int, N: int) -> tuple[torch.Tensor, int]:
+    """(fp32 scales, kind) for the library: [M] per row (kind 0) from an [M],
+    [M, 1] or row-constant [M, N] scale, else [M, N] per element (kind 1)."""
     s = nat.to_gpu(scale).float()
-    if s.dim() == 2 and s.shape == (M, N):
-        if s.stride(1) != 0 and not torch.equal(s, s[:, :1].expand(M, N)):
-            raise NotImplementedError("greedy search: per-element scales must be constant along each row")
-        s = s[:, 0]
-    return s.reshape(M).contiguous()
+    if s.dim() == 2 and tuple(s.shape) == (M, N):
+        if s.stride(1) == 0 or torch.equal(s, s[:, :1].expand(M, N)):
+            return s[:, 0].contiguous(), 0
+        return s.contiguous(), 1
+    if s.numel() != M:
+        raise ValueError(f"greedy search: scale of shape {tuple(scale.shape)} for weights [{M}, {N}]")
+    return s.reshape(M).contiguous(), 0
 
 
 def _prep(W, Q, scale, H):
@@ -67,18 +71,18 @@ def _prep(W, Q, scale, H):
         raise ValueError(f"greedy search needs a 2-D Hessian [{N}, {N}], got {tuple(H.shape)}")
     Qg = nat.to_gpu(Q)
     Qg = (Qg.round().clamp(-128, 127) if Qg.is_floating_point() else Qg).to(torch.int8).contiguous()
-    return Wg, Qg, _row_scale(scale, M, N, Wg.device), Hg
+    s, kind = _scale_arg(scale, M, N)
+    return Wg, Qg, s, kind, Hg
 
 
 def greedy_local_search(W, Q, scale, H, num_passes: int, clamp_min: int, clamp_max: int) -> torch.Tensor:
     """Full-rank greedy search; returns the new int8 codes (Q is not modified)."""
     bits = _bits(clamp_min, clamp_max)
-    Wg, Qg, s, Hg = _prep(W, Q, scale, H)
+    Wg, Qg, s, kind, Hg = _prep(W, Q, scale, H)
     M, N = Wg.shape
     Qo = Qg.clone()
     ws = nat.workspace(_lib().ic_greedy_workspace_bytes(M, N), Wg.device)
-    nat.check(_lib().ic_greedy(Wg.data_ptr(), Qo.data_ptr(), s.data_ptr(), Hg.data_ptr(), M, N, int(num_passes),
-                               bits, ws.data_ptr(), nat.stream()), "ic_greedy")
+    nat.check(_lib().ic_greedy(Wg, Qo, s, kind, Hg, M, N, int(num_passes), bits, ws, nat.stream()), "ic_greedy")
     return Qo.to(W.device)
 
 
@@ -105,8 +109,8 @@ def lowrank_decompose(H, rank_threshold: float = 0.01, max_rank_frac: float = LO
     ws = nat.workspace(_lib().ic_lowrank_workspace_bytes(N, p), Hg.device)
     sweeps = nat._c.c_int(0)
     # p > k_cap: a certificate that p eigenvalues exceed the cut settles the refusal early
-    rc = _lib().ic_lowrank_eigs(Hg.data_ptr(), N, p, iters, LOWRANK_SEED, float(rank_threshold), evals.data_ptr(),
-                                evecs.data_ptr(), nat._c.byref(sweeps), ws.data_ptr(), nat.stream())
+    rc = _lib().ic_lowrank_eigs(Hg, N, p, iters, LOWRANK_SEED, float(rank_threshold), evals,
+                                evecs, nat._c.byref(sweeps), ws, nat.stream())
     if rc == 1:    # IC_LOWRANK_REFUSED: at least p > k_cap eigenvalues above the cut
         return None, None, p, False
     if rc == -3:   # orthonormalisation failed: no low-rank basis (the reference's eigh failure path)
@@ -130,17 +134,17 @@ def greedy_lowrank(W, Q, scale, H, num_passes: int, clamp_min: int, clamp_max: i
     """Low-rank greedy search; (codes, k, used_lowrank).  Falls back to the
     full-rank search when the Hessian's effective rank is too high."""
     bits = _bits(clamp_min, clamp_max)
-    Wg, Qg, s, Hg = _prep(W, Q, scale, H)
+    Wg, Qg, s, kind, Hg = _prep(W, Q, scale, H)
     M, N = Wg.shape
     s_k, U_k, k, used = lowrank_decompose(Hg, rank_threshold, max_rank_frac)
     if not used:
-        return greedy_local_search(Wg, Qg, s, Hg, num_passes, clamp_min, clamp_max).to(W.device), k, False
+        sc = s if kind == 1 else s.reshape(M, 1)
+        return greedy_local_search(Wg, Qg, sc, Hg, num_passes, clamp_min, clamp_max).to(W.device), k, False
     Qo = Qg.clone()
     ws = nat.workspace(_lib().ic_greedy_lowrank_workspace_bytes(M, N, k), Wg.device)
     done = nat._c.c_int(0)
-    nat.check(_lib().ic_greedy_lowrank(Wg.data_ptr(), Qo.data_ptr(), s.data_ptr(), Hg.data_ptr(), U_k.data_ptr(),
-                                       k, s_k.data_ptr(), k, M, N, int(num_passes), bits, nat._c.byref(done),
-                                       ws.data_ptr(), nat.stream()), "ic_greedy_lowrank")
+    nat.check(_lib().ic_greedy_lowrank(Wg, Qo, s, kind, Hg, U_k, k, s_k, k, M, N, int(num_passes), bits,
+                                       nat._c.byref(done), ws, nat.stream()), "ic_greedy_lowrank")
     if done.value < num_passes:
         logger.warning("Greedy[lowrank] stalled at pass %d", done.value + 1)
     return Qo.to(W.device), k, True

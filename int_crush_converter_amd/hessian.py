@@ -24,7 +24,7 @@ def _damped(H: torch.Tensor, damping: float) -> torch.Tensor:
     """H + damping * max(mean(diag H), 1e-6) * I as a new tensor (the
     library's damping kernel, the reference's CPU summation order)."""
     out = H.float().contiguous().clone()
-    nat.check(nat.lib().ic_damp_hessian(out.data_ptr(), 1, out.shape[0], float(damping), nat.stream()),
+    nat.check(nat.lib().ic_damp_hessian(out, 1, out.shape[0], float(damping), nat.stream()),
               "ic_damp_hessian")
     return out
 
@@ -71,8 +71,8 @@ def inverse_batch(H: torch.Tensor, damping: float, method: str = "hinv",
         code = 2
     info = torch.zeros(2 * batch, dtype=torch.int32, device=out.device)
     ws = nat.workspace(nat.lib().ic_hessian_inverse_workspace_bytes(batch, n), out.device)
-    nat.check(nat.lib().ic_hessian_inverse(out.data_ptr(), batch, n, float(damping), code, info.data_ptr(),
-                                           ws.data_ptr(), nat.stream()), "ic_hessian_inverse")
+    nat.check(nat.lib().ic_hessian_inverse(out, batch, n, float(damping), code, info,
+                                           ws, nat.stream()), "ic_hessian_inverse")
     del ws
     inf = info.tolist()
     orig = None

@@ -58,8 +58,8 @@ def rtn_codes(W_work: torch.Tensor, int_bits: int, asymmetric: bool, clipping_ra
     codes = torch.empty(M, N, dtype=torch.int8, device=W_work.device)
     packed = torch.empty(M, (N + 1) // 2, dtype=torch.uint8, device=W_work.device) if int_bits == 4 else None
     z = None if zp is None else zp.float()
-    nat.check(nat.lib().ic_rtn_quantize(W_work.data_ptr(), M, N, N, int_bits, s16.data_ptr(), 0, nat.ptr(z),
-                                        codes.data_ptr(), N, nat.ptr(packed), packed.shape[1] if packed is not None
+    nat.check(nat.lib().ic_rtn_quantize(W_work, M, N, N, int_bits, s16, 0, nat.ptr(z),
+                                        codes, N, nat.ptr(packed), packed.shape[1] if packed is not None
                                         else 0, nat.stream()), "ic_rtn_quantize")
     return codes, s16.reshape(M, 1), None if zp is None else zp.reshape(M, 1), packed
 
@@ -206,11 +206,11 @@ def finish(W_work, codes, s16, z8, int_bits, packed=None, **kw) -> LayerOutput:
     if W_work.numel():
         launch_quant_error(W_work, codes, s16, z8, base, base + 8)
     sc, kind = scale_operand(s16)
-    nat.check(nat.lib().ic_scale_status(sc.data_ptr(), kind, sc.numel(), base + 12, nat.stream()), "ic_scale_status")
+    nat.check(nat.lib().ic_scale_status(sc, kind, sc.numel(), base + 12, nat.stream()), "ic_scale_status")
     if int_bits == 4 and packed is None:
         packed = torch.empty(M, (N + 1) // 2, dtype=torch.uint8, device=dev)
         if codes.numel():
-            nat.check(nat.lib().ic_pack_int4(codes.data_ptr(), 0, M, N, N, packed.data_ptr(), packed.shape[1],
+            nat.check(nat.lib().ic_pack_int4(codes, 0, M, N, N, packed, packed.shape[1],
                                              base + 16, nat.stream()), "ic_pack_int4")
     host = status.cpu()
     words = host.view(torch.int32)

@@ -36,7 +36,7 @@ def _lib():
 def _row_absmax(W):
     M, N = W.shape
     ramax = torch.empty(M, dtype=torch.float32, device=W.device)
-    nat.check(_lib().ic_row_stats(W.data_ptr(), M, N, N, None, None, ramax.data_ptr(), nat.stream()), "ic_row_stats")
+    nat.check(_lib().ic_row_stats(W, M, N, N, None, None, ramax, nat.stream()), "ic_row_stats")
     return ramax
 
 
@@ -44,7 +44,7 @@ def _gemm_tn(W: torch.Tensor, alpha: float) -> torch.Tensor:
     """alpha * W^T W on the matrix cores (fp32; one triangle computed, mirrored)."""
     M, N = W.shape
     C = torch.empty(N, N, dtype=torch.float32, device=W.device)
-    nat.check(_lib().ic_gram_tn(W.data_ptr(), M, N, N, alpha, C.data_ptr(), nat.stream()), "ic_gram_tn")
+    nat.check(_lib().ic_gram_tn(W, M, N, N, alpha, C, nat.stream()), "ic_gram_tn")
     return C
 
 
@@ -53,7 +53,7 @@ def _damp_only(H: torch.Tensor, damping: float) -> torch.Tensor:
     library's damping kernel (ldlq.py:207-209: the damped weight-only H
     that the greedy search uses)."""
     out = H.float().contiguous().clone()
-    nat.check(_lib().ic_damp_hessian(out.data_ptr(), 1, out.shape[0], float(damping), nat.stream()),
+    nat.check(_lib().ic_damp_hessian(out, 1, out.shape[0], float(damping), nat.stream()),
               "ic_damp_hessian")
     return out
 
@@ -63,21 +63,21 @@ def _single_pass(W: torch.Tensor, Hinv: torch.Tensor, S: torch.Tensor, block: in
     S = S.contiguous()
     if not bool(torch.isfinite(S).all().item()):
         S = S.clone()
-        nat.check(_lib().ic_sanitize_scales(S.data_ptr(), S.numel(), nat.stream()), "ic_sanitize_scales")
+        nat.check(_lib().ic_sanitize_scales(S, S.numel(), nat.stream()), "ic_sanitize_scales")
     W_work = W.clone()
     Q = torch.empty(M, N, dtype=torch.int8, device=W.device)
     blk = min(int(block), SWEEP_MAX_BLOCK)
     ws = nat.workspace(_lib().ic_gptq_workspace_bytes(M, 1, blk), W.device)
-    nat.check(_lib().ic_ldlq_quantize(W_work.data_ptr(), M, N, Hinv.data_ptr(), S.data_ptr(), bits, blk,
-                                      Q.data_ptr(), ws.data_ptr(), nat.stream()), "ic_ldlq_quantize")
+    nat.check(_lib().ic_ldlq_quantize(W_work, M, N, Hinv, S, bits, blk,
+                                      Q, ws, nat.stream()), "ic_ldlq_quantize")
     return Q
 
 
 def _mse(W, Q, S) -> float:
     out = torch.zeros(1, dtype=torch.float64, device=W.device)
     ws = nat.workspace(1024 * 8, W.device)
-    nat.check(_lib().ic_ldlq_mse(W.data_ptr(), Q.data_ptr(), S.data_ptr(), W.numel(), out.data_ptr(),
-                                 ws.data_ptr(), nat.stream()), "ic_ldlq_mse")
+    nat.check(_lib().ic_ldlq_mse(W, Q, S, W.numel(), out,
+                                 ws, nat.stream()), "ic_ldlq_mse")
     return out.item() / max(W.numel(), 1)
 
 
@@ -85,8 +85,8 @@ def _update_scales(W, Q, cur, flat, smin: float, smax: float) -> torch.Tensor:
     lo = max(smin * 0.1, 1e-8)
     hi = smax * 10.0
     out = torch.empty_like(cur)
-    nat.check(_lib().ic_ldlq_update_scales(W.data_ptr(), Q.data_ptr(), cur.data_ptr(), flat.data_ptr(), W.numel(),
-                                           LDLQ_SCALE_MOMENTUM, lo, hi, out.data_ptr(), nat.stream()),
+    nat.check(_lib().ic_ldlq_update_scales(W, Q, cur, flat, W.numel(),
+                                           LDLQ_SCALE_MOMENTUM, lo, hi, out, nat.stream()),
               "ic_ldlq_update_scales")
     return out
 
@@ -95,7 +95,7 @@ def _iterative(W, Hinv, flat, iters, block, bits):
     """converter/ldlq.py:479-550."""
     cur = flat.clone()
     if not bool(torch.isfinite(cur).all().item()):
-        nat.check(_lib().ic_sanitize_scales(cur.data_ptr(), cur.numel(), nat.stream()), "ic_sanitize_scales")
+        nat.check(_lib().ic_sanitize_scales(cur, cur.numel(), nat.stream()), "ic_sanitize_scales")
     smin, smax = (v.item() for v in flat.aminmax())
     Qr = None
     prev = float("inf")
@@ -128,7 +128,7 @@ def _iterative(W, Hinv, flat, iters, block, bits):
 def _ls_scales(Q, W) -> torch.Tensor:
     M, N = W.shape
     out = torch.empty(M, dtype=torch.float32, device=W.device)
-    nat.check(_lib().ic_ls_scales(Q.data_ptr(), W.data_ptr(), M, N, out.data_ptr(), nat.stream()), "ic_ls_scales")
+    nat.check(_lib().ic_ls_scales(Q, W, M, N, out, nat.stream()), "ic_ls_scales")
     return out
 
 
@@ -218,7 +218,7 @@ def ldlq_quantize_layer(
     ramax = _row_absmax(Wg)
     srow = torch.empty(M, dtype=torch.float32, device=Wg.device)
     flat = torch.empty(M, N, dtype=torch.float32, device=Wg.device)
-    nat.check(_lib().ic_ldlq_init_scales(ramax.data_ptr(), M, N, int_bits, srow.data_ptr(), flat.data_ptr(),
+    nat.check(_lib().ic_ldlq_init_scales(ramax, M, N, int_bits, srow, flat,
                                          nat.stream()), "ic_ldlq_init_scales")
     if iterations > 1:
         Q, _ = _iterative(Wg, Hinv, flat, iterations, block_size, int_bits)

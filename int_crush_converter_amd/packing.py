@@ -29,8 +29,8 @@ def _as_rows(t: torch.Tensor):
 def _validate_rows(g: torch.Tensor, kind: int, dst: torch.Tensor | None) -> None:
     flags = torch.zeros(3, dtype=torch.int32, device=g.device)
     rows, cols = g.shape
-    nat.check(nat.lib().ic_pack_int4(g.data_ptr(), kind, rows, cols, cols, nat.ptr(dst),
-                                     dst.shape[1] if dst is not None else 0, flags.data_ptr(), nat.stream()),
+    nat.check(nat.lib().ic_pack_int4(g, kind, rows, cols, cols, nat.ptr(dst),
+                                     dst.shape[1] if dst is not None else 0, flags, nat.stream()),
               "ic_pack_int4")
     nf, lo, hi = flags.tolist()
     if nf:
@@ -67,6 +67,6 @@ def unpack_int4(packed: torch.Tensor, K: int) -> torch.Tensor:
         return torch.zeros(*lead, K, dtype=torch.int8, device=packed.device)
     g = nat.to_gpu(packed).contiguous().reshape(-1, packed.shape[-1])
     out = torch.empty(g.shape[0], K, dtype=torch.int8, device=g.device)
-    nat.check(nat.lib().ic_unpack_int4(g.data_ptr(), g.shape[0], K, g.shape[1], out.data_ptr(), K, nat.stream()),
+    nat.check(nat.lib().ic_unpack_int4(g, g.shape[0], K, g.shape[1], out, K, nat.stream()),
               "ic_unpack_int4")
     return out.reshape(*lead, K).to(packed.device)

@@ -62,7 +62,7 @@ def channel_second_moments(W: torch.Tensor) -> torch.Tensor:
     if M == 0:
         return mu2.fill_(float("nan"))
     ws = nat.workspace(_lib().ic_col_moments_workspace_bytes(M, N), Wg.device)
-    nat.check(_lib().ic_col_moments(Wg.data_ptr(), M, N, Wg.stride(0), _cpu_vec(), mu2.data_ptr(), ws.data_ptr(),
+    nat.check(_lib().ic_col_moments(Wg, M, N, Wg.stride(0), _cpu_vec(), mu2, ws,
                                     nat.stream()), "ic_col_moments")
     return mu2
 
@@ -75,7 +75,7 @@ def argsort_descending(v: torch.Tensor) -> torch.Tensor:
     if n == 0:
         return perm
     ws = nat.workspace(_lib().ic_argsort_workspace_bytes(n), vg.device)
-    nat.check(_lib().ic_argsort_desc(vg.data_ptr(), n, perm.data_ptr(), ws.data_ptr(), nat.stream()),
+    nat.check(_lib().ic_argsort_desc(vg, n, perm, ws, nat.stream()),
               "ic_argsort_desc")
     return perm
 
@@ -109,8 +109,8 @@ def _quant_error(Wg: torch.Tensor, perm: torch.Tensor | None, group_size: int, i
         pp = nat.to_gpu(perm).to(torch.int64).contiguous()
         if pp.numel() != N:
             raise ValueError(f"permutation of length {pp.numel()} for {N} columns")
-    nat.check(_lib().ic_group_quant_error(Wg.data_ptr(), M, N, Wg.stride(0), nat.ptr(pp), int(group_size), int_bits,
-                                          T, out.data_ptr(), ws.data_ptr(), nat.stream()), "ic_group_quant_error")
+    nat.check(_lib().ic_group_quant_error(Wg, M, N, Wg.stride(0), nat.ptr(pp), int(group_size), int_bits,
+                                          T, out, ws, nat.stream()), "ic_group_quant_error")
     return float(out.item())
 
 
@@ -191,7 +191,7 @@ def permute_columns(W: torch.Tensor, perm: torch.Tensor, out: torch.Tensor | Non
         out = torch.empty(M, n, dtype=torch.float32, device=Wg.device)
     if out.shape != (M, n) or out.dtype != torch.float32 or out.stride(1) != 1:
         raise ValueError("permute_columns: out must be fp32 [rows, len(perm)] with unit column stride")
-    nat.check(_lib().ic_permute_cols(Wg.data_ptr(), M, Wg.shape[1], Wg.stride(0), pp.data_ptr(), n, out.data_ptr(),
+    nat.check(_lib().ic_permute_cols(Wg, M, Wg.shape[1], Wg.stride(0), pp, n, out,
                                      out.stride(0), nat.stream()), "ic_permute_cols")
     return out
 
@@ -206,7 +206,7 @@ def permute_hessian(H: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
     pp = nat.to_gpu(perm).to(torch.int64).contiguous()
     n = pp.numel()
     out = torch.empty(n, n, dtype=torch.float32, device=Hg.device)
-    nat.check(_lib().ic_permute_sym(Hg.data_ptr(), Hg.shape[0], Hg.stride(0), pp.data_ptr(), n, out.data_ptr(), n,
+    nat.check(_lib().ic_permute_sym(Hg, Hg.shape[0], Hg.stride(0), pp, n, out, n,
                                     nat.stream()), "ic_permute_sym")
     return out
 

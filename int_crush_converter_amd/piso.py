@@ -51,8 +51,8 @@ def _search(W, hessian_diag, num_coarse, num_fine, bits, asym, coarse):
     scales = torch.empty(M, dtype=torch.float32, device=dev)
     zp = torch.empty(M, dtype=torch.int8, device=dev) if asym else None
     if M and N:
-        nat.check(nat.lib().ic_piso_scales(Wg.data_ptr(), M, N, Wg.stride(0), hg.data_ptr(), bits, int(asym),
-                                           cf.data_ptr(), num_coarse, ff.data_ptr(), num_fine, scales.data_ptr(),
+        nat.check(nat.lib().ic_piso_scales(Wg, M, N, Wg.stride(0), hg, bits, int(asym),
+                                           cf, num_coarse, ff, num_fine, scales,
                                            nat.ptr(zp), nat.stream()), "ic_piso_scales")
     elif M:
         raise ValueError("PiSO needs at least one input feature")
@@ -145,7 +145,7 @@ def rtn_piso_codes(W: torch.Tensor, scales: torch.Tensor, zero_points: torch.Ten
     codes = torch.empty(M, N, dtype=torch.int8, device=W.device)
     packed = torch.empty(M, (N + 1) // 2, dtype=torch.uint8, device=W.device) if int_bits == 4 else None
     z = None if z8 is None else z8.float().contiguous()
-    nat.check(nat.lib().ic_rtn_quantize(W.data_ptr(), M, N, W.stride(0), int_bits, s16.data_ptr(), 0, nat.ptr(z),
-                                        codes.data_ptr(), N, nat.ptr(packed), packed.shape[1] if packed is not None
+    nat.check(nat.lib().ic_rtn_quantize(W, M, N, W.stride(0), int_bits, s16, 0, nat.ptr(z),
+                                        codes, N, nat.ptr(packed), packed.shape[1] if packed is not None
                                         else 0, nat.stream()), "ic_rtn_quantize")
     return codes, s16.reshape(M, 1), z8, packed

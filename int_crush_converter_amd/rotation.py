@@ -118,7 +118,7 @@ def rotate_rows_gpu(W: torch.Tensor, rot_size: int, zero_above: float = 0.0,
     L = nat.lib()
     exact = _kernel == "exact" and rot_size <= 512
     fn, name = (L.ic_rotate_rows_exact, "ic_rotate_rows_exact") if exact else (L.ic_rotate_rows, "ic_rotate_rows")
-    nat.check(fn(W.data_ptr(), nat.dtype_code(W), rows, cols, cols, out.data_ptr(), cols_pad, cols_pad, rot_size,
+    nat.check(fn(W, nat.dtype_code(W), rows, cols, cols, out, cols_pad, cols_pad, rot_size,
                  float(zero_above), nat.ptr(n_zeroed), nat.stream()), name)
     return out
 
@@ -177,11 +177,11 @@ def rotate_hessian_gpu(H: torch.Tensor, rot_size: int, lower_only: bool = False,
     if out.numel():
         L = nat.lib()
         if _kernel == "exact" and rot_size <= 256:
-            nat.check(L.ic_rotate_hessian_exact(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size,
+            nat.check(L.ic_rotate_hessian_exact(src, out, batch, n, n, rot_size,
                                                 int(bool(lower_only) and batch == 1), nat.stream()),
                       "ic_rotate_hessian_exact")
         else:
-            nat.check(L.ic_rotate_hessian(src.data_ptr(), out.data_ptr(), batch, n, n, rot_size, nat.stream()),
+            nat.check(L.ic_rotate_hessian(src, out, batch, n, n, rot_size, nat.stream()),
                       "ic_rotate_hessian")
     return out
 

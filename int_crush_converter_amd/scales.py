@@ -45,8 +45,8 @@ def _scales_rows(Wr: torch.Tensor, bits: int, asym: bool, ratios):
         rp, nr = arr, len(ratios)
     else:
         rp, nr = None, 0
-    nat.check(nat.lib().ic_rtn_scales(Wr.data_ptr(), rows, cols, cols, bits, int(asym), rp, nr,
-                                      s16.data_ptr(), nat.ptr(zp), nat.stream()), "ic_rtn_scales")
+    nat.check(nat.lib().ic_rtn_scales(Wr, rows, cols, cols, bits, int(asym), rp, nr,
+                                      s16, nat.ptr(zp), nat.stream()), "ic_rtn_scales")
     return s16, zp
 
 
@@ -64,13 +64,13 @@ def _quant_rows(Wr: torch.Tensor, bits: int, scales: torch.Tensor, zps: torch.Te
         raise ValueError("scales / zero_points do not match the number of rows or groups")
     if packed:
         out = torch.empty(rows, (cols + 1) // 2, dtype=torch.uint8, device=Wr.device)
-        nat.check(nat.lib().ic_rtn_quantize(Wr.data_ptr(), rows, cols, cols, bits, sc.data_ptr(), kind,
-                                            nat.ptr(z), None, cols, out.data_ptr(), out.shape[1], nat.stream()),
+        nat.check(nat.lib().ic_rtn_quantize(Wr, rows, cols, cols, bits, sc, kind,
+                                            nat.ptr(z), None, cols, out, out.shape[1], nat.stream()),
                   "ic_rtn_quantize")
     else:
         out = torch.empty(rows, cols, dtype=torch.int8, device=Wr.device)
-        nat.check(nat.lib().ic_rtn_quantize(Wr.data_ptr(), rows, cols, cols, bits, sc.data_ptr(), kind,
-                                            nat.ptr(z), out.data_ptr(), cols, None, 0, nat.stream()),
+        nat.check(nat.lib().ic_rtn_quantize(Wr, rows, cols, cols, bits, sc, kind,
+                                            nat.ptr(z), out, cols, None, 0, nat.stream()),
                   "ic_rtn_quantize")
     return out
 

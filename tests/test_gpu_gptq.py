@@ -277,7 +277,8 @@ def test_sweep_exact_fallback_bit_exact(gpu_dev, case, rows):
     the block with the IEEE-exact test: rows of values near 1e-25 (residuals
     below 2^-60), an inverse Hessian scaled to pivots below 2^-30, and rows
     near 1e20 (residuals from 2^61 on).  Codes equal the CPU sweep's given
-    the same Hinv, for the 2-rows-per-wave and 8-rows-per-wave kernels."""
+    the same Hinv.  One matrix of whole blocks runs the row sweep
+    (sweep16_kernel, 4 and 16 waves per work-group at these row counts)."""
     from int_crush_converter_amd.gptq import row_params, sweep
     g = torch.Generator().manual_seed(rows + len(case))
     N = 128
@@ -297,6 +298,59 @@ def test_sweep_exact_fallback_bit_exact(gpu_dev, case, rows):
     s32, z32, _, _ = row_params(Wg, 4, False)
     Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, 128).cpu()
     assert torch.equal(Qg, Q)
+
+
+@pytest.mark.parametrize("case", ["tiny_rows", "tiny_pivots", "huge_rows"])
+def test_sweep_exact_fallback_batched_groups(gpu_dev, case):
+    """The quad sweep of block-diagonal groups (sweep4_kernel, 4 groups of
+    128 columns) redoes a row exactly, in the row's error output, when its
+    values leave the fast division's domain: codes equal the CPU sweep's per
+    group given the same Hinv."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(90 + len(case))
+    M, G, bs = 300, 4, 128
+    W = torch.randn(M, G * bs, generator=g) * 0.02
+    Hinv = torch.stack([ref.prepare_hinv(lognormal_hessian(bs, 3 * bs, 60 + k), 0.01) for k in range(G)])
+    if case == "tiny_rows":
+        W[3] = W[3] * 1e-23
+        W[150] = W[150] * 1e-30
+    elif case == "tiny_pivots":
+        Hinv[2] = Hinv[2] * 1e-12
+    else:
+        W[7] = W[7] * 1e22
+    s, z = ref.gptq_row_params(W, 4, False)
+    Q = torch.zeros(M, G * bs, dtype=torch.int8)
+    for k in range(G):
+        Qk = torch.zeros(M, bs, dtype=torch.int8)
+        ref.gptq_block(W[:, k * bs:(k + 1) * bs].clone(), Qk, s, Hinv[k], 0, bs, bs, -8, 7, z)
+        Q[:, k * bs:(k + 1) * bs] = Qk
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, 4, False)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev).contiguous(), s32, z32, 4, bs, G).cpu()
+    assert torch.equal(Qg, Q)
+
+
+@pytest.mark.parametrize("case", ["tiny_weights", "huge_weights"])
+@pytest.mark.parametrize("rows", [77, 12300])
+def test_ldlq_sweep_exact_fallback_bit_exact(gpu_dev, case, rows):
+    """The LDLQ row sweep's exact rerun: nonzero weights below 2^-60 (scale
+    at its 1e-5 floor) or from 2^61 on (scale above 2^31) leave the fast
+    division's domain; codes equal the CPU LDLQ pass given the same Hinv."""
+    from int_crush_converter_amd.ldlq import _single_pass
+    g = torch.Generator().manual_seed(rows + 7 * len(case))
+    N = 128
+    W = torch.randn(rows, N, generator=g) * 0.02
+    Hinv = ref.prepare_hinv(lognormal_hessian(N, 3 * N, 23), 0.01)
+    if case == "tiny_weights":
+        W[1] = W[1] * 1e-18
+        W[rows // 2, :5] = 1e-20
+    else:
+        W[2] = W[2] * 1e21
+    S = (W.abs().amax(dim=1, keepdim=True) / 7.0).clamp(min=1e-5).expand(rows, N)
+    S = S * (1 + 0.1 * torch.rand(rows, N, generator=g))
+    want = ref.ldlq_single_pass(W, Hinv, S.reshape(-1).clone(), N, -8, 7)
+    got = _single_pass(W.to(gpu_dev), Hinv.to(gpu_dev), S.contiguous().to(gpu_dev), N, 4).cpu()
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("bits,asym", [(4, False), (8, True)])

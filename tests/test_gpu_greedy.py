@@ -135,7 +135,7 @@ def test_greedy_lowrank_loop_given_reference_basis(gpu_dev, golden_greedy_gpu, c
     k = U.shape[1]
     ws = nat.workspace(lib.ic_greedy_lowrank_workspace_bytes(M, N, k), gpu_dev)
     done = nat._c.c_int(0)
-    nat.check(lib.ic_greedy_lowrank(W.data_ptr(), Q.data_ptr(), s.data_ptr(), H.data_ptr(), U.data_ptr(), k,
+    nat.check(lib.ic_greedy_lowrank(W.data_ptr(), Q.data_ptr(), s.data_ptr(), 0, H.data_ptr(), U.data_ptr(), k,
                                     sk.data_ptr(), k, M, N, m["passes"], m["bits"], nat._c.byref(done),
                                     ws.data_ptr(), nat.stream()), "ic_greedy_lowrank")
     assert (Q.cpu() == t[f"{case}.q"]).float().mean().item() >= 0.999
@@ -197,3 +197,23 @@ def test_ldlq_greedy_auto_vs_oracle_dispatch(gpu_dev, golden):
         agree = (r.quantized_W.cpu() == want).float().mean().item()
         print(f"[parity] ldlq_greedy_auto {case} agreement={agree:.6f}", flush=True)
         assert agree >= 0.999
+
+
+def test_greedy_lowrank_per_element_scales(gpu_dev):
+    """The low-rank search with a genuinely per-element scale_2d (the
+    reference's greedy.py:400-479 reads scale_2d[:, j] per column) against
+    the oracle's low-rank loop on a planted low-rank Hessian."""
+    from int_crush_converter_amd.greedy import greedy_lowrank
+    g = torch.Generator().manual_seed(31)
+    M, N = 96, 320
+    evs = torch.cat([torch.linspace(20.0, 1.0, 24), torch.full((N - 24,), 1e-4)])
+    H = _planted(N, evs, 13)
+    W = torch.randn(M, N, generator=g) * 0.02
+    S = (W.abs().amax(dim=1, keepdim=True) / 7).clamp(min=1e-5) * (0.75 + 0.5 * torch.rand(M, N, generator=g))
+    Q0 = ref.rhaz(W / S).clamp(-8, 7)
+    q, k, used = greedy_lowrank(W.to(gpu_dev), Q0.to(gpu_dev), S.to(gpu_dev), H.to(gpu_dev), 3, -8, 7)
+    oq, ok, oused = ref.greedy_gpu(W, Q0.clone(), S, H, 3, -8, 7)
+    assert used and oused and k == ok
+    agree = (q.cpu() == oq).float().mean().item()
+    print(f"[parity] greedy_lowrank_per_element agreement={agree:.6f}", flush=True)
+    assert agree >= 0.995

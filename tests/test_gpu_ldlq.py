@@ -133,6 +133,56 @@ def test_greedy_outside_window_domain(gpu_dev):
     assert agree >= 0.999 and agree_odd >= 0.99
 
 
+@pytest.mark.parametrize("M,N", [(64, 192), (48, 520)])
+def test_greedy_per_element_scales_vs_oracle(gpu_dev, M, N):
+    """A genuinely per-element scale_2d (the reference's greedy reads
+    scale_2d[:, j] per column, converter/greedy.py:487-541): the full-rank
+    search against the oracle's greedy_pytorch (>= 99.9 % equal codes, the
+    proxy within 1e-3), a partial last block included."""
+    from int_crush_converter_amd.greedy import greedy_local_search
+    g = torch.Generator().manual_seed(M + N)
+    W = torch.randn(M, N, generator=g) * 0.02
+    H = ref.damp(lognormal_hessian(N, 2 * N, 9), 0.01)
+    S = (W.abs().amax(dim=1, keepdim=True) / 7).clamp(min=1e-5) * (0.75 + 0.5 * torch.rand(M, N, generator=g))
+    Q0 = ref.rhaz(W / S).clamp(-8, 7)
+    want = ref.greedy_pytorch(W, Q0.clone(), S.clone(), H, 2, -8, 7)
+    got = greedy_local_search(W.to(gpu_dev), Q0.to(gpu_dev), S.to(gpu_dev), H.to(gpu_dev), 2, -8, 7).cpu()
+    agree = (got == want).float().mean().item()
+
+    def proxy(Q):
+        d = Q.double() * S.double() - W.double()
+        return (d @ H.double() * d).sum().item()
+
+    rel = proxy(got) / proxy(want) - 1
+    print(f"[parity] greedy_per_element {M}x{N} agreement={agree:.6f} proxy_rel={rel:.2e}", flush=True)
+    assert agree >= 0.999 and abs(rel) <= 1e-3
+
+
+def test_greedy_per_element_kernel_equals_row_kernel(gpu_dev):
+    """Row-constant scales through the per-element kernels (scale_kind 1)
+    give the per-row kernels' codes bit for bit, and an [M, N] row-constant
+    scale_2d takes the per-row path."""
+    from int_crush_converter_amd import _native as nat
+    from int_crush_converter_amd.greedy import greedy_local_search
+    g = torch.Generator().manual_seed(5)
+    M, N = 80, 384
+    W = (torch.randn(M, N, generator=g) * 0.02).to(gpu_dev)
+    H = ref.damp(lognormal_hessian(N, 2 * N, 3), 0.01).to(gpu_dev)
+    s = (W.abs().amax(dim=1) / 7).clamp(min=1e-5)
+    s[7] *= 1e-3                     # a row outside the window's domain (full-grid rerun)
+    Q0 = ref.rhaz(W.cpu() / s.cpu()[:, None]).clamp(-8, 7).to(torch.int8).to(gpu_dev)
+    lib = nat.lib()
+    outs = []
+    for kind, sc in ((0, s.contiguous()), (1, s[:, None].expand(M, N).contiguous())):
+        Q = Q0.clone()
+        ws = nat.workspace(lib.ic_greedy_workspace_bytes(M, N), gpu_dev)
+        nat.check(lib.ic_greedy(W, Q, sc, kind, H, M, N, 2, 4, ws, nat.stream()), "ic_greedy")
+        outs.append(Q.cpu())
+    assert torch.equal(outs[0], outs[1])
+    via_api = greedy_local_search(W, Q0, s[:, None].expand(M, N).contiguous(), H, 2, -8, 7).cpu()
+    assert torch.equal(via_api, outs[0])
+
+
 def test_ldlq_layer_vs_oracle_moderate(gpu_dev):
     from int_crush_converter_amd.ldlq import ldlq_quantize_layer
     g = torch.Generator().manual_seed(8)
