@@ -94,16 +94,28 @@ __device__ __forceinline__ void flush_zeroed(unsigned cnt, unsigned long long* n
 
 // ------------------------------------------------------------------ rows
 
-constexpr int XR_ROWS = 64;            // rows per work-group (4 row tiles of 16)
+constexpr int XR_ROWS = 64;            // rows per tile (4 row tiles of 16 per MFMA)
 constexpr int XR_SLICE = 256;          // output columns per work-group: 4 waves x 4 tiles x 16
 constexpr int XR_LD = XR_SLICE + 4;    // LDS pitch: lanes 4 banks apart, 16-byte reads conflict-free
 
-// One work-group: rows [r0, r0 + 64) x output columns [s0, s0 + 256).  For
-// R <= 256 the slice holds whole groups and its input is the same 256
-// columns; for R = 512 the group's 512 inputs are staged in two chunks of
-// 256 whose chains are added at the end.  TRI: only blocks (bi, bj) of
-// size R with bj <= bi of the (n_tri x n_tri) matrix are needed, and a
-// work-group whose every block lies above the diagonal returns at once.
+// Work-group y takes output columns [s0, s0 + 256) of every 64-row tile
+// blockIdx.x, blockIdx.x + gridDim.x, ...; a tile's input columns are staged
+// in LDS (for R <= 256 the slice holds whole groups and its input is the same
+// 256 columns; R = 512 stages the group's inputs in two chunks of 256 whose
+// chains are added at the end), and the next tile's global loads are in
+// flight while the current one runs on the matrix cores.
+//
+// Signs.  Tile c (0..3) of wave w covers in-group columns 16 (U + c) .. + 15
+// with U a multiple of 4 (R >= 64; for R = 32 its in-group block is c & 1,
+// for R = 16 it is 0).  For k = 16 kh + q the entry's sign is
+//     s(q, lane & 15)  ^  s(kh & 3, c)  ^  s(kh >> 2, U >> 2)
+// (both Hadamard kinds factor over these digit / bit groups).  The first is
+// the lane's B register, the second is known at compile time (kh and c are
+// unrolled) and picks the register holding the negated value, the third is
+// wave-uniform and flips the sign of A, which all four tiles share: no
+// per-MFMA sign arithmetic.  TRI (one matrix, rows == n_tri): only blocks
+// (bi, bj) of size R with bj <= bi are needed; the work-group walks the row
+// tiles from the first that reaches block row s0 / R.
 template <int R, int DT, bool TRI>
 __global__ __launch_bounds__(256, 2) void rot_rows_exact_kernel(const void* __restrict__ src, int64_t rows, int64_t cols,
                                                                int64_t ld_src, float* __restrict__ dst,
@@ -116,37 +128,47 @@ __global__ __launch_bounds__(256, 2) void rot_rows_exact_kernel(const void* __re
     __shared__ __align__(16) float xs[XR_ROWS * XR_LD];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t r0 = (int64_t)blockIdx.x * XR_ROWS;
     const int64_t s0 = (int64_t)blockIdx.y * XR_SLICE;
-    if (TRI && s0 / R > ((r0 % n_tri) + XR_ROWS - 1) / R) return;
+    const int64_t ntile = cdiv(rows, XR_ROWS);
     const int64_t kb = R > XR_SLICE ? (s0 / R) * R : s0;   // first input column of chunk 0
     // the first slice of a group counts its outliers (every input once)
     const bool count = zero_above > 0.0f && (R <= XR_SLICE || s0 % R == 0);
+    // TRI (one matrix, rows == n_tri): the row tiles that reach block row s0 / R
+    const int64_t rt0 = TRI ? std::max<int64_t>(0, ((s0 / R) * R - (XR_ROWS - 1) + XR_ROWS - 1) / XR_ROWS) : 0;
+    int64_t rt = rt0 + blockIdx.x;
+    if (rt >= ntile) return;
 
-    uint32_t blo[16];
+    float bp[16], bn[16];   // m (-1)^s(q, lane & 15) and its negation
 #pragma unroll
-    for (int q = 0; q < 16; ++q) blo[q] = mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31);
-    int acol[4], jhi[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int jt = 64 * w + 16 * c;                                  // tile's column in the slice
-        acol[c] = R <= XR_SLICE ? (jt / R) * R : 0;                       // its group's first LDS column
-        jhi[c] = (R <= XR_SLICE ? jt % R : (int)(s0 % R) + jt) >> 4;     // in-group column / 16
+    for (int q = 0; q < 16; ++q) {
+        bp[q] = __uint_as_float(mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31));
+        bn[q] = -bp[q];
     }
-    f32x16 acc[4], part[4];
-    unsigned cnt = 0;
+    // U >> 2 of the wave's tiles (uniform)
+    const uint32_t uhi = R >= 512 ? (uint32_t)((s0 % R) >> 6) + (uint32_t)w
+                         : R == 256 ? (uint32_t)w : R == 128 ? (uint32_t)(w & 1) : 0u;
+    int acol[4];   // the first LDS column of tile c's group
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        if (ch) __syncthreads();   // every wave is done with the previous chunk
-        const int64_t c0 = kb + (int64_t)ch * XR_SLICE;
-        float v[16][4];
+    for (int c = 0; c < 4; ++c) acol[c] = R <= XR_SLICE ? ((64 * w + 16 * c) / R) * R : 0;
+
+    float v[16][4];
+    auto gload = [&](int64_t t, int ch) {
+        const int64_t c0 = kb + (int64_t)ch * XR_SLICE, r0 = t * XR_ROWS;
 #pragma unroll
         for (int it = 0; it < 16; ++it) {
             const int u = it * 256 + tid, rr = u >> 6, cq = (u & 63) * 4;
             const int64_t r = r0 + rr, c = c0 + cq;
-            if (r < rows) load4<DT>(src, r * ld_src + c, c, cols, vec != 0, v[it]);
+            if (r < rows) load4<DT>(src, r * ld_src + c, c, cols, (vec & 1) != 0, v[it]);
             else v[it][0] = v[it][1] = v[it][2] = v[it][3] = 0.0f;
         }
+    };
+    gload(rt, 0);
+    f32x16 acc[4], part[4];
+    unsigned cnt = 0;
+    int ch = 0;
+    const float* xrow = &xs[lane * XR_LD];
+    for (;;) {
+        __syncthreads();   // every wave is done with the previous item's LDS
 #pragma unroll
         for (int it = 0; it < 16; ++it) {
             if (zero_above > 0.0f) {
@@ -161,65 +183,113 @@ __global__ __launch_bounds__(256, 2) void rot_rows_exact_kernel(const void* __re
             *reinterpret_cast<float4*>(&xs[rr * XR_LD + cq]) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
         }
         __syncthreads();
+        // the next item's loads fly while this one runs
+        int64_t nrt = rt;
+        int nch = ch + 1;
+        if (nch == NCH) {
+            nch = 0;
+            nrt = rt + gridDim.x;
+        }
+        const bool more = nrt < ntile;
+        if (more) gload(nrt, nch);
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
-        const float* xrow = &xs[lane * XR_LD];
-        for (int kh = 0; kh < KL / 16; ++kh) {
-            uint32_t shi[4];
+        // steps t = 4 kh + q4 of four k each; each step's A values are read
+        // from LDS one step ahead, so the read is in flight during the
+        // previous step's MFMAs
+        float4 a4n[4];
+        auto read_a = [&](int t, float4 (&a4)[4]) {
+            if constexpr (R >= 64) {
+                a4[0] = *reinterpret_cast<const float4*>(xrow + acol[0] + 4 * t);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) a4[c] = *reinterpret_cast<const float4*>(xrow + acol[c] + 4 * t);
+            }
+        };
+        read_a(0, a4n);
+        auto step = [&](auto TT) {
+            constexpr int t = decltype(TT)::value, kh = t / 4, q4 = t % 4;
+            float4 a4[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a4[c] = a4n[c];
+            if constexpr (t + 1 < KL / 4) read_a(t + 1, a4n);
+            __builtin_amdgcn_sched_barrier(0);   // keep the next read ahead of these MFMAs
+            if constexpr (R >= 64) {
+                if constexpr (R >= 128) {
+                    const uint32_t gs = hd_sign<REG>((uint32_t)(ch * (XR_SLICE / 16) + kh) >> 2, uhi) << 31;
+                    a4[0].x = __uint_as_float(__float_as_uint(a4[0].x) ^ gs);
+                    a4[0].y = __uint_as_float(__float_as_uint(a4[0].y) ^ gs);
+                    a4[0].z = __uint_as_float(__float_as_uint(a4[0].z) ^ gs);
+                    a4[0].w = __uint_as_float(__float_as_uint(a4[0].w) ^ gs);
+                }
+                a4[1] = a4[2] = a4[3] = a4[0];
+            }
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int q = 4 * q4 + qq;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int jc = R >= 64 ? c : R == 32 ? (c & 1) : 0;
+                    const bool neg = hd_sign<REG>((uint32_t)(kh & 3), (uint32_t)jc) != 0;
+                    const float a = qq == 0 ? a4[c].x : qq == 1 ? a4[c].y : qq == 2 ? a4[c].z : a4[c].w;
+                    acc[c] = mfma_k1(a, neg ? bn[q] : bp[q], acc[c]);
+                }
+            }
+        };
+        static_for<0, KL / 4>(step);
+        if constexpr (NCH > 1) {
+            if (ch == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) part[c] = acc[c];
+            }
+        }
+        if (ch == NCH - 1) {
+            // the output tile goes through LDS (its input is no longer
+            // needed) so that whole rows leave in 16-byte stores
+            __syncthreads();
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                shi[c] = hd_sign<REG>((uint32_t)(ch * (XR_SLICE / 16) + kh), (uint32_t)jhi[c]) << 31;
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                float4 a4[4];
-                if (R >= 64) {
-                    a4[0] = *reinterpret_cast<const float4*>(xrow + acol[0] + 16 * kh + 4 * q4);
-                    a4[1] = a4[2] = a4[3] = a4[0];
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        a4[c] = *reinterpret_cast<const float4*>(xrow + acol[c] + 16 * kh + 4 * q4);
+                for (int e = 0; e < 16; ++e) {
+                    float y = acc[c][e];
+                    if constexpr (NCH > 1) y = part[c][e] + y;
+                    xs[(16 * (e >> 2) + 4 * (lane >> 4) + (e & 3)) * XR_LD + 64 * w + 16 * c + (lane & 15)] = y;
                 }
+            __syncthreads();
+            const int64_t r0 = rt * XR_ROWS;
 #pragma unroll
-                for (int qq = 0; qq < 4; ++qq) {
-                    const int q = 4 * q4 + qq;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const float a = qq == 0 ? a4[c].x : qq == 1 ? a4[c].y : qq == 2 ? a4[c].z : a4[c].w;
-                        acc[c] = mfma_k1(a, __uint_as_float(blo[q] ^ shi[c]), acc[c]);
-                    }
+            for (int it = 0; it < 16; ++it) {
+                const int u = it * 256 + tid, rr = u >> 6, cq = (u & 63) * 4;
+                const int64_t r = r0 + rr, col = s0 + cq;   // cols_pad is a multiple of 16
+                if (r >= rows || col >= cols_pad) continue;
+                const float4 y = *reinterpret_cast<const float4*>(&xs[rr * XR_LD + cq]);
+                float* o = dst + r * ld_dst + col;
+                if (vec & 2) {
+                    *reinterpret_cast<float4*>(o) = y;
+                } else {
+                    o[0] = y.x; o[1] = y.y; o[2] = y.z; o[3] = y.w;
                 }
             }
         }
-        if (NCH > 1 && ch == 0) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) part[c] = acc[c];
-        }
+        if (!more) break;
+        rt = nrt;
+        ch = nch;
     }
     if (count) flush_zeroed(cnt, nz);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int64_t col = s0 + 64 * w + 16 * c + (lane & 15);
-        if (s0 + 64 * w + 16 * c >= cols_pad) continue;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t r = r0 + 16 * (v >> 2) + 4 * (lane >> 4) + (v & 3);
-            float y = acc[c][v];
-            if (NCH > 1) y = part[c][v] + y;
-            if (r < rows) dst[r * ld_dst + col] = y;
-        }
-    }
 }
 
 // ------------------------------------------------------------------ columns
 
 constexpr int XC_ROWS = 256;   // T rows per work-group: 4 waves x 4 tiles x 16
-constexpr int XC_COLS = 64;    // columns per work-group: 4 blocks of 16
+constexpr int XC_COLS = 64;    // columns per tile: 4 blocks of 16
 
-// One work-group: T rows [r0, r0 + 256) x columns [l0, l0 + 64) of matrix
-// blockIdx.z; R <= 256, so the rows hold whole groups.  In place is safe:
-// a work-group reads exactly the region it writes, all of it before its
-// first store.
+// Work-group (x, y, z): T rows [r0, r0 + 256) (r0 = 256 y) of matrix z, for
+// the 64-column tiles x, x + gridDim.x, ...; R <= 256, so the rows hold whole
+// groups.  The next tile's loads are in flight while the current one runs.
+// In place is safe: a tile's region is read whole before it is written, and
+// no other work-group touches it.  Signs as in the row kernel, with the roles
+// of A (the Hadamard entries, per lane p) and B (the data, shared by the
+// four tiles: the uniform part of the sign flips it).
 template <int R, bool TRI>
 __global__ __launch_bounds__(256, 2) void rot_cols_exact_kernel(const float* __restrict__ src, float* __restrict__ dst,
                                                                int64_t n, int64_t ld, int64_t bstride,
@@ -228,65 +298,113 @@ __global__ __launch_bounds__(256, 2) void rot_cols_exact_kernel(const float* __r
     __shared__ __align__(16) float hs[XC_ROWS * XC_COLS];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t l0 = (int64_t)blockIdx.x * XC_COLS;
     const int64_t r0 = (int64_t)blockIdx.y * XC_ROWS;
-    if (TRI && l0 / R > (r0 + XC_ROWS - 1) / R) return;
+    const int64_t ntile = cdiv(n, XC_COLS);
     const float* S = src + (int64_t)blockIdx.z * bstride;
     float* D = dst + (int64_t)blockIdx.z * bstride;
-    {
-        float v[16][4];
+    // TRI: the column tiles that start at or before the last block column
+    // of these rows' block rows
+    const int64_t ncap = TRI ? std::min<int64_t>(ntile, cdiv(((r0 + XC_ROWS - 1) / R + 1) * R, XC_COLS)) : ntile;
+    int64_t lt = blockIdx.x;
+    if (lt >= ncap) return;
+
+    float ap[16], an[16];   // m (-1)^s(q, lane & 15) and its negation
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        ap[q] = __uint_as_float(mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31));
+        an[q] = -ap[q];
+    }
+    const uint32_t uhi = R == 256 ? (uint32_t)w : 0u;   // U >> 2 of the wave's tiles
+    int brow[4];   // the first LDS row of tile c's group
+#pragma unroll
+    for (int c = 0; c < 4; ++c) brow[c] = ((64 * w + 16 * c) / R) * R;
+
+    float v[16][4];
+    auto gload = [&](int64_t t) {
+        const int64_t l0 = t * XC_COLS;
 #pragma unroll
         for (int it = 0; it < 16; ++it) {
             const int u = it * 256 + tid, rr = u >> 4, cq = (u & 15) * 4;
             const int64_t r = r0 + rr, c = l0 + cq;
-            if (r < n) load4<IC_DTYPE_F32>(S, r * ld + c, c, n, vec != 0, v[it]);
+            if (r < n) load4<IC_DTYPE_F32>(S, r * ld + c, c, n, (vec & 1) != 0, v[it]);
             else v[it][0] = v[it][1] = v[it][2] = v[it][3] = 0.0f;
         }
+    };
+    gload(lt);
+    f32x16 acc[4];
+    for (;;) {
+        __syncthreads();   // every wave is done with the previous tile's LDS
 #pragma unroll
         for (int it = 0; it < 16; ++it) {
             const int u = it * 256 + tid, rr = u >> 4, cq = (u & 15) * 4;
             *reinterpret_cast<float4*>(&hs[rr * XC_COLS + cq]) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
         }
-    }
-    __syncthreads();
-    uint32_t alo[16];
+        __syncthreads();
+        const int64_t nlt = lt + gridDim.x;
+        const bool more = nlt < ncap;
+        if (more) gload(nlt);
 #pragma unroll
-    for (int q = 0; q < 16; ++q) alo[q] = mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31);
-    int brow[4], phi[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int pt = 64 * w + 16 * c;   // tile's first row in the work-group
-        brow[c] = (pt / R) * R;           // its group's first row (LDS)
-        phi[c] = (pt % R) >> 4;           // in-group row / 16
-    }
-    f32x16 acc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
-    for (int kh = 0; kh < R / 16; ++kh) {
-        uint32_t shi[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) shi[c] = hd_sign<REG>((uint32_t)kh, (uint32_t)phi[c]) << 31;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            float b[4];
-            if (R >= 64) {
-                b[0] = b[1] = b[2] = b[3] = hs[(brow[0] + 16 * kh + q) * XC_COLS + lane];
+        for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
+        // steps t = 16 kh + q of one k each; B is read from LDS one step ahead
+        float bnx[4];
+        auto read_b = [&](int t, float (&b)[4]) {
+            if constexpr (R >= 64) {
+                b[0] = hs[(brow[0] + t) * XC_COLS + lane];
             } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) b[c] = hs[(brow[c] + 16 * kh + q) * XC_COLS + lane];
+                for (int c = 0; c < 4; ++c) b[c] = hs[(brow[c] + t) * XC_COLS + lane];
+            }
+        };
+        read_b(0, bnx);
+        auto step = [&](auto TT) {
+            constexpr int t = decltype(TT)::value, kh = t / 16, q = t % 16;
+            float b[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) b[c] = bnx[c];
+            if constexpr (t + 1 < R) read_b(t + 1, bnx);
+            __builtin_amdgcn_sched_barrier(0);   // keep the next read ahead of these MFMAs
+            if constexpr (R >= 64) {
+                if constexpr (R == 256) {
+                    const uint32_t gs = hd_sign<REG>((uint32_t)kh >> 2, uhi) << 31;
+                    b[0] = __uint_as_float(__float_as_uint(b[0]) ^ gs);
+                }
+                b[1] = b[2] = b[3] = b[0];
             }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] = mfma_k1(__uint_as_float(alo[q] ^ shi[c]), b[c], acc[c]);
-        }
-    }
+            for (int c = 0; c < 4; ++c) {
+                const int pc = R >= 64 ? c : 0;
+                const bool neg = hd_sign<REG>((uint32_t)(kh & 3), (uint32_t)pc) != 0;
+                acc[c] = mfma_k1(neg ? an[q] : ap[q], b[c], acc[c]);
+            }
+        };
+        static_for<0, R>(step);
+        // the output tile through LDS: rows of 64 columns in 16-byte stores
+        __syncthreads();
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t r = r0 + 64 * w + 16 * c + 4 * (lane >> 4) + (v & 3);
-            const int64_t col = l0 + 16 * (v >> 2) + (lane & 15);
-            if (r < n && col < n) D[r * ld + col] = acc[c][v];
+            for (int e = 0; e < 16; ++e)
+                hs[(64 * w + 16 * c + 4 * (lane >> 4) + (e & 3)) * XC_COLS + 16 * (e >> 2) + (lane & 15)] = acc[c][e];
+        __syncthreads();
+        const int64_t l0 = lt * XC_COLS;
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int u = it * 256 + tid, rr = u >> 4, cq = (u & 15) * 4;
+            const int64_t r = r0 + rr, col = l0 + cq;
+            if (r >= n || col >= n) continue;
+            const float4 y = *reinterpret_cast<const float4*>(&hs[rr * XC_COLS + cq]);
+            float* o = D + r * ld + col;
+            if ((vec & 2) && col + 3 < n) {
+                *reinterpret_cast<float4*>(o) = y;
+            } else {
+                o[0] = y.x;
+                if (col + 1 < n) o[1] = y.y;
+                if (col + 2 < n) o[2] = y.z;
+                if (col + 3 < n) o[3] = y.w;
+            }
         }
+        if (!more) break;
+        lt = nlt;
     }
 }
 
@@ -360,6 +478,9 @@ static float hd_mag(int rot) {
     return (float)(1.0 / std::sqrt((double)rot));
 }
 
+// work-groups a launch aims at (four per CU: two resident, two queued)
+constexpr int64_t XR_WGS = 1024;
+
 static int small_grid(int64_t work) {
     return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 256 * 32));
 }
@@ -386,11 +507,16 @@ static int rows_exact(const void* src, int dt, int64_t rows, int64_t cols, int64
         return IC_OK;
     }
     const size_t esz = dt == IC_DTYPE_F32 ? 4 : 2;
-    const int vec = ((uintptr_t)src % (4 * esz) == 0) && ((ld_src * esz) % (4 * esz) == 0);
+    // bit 0: 16-byte (8-byte for 16-bit types) source loads; bit 1: 16-byte stores
+    const int vec = (((uintptr_t)src % (4 * esz) == 0) && ((ld_src * esz) % (4 * esz) == 0) ? 1 : 0) |
+                    (((uintptr_t)dst % 16 == 0) && (ld_dst % 4 == 0) ? 2 : 0);
     const bool tri = n_tri > 0;
     IC_REQUIRE(!tri || n_tri % XR_ROWS == 0, "rotate_exact: the triangle needs n % 64 == 0");
     IC_REQUIRE(cdiv(rows, XR_ROWS) < (1LL << 31) && cdiv(cols_pad, XR_SLICE) <= 65535, "rotate_exact: too large");
-    dim3 grid((unsigned)cdiv(rows, XR_ROWS), (unsigned)cdiv(cols_pad, XR_SLICE));
+    // a few tiles per work-group, so that each one's loads overlap the previous one's MFMAs
+    const int64_t ntile = cdiv(rows, XR_ROWS), slices = cdiv(cols_pad, XR_SLICE);
+    const int64_t per = tri ? 4 : std::max<int64_t>(1, std::min<int64_t>(8, ntile * slices / XR_WGS));
+    dim3 grid((unsigned)cdiv(ntile, per), (unsigned)slices);
     ProfScope prof_scope(st, tag, 2.0 * rot * rows * cols_pad * (tri ? 0.5 : 1.0),
                          4.0 * rows * cols_pad * (tri ? 0.5 : 1.0) + (double)esz * rows * cols * (tri ? 0.5 : 1.0));
     uint32_t mb;
@@ -462,10 +588,13 @@ extern "C" int ic_rotate_hessian_exact(const float* src, float* H, int64_t batch
         IC_CHECK_LAUNCH();
     } else {
         IC_REQUIRE(cdiv(n, XC_COLS) < (1LL << 31) && cdiv(n, XC_ROWS) <= 65535, "ic_rotate_hessian_exact: too large");
-        const int vec = ((uintptr_t)src % 16 == 0) && (ld % 4 == 0);
+        const int vec = (((uintptr_t)src % 16 == 0) && (ld % 4 == 0) ? 1 : 0) |
+                        (((uintptr_t)H % 16 == 0) && (ld % 4 == 0) ? 2 : 0);
         uint32_t mb;
         std::memcpy(&mb, &mag, 4);
-        dim3 grid((unsigned)cdiv(n, XC_COLS), (unsigned)cdiv(n, XC_ROWS), (unsigned)batch);
+        const int64_t ntile = cdiv(n, XC_COLS), nrow = cdiv(n, XC_ROWS);
+        const int64_t per = tri ? 4 : std::max<int64_t>(1, std::min<int64_t>(8, ntile * nrow * batch / XR_WGS));
+        dim3 grid((unsigned)cdiv(ntile, per), (unsigned)nrow, (unsigned)batch);
         ProfScope prof_scope(st, PT_ROTATE_H, 2.0 * rot * batch * n * n * (tri ? 0.5 : 1.0),
                              8.0 * batch * n * n * (tri ? 0.5 : 1.0));
 #define ICQ_XC(RR) do { if (tri) hipLaunchKernelGGL((rot_cols_exact_kernel<RR, true>), grid, dim3(256), 0, st, src, H, \
