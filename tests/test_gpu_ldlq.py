@@ -320,3 +320,52 @@ def test_ldlq_c4_shaped_vs_reference_noise(gpu_dev, n):
     # has another least-squares scale; equal codes give equal scales
     # (test_ls_scales_bit_exact)
     assert ulps <= max(1, 2 * ulps_self)
+
+
+def test_ldlq_c4_full_size_vs_reference_noise(gpu_dev):
+    """configs[3] at its real size, M = N = 4096 (one of its 8 layers):
+    the same recipe and bars as the test above, with the oracle's noise
+    taken from the one alternative that changes both summation orders
+    (a two-half W^T W and half the CPU threads), to bound the CPU time.
+    The scale bar is stated against that noise; north-star's literal bar is
+    1 fp16 ulp, and the measured maximum is printed beside it."""
+    from int_crush_converter_amd.ldlq import ldlq_quantize_layer
+    n = 4096
+    g = torch.Generator().manual_seed(n + 3)
+    W = ref.rotate_weights(_student_t(n, n, g), 256)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        want = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5, greedy_device="gpu")
+        h = n // 2
+        gram = (W[:h].T @ W[:h] + W[h:].T @ W[h:]) / n
+        threads = torch.get_num_threads()
+        torch.set_num_threads(max(1, threads // 2))
+        try:
+            alt = ref.ldlq_quantize_layer(W, None, 128, 0.01, 4, iterations=2, greedy_passes=5,
+                                          greedy_device="gpu", weight_only_gram=gram)
+        finally:
+            torch.set_num_threads(threads)
+        got = ldlq_quantize_layer(W.to(gpu_dev), None, 128, 0.01, 4, iterations=2, greedy_passes=5)
+    Hg = (W.T.double() @ W.double()).to(gpu_dev) / n
+    Wg = W.double().to(gpu_dev)
+
+    def proxy(Q, s):
+        d = Q.to(gpu_dev).double() * s.to(gpu_dev).double() - Wg
+        return ((d @ Hg) * d).sum().item()
+
+    q = got.quantized_W.cpu()
+    p_ref = proxy(want.quantized_W, want.scales.float())
+    rel = proxy(q, got.scales.cpu().float()) / p_ref - 1
+    rel_self = abs(proxy(alt.quantized_W, alt.scales.float()) / p_ref - 1)
+    agree = (q == want.quantized_W).float().mean().item()
+    self_agree = (alt.quantized_W == want.quantized_W).float().mean().item()
+    ulps = _fp16_ulps(got.scales.cpu(), want.scales)
+    ulps_self = _fp16_ulps(alt.scales, want.scales)
+    rows_ulp = int((got.scales.cpu() != want.scales).sum())
+    rows_1ulp = int(((got.scales.cpu().view(torch.int16).int() - want.scales.view(torch.int16).int()).abs() <= 1).sum())
+    print(f"[parity] ldlq_c4 n={n} agreement={agree:.6f} self_both={self_agree:.6f} proxy_rel={rel:.3g} "
+          f"self_proxy_rel={rel_self:.3g} scale_max_ulps={ulps} self_scale_max_ulps={ulps_self} "
+          f"scale_rows_differing={rows_ulp} rows_within_1ulp={rows_1ulp} of {n}", flush=True)
+    assert agree >= self_agree - 5e-4, (agree, self_agree)
+    assert abs(rel) <= max(1e-3, 2 * rel_self), (rel, rel_self)
+    assert ulps <= max(1, 2 * ulps_self)
