@@ -373,24 +373,36 @@ def measured_traffic(workload, kernel):
 
 
 def roofline_from(prof, workload):
-    """Dominant kernel (most summed time over the timed steps) -> roofline.
-    achieved = algorithmic work per launch / average launch duration."""
-    from int_crush_converter_amd._native import PROFILE_KERNELS
-    kernels = {}
-    for kname, phases in PROFILE_KERNELS.items():
+    """The roofline of the dominant MFMA- or HBM-bound kernel (most summed
+    time over the timed steps): achieved = algorithmic work per launch /
+    average launch duration.  Kernels bound by a dependency chain or by
+    instruction issue (the column sweep, the greedy block kernel, the
+    diagonal-block factorisation) have no roofline; they are reported as
+    shares of the profiled time instead (`latency_shares`)."""
+    from int_crush_converter_amd._native import FWHT_KERNELS, PROFILE_KERNELS
+    from int_crush_converter_amd.rotation import rotation_kernel
+    kernels, total = {}, sum(v["ms"] for v in prof.values())
+    for kname, (phases, bound) in PROFILE_KERNELS.items():
+        if rotation_kernel() == "fwht" and kname in FWHT_KERNELS:
+            kname, bound = FWHT_KERNELS[kname]
         kernels[kname] = {k: sum(prof[p][k] for p in phases) for k in ("ms", "flops", "bytes", "launches")}
-    name, ph = max(kernels.items(), key=lambda kv: kv[1]["ms"])
-    mfma = {"gemm_f32_kernel"}
+        kernels[kname]["bound"] = bound
+    shares = {k: round(v["ms"] / total, 4) for k, v in kernels.items()
+              if v["bound"] == "latency" and v["ms"] > 0 and total > 0}
+    bounded = {k: v for k, v in kernels.items() if v["bound"] != "latency"}
+    name, ph = max(bounded.items(), key=lambda kv: kv[1]["ms"])
     n = max(ph["launches"], 1)
     avg_ms = ph["ms"] / n
-    if name in mfma:
+    if ph["bound"] == "mfma":
         achieved = (ph["flops"] / n) / (avg_ms * 1e-3) / 1e12 if avg_ms > 0 else 0.0
         bound, peak, unit = "mfma", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
     else:
         achieved = (ph["bytes"] / n) / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
         bound, peak, unit = "hbm", PEAK_HBM_GBS, "GB/s"
     return name, {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                  "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, name)}
+                  "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, name),
+                  "share_of_profiled_time": round(ph["ms"] / total, 4) if total > 0 else None,
+                  "latency_shares": shares}
 
 
 def hbm_ceiling(nbytes=1 << 30, reps=10):

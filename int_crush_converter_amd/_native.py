@@ -95,20 +95,27 @@ PROFILE_TAGS = ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "diag_factor",
                 "rotate_h", "rtn_quant_pack", "greedy", "other", "gemm_greedy", "chol_panel", "rtn_scales",
                 "verify", "permute", "permute_sum", "dlr", "dlr_gemm", "piso"]
 
-# kernel -> the profiler phases its launches are tagged with
+# kernel family -> (the profiler phases its launches are tagged with, the
+# bound it is graded against: "mfma", "hbm", or "latency" for kernels whose
+# time is a dependency chain / instruction issue, reported as a share of the
+# step).  The rotation phases are MFMA-bound with the exact kernels (the
+# default) and HBM-bound with the fast Walsh-Hadamard transform.
 PROFILE_KERNELS = {
-    "gemm_f32_kernel": ["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy", "dlr", "dlr_gemm"],
-    "potrf_diag_kernel": ["diag_factor"],
-    "panel64_kernel": ["chol_panel"],
-    "sweep_kernel": ["sweep"],
-    "greedy_block_kernel": ["greedy"],
-    "rotate_rows_reg": ["rotate_w"],
-    "rtn_scales_kernel": ["rtn_scales"],
-    "rtn_quant_kernel": ["rtn_quant_pack"],
-    "quant_error_partial": ["verify"],
-    "fsum_group_kernel": ["permute_sum"],   # (fsum_block_kernel: its fallback for cascade groups above 32)
-    "piso_kernel": ["piso"],
+    "gemm_f32_kernel": (["gemm_trailing", "gemm_cholesky", "gemm_inverse", "gemm_greedy", "dlr", "dlr_gemm"], "mfma"),
+    "potrf_diag_kernel": (["diag_factor"], "latency"),
+    "panel64_kernel": (["chol_panel"], "latency"),
+    "sweep16_kernel / sweep4_kernel": (["sweep"], "latency"),
+    "greedy_sb_kernel": (["greedy"], "latency"),
+    "rot_rows_exact_kernel": (["rotate_w"], "mfma"),
+    "rot_cols_exact_kernel + rot_rows_exact_kernel": (["rotate_h"], "mfma"),
+    "rtn_scales_kernel": (["rtn_scales"], "latency"),
+    "rtn_quant_kernel": (["rtn_quant_pack"], "hbm"),
+    "quant_error_partial": (["verify"], "hbm"),
+    "fsum_group_kernel": (["permute_sum"], "hbm"),   # (fsum_block_kernel: its fallback for cascade groups above 32)
+    "piso_kernel": (["piso"], "latency"),
 }
+FWHT_KERNELS = {"rot_rows_exact_kernel": ("rotate256_coal / rotate_rows_reg", "hbm"),
+                "rot_cols_exact_kernel + rot_rows_exact_kernel": ("rotate_cols256_kernel + rotate256_coal", "hbm")}
 
 
 def profile_enable(on: bool) -> None:
