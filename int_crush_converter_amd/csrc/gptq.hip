@@ -772,8 +772,9 @@ __global__ void gptq_params_kernel(const float* rmin, const float* rmax, const f
 // groups * rows * min(B,128) floats.
 // Two-level lazy update.  Columns are taken in super-blocks of up to
 // SUPER columns (one group when groups > 1).  Inside a super-block, the
-// errors of each block update only the rest of the super-block (rank-nb);
-// the columns after it receive one update with all of its errors at once,
+// errors of the blocks reach the later blocks of the super-block in a
+// Fenwick order (layer_sweep); the columns after it receive one update
+// with all of its errors at once,
 // W[:, end:] -= E_sb @ Hinv[sb, end:], a GEMM with K = SUPER.  Same flops
 // as one update per block, with the trailing matrix read and written once
 // per super-block instead of once per block.
@@ -809,15 +810,26 @@ static int layer_sweep(const float* Win, float* W, int64_t ldw, int64_t rows, in
     };
     for (int64_t sb0 = 0; sb0 < gw; sb0 += SB) {
         const int64_t sbe = std::min<int64_t>(gw, sb0 + SB);
-        for (int64_t b0 = sb0; b0 < sbe; b0 += B) {
+        for (int64_t b0 = sb0, j = 0; b0 < sbe; b0 += B, ++j) {
             const int nb = (int)std::min<int64_t>(B, sbe - b0);
             // the sweep reads W (never writes it); the first block is read from Win
             SweepArgs a{b0 == 0 ? const_cast<float*>(Win) : W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh,
                         hg, s, lds, zp, qmin, qmax, Q, ldq, E + (b0 - sb0), SB, rows * SB, mode};
             int rc = launch_sweep(a, (int)groups, st);
             if (rc) return rc;
-            if (b0 + nb < sbe) {
-                rc = update(b0 - sb0, b0, nb, b0 + nb, sbe - b0 - nb, b0 == 0);
+            // Fenwick order inside the super-block: after block j, the errors
+            // of blocks j - lb + 1 .. j (lb = lowest set bit of j + 1) go to
+            // blocks j + 1 .. j + lb.  Every block m receives the errors of
+            // blocks 0 .. m - 1 once each, in increasing order (the ranges of
+            // the binary digits of m), so its weights see the reference's
+            // per-block updates in the reference's order, while the columns
+            // rewritten per super-block fall from (n - 1) n / 2 blocks to
+            // about n log2(n) / 2.  Blocks before the last one are whole.
+            const int64_t lb = (j + 1) & -(j + 1);
+            const int64_t c0 = b0 + nb, c1 = std::min<int64_t>(sbe, b0 + nb + (lb - 1) * B + B);
+            if (c0 < c1) {
+                const int64_t e0 = (j + 1 - lb) * B;
+                rc = update(e0, sb0 + e0, (j + 1) * B - e0, c0, c1 - c0, sb0 == 0 && e0 == 0);
                 if (rc) return rc;
             }
         }
