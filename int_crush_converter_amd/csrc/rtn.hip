@@ -302,6 +302,233 @@ __global__ __launch_bounds__(256) void rtn_clip_kernel(const float* __restrict__
     }
 }
 
+// The same clip search with the row in registers, for rows whose 32
+// inner-sum sequences (values 32 m + q, m < n4 = cols / 32) are whole groups
+// of 16 of torch's cascade (n4 a multiple of 16 up to 128: 512 .. 4127
+// columns with such an n4).  Such a cascade never reaches its third
+// accumulator: each group of 16 is summed from zero and added to a1, and
+// the sequence's sum is ((0 + a1) + 0) + 0 = a1.  One wave per row: lanes q
+// and q + 32 hold the first and second half of sequence q's groups, and
+// each lane runs every candidate over its values in one pass (each value is
+// fetched once for all candidates).  Group sums stay separate until lane q's
+// chain a1 reaches lane q + 32, which continues it over its own groups in
+// order.  The lanes' sums meet in LDS, where lane k < K finishes candidate
+// k's inner sum (inner_sum_finish: the row's leftover values come from
+// global memory) and lane 0 keeps the first strict minimum.  While a wave
+// searches one row, the loads of its next row are in flight: each group's
+// registers are refilled as soon as the group is summed.  Rows whose
+// values or scales leave the fast division's domain take the IEEE division.
+constexpr int CLIP_REG_MAX_K = 8;
+
+// Orders one wave's LDS writes before its later LDS reads by other lanes
+// (a wave's LDS operations complete in issue order; this keeps the compiler
+// from moving them and waits for the writes).  The clip search's LDS slots
+// belong to one wave each, so no work-group barrier is needed.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+constexpr int CLIP_VPL = 64;   // values per lane: up to 4 groups of 16
+
+// Group sums of one lane's values for every candidate (fast division);
+// after group g is summed, refill(g) may overwrite its 16 registers (the
+// next row's loads).
+template <int K, bool ASYM, typename Refill>
+__device__ __forceinline__ void clip_group_sums(float (&v)[CLIP_VPL], int cnt, const Cand (&c)[K],
+                                                const float (&rs)[K], float qmin, float qmax,
+                                                float (&gs)[K][CLIP_VPL / 16], Refill refill) {
+#pragma unroll
+    for (int g = 0; g < CLIP_VPL / 16; ++g) {
+        if (g < cnt) {
+            float a0[K];
+#pragma unroll
+            for (int k = 0; k < K; ++k) a0[k] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+#pragma unroll
+                for (int k = 0; k < K; ++k)
+                    a0[k] = a0[k] + cand_sq<true, ASYM>(v[16 * g + j], c[k], rs[k], qmin, qmax);
+                // one value at a time: the K chains are enough to fill the
+                // VALU, and the registers stay few
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int k = 0; k < K; ++k) gs[k][g] = a0[k];
+            refill(g);
+        }
+    }
+}
+
+template <int K, bool ASYM>
+__global__ __launch_bounds__(256, 2) void rtn_clip_reg_kernel(const float* __restrict__ W, int64_t rows, int64_t cols,
+                                                           int64_t ld, int bits, Ratios rt, int64_t iters,
+                                                           uint16_t* __restrict__ scale16, int8_t* __restrict__ zp) {
+    __shared__ float part[4][K][SUM_SEQ];
+    __shared__ float mses[4][K];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, q = lane & 31, h = lane >> 5;
+    const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
+    const int ng = (int)(cols / SUM_SEQ / 16);               // groups per sequence
+    const int hA = (ng + 1) / 2;                              // groups of the first half
+    const int g0 = h * hA, cnt = h ? ng - hA : hA;            // this lane's groups
+    const int64_t rest0 = (int64_t)ng * 16 * SUM_SEQ;         // values past the sequences (< 32)
+    const int64_t nwv = (int64_t)gridDim.x * 4;
+    int64_t r = (int64_t)blockIdx.x * 4 + wv;                 // every wave runs `iters` rounds
+    float cur[CLIP_VPL];
+    // group g of this lane's values of a row
+    auto load_group = [&](int g, int64_t row) {
+        const float* x = W + row * ld + q + (int64_t)(16 * (g0 + g)) * SUM_SEQ;
+#pragma unroll
+        for (int gg = 0; gg < CLIP_VPL / 16; ++gg)
+            if (gg == g) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) cur[16 * gg + j] = x[j * SUM_SEQ];
+            }
+    };
+    if (r < rows) {
+#pragma unroll
+        for (int g = 0; g < CLIP_VPL / 16; ++g)
+            if (g < cnt) load_group(g, r);
+    }
+    for (int64_t it = 0; it < iters; ++it, r += nwv) {
+        const bool live = r < rows;   // wave-uniform
+        const bool more = r + nwv < rows;
+        float mn = INFINITY, mx = -INFINITY, am = 0.0f;
+        bool bad = false, tiny = false;
+        if (live) {
+#pragma unroll
+            for (int g = 0; g < CLIP_VPL / 16; ++g)
+                if (g < cnt) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float u = cur[16 * g + j];
+                        mn = fminf(mn, u); mx = fmaxf(mx, u); am = fmaxf(am, fabsf(u));
+                        bad = bad || u != u;
+                        tiny = tiny || (fabsf(u) < 0x1p-60f && u != 0.0f);
+                    }
+                }
+            if (h == 0 && rest0 + q < cols) {
+                const float u = W[r * ld + rest0 + q];
+                mn = fminf(mn, u); mx = fmaxf(mx, u); am = fmaxf(am, fabsf(u));
+                bad = bad || u != u;
+                tiny = tiny || (fabsf(u) < 0x1p-60f && u != 0.0f);
+            }
+        }
+        // the row's stats: minimum, maximum and largest magnitude, NaN if any
+        // value is NaN (torch's amin / amax); every value in the fast
+        // division's numerator domain iff no NaN, no magnitude in (0, 2^-60)
+        // and the largest one below 2^61
+        mn = wave_nmin(mn);
+        mx = wave_nmax(mx);
+        am = wave_nmax(am);
+        const bool nan_row = __builtin_amdgcn_ballot_w64(bad) != 0;
+        const bool tiny_row = __builtin_amdgcn_ballot_w64(tiny) != 0;
+        if (nan_row) mn = mx = am = __builtin_nanf("");
+        const RowStats st{mn, mx, am};
+        Cand c[K];
+        float rs[K];
+        bool fast = !nan_row && !tiny_row && am < 0x1p61f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            c[k] = rtn_candidate(st, bits, ASYM, true, rt.v[k]);
+            rs[k] = 1.0f / c[k].s;
+            fast = fast && div_b_ok(c[k].s);
+        }
+        float gs[K][CLIP_VPL / 16];
+        // each group's registers take the next row's values once summed
+        auto refill = [&](int g) {
+            if (more) load_group(g, r + nwv);
+        };
+        if (live && fast) {
+            clip_group_sums<K, ASYM>(cur, cnt, c, rs, qmin, qmax, gs, refill);
+        } else if (live) {
+            // IEEE division (rare): the values again from memory, one at a time
+            const float* x = W + r * ld + q + (int64_t)(16 * g0) * SUM_SEQ;
+#pragma unroll
+            for (int g = 0; g < CLIP_VPL / 16; ++g)
+                if (g < cnt) {
+#pragma unroll
+                    for (int k = 0; k < K; ++k) {
+                        float a0 = 0.0f;
+#pragma unroll 1
+                        for (int j = 0; j < 16; ++j)
+                            a0 = a0 + cand_sq<false, ASYM>(x[(16 * g + j) * SUM_SEQ], c[k], rs[k], qmin, qmax);
+                        gs[k][g] = a0;
+                    }
+                    refill(g);
+                }
+        }
+        // sequence q's chain: lane q over the first groups, then lane q + 32
+        // from lane q's value over the rest
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float a1 = 0.0f;
+#pragma unroll
+            for (int g = 0; g < CLIP_VPL / 16; ++g)
+                if (g < cnt) a1 = a1 + gs[k][g];
+            const float from_first = __shfl_xor(a1, 32, 64);
+            if (h) {
+                a1 = from_first;
+#pragma unroll
+                for (int g = 0; g < CLIP_VPL / 16; ++g)
+                    if (g < cnt) a1 = a1 + gs[k][g];
+                part[wv][k][q] = a1;
+            }
+        }
+        wave_lds_sync();
+        if (live && lane < K) {
+            Cand cq = c[0];
+            float rq = rs[0];
+#pragma unroll
+            for (int k = 1; k < K; ++k)
+                if (lane == k) { cq = c[k]; rq = rs[k]; }
+            const float* xr = W + r * ld;
+            auto sq = [&](int64_t i) { return cand_sq<false, ASYM>(xr[i], cq, rq, qmin, qmax); };
+            mses[wv][lane] = inner_sum_finish(part[wv][lane], sq, cols) / (float)cols;
+        }
+        wave_lds_sync();
+        if (live && lane == 0) {
+            int best = 0;
+            float bm = mses[wv][0];
+#pragma unroll
+            for (int k = 1; k < K; ++k)
+                if (mses[wv][k] < bm) { bm = mses[wv][k]; best = k; }
+            Cand cb = c[0];
+#pragma unroll
+            for (int k = 1; k < K; ++k)
+                if (best == k) cb = c[k];
+            scale16[r] = f32_to_f16_bits(cb.s);
+            if (ASYM && zp) zp[r] = (int8_t)(int)cb.z;
+        }
+        wave_lds_sync();   // part / mses are reused by the next round
+    }
+}
+
+template <int K, bool ASYM>
+static void launch_clip_reg(const float* W, int64_t rows, int64_t cols, int64_t ld, int bits, const Ratios& rt,
+                            uint16_t* scale16, int8_t* zp, hipStream_t st) {
+    // two rows per wave where the rows allow (the second row's loads overlap
+    // the first row's search); four waves per work-group
+    const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(cdiv(rows, 8), 65535));
+    const int64_t iters = cdiv(rows, wgs * 4);
+    hipLaunchKernelGGL((rtn_clip_reg_kernel<K, ASYM>), dim3((unsigned)wgs), dim3(256), 0, st, W, rows, cols, ld, bits,
+                       rt, iters, scale16, zp);
+}
+
+template <int K>
+static void launch_clip_reg_k(int n_ratios, bool asym, const float* W, int64_t rows, int64_t cols, int64_t ld,
+                              int bits, const Ratios& rt, uint16_t* scale16, int8_t* zp, hipStream_t st) {
+    if constexpr (K <= CLIP_REG_MAX_K) {
+        if (n_ratios == K) {
+            if (asym) launch_clip_reg<K, true>(W, rows, cols, ld, bits, rt, scale16, zp, st);
+            else launch_clip_reg<K, false>(W, rows, cols, ld, bits, rt, scale16, zp, st);
+        } else {
+            launch_clip_reg_k<K + 1>(n_ratios, asym, W, rows, cols, ld, bits, rt, scale16, zp, st);
+        }
+    }
+}
+
 __device__ __forceinline__ uint8_t nib(float q) { return (uint8_t)(((int)q) & 0xF); }
 
 // One wave per row, 4 consecutive columns per lane and step: 16-byte W
@@ -614,7 +841,10 @@ extern "C" int ic_rtn_scales(const float* W, int64_t rows, int64_t cols, int64_t
     Ratios rt;
     for (int i = 0; i < MAX_RATIOS; ++i) rt.v[i] = i < n_ratios ? ratios[i] : 1.0f;
     ProfScope prof_scope(as_stream(stream), PT_RTN_SCALES, 0.0, (double)rows * cols * 4.0 + rows * 3.0);
-    if (n_ratios > 0 && cols <= CLIP_LDS_COLS) {
+    if (n_ratios >= 1 && n_ratios <= CLIP_REG_MAX_K && cols >= 16 * SUM_SEQ && cols / SUM_SEQ <= 128 &&
+        (cols / SUM_SEQ) % 16 == 0)
+        launch_clip_reg_k<1>(n_ratios, asym != 0, W, rows, cols, ld, bits, rt, scale16, zp, as_stream(stream));
+    else if (n_ratios > 0 && cols <= CLIP_LDS_COLS) {
         const int threads = (int)std::min<int64_t>(256, cdiv((int64_t)n_ratios * SUM_SEQ, 64) * 64);
         if (asym)
             hipLaunchKernelGGL(rtn_clip_kernel<true>, dim3((unsigned)std::min<int64_t>(rows, 65536)), dim3(threads),

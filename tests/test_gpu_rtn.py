@@ -312,6 +312,42 @@ def test_clip_search_bit_exact_widths(gpu_dev, rows, cols, bits, asym):
         assert torch.equal(z_got.cpu(), z_want)
 
 
+@pytest.mark.parametrize("cols", [512, 1031, 2079, 4096, 4127])
+@pytest.mark.parametrize("nr", [1, 3, 5, 8])
+@pytest.mark.parametrize("bits,asym", [(8, True), (4, False), (4, True), (8, False)])
+def test_clip_search_register_rows(gpu_dev, cols, nr, bits, asym):
+    """Rows whose 32 inner-sum sequences are whole groups of 16 (512 ..
+    4127 columns) take the register-resident clip search with every
+    candidate in one pass: 1 to 8 ratios, leftover columns past the
+    sequences, a row count that leaves work-group slots empty, a zero row,
+    rows far from zero, and rows outside the fast division's domain (huge
+    and tiny magnitudes) - scales and zero-points equal the oracle's."""
+    from int_crush_converter_amd import scales as S
+    ratios = [1.0 - 0.05 * i for i in range(nr)][::-1] if nr > 1 else [0.9]
+    W = _w(37, cols, cols + nr + bits, outliers=3)
+    W[2] = 0.0
+    W[3] = W[3] + 3.0
+    W[4] = W[4] - 5.0
+    W[5, 7] = 3.0e19          # beyond 2^61: the IEEE division for the whole row
+    W[6] = W[6] * 1e-18       # values below 2^-60
+    Wg = W.to(gpu_dev)
+    if bits == 4 and not asym:
+        s_want, z_want = ref.scales_int4_sym(W, cols, ratios), None
+        s_got, z_got = S.calculate_scales(Wg, cols, clipping_ratios=ratios), None
+    elif bits == 4:
+        s_want, z_want = ref.scales_int4_asym(W, cols, ratios)
+        s_got, z_got = S.calculate_scales_asymmetric(Wg, cols, clipping_ratios=ratios)
+    elif not asym:
+        s_want, z_want = ref.scales_int8_sym(W, ratios), None
+        s_got, z_got = S.calculate_scales_int8(Wg, clipping_ratios=ratios), None
+    else:
+        s_want, z_want = ref.scales_int8_asym(W, ratios)
+        s_got, z_got = S.calculate_scales_int8_asymmetric(Wg, clipping_ratios=ratios)
+    assert torch.equal(s_got.cpu(), s_want)
+    if z_want is not None:
+        assert torch.equal(z_got.cpu(), z_want)
+
+
 def test_rtn_group_wise(gpu_dev):
     from int_crush_converter_amd import scales as S
     W = _w(16, 200, 9, std=1.0)
