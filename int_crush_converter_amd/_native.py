@@ -16,7 +16,9 @@ import threading
 import torch
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG, "libicq.so")
+# IC_LIBICQ_PATH names another build of the same library (the host-sanitizer
+# build of build.py --asan-check); by default the in-tree libicq.so
+LIB_PATH = os.environ.get("IC_LIBICQ_PATH") or os.path.join(_PKG, "libicq.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG), "include", "ic_abi.h")
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2

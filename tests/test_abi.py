@@ -138,3 +138,34 @@ def test_host_tensor_refused_before_the_call(libicq):
     assert rc == -1 and b"null" in L.ic_last_error()
     rc = L.ic_greedy(1, 1, 1, 2, 1, 4, 4, 1, 4, 1, None)
     assert rc == -1 and b"scale_kind" in L.ic_last_error()
+
+
+def test_every_entry_point_checks_its_arguments_without_gpu(libicq):
+    """Each entry point called with NULL for every pointer and small sizes
+    answers on the host: a status entry point returns -1 with a message
+    (before any GPU work), a size query returns a count.  Run under the
+    host-sanitizer build (asan_check.py) this walks every argument check."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("NULL-argument calls are for a host without a GPU")
+    nat.load(require_gpu=False)
+    raw = ctypes.CDLL(nat.LIB_PATH)
+    values = {"ptr": None, "i32": 1, "i64": 16, "f32": 0.5, "f64": 0.5, "u64": 1}
+    ctype = {"ptr": ctypes.c_void_p, "i32": ctypes.c_int, "i64": ctypes.c_int64, "f32": ctypes.c_float,
+             "f64": ctypes.c_double, "u64": ctypes.c_ulonglong}
+    raw.ic_last_error.restype = ctypes.c_char_p
+    checked = 0
+    for name, (ret, args) in _header_sigs().items():
+        if name in ("ic_abi_version", "ic_last_error") or not args:
+            continue
+        fn = getattr(raw, name)
+        fn.argtypes = [ctype[a] for a in args]
+        fn.restype = ctype[ret] if ret != "void" else None
+        rc = fn(*[values[a] for a in args])
+        if ret == "i32" and "ptr" in args:
+            assert rc == -1, (name, rc)
+            assert raw.ic_last_error(), name
+            checked += 1
+        elif ret == "i64":
+            assert rc >= 0, (name, rc)
+    assert checked >= 20
