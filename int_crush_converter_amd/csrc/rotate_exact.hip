@@ -278,6 +278,189 @@ __global__ __launch_bounds__(256, 2) void rot_rows_exact_kernel(const void* __re
     if (count) flush_zeroed(cnt, nz);
 }
 
+// Rows out of place, one wave per output slice (R = 64, 128, 256; rows whose
+// width is a whole number of groups, aligned for vector loads): work items
+// are (256-column slice, 64-row tile) pairs, one round of work-groups takes
+// them in turn, and wave w owns the item's output columns 64 w .. + 63, all
+// inside one group.  Each lane reads its own row's four values of a step
+// straight from memory (the four waves of a work-group share the rows
+// through the caches), several steps ahead in registers - the next item's
+// first steps while this one's last run; the products leave straight from
+// the accumulators.  No LDS and no barrier: the waves of a SIMD drift apart,
+// so one wave's loads and stores overlap another's matrix-core work.  In
+// place (the Hessian's right product) takes the row kernel above, whose
+// tile is read whole before it is written.  Signs, chains and results are
+// the row kernel's (the same MFMA sequence per output).
+constexpr int XW_PF = 8;   // steps (4 k each) of A in flight
+
+// Four consecutive source elements of a row as they are stored (one 16-byte
+// load for f32, one 8-byte load for 16-bit types), and their fp32 values;
+// the conversion happens where the values are used, so a load never waits.
+template <int DT>
+struct Raw4 {
+    static constexpr bool F32 = DT == IC_DTYPE_F32;
+    uint32_t u[F32 ? 4 : 2];
+    __device__ __forceinline__ void load(const void* src, int64_t off) {
+        if constexpr (F32) {
+            const uint4 t = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(src) + off);
+            u[0] = t.x; u[1] = t.y; u[2] = t.z; u[3] = t.w;
+        } else {
+            const uint2 t = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(src) + off);
+            u[0] = t.x; u[1] = t.y;
+        }
+    }
+    __device__ __forceinline__ float get(int i) const {
+        if constexpr (F32) return __uint_as_float(u[i]);
+        const uint32_t h = i & 1 ? u[i >> 1] >> 16 : u[i >> 1] & 0xffffu;
+        if constexpr (DT == IC_DTYPE_BF16) return __uint_as_float(h << 16);
+        return f16_bits_to_f32((uint16_t)h);
+    }
+};
+
+template <int R, int DT, bool ZA>
+__global__ __launch_bounds__(256, 2) void rot_rows_wave_kernel(const void* __restrict__ src, int64_t rows,
+                                                              int64_t cols, int64_t ld_src, float* __restrict__ dst,
+                                                              int64_t cols_pad, int64_t ld_dst, uint32_t mag_bits,
+                                                              float zero_above, unsigned long long* __restrict__ nz,
+                                                              int vec) {
+    static_assert(R == 64 || R == 128 || R == 256, "one group per 64-column slice");
+    constexpr bool REG = (R & 0x55555555) == R;
+    constexpr int T = R / 4;   // steps per chain
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // items: (column slice y, row tile rt), the row tiles of a slice
+    // consecutive; work-group i takes items i, i + gridDim.x, ...
+    const int64_t ntile = cdiv(rows, XR_ROWS), nitems = ntile * cdiv(cols_pad, XR_SLICE);
+    int64_t item = blockIdx.x;
+    if (item >= nitems) return;
+    int64_t y = item / ntile, rt = item - y * ntile;
+
+    float bp[16], bn[16];   // m (-1)^s(q, lane & 15) and its negation
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        bp[q] = __uint_as_float(mag_bits | (hd_sign<REG>((uint32_t)q, (uint32_t)(lane & 15)) << 31));
+        bn[q] = -bp[q];
+    }
+    unsigned cnt = 0;
+    // the wave's columns of slice y: output c0 .. c0 + 63 (inside one group
+    // when active: cols_pad is a multiple of R >= 64), inputs from g0
+    auto slice_c0 = [&](int64_t yy) { return yy * XR_SLICE + 64 * w; };
+    // offset of (this lane's row of tile t, the group's first column); rows
+    // past the matrix read its last row (their products are never stored)
+    auto row_off = [&](int64_t yy, int64_t tile) {
+        const int64_t c = slice_c0(yy);
+        return std::min<int64_t>(tile * XR_ROWS + lane, rows - 1) * ld_src + (c < cols_pad ? (c / R) * R : 0);
+    };
+    Raw4<DT> a[XW_PF];
+    auto load_step = [&](int slot, int64_t off, int t) { a[slot].load(src, off + 4 * t); };
+    int64_t off = row_off(y, rt);
+    if (slice_c0(y) < cols_pad) {
+#pragma unroll
+        for (int t = 0; t < XW_PF; ++t) load_step(t, off, t);
+    }
+    for (;;) {
+        const int64_t c0 = slice_c0(y);
+        const bool active = c0 < cols_pad;               // wave-uniform
+        const int64_t g0 = (c0 / R) * R;
+        const uint32_t uhi = (uint32_t)((c0 - g0) >> 6); // U >> 2 of its four tiles
+        // outliers this lane counts: the group's first slice, its own row
+        const unsigned mine = (ZA && active && c0 == g0 && rt * XR_ROWS + lane < rows) ? 1u : 0u;
+        const bool more = item + gridDim.x < nitems;
+        const int64_t ny = (item + gridDim.x) / ntile, nrt = (item + gridDim.x) - ny * ntile;
+        const bool nact = more && slice_c0(ny) < cols_pad;
+        const int64_t noff = nact ? row_off(ny, nrt) : off;
+        f32x16 acc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
+        auto step = [&](auto TT) {
+            constexpr int t = decltype(TT)::value, kh = t / 4, q4 = t % 4, slot = t % XW_PF;
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = a[slot].get(i);
+            if constexpr (ZA) {
+                // outliers become 0
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float m = fabsf(x[i]);
+                    cnt += m > zero_above ? mine : 0u;
+                    x[i] = m > zero_above ? 0.0f : x[i];
+                }
+                asm volatile("" : "+v"(cnt));   // count now: the compares' masks die here
+            }
+            // refill the slot: a later step of this item, or the next item's
+            if constexpr (t + XW_PF < T) {
+                if (active) load_step(slot, off, t + XW_PF);
+            } else {
+                if (nact) load_step(slot, noff, t + XW_PF - T);
+            }
+            if constexpr (R >= 128) {
+                const uint32_t gs = hd_sign<REG>((uint32_t)kh >> 2, uhi) << 31;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(__float_as_uint(x[i]) ^ gs);
+            }
+            // the step's four A values in four registers before its MFMAs, so
+            // that no A register is rewritten while an MFMA still reads it
+            asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int q = 4 * q4 + qq;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool neg = hd_sign<REG>((uint32_t)(kh & 3), (uint32_t)c) != 0;
+                    acc[c] = mfma_k1(x[qq], neg ? bn[q] : bp[q], acc[c]);
+                }
+            }
+        };
+        static_for<0, T>(step);
+        if (active) {
+            const int64_t rb = rt * XR_ROWS + 4 * (lane >> 4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float* o = dst + c0 + 16 * c + (lane & 15);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t r = rb + 16 * (v >> 2) + (v & 3);
+                    if (r < rows) o[r * ld_dst] = acc[c][v];
+                }
+            }
+        }
+        if (!more) break;
+        item += gridDim.x;
+        y = ny;
+        rt = nrt;
+        off = noff;
+    }
+    if (ZA) flush_zeroed(cnt, nz);
+}
+
+// Work-groups of a 256-thread kernel without dynamic LDS that fit the
+// current device at once (0 when the runtime cannot say).
+static int64_t resident_wgs(const void* kernel) {
+    int dev = 0, per_cu = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return (int64_t)per_cu * cus;
+}
+
+// One round of work-groups (as many as are resident at once, each taking
+// whole items in turn), so no partial second round idles the chip; fewer
+// than two rounds' worth of items run one per work-group.
+template <int R, int DT, bool ZA>
+static void launch_rows_wave(const void* src, int64_t rows, int64_t cols, int64_t ld_src, float* dst,
+                             int64_t cols_pad, int64_t ld_dst, uint32_t mb, float zero_above,
+                             unsigned long long* nz, int vec, hipStream_t st) {
+    const void* k = reinterpret_cast<const void*>(&rot_rows_wave_kernel<R, DT, ZA>);
+    static int64_t cap = 0;   // the same on every device this library runs on (one GPU model)
+    if (cap <= 0) cap = resident_wgs(k);
+    const int64_t n = cdiv(rows, XR_ROWS) * cdiv(cols_pad, XR_SLICE), c = cap > 0 ? cap : 512;
+    // below two rounds of items, one item per work-group balances best
+    const int64_t per = n >= 2 * c ? cdiv(n, c) : 1;
+    const int64_t grid = std::max<int64_t>(1, cdiv(n, per));
+    hipLaunchKernelGGL((rot_rows_wave_kernel<R, DT, ZA>), dim3((unsigned)grid), dim3(256), 0, st, src, rows, cols,
+                       ld_src, dst, cols_pad, ld_dst, mb, zero_above, nz, vec);
+}
+
 // ------------------------------------------------------------------ columns
 
 constexpr int XC_ROWS = 256;   // T rows per work-group: 4 waves x 4 tiles x 16
@@ -527,14 +710,25 @@ static int rows_exact(const void* src, int dt, int64_t rows, int64_t cols, int64
                            else if (dt == IC_DTYPE_F32) ICQ_XR(RR, IC_DTYPE_F32, false); \
                            else if (dt == IC_DTYPE_BF16) ICQ_XR(RR, IC_DTYPE_BF16, false); \
                            else ICQ_XR(RR, IC_DTYPE_F16, false); } while (0)
+    // rot_rows_wave_kernel's domain: out of place, whole groups, vector loads
+    const bool wave = !tri && src != (const void*)dst && (vec & 1) && cols == cols_pad;
+#define ICQ_XW(RR, D, Z) launch_rows_wave<RR, D, Z>(src, rows, cols, ld_src, dst, cols_pad, ld_dst, mb, zero_above, \
+                                                    nz, vec, st)
+#define ICQ_XW_Z(RR, D) do { if (zero_above > 0.0f) ICQ_XW(RR, D, true); else ICQ_XW(RR, D, false); } while (0)
+#define ICQ_XW_DT(RR) do { if (dt == IC_DTYPE_F32) ICQ_XW_Z(RR, IC_DTYPE_F32); \
+                           else if (dt == IC_DTYPE_BF16) ICQ_XW_Z(RR, IC_DTYPE_BF16); \
+                           else ICQ_XW_Z(RR, IC_DTYPE_F16); } while (0)
     switch (rot) {
         case 16: ICQ_XR_DT(16); break;
         case 32: ICQ_XR_DT(32); break;
-        case 64: ICQ_XR_DT(64); break;
-        case 128: ICQ_XR_DT(128); break;
-        case 256: ICQ_XR_DT(256); break;
+        case 64: if (wave) ICQ_XW_DT(64); else ICQ_XR_DT(64); break;
+        case 128: if (wave) ICQ_XW_DT(128); else ICQ_XR_DT(128); break;
+        case 256: if (wave) ICQ_XW_DT(256); else ICQ_XR_DT(256); break;
         default: ICQ_XR_DT(512); break;
     }
+#undef ICQ_XW_DT
+#undef ICQ_XW_Z
+#undef ICQ_XW
 #undef ICQ_XR_DT
 #undef ICQ_XR
     IC_CHECK_LAUNCH();
