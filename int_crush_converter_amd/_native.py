@@ -108,15 +108,15 @@ PROFILE_KERNELS = {
     "panel64_kernel": (["chol_panel"], "latency"),
     "sweep16_kernel / sweep4_kernel": (["sweep"], "latency"),
     "greedy_sb_kernel": (["greedy"], "latency"),
-    "rot_rows_exact_kernel": (["rotate_w"], "mfma"),
+    "rot_rows_wave_kernel / rot_rows_exact_kernel": (["rotate_w"], "mfma"),
     "rot_cols_exact_kernel + rot_rows_exact_kernel": (["rotate_h"], "mfma"),
-    "rtn_scales_kernel": (["rtn_scales"], "latency"),
+    "rtn_clip_reg_kernel / rtn_clip_kernel": (["rtn_scales"], "latency"),   # VALU-bound: a share of the step
     "rtn_quant_kernel": (["rtn_quant_pack"], "hbm"),
     "quant_error_partial": (["verify"], "hbm"),
     "fsum_group_kernel": (["permute_sum"], "hbm"),   # (fsum_block_kernel: its fallback for cascade groups above 32)
     "piso_kernel": (["piso"], "latency"),
 }
-FWHT_KERNELS = {"rot_rows_exact_kernel": ("rotate256_coal / rotate_rows_reg", "hbm"),
+FWHT_KERNELS = {"rot_rows_wave_kernel / rot_rows_exact_kernel": ("rotate256_coal / rotate_rows_reg", "hbm"),
                 "rot_cols_exact_kernel + rot_rows_exact_kernel": ("rotate_cols256_kernel + rotate256_coal", "hbm")}
 
 
