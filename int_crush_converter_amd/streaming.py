@@ -5,8 +5,10 @@ converter/pipeline.py:268, 1116-1121).
 * ``SafetensorsIndex`` parses a file's header: tensors in data order, which
   is the order ``load_file`` returns them in (the reference's loop order).
 * ``Prefetcher`` reads the next layers' bytes on a host thread into pinned
-  buffers and copies them to the GPU on a copy stream while the current
-  layer computes.
+  buffers (each large tensor split over several reader threads: one
+  thread's copies out of the page cache run at well under the host's
+  memory bandwidth) and copies them to the GPU on a copy stream while the
+  current layer computes.
 * ``StreamWriter`` writes outputs as they are produced: device results are
   copied to pooled pinned chunks on a D2H stream, host threads write them at
   the offsets assigned on arrival (positional writes, in parallel), and
@@ -19,6 +21,7 @@ converter/pipeline.py:268, 1116-1121).
 
 from __future__ import annotations
 
+import concurrent.futures as cf
 import json
 import os
 import queue
@@ -61,23 +64,44 @@ class SafetensorsIndex:
         _, _, b, e = self.entries[name]
         return e - b
 
-    def read(self, name: str, out: torch.Tensor | None = None) -> torch.Tensor:
+    def read(self, name: str, out: torch.Tensor | None = None, pool: cf.Executor | None = None,
+             parts: int = 1) -> torch.Tensor:
         """The tensor as a CPU tensor (into `out`'s storage when given: a
-        uint8 buffer of at least nbytes, e.g. pinned)."""
+        uint8 buffer of at least nbytes, e.g. pinned).  With `pool`, a
+        tensor of at least READ_SPLIT bytes is read as up to `parts`
+        positional reads of consecutive byte ranges on the pool's threads."""
         dtype, shape, b, e = self.entries[name]
         n = e - b
         buf = out[:n] if out is not None else torch.empty(n, dtype=torch.uint8)
-        with open(self.path, "rb", buffering=0) as f:
-            f.seek(b)
-            mv = memoryview(buf.numpy())
-            got = 0
-            while got < n:
-                r = f.readinto(mv[got:])
-                if not r:
-                    raise IOError(f"{self.path}: short read of {name}")
-                got += r
+        mv = memoryview(buf.numpy())
+        fd = os.open(self.path, os.O_RDONLY)
+        try:
+            k = max(1, min(parts, n // READ_SPLIT)) if pool is not None else 1
+            step = -(-n // k)
+            spans = [(o, min(n, o + step)) for o in range(0, n, step)] if n else []
+            if k == 1:
+                for lo, hi in spans:
+                    _pread_into(fd, mv[lo:hi], b + lo, self.path, name)
+            else:
+                futs = [pool.submit(_pread_into, fd, mv[lo:hi], b + lo, self.path, name) for lo, hi in spans]
+                for f in futs:
+                    f.result()
+        finally:
+            os.close(fd)
         t = buf.view(dtype) if n else torch.empty(0, dtype=dtype)
         return t.reshape(shape)
+
+
+READ_SPLIT = 8 << 20      # smallest byte range a parallel read hands to one thread
+
+
+def _pread_into(fd: int, mv: memoryview, pos: int, path: str, name: str) -> None:
+    got = 0
+    while got < len(mv):
+        r = os.preadv(fd, [mv[got:]], pos + got)
+        if not r:
+            raise IOError(f"{path}: short read of {name}")
+        got += r
 
 
 class PinnedPool:
@@ -112,8 +136,10 @@ class Prefetcher:
     overlaps the caller's work on layer k.  Names must be requested in
     order."""
 
-    def __init__(self, index: SafetensorsIndex, names: list[str], device, depth: int = 2):
+    def __init__(self, index: SafetensorsIndex, names: list[str], device, depth: int = 2, readers: int = 8):
         self.index = index
+        self.readers = readers
+        self.pool = cf.ThreadPoolExecutor(max_workers=readers) if readers > 1 else None
         self.names = list(names)
         self.device = device
         cap = max([index.nbytes(n) for n in self.names] + [1])
@@ -135,7 +161,7 @@ class Prefetcher:
                 buf = self.free.get()
                 if buf is None:
                     return
-                t = self.index.read(name, buf)
+                t = self.index.read(name, buf, self.pool, self.readers)
                 self.ready.put((name, buf, t))
         except BaseException as e:  # surfaced to the consumer
             self.error = e
@@ -177,6 +203,9 @@ class Prefetcher:
         for g, buf, ev in self.inflight.values():
             ev.synchronize()
         self.inflight.clear()
+        if self.pool is not None:
+            self.pool.shutdown(wait=True)
+            self.pool = None
         for b in self.bufs:
             POOL.give(b)
         self.bufs = []
