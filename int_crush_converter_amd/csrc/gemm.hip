@@ -73,16 +73,32 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
 // fraction of the chip.
 constexpr int64_t SMALL_TILE_LIMIT = 256;
 constexpr int64_t CHIP_CUS = 256;
-// C = X^T X with K from max(tile row, tile column) (the inverse's X^T X on a
-// triangular grid): the (0, 0) tile runs all of K.  When that one tile,
-// sharing its CU with a second work-group, outlasts the average 128-tile
-// work per CU, the launch is bound by it, and 64-tiles cut it to a quarter
-// (same chunks of K, same order of accumulation).
+// Tiles whose K range depends on their position (the inverse's merges, K
+// from the tile column or up to the tile row, and its X^T X, K from max(tile
+// row, tile column)): when the longest 128-tile, sharing its CU with a
+// second work-group, outlasts the average 128-tile work per CU, the launch
+// is bound by that one tile, and 64-tiles cut it to a quarter (same chunks
+// of K, same order of accumulation, so the same results).
 static bool long_tile_bound(const GemmArgs& g) {
-    const int64_t tm = cdiv(g.M, 128);
-    double total = 0.0;   // K stages over all kept tiles
-    for (int64_t j = 0; j < tm; ++j) total += (double)(j + 1) * std::max<int64_t>(0, g.K - 128 * j) / BK;
-    return 2.0 * g.K / BK > total * g.batch / CHIP_CUS;
+    if (g.krange == KR_FULL) return false;
+    const int64_t tm = cdiv(g.M, 128), tn = cdiv(g.N, 128);
+    double total = 0.0, longest = 0.0;   // K stages
+    for (int64_t ti = 0; ti < tm; ++ti)
+        for (int64_t tj = 0; tj < tn; ++tj) {
+            const int64_t i0 = ti * 128, j0 = tj * 128;
+            if (g.cmask == CMASK_LOWER && i0 + 127 < j0) continue;
+            if (g.cmask == CMASK_UPPER && j0 + 127 < i0) continue;
+            int64_t klo = 0, khi = g.K;
+            if (g.krange == KR_FROM_MAXIJ) klo = std::max(i0, j0);
+            else if (g.krange == KR_FROM_J) klo = j0;
+            else if (g.krange == KR_TO_I) khi = std::min(g.K, i0 + 128);
+            else if (g.krange == KR_FROM_I) klo = i0;
+            klo = std::min((klo / 4) * 4, g.K);
+            const double st = (double)cdiv(std::max<int64_t>(0, khi - klo), BK);
+            total += st;
+            longest = std::max(longest, st);
+        }
+    return 2.0 * longest > total * g.batch / CHIP_CUS;
 }
 constexpr int64_t SHORT_K = 256, SHORT_K_TILE_LIMIT = 1024;
 
@@ -100,7 +116,7 @@ int gemm_f32(const GemmArgs& g, hipStream_t st) {
     bool tri;
     const int64_t t128 = tile_count<128>(g, tri) * g.batch;
     if (t128 < SMALL_TILE_LIMIT || (g.K <= SHORT_K && t128 < SHORT_K_TILE_LIMIT)) return launch_gemm<64>(g, aligned, st);
-    if (tri && g.krange == KR_FROM_MAXIJ && long_tile_bound(g)) return launch_gemm<64>(g, aligned, st);
+    if (long_tile_bound(g)) return launch_gemm<64>(g, aligned, st);
     return launch_gemm<128>(g, aligned, st);
 }
 
