@@ -61,6 +61,13 @@ struct SweepArgs {
     int8_t* Q; int64_t ldq;         // codes, same column indexing as W
     float* E; int64_t lde; int64_t eg;   // errors [rows, nb] per group (group stride eg)
     int mode;
+    // Row sweep only (whole blocks of one matrix): the next block's update by
+    // this block's errors, Wn = Cn - E Hinv[blk, next] over 128 columns
+    // (pitch ldw), run by the sweep's own work-groups; Hn = Hinv[blk, next]
+    // (pitch ldh).  Hn null: no such update.
+    const float* Hn = nullptr;
+    const float* Cn = nullptr;
+    float* Wn = nullptr;
 };
 
 __device__ __forceinline__ float rdlanef(float v, int l) {
@@ -502,6 +509,17 @@ __global__ __launch_bounds__(64 * WV) void sweep4_kernel(SweepArgs a) {
 // [2^-60, 2^61)) sends the wave's rows through the block once more, one lane
 // per row from LDS, with the IEEE-exact test on every division (rare).  WV
 // waves share the staged Hinv block.
+//
+// FUSE: the work-group then applies the next block's update by this block's
+// errors to its own rows, W[:, next] = C - E_blk Hinv[blk, next] (the first
+// update of the lazy-batch sequence that reaches the next block), on the
+// matrix cores: wave w takes rows 16 (w / 4) .. + 15 and columns
+// 32 (w % 4) .. + 31, the errors pass through LDS as the A operand, and
+// Hinv[blk, next] and C are fetched into registers while the block is swept.
+// Every output is formed as gemm_f32 forms it for a single chunk (fresh
+// accumulators, one 16x16x4 MFMA step per 4 k in increasing k, then
+// -(0 + sum) + C), so the result is that GEMM's bit for bit, without its
+// launch.
 constexpr int SR_L = 16;             // lanes per row
 constexpr int SR_M = SW_NB / SR_L;   // columns per lane
 constexpr int SR_ROWS = 64 / SR_L;   // rows per wave
@@ -512,7 +530,9 @@ __device__ __forceinline__ float row_bcast16(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xf, 0xf, false));
 }
 
-template <int MODE, bool ZP, int WV>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int MODE, bool ZP, int WV, bool FUSE>
 __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
     __shared__ __align__(16) float Hq[SW_NB][SR_L][SR_M];   // Hq[j][p][m] = Hinv[j][16 m + p]
     __shared__ __align__(16) float4 piv[SW_NB];          // {Hinv_jj, 1 / d_j, d_j in the fast domain, 0}
@@ -567,6 +587,28 @@ __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
             sc[m] = v;
             scr[m] = 1.0f / v;
         }
+    }
+    // FUSE: this wave's B operand (Hinv[blk, next], k = 4 s + lane / 16,
+    // column 32 (w % 4) + 16 c + lane % 16) and C elements (row
+    // 16 (w / 4) + 4 (lane / 16) + v of the work-group, same columns), in
+    // flight during the sweep; issued after the sweep's own loads
+    const int fw = tid >> 6, frt = fw >> 2, fcol = 32 * (fw & 3) + (t & 15), fk = t >> 4;
+    float fb[FUSE ? 2 : 1][FUSE ? SW_NB / 4 : 1], fc[FUSE ? 2 : 1][4];
+    if constexpr (FUSE) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int ldh = (int)a.ldh;   // (SW_NB - 1) ldh + 2 SW_NB < 2^31 (launch_sweep checks it)
+#pragma unroll
+        for (int s = 0; s < SW_NB / 4; ++s)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) fb[c][s] = a.Hn[(4 * s + fk) * ldh + fcol + 16 * c];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t r = (int64_t)blockIdx.x * (WV * SR_ROWS) + 16 * frt + 4 * fk + v;
+            const float* cr = a.Cn + (r < a.rows ? r : a.rows - 1) * a.ldw + fcol;
+            fc[0][v] = cr[0];
+            fc[1][v] = cr[16];
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     const float s_rrow = 1.0f / s_row;
     const bool srow_ok = div_b_ok(s_row);
@@ -672,10 +714,55 @@ __global__ __launch_bounds__(64 * WV) void sweep16_kernel(SweepArgs a) {
             a.E[row * a.lde + c] = ev[m];
         }
     }
+    if constexpr (FUSE) {
+        // the errors, row-major in LDS (the rerun rows; a wave rewrites only
+        // its own rows, which its rerun has finished with), then every wave's
+        // 16 x 32 share of E Hinv[blk, next] with the gemm_f32 operand layout:
+        // A[i = lane % 16][k = 4 s + lane / 16], B[k][j = lane % 16],
+        // accumulator v at row 4 (lane / 16) + v, column lane % 16
+#pragma unroll
+        for (int m = 0; m < SR_M; ++m) Xr[rw][SR_L * m + p] = ev[m];
+        __syncthreads();
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < SW_NB / 4; ++s) {
+            const float av = Xr[16 * frt + (t & 15)][4 * s + fk];
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av, fb[0][s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av, fb[1][s], acc1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t r = (int64_t)blockIdx.x * (WV * SR_ROWS) + 16 * frt + 4 * fk + v;
+            if (r < a.rows) {
+                float* wr = a.Wn + r * a.ldw + fcol;
+                // gemm_f32's single-chunk epilogue: run = 0 + sum; C <- -run + C
+                const float run0 = 0.0f + acc0[v], run1 = 0.0f + acc1[v];
+                wr[0] = -run0 + fc[0][v];
+                wr[16] = -run1 + fc[1][v];
+            }
+        }
+    }
+}
+
+// Waves per work-group of the row sweep for `rows` rows (4 rows per wave,
+// one work-group per CU where that covers the rows).
+static int row_sweep_waves(int64_t rows) {
+    const int64_t need = cdiv(cdiv(rows, SR_ROWS), 256);
+    return need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
+}
+
+// Whether the row sweep takes the next block's update (SweepArgs::Hn): whole
+// blocks of one matrix, at most 12 waves per work-group (the fetched operands
+// take 72 more registers per lane), and 32-bit offsets across the two Hinv
+// blocks.
+static bool row_sweep_fuses(int64_t rows, int groups, int nb, int64_t ldh) {
+    return groups == 1 && nb == SW_NB && row_sweep_waves(rows) <= 12 &&
+           (SW_NB - 1) * ldh + 2 * SW_NB < (int64_t(1) << 31);
 }
 
 static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
     IC_REQUIRE(a.nb >= 1 && a.nb <= SW_NB, "sweep: block size must be in [1, 128]");
+    IC_REQUIRE(!a.Hn || row_sweep_fuses(a.rows, groups, a.nb, a.ldh), "sweep: no fused update for this shape");
     const bool wide = a.rows * groups >= SW_THROUGHPUT_ROWS;
     const int64_t wgs = cdiv(a.rows, wide ? sw_rows<SW_LPR_THROUGHPUT>() : sw_rows<SW_LPR_LATENCY>());
     ProfScope prof_scope(st, PT_SWEEP, (double)groups * a.rows * a.nb * (a.nb - 1.0),
@@ -701,17 +788,24 @@ static int launch_sweep(const SweepArgs& a, int groups, hipStream_t st) {
         // as one work-group per CU needs to cover the rows
         // the kernel addresses the staged Hinv block with 32-bit offsets
         IC_REQUIRE((SW_NB - 1) * a.ldh + SW_NB < (int64_t(1) << 31), "sweep: Hinv pitch too large");
-        const int64_t need = cdiv(cdiv(a.rows, SR_ROWS), 256);
-        const int WVs = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
+        const int WVs = row_sweep_waves(a.rows);
         const dim3 g16((unsigned)cdiv(a.rows, WVs * SR_ROWS));
         const bool zp = a.zp != nullptr;
-#define ICQ_SWEEP16(M, Z, W) hipLaunchKernelGGL((sweep16_kernel<M, Z, W>), g16, dim3(64 * W), 0, st, a)
-#define ICQ_SWEEP16_WV(M, Z)                    \
-    switch (WVs) {                              \
-        case 4: ICQ_SWEEP16(M, Z, 4); break;    \
-        case 8: ICQ_SWEEP16(M, Z, 8); break;    \
-        case 12: ICQ_SWEEP16(M, Z, 12); break;  \
-        default: ICQ_SWEEP16(M, Z, 16); break;  \
+#define ICQ_SWEEP16(M, Z, W, F) hipLaunchKernelGGL((sweep16_kernel<M, Z, W, F>), g16, dim3(64 * W), 0, st, a)
+#define ICQ_SWEEP16_WV(M, Z)                                   \
+    if (a.Hn) {                                                \
+        switch (WVs) {                                         \
+            case 4: ICQ_SWEEP16(M, Z, 4, true); break;         \
+            case 8: ICQ_SWEEP16(M, Z, 8, true); break;         \
+            default: ICQ_SWEEP16(M, Z, 12, true); break;       \
+        }                                                      \
+    } else {                                                   \
+        switch (WVs) {                                         \
+            case 4: ICQ_SWEEP16(M, Z, 4, false); break;        \
+            case 8: ICQ_SWEEP16(M, Z, 8, false); break;        \
+            case 12: ICQ_SWEEP16(M, Z, 12, false); break;      \
+            default: ICQ_SWEEP16(M, Z, 16, false); break;      \
+        }                                                      \
     }
         if (a.mode == SWEEP_GPTQ) {
             if (zp) ICQ_SWEEP16_WV(SWEEP_GPTQ, true)
@@ -815,8 +909,6 @@ static int layer_sweep(const float* Win, float* W, int64_t ldw, int64_t rows, in
             // the sweep reads W (never writes it); the first block is read from Win
             SweepArgs a{b0 == 0 ? const_cast<float*>(Win) : W, ldw, rows, b0, nb, gw, Hinv + b0 * ldh + b0, ldh,
                         hg, s, lds, zp, qmin, qmax, Q, ldq, E + (b0 - sb0), SB, rows * SB, mode};
-            int rc = launch_sweep(a, (int)groups, st);
-            if (rc) return rc;
             // Fenwick order inside the super-block: after block j, the errors
             // of blocks j - lb + 1 .. j (lb = lowest set bit of j + 1) go to
             // blocks j + 1 .. j + lb.  Every block m receives the errors of
@@ -827,9 +919,21 @@ static int layer_sweep(const float* Win, float* W, int64_t ldw, int64_t rows, in
             // about n log2(n) / 2.  Blocks before the last one are whole.
             const int64_t lb = (j + 1) & -(j + 1);
             const int64_t c0 = b0 + nb, c1 = std::min<int64_t>(sbe, b0 + nb + (lb - 1) * B + B);
-            if (c0 < c1) {
-                const int64_t e0 = (j + 1 - lb) * B;
-                rc = update(e0, sb0 + e0, (j + 1) * B - e0, c0, c1 - c0, sb0 == 0 && e0 == 0);
+            const int64_t e0 = (j + 1 - lb) * B;
+            const bool first = sb0 == 0 && e0 == 0;
+            // lb = 1 with a whole next block: the update is this block's errors
+            // times Hinv[blk, next] (K = one chunk of 128), which the row sweep
+            // applies itself
+            const bool fused = lb == 1 && c1 - c0 == SW_NB && row_sweep_fuses(rows, (int)groups, nb, ldh);
+            if (fused) {
+                a.Hn = Hinv + b0 * ldh + c0;
+                a.Cn = (first && Win != W ? Win : W) + c0;
+                a.Wn = W + c0;
+            }
+            int rc = launch_sweep(a, (int)groups, st);
+            if (rc) return rc;
+            if (c0 < c1 && !fused) {
+                rc = update(e0, sb0 + e0, (j + 1) * B - e0, c0, c1 - c0, first);
                 if (rc) return rc;
             }
         }
