@@ -11,20 +11,42 @@ using namespace gk;
 // epilogue C <- alpha * sum + beta * C.
 // Two work-groups per CU (one wave of each per SIMD) hide each other's
 // barriers and LDS staging: the register budget is held to 256 per lane.
+// remap bit 0: the XCD-aware tile order (xcd_tile); bit 1: batch entries of
+// odd index walk their tiles in reverse.  The hardware deals the work-groups
+// of consecutive batch entries to the CUs in the same pattern, so in a launch
+// that is resident in one round a CU would otherwise get the same tile
+// position, and so the same K range, from every entry.
 template <int TA, int TB, bool CHECK, int T, int CHUNK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f32_kernel(GemmArgs g,
                                                                                               int64_t ntiles,
                                                                                               int remap) {
     __shared__ __attribute__((aligned(16))) float lds[2 * Geo<T>::TILE_F];
     TileRange tr;
-    if (remap) {
-        if (!xcd_tile<T>(g, blockIdx.x, tr)) return;
+    const bool mirror = (remap & 2) && (blockIdx.z & 1);
+    if (remap & 1) {
+        if (!xcd_tile<T>(g, blockIdx.x, tr, mirror)) return;
     } else {
         if ((int64_t)blockIdx.x >= ntiles) return;
-        tr = tile_of<T>(g, blockIdx.x);
+        tr = tile_of<T>(g, mirror ? ntiles - 1 - (int64_t)blockIdx.x : (int64_t)blockIdx.x);
     }
     if (tr.skip) return;
     gemm_tile<TA, TB, CHECK, T, CHUNK>(g, tr, blockIdx.z, lds);
+}
+
+constexpr int64_t CHIP_CUS = 256;
+
+// Work-groups of gemm_f32_kernel<0, 0, CHECK, T, CHUNK_SUM> resident per CU
+// (the instances of one T and CHECK differ little in registers).
+template <int T, bool CHECK>
+static int resident_per_cu() {
+    static const int n = [] {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, gemm_f32_kernel<0, 0, CHECK, T, CHUNK_SUM>, 256, 0) !=
+            hipSuccess)
+            v = 1;
+        return v > 0 ? v : 1;
+    }();
+    return n;
 }
 
 template <int T>
@@ -35,12 +57,20 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
     IC_REQUIRE(tiles < (1LL << 30) && g.batch <= 65535, "gemm_f32: problem too large");
     // triangular enumerations keep their own (long-K-first) order; other
     // grids with at least NXCD tile rows use the XCD row assignment
-    const int remap = (!tri && tm >= NXCD) ? 1 : 0;
-    const int64_t grid = remap ? cdiv(tm, NXCD) * tn * NXCD : tiles;
+    const int xcd = (!tri && tm >= NXCD) ? 1 : 0;
+    const int64_t grid = xcd ? cdiv(tm, NXCD) * tn * NXCD : tiles;
     IC_REQUIRE(grid < (1LL << 23), "gemm_f32: problem too large");
     const dim3 gd((unsigned)grid, 1, (unsigned)g.batch);
     // whole tiles and whole K stages everywhere: the kernel without bounds checks
     const bool exact = aligned && g.M % T == 0 && g.N % T == 0 && g.K % BK == 0;
+    // batched rectangular launches whose K range depends on the tile position
+    // and that are resident in one round: odd batch entries in reverse, so
+    // that every CU gets long and short tiles alike
+    int remap = xcd;
+    if (g.batch > 1 && !tri && g.krange != KR_FULL) {
+        const int per_cu = exact ? resident_per_cu<T, false>() : resident_per_cu<T, true>();
+        if (grid * g.batch <= (int64_t)per_cu * CHIP_CUS) remap |= 2;
+    }
     // exact rank-kc update sequences subtract chunk by chunk; everything else
     // sums the chunks and applies alpha, beta once.  With one chunk (K <= kc)
     // the two are the same: fl(-P + C) = fl(C - P), and the sum form keeps C
@@ -72,7 +102,6 @@ static int launch_gemm(const GemmArgs& g, bool aligned, hipStream_t st) {
 // there the 128-tile's few long stages leave the tail of the launch on a
 // fraction of the chip.
 constexpr int64_t SMALL_TILE_LIMIT = 256;
-constexpr int64_t CHIP_CUS = 256;
 // Tiles whose K range depends on their position (the inverse's merges, K
 // from the tile column or up to the tile row, and its X^T X, K from max(tile
 // row, tile column)): when the longest 128-tile, sharing its CU with a

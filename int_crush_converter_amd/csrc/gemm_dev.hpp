@@ -122,15 +122,18 @@ __device__ TileRange tile_of(const GemmArgs& g, int64_t id) {
 // panels in its L2); row-dependent work (KR_TO_I, KR_FROM_I) walks rows
 // one after another, longest first, so that every engine gets every 4th
 // tile of every row.  False: no tile.
+// mirror: the XCD's sequence of tiles reversed (batch entries of odd index,
+// see gemm_f32_kernel).
 template <int T>
-__device__ __forceinline__ bool xcd_tile(const GemmArgs& g, int64_t b, TileRange& t) {
+__device__ __forceinline__ bool xcd_tile(const GemmArgs& g, int64_t b, TileRange& t, bool mirror = false) {
     const int64_t tm = (g.M + T - 1) / T, tn = (g.N + T - 1) / T;
     const int x = (int)(b % NXCD);
-    const int64_t l = b / NXCD;
+    int64_t l = b / NXCD;
     const int64_t full = tm / NXCD, rem = tm - full * NXCD;
     const int lastpos = (full & 1) ? (NXCD - 1 - x) : x;
     const int64_t nr = full + (lastpos < rem ? 1 : 0);   // tile rows of XCD x
     if (l >= nr * tn) return false;
+    if (mirror) l = nr * tn - 1 - l;
     int64_t q, tj;                                       // q: round = row index within XCD x
     if (g.krange == KR_TO_I || g.krange == KR_FROM_I) {
         q = l / tn;
