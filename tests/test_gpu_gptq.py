@@ -546,6 +546,26 @@ def test_sweep_one_group_many_rows_bit_exact(gpu_dev, bits, N):
     assert torch.equal(Qg, Q)
 
 
+@pytest.mark.parametrize("M", [1000, 4100, 12283])
+def test_sweep_fused_next_block_update_bit_exact(gpu_dev, M):
+    """Four 128-column blocks given the same Hinv, with 4, 8 and 12 waves per
+    work-group of the row sweep (M = 1000, 4100, 12283; none a multiple of
+    the work-group's rows): the sweeps of blocks 0 and 2 also apply the next
+    block's first lazy update, and the codes equal the CPU sweep's."""
+    from int_crush_converter_amd.gptq import row_params, sweep
+    g = torch.Generator().manual_seed(M)
+    N = 512
+    W = ref.rotate_weights(torch.randn(M, N, generator=g) * 0.02, 256)
+    Hinv = ref.prepare_hinv(ref.rotate_hessian(lognormal_hessian(N, 1024, 23), 256), 0.01)
+    s, z = ref.gptq_row_params(W, 4, True)
+    Q = torch.zeros(M, N, dtype=torch.int8)
+    ref.gptq_block(W.clone(), Q, s, Hinv, 0, N, 128, -8, 7, z)
+    Wg = W.to(gpu_dev)
+    s32, z32, _, _ = row_params(Wg, 4, True)
+    Qg = sweep(Wg.clone(), Hinv.to(gpu_dev), s32, z32, 4, 128).cpu()
+    assert torch.equal(Qg, Q)
+
+
 def test_sweep_many_rows_multi_block_close(gpu_dev):
     """12288 rows over 4 blocks of 128 (8 lanes per row, lazy updates on the
     matrix cores) given the same Hinv: >= 99.9 % of codes equal."""
